@@ -1,0 +1,127 @@
+// Residual add + RMSNorm over rows of bf16 (config: T x 2560).
+//
+// Arithmetic (rounding points of core/kernels/add_norm/rows.py:65-79, which are
+// mx.fast.rms_norm's):
+//   s_i = bf16(x_i + b_i)
+//   inv = 1 / sqrt(sum_i s_i^2 / H + eps)          (fp32, IEEE sqrt and divide)
+//   n_i = bf16(w_i * bf16(s_i * inv))
+//
+// Layout: one wave64 per row. Lane l owns the 16-byte vectors l, l+64, l+128, ...
+// of the row, so every load and store instruction of the wave covers 1 KiB of
+// contiguous memory. All loads of x and the branch are issued before any math, the
+// sum of squares is a butterfly over the wave, and both outputs are written in the
+// same pass: each tensor crosses HBM exactly once. The norm weight (H * 2 bytes) is
+// shared by every row and stays in L2.
+#include "common.hpp"
+#include "host.hpp"
+
+namespace omnia {
+namespace {
+
+constexpr int kMaxVectorsPerLane = 16;  // hidden <= 64 lanes * 16 vectors * 8 = 8192
+
+template <int VPL>
+__global__ __launch_bounds__(256) void add_rms_norm_kernel(
+    const u32x4* __restrict__ x, const u32x4* __restrict__ branch,
+    const u32x4* __restrict__ weight, u32x4* __restrict__ summed,
+    u32x4* __restrict__ normalized, int64_t rows, int vecs, float hidden, float eps) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row =
+      static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= rows) return;  // whole wave leaves together; no barrier follows
+  const int64_t base = row * vecs;
+
+  u32x4 xv[VPL], bv[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int v = lane + i * kWave;
+    if (v < vecs) {
+      xv[i] = load_nt(x + base + v);
+      bv[i] = load_nt(branch + base + v);
+    }
+  }
+
+  float s[VPL][8];
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int v = lane + i * kWave;
+    if (v < vecs) {
+      float a[8], b[8];
+      unpack8(xv[i], a);
+      unpack8(bv[i], b);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        s[i][j] = round_bf16(a[j] + b[j]);
+        acc += s[i][j] * s[i][j];
+      }
+    }
+  }
+  acc = group_sum<kWave>(acc);
+  const float inv = 1.0f / sqrtf(acc / hidden + eps);
+
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int v = lane + i * kWave;
+    if (v < vecs) {
+      float w[8], n[8];
+      unpack8(weight[v], w);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) n[j] = w[j] * round_bf16(s[i][j] * inv);
+      store_nt(summed + base + v, pack8(s[i]));
+      store_nt(normalized + base + v, pack8(n));
+    }
+  }
+}
+
+template <int VPL>
+void launch(int waves_per_block, int64_t blocks, hipStream_t stream, const u32x4* x,
+            const u32x4* b, const u32x4* w, u32x4* s, u32x4* n, int64_t rows, int vecs,
+            float hidden, float eps) {
+  add_rms_norm_kernel<VPL><<<dim3(static_cast<unsigned>(blocks)),
+                             dim3(waves_per_block * kWave), 0, stream>>>(
+      x, b, w, s, n, rows, vecs, hidden, eps);
+}
+
+using Launcher = void (*)(int, int64_t, hipStream_t, const u32x4*, const u32x4*,
+                          const u32x4*, u32x4*, u32x4*, int64_t, int, float, float);
+
+constexpr Launcher kLaunchers[kMaxVectorsPerLane] = {
+    launch<1>,  launch<2>,  launch<3>,  launch<4>,  launch<5>,  launch<6>,
+    launch<7>,  launch<8>,  launch<9>,  launch<10>, launch<11>, launch<12>,
+    launch<13>, launch<14>, launch<15>, launch<16>};
+
+}  // namespace
+}  // namespace omnia
+
+extern "C" int32_t omnia_add_rms_norm(const uint16_t* x, const uint16_t* branch,
+                                      const uint16_t* weight, uint16_t* summed,
+                                      uint16_t* normalized, int64_t rows, int64_t hidden,
+                                      float eps, hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(rows >= 0, "add_rms_norm: rows must be >= 0");
+  OMNIA_REQUIRE(hidden > 0 && hidden % 8 == 0 && hidden <= 8 * kWave * kMaxVectorsPerLane,
+                "add_rms_norm: hidden must be a multiple of 8 in [8, 8192]");
+  OMNIA_REQUIRE(rows < (int64_t{1} << 31), "add_rms_norm: too many rows");
+  if (rows == 0) return 0;
+  OMNIA_REQUIRE(x && branch && weight && summed && normalized,
+                "add_rms_norm: null pointer");
+  OMNIA_REQUIRE(aligned16(x) && aligned16(branch) && aligned16(weight) &&
+                    aligned16(summed) && aligned16(normalized),
+                "add_rms_norm: pointers must be 16-byte aligned");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+
+  const int vecs = static_cast<int>(hidden / 8);
+  const int vpl = (vecs + kWave - 1) / kWave;
+  // Small blocks while the grid would not cover the chip; four waves otherwise.
+  const int waves_per_block = rows >= 4096 ? 4 : 1;
+  const int64_t blocks = (rows + waves_per_block - 1) / waves_per_block;
+  kLaunchers[vpl - 1](waves_per_block, blocks, stream,
+                      reinterpret_cast<const u32x4*>(x),
+                      reinterpret_cast<const u32x4*>(branch),
+                      reinterpret_cast<const u32x4*>(weight),
+                      reinterpret_cast<u32x4*>(summed), reinterpret_cast<u32x4*>(normalized),
+                      rows, vecs, static_cast<float>(hidden), eps);
+  return launched("add_rms_norm");
+}

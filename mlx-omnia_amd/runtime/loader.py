@@ -1,0 +1,89 @@
+"""ctypes binding of `libomnia_hip.so`, the C ABI declared in `include/omnia_hip.h`.
+
+The library is loaded once per process from the package directory. Nothing here falls
+back to another implementation: a missing library raises `LibraryMissing`, a rejected
+argument raises `ValueError` and a failed launch `RuntimeError`, each carrying the text
+of `omnia_last_error()`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import errno
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libomnia_hip.so"
+ABI_VERSION = 1
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F32 = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/omnia_hip.h.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "omnia_abi_version": (_I32, []),
+    "omnia_last_error": (ctypes.c_char_p, []),
+    "omnia_add_rms_norm": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _F32, _P]),
+}
+
+
+class LibraryMissing(RuntimeError):
+    """`libomnia_hip.so` is not built (or not loadable) in this tree."""
+
+
+_lock = threading.Lock()
+_library: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """The loaded library, with every declared signature bound."""
+    global _library
+    if _library is not None:
+        return _library
+    with _lock:
+        if _library is not None:
+            return _library
+        if not LIBRARY_PATH.exists():
+            raise LibraryMissing(
+                f"{LIBRARY_PATH} is not built; run `python __graft_entry__.py` or "
+                "`python mlx-omnia_amd/build.py` first"
+            )
+        try:
+            lib = ctypes.CDLL(str(LIBRARY_PATH))
+        except OSError as exc:  # pragma: no cover - depends on the host
+            raise LibraryMissing(f"cannot load {LIBRARY_PATH}: {exc}") from exc
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.omnia_abi_version()
+        if version != ABI_VERSION:
+            raise LibraryMissing(f"ABI version {version}, expected {ABI_VERSION}")
+        _library = lib
+        return lib
+
+
+def available() -> bool:
+    try:
+        library()
+    except LibraryMissing:
+        return False
+    return True
+
+
+def last_error() -> str:
+    raw = library().omnia_last_error()
+    return raw.decode() if raw else ""
+
+
+def call(name: str, *args: object) -> None:
+    """Invoke one entry point and turn a non-zero return code into an exception."""
+    rc = getattr(library(), name)(*args)
+    if rc == 0:
+        return
+    message = f"{name}: {last_error()} (code {rc})"
+    if rc == -errno.EINVAL:
+        raise ValueError(message)
+    raise RuntimeError(message)
