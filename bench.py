@@ -1,0 +1,326 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused per-layer kernels on one MI355X.
+
+Metric: achieved HBM GB/s (% of the 8 TB/s peak) and µs per fused
+kernel, on one GPU. A "step" is one launch of a fused kernel over one batch of its
+config's synthetic input; the headline line is configs[1], the per-head QK-norm + RoPE
+at the T=4096 prefill shape, and every other config's kernel is measured in the same run
+and reported under "kernels".
+
+Method, per kernel:
+- inputs are seeded numpy draws rounded to bf16 (RNE), placed in HBM before timing;
+- the launch cycles through enough copies of inputs and outputs that one cycle touches
+  >= 512 MB (twice the 256 MB Infinity Cache), so no launch is served from cache;
+- `--warmup` launches, then exactly `--steps` launches captured in one HIP graph (so the
+  host never starves the GPU) and replayed once between two HIP events recorded on the
+  stream the kernels run on, with a device synchronise on both sides;
+- achieved = algorithmic bytes per launch (each input read once, each output written
+  once) / average launch duration.
+The CPU baseline is the repo's numpy oracle (a port of the reference's Core chains;
+MLX does not exist on these machines) timed on a bounded sample of the headline
+workload, single-threaded.
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only NAME[,NAME]]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Callable
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+PEAK_GBS = 8000.0
+ROTATE_BYTES = 512 * 2**20
+MAX_COPIES = 64
+METRIC = "achieved HBM GB/s (% of MI355X peak) and µs per fused kernel, 1 GPU"
+HEADLINE = "qk_norm_rope_prefill"
+
+
+@dataclass
+class Workload:
+    name: str
+    kernel: str                      # kernel symbol substring, as rocprof names it
+    description: str
+    bytes_per_launch: int
+    setup: Callable[[object, int], list]   # (device, copies) -> per-copy argument sets
+    launch: Callable[[object], None]
+    details: dict = field(default_factory=dict)
+
+
+def _normal(rng: np.random.Generator, shape, scale=1.0, shift=0.0) -> np.ndarray:
+    return (shift + scale * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32)
+
+
+def _to_bf16_device(values: np.ndarray, device):
+    """fp32 numpy -> bf16 (RNE, torch's conversion) on the device."""
+    import torch
+
+    return torch.from_numpy(values).to(device).to(torch.bfloat16)
+
+
+def _copies(first: dict, copies: int) -> list[dict]:
+    """`copies` argument sets: the first as given, the rest fresh device buffers."""
+    sets = [first]
+    for _ in range(copies - 1):
+        sets.append({k: (v.clone() if hasattr(v, "clone") else v) for k, v in first.items()})
+    return sets
+
+
+def workloads() -> list[Workload]:
+    import torch
+
+    from mlx_omnia_amd.runtime import ops
+
+    out: list[Workload] = []
+
+    # residual add + RMSNorm, Qwen3-4B shape.
+    for rows, tag in ((512, "prefill"), (1, "decode")):
+        hidden = 2560
+
+        def setup(device, copies, rows=rows, hidden=hidden):
+            rng = np.random.default_rng(1)
+            first = dict(
+                x=_to_bf16_device(_normal(rng, (rows, hidden)), device),
+                r=_to_bf16_device(_normal(rng, (rows, hidden)), device),
+                w=_to_bf16_device(_normal(rng, (hidden,), 0.1, 1.0), device),
+                s=torch.empty((rows, hidden), dtype=torch.bfloat16, device=device),
+                n=torch.empty((rows, hidden), dtype=torch.bfloat16, device=device),
+            )
+            return _copies(first, copies)
+
+        out.append(Workload(
+            name=f"add_rms_norm_{tag}",
+            kernel="add_rms_norm_kernel",
+            description=f"x, residual bf16 [{rows}, {hidden}] -> summed, normed; eps 1e-6",
+            bytes_per_launch=rows * 4 * 2 * hidden + 2 * hidden,
+            setup=setup,
+            launch=lambda a: ops.add_rms_norm(a["x"], a["r"], a["w"], 1e-6,
+                                              summed=a["s"], normalized=a["n"]),
+        ))
+
+    # per-head QK-norm + RoPE from a cos/sin table.
+    table_rows, pairs = 40960, 64
+
+    def make_tables(device):
+        inverse = np.exp(-np.log(1e6) * np.arange(pairs) / pairs)
+        theta = np.arange(table_rows)[:, None] * inverse[None, :]
+        return (torch.from_numpy(np.cos(theta).astype(np.float32)).to(device),
+                torch.from_numpy(np.sin(theta).astype(np.float32)).to(device))
+
+    for length, tag in ((4096, "prefill"), (64, "decode")):
+        hq, hkv, d = 32, 8, 128
+
+        def setup(device, copies, length=length, hq=hq, hkv=hkv, d=d):
+            rng = np.random.default_rng(2)
+            cos, sin = make_tables(device)
+            sets = []
+            base = dict(
+                q=_to_bf16_device(_normal(rng, (length, hq, d)), device),
+                k=_to_bf16_device(_normal(rng, (length, hkv, d)), device),
+                qw=_to_bf16_device(_normal(rng, (d,), 0.1, 1.0), device),
+                kw=_to_bf16_device(_normal(rng, (d,), 0.1, 1.0), device),
+                cos=cos, sin=sin,
+            )
+            for i in range(copies):
+                entry = dict(base) if i == 0 else {
+                    **base, "q": base["q"].clone(), "k": base["k"].clone()}
+                entry["offset"] = int(rng.integers(0, 32768))
+                entry["oq"] = torch.empty((hq, length, d), dtype=torch.bfloat16, device=device)
+                entry["ok"] = torch.empty((hkv, length, d), dtype=torch.bfloat16, device=device)
+                sets.append(entry)
+            return sets
+
+        out.append(Workload(
+            name=f"qk_norm_rope_{tag}",
+            kernel="qk_norm_rope_kernel",
+            description=(f"q [{length},{hq},{d}], k [{length},{hkv},{d}] bf16, cos/sin "
+                         f"[{table_rows},{pairs}] fp32 theta=1e6, offset ~U[0,32768)"),
+            bytes_per_launch=length * (2 * (hq + hkv) * d * 2 + 2 * pairs * 4) + 2 * d * 2,
+            setup=setup,
+            launch=lambda a: ops.qk_norm_rope(
+                a["q"], a["k"], a["qw"], a["kw"], a["cos"], a["sin"], offset=a["offset"],
+                eps=1e-6, rotary_pairs=pairs, queries=a["oq"], keys=a["ok"]),
+        ))
+
+    # configs[1], epilogue form: angles derived in-kernel from a fused qkv projection.
+    def setup_epilogue(device, copies, length=4096, hq=32, hkv=8, d=128):
+        rng = np.random.default_rng(3)
+        first = dict(
+            fused=_to_bf16_device(_normal(rng, (length, (hq + 2 * hkv) * d)), device),
+            qw=_to_bf16_device(_normal(rng, (d,), 0.1, 1.0), device),
+            kw=_to_bf16_device(_normal(rng, (d,), 0.1, 1.0), device),
+        )
+        sets = []
+        for i in range(copies):
+            entry = dict(first) if i == 0 else {**first, "fused": first["fused"].clone()}
+            entry["offset"] = int(rng.integers(0, 32768))
+            entry["oq"] = torch.empty((hq, length, d), dtype=torch.bfloat16, device=device)
+            entry["ok"] = torch.empty((hkv, length, d), dtype=torch.bfloat16, device=device)
+            sets.append(entry)
+        return sets
+
+    out.append(Workload(
+        name="rope_epilogue_prefill",
+        kernel="qk_norm_rope_kernel",
+        description="fused qkv [4096, 48*128] bf16 -> q [32,4096,128], k [8,4096,128]; "
+                    "angles in-kernel, theta=1e6",
+        bytes_per_launch=4096 * (2 * 40 * 128 * 2) + 2 * 128 * 2,
+        setup=setup_epilogue,
+        launch=lambda a: ops.rope_epilogue(
+            a["fused"], a["qw"], a["kw"], query_heads=32, kv_heads=8, head_dim=128,
+            offset=a["offset"], log2_base=math.log2(1e6), eps=1e-6,
+            queries=a["oq"], keys=a["ok"]),
+    ))
+    return out
+
+
+def time_workload(w: Workload, steps: int, warmup: int, device) -> dict:
+    import torch
+
+    copies = max(1, min(MAX_COPIES, math.ceil(ROTATE_BYTES / max(1, w.bytes_per_launch))))
+    sets = w.setup(device, copies)
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            w.launch(sets[i % copies])
+        torch.cuda.synchronize(device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                w.launch(sets[i % copies])
+        graph.replay()  # untimed: first replay uploads the graph
+        torch.cuda.synchronize(device)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize(device)
+    elapsed_ms = start.elapsed_time(end)
+    us = elapsed_ms * 1000.0 / steps
+    gbs = w.bytes_per_launch / (us * 1e-6) / 1e9
+    del graph, sets
+    torch.cuda.empty_cache()
+    return dict(us=round(us, 3), GBps=round(gbs, 1), frac=round(gbs / PEAK_GBS, 4),
+                bytes=w.bytes_per_launch, copies=copies, kernel=w.kernel,
+                workload=w.description, ms_total=round(elapsed_ms, 4))
+
+
+def cpu_baseline(seconds: float = 12.0) -> dict:
+    """The numpy oracle (single-threaded port of the Core chain) on a bounded sample of
+    the headline workload: repeated 256-token slices of the T=4096 prefill shape."""
+    from oracle import rope
+
+    rng = np.random.default_rng(2)
+    tokens, hq, hkv, d, pairs = 256, 32, 8, 128, 64
+    from oracle.bf16 import from_float
+
+    raw_q = from_float(rng.standard_normal((tokens, hq, d)))
+    raw_k = from_float(rng.standard_normal((tokens, hkv, d)))
+    qw = from_float(1 + 0.1 * rng.standard_normal(d))
+    kw = from_float(1 + 0.1 * rng.standard_normal(d))
+    cos, sin = rope.angle_table(40960, pairs, 1e6)
+    bytes_per_token = 2 * (hq + hkv) * d * 2 + 2 * pairs * 4
+    done, start = 0, time.perf_counter()
+    while time.perf_counter() - start < seconds:
+        offset = int(rng.integers(0, 32768))
+        rope.qk_norm_rope(raw_q, raw_k, qw, kw, cos, sin, offset, 1e-6, pairs)
+        done += tokens
+    elapsed = time.perf_counter() - start
+    return dict(value=round(done * bytes_per_token / elapsed / 1e9, 4), unit="GB/s",
+                cores=1, kind="port",
+                sample=f"numpy oracle (oracle/rope.py) on {done} tokens of the T=4096 "
+                       f"q/k shape in 256-token slices, {elapsed:.1f} s, one thread")
+
+
+def _traffic(kernel_name: str) -> int | None:
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    table = REPO / "profiles" / "hbm_traffic.md"
+    if not table.exists():
+        return None
+    for line in table.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == kernel_name and re.fullmatch(r"\d+", cells[4]):
+            return int(cells[4])
+    return None
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--only", default="", help="comma-separated workload names")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not run "
+              "(the fused kernels shard by tokens with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm device visible", file=sys.stderr)
+        return 1
+    device = torch.device("cuda:0")
+    selected = [w for w in workloads() if not args.only or w.name in args.only.split(",")]
+    results = {}
+    for w in selected:
+        print(f"[bench] {w.name}: {w.description}", file=sys.stderr, flush=True)
+        results[w.name] = time_workload(w, args.steps, args.warmup, device)
+        r = results[w.name]
+        print(f"[bench] {w.name}: {r['us']} us  {r['GBps']} GB/s  ({100 * r['frac']:.1f}% of peak)",
+              file=sys.stderr, flush=True)
+
+    head = results.get(HEADLINE) or next(iter(results.values()))
+    head_name = HEADLINE if HEADLINE in results else next(iter(results))
+    baseline = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": METRIC,
+        "value": head["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us"] / 1000.0, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded numpy normal draws rounded to bf16 (RNE), resident in HBM",
+        "config": {"workload": f"{head_name}: {head['workload']}",
+                   "us_per_launch": head["us"], "frac_of_peak": head["frac"]},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": head["GBps"],
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": head["frac"],
+            "traffic": _traffic(head_name),
+        },
+        "cpu_baseline": baseline,
+        "kernels": results,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -49,6 +49,48 @@ int32_t omnia_add_rms_norm(const uint16_t* x, const uint16_t* branch,
                            uint16_t* normalized, int64_t rows, int64_t hidden,
                            float eps, hipStream_t stream);
 
+/* Per-head q/k RMSNorm + table-driven half-split rotary for a segment of `length`
+ * tokens at positions offset .. offset+length-1.
+ *   raw_queries [length, query_heads, head_dim] (row stride `query_stride` elements),
+ *   raw_keys    [length, kv_heads, head_dim]    (row stride `key_stride`),
+ *   query_weight, key_weight [head_dim] bf16,
+ *   cos_table, sin_table: fp32 rows of `rotary_pairs` values, `table_stride` floats
+ *     apart, `table_rows` rows; row offset+t is used for token t. (The reference's
+ *     `[positions, 2P]` cos||sin atlas is cos_table = atlas, sin_table = atlas + P,
+ *     table_stride = 2P.)
+ *   queries [query_heads, length, head_dim], keys [kv_heads, length, head_dim] out.
+ * Elements [2*rotary_pairs, head_dim) are the normed values verbatim; the rotary inputs
+ * are pre-scaled through bf16(x * bf16(mscale)) (pass 1.0 for a plain rotary).
+ * Replaces: core/kernels/qkv_rope/qk_norm_rope.py:64-327 (`qk_norm_rope_decode`,
+ * `qk_norm_rope_prefill`, `qk_norm_rope_prefill_scaled`, QkNormRope.__call__ at
+ * :653-708); Core chain core/kernels/qkv_rope/default.py:75-84.
+ * head_dim in {64, 128, 256}; rotary_pairs = 8 * 2^k with 2*rotary_pairs <= head_dim;
+ * strides multiples of 8. */
+int32_t omnia_qk_norm_rope(const uint16_t* raw_queries, int64_t query_stride,
+                           const uint16_t* raw_keys, int64_t key_stride,
+                           const uint16_t* query_weight, const uint16_t* key_weight,
+                           const float* cos_table, const float* sin_table,
+                           int64_t table_stride, int64_t table_rows, int64_t offset,
+                           uint16_t* queries, uint16_t* keys, int64_t length,
+                           int64_t query_heads, int64_t kv_heads, int64_t head_dim,
+                           int64_t rotary_pairs, float eps, float mscale,
+                           hipStream_t stream);
+
+/* The rope epilogue of a fused qkv projection: rows of `fused` are
+ * [q (query_heads*head_dim) | k (kv_heads*head_dim) | v (kv_heads*head_dim)], row
+ * stride `fused_stride`. q and k are normed per head and fully rotated with the angle
+ * derived in-kernel, angle_i = f32(offset + t) * exp2(-(i / (head_dim/2)) * log2_base);
+ * v is not touched. Outputs are head-major like omnia_qk_norm_rope's.
+ * Replaces: core/kernels/qkv_rope/epilogue.py:34-115 (`rope_epilogue`,
+ * RopeEpilogue.__call__ at :202-217), generalised from one token to `length` tokens.
+ * Positions must stay below 2^24. */
+int32_t omnia_rope_epilogue(const uint16_t* fused, int64_t fused_stride,
+                            const uint16_t* query_weight, const uint16_t* key_weight,
+                            int64_t offset, uint16_t* queries, uint16_t* keys,
+                            int64_t length, int64_t query_heads, int64_t kv_heads,
+                            int64_t head_dim, float log2_base, float eps,
+                            hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

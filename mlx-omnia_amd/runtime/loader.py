@@ -26,6 +26,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "omnia_abi_version": (_I32, []),
     "omnia_last_error": (ctypes.c_char_p, []),
     "omnia_add_rms_norm": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _F32, _P]),
+    "omnia_qk_norm_rope": (
+        _I32,
+        [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64,
+         _I64, _I64, _F32, _F32, _P],
+    ),
+    "omnia_rope_epilogue": (
+        _I32, [_P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _F32, _F32, _P]
+    ),
 }
 
 
@@ -50,6 +58,11 @@ def library() -> ctypes.CDLL:
                 f"{LIBRARY_PATH} is not built; run `python __graft_entry__.py` or "
                 "`python mlx-omnia_amd/build.py` first"
             )
+        # torch ships its own libamdhip64.so.7; importing it first makes this library's
+        # libamdhip64.so.7 dependency bind to that same runtime instance, so torch's
+        # stream handles are valid in our launches (one HIP runtime per process).
+        import torch  # noqa: F401
+
         try:
             lib = ctypes.CDLL(str(LIBRARY_PATH))
         except OSError as exc:  # pragma: no cover - depends on the host

@@ -74,3 +74,99 @@ def add_rms_norm(
         rows, hidden, float(eps), _stream(x),
     )
     return summed, normalized
+
+
+def _token_stride(t: torch.Tensor, name: str) -> int:
+    """Token stride (elements) of a [T, H, D] view whose heads and head_dim are packed
+    (a contiguous tensor, or a column slice of wider rows such as a fused qkv)."""
+    _require(t.dtype == BF16, f"{name}: expected bfloat16")
+    _require(t.dim() == 3, f"{name}: expected [T, H, D]")
+    _require(t.stride(2) == 1 and t.stride(1) == t.shape[2], f"{name}: heads must be packed")
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1] * t.shape[2]
+
+
+def qk_norm_rope(
+    raw_queries: torch.Tensor,
+    raw_keys: torch.Tensor,
+    query_weight: torch.Tensor,
+    key_weight: torch.Tensor,
+    cos_table: torch.Tensor,
+    sin_table: torch.Tensor,
+    *,
+    offset: int,
+    eps: float,
+    rotary_pairs: int,
+    mscale: float = 1.0,
+    queries: torch.Tensor | None = None,
+    keys: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-head q/k RMSNorm + table RoPE; see `omnia_qk_norm_rope`.
+
+    raw_queries [T, Hq, D] and raw_keys [T, Hkv, D] may be views with a token stride
+    (e.g. slices of a fused qkv row); cos_table/sin_table are fp32 [rows, >= P] views
+    with unit inner stride. Returns q [Hq, T, D] and k [Hkv, T, D].
+    """
+    _require(raw_queries.dim() == 3 and raw_keys.dim() == 3, "qk_norm_rope: q, k must be [T, H, D]")
+    length, query_heads, head_dim = raw_queries.shape
+    _require(raw_keys.shape[0] == length and raw_keys.shape[2] == head_dim, "qk_norm_rope: k shape")
+    kv_heads = raw_keys.shape[1]
+    _require(on_rocm(raw_queries, raw_keys, query_weight, key_weight, cos_table, sin_table),
+             "qk_norm_rope: tensors must share one ROCm device")
+    q_stride = _token_stride(raw_queries, "raw_queries")
+    k_stride = _token_stride(raw_keys, "raw_keys")
+    _dense(query_weight, BF16, "query_weight")
+    _dense(key_weight, BF16, "key_weight")
+    _require(query_weight.numel() == head_dim and key_weight.numel() == head_dim,
+             "qk_norm_rope: norm weights must have head_dim elements")
+    for table, name in ((cos_table, "cos_table"), (sin_table, "sin_table")):
+        _require(table.dtype == F32 and table.dim() == 2 and table.stride(1) == 1,
+                 f"{name}: fp32 [rows, width] with unit inner stride")
+        _require(table.shape[1] >= rotary_pairs, f"{name}: narrower than rotary_pairs")
+    _require(cos_table.shape[0] == sin_table.shape[0] and cos_table.stride(0) == sin_table.stride(0),
+             "qk_norm_rope: cos and sin tables must share rows and stride")
+    queries = _out(queries, raw_queries, (query_heads, length, head_dim), BF16, "queries")
+    keys = _out(keys, raw_queries, (kv_heads, length, head_dim), BF16, "keys")
+    call(
+        "omnia_qk_norm_rope",
+        raw_queries.data_ptr(), q_stride, raw_keys.data_ptr(), k_stride,
+        query_weight.data_ptr(), key_weight.data_ptr(),
+        cos_table.data_ptr(), sin_table.data_ptr(), cos_table.stride(0), cos_table.shape[0],
+        int(offset), queries.data_ptr(), keys.data_ptr(), length,
+        query_heads, kv_heads, head_dim, int(rotary_pairs), float(eps), float(mscale),
+        _stream(raw_queries),
+    )
+    return queries, keys
+
+
+def rope_epilogue(
+    fused: torch.Tensor,
+    query_weight: torch.Tensor,
+    key_weight: torch.Tensor,
+    *,
+    query_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    offset: int,
+    log2_base: float,
+    eps: float,
+    queries: torch.Tensor | None = None,
+    keys: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Norm + in-kernel-angle RoPE over the q/k slices of fused qkv rows [T, W]; see
+    `omnia_rope_epilogue`. Returns q [Hq, T, D] and k [Hkv, T, D]."""
+    _require(fused.dim() == 2 and fused.stride(1) == 1 and fused.dtype == BF16,
+             "rope_epilogue: fused must be bf16 [T, W] with unit inner stride")
+    _require(on_rocm(fused, query_weight, key_weight), "rope_epilogue: tensors must share one ROCm device")
+    _dense(query_weight, BF16, "query_weight")
+    _dense(key_weight, BF16, "key_weight")
+    length = fused.shape[0]
+    queries = _out(queries, fused, (query_heads, length, head_dim), BF16, "queries")
+    keys = _out(keys, fused, (kv_heads, length, head_dim), BF16, "keys")
+    call(
+        "omnia_rope_epilogue",
+        fused.data_ptr(), fused.stride(0) if length > 1 else fused.shape[1],
+        query_weight.data_ptr(), key_weight.data_ptr(), int(offset),
+        queries.data_ptr(), keys.data_ptr(), length, query_heads, kv_heads, head_dim,
+        float(log2_base), float(eps), _stream(fused),
+    )
+    return queries, keys

@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent.parent))
 
-from oracle import add_norm  # noqa: E402
+from oracle import add_norm, rope  # noqa: E402
 from oracle.bf16 import from_float  # noqa: E402
 
 
@@ -32,7 +32,26 @@ def make_add_norm() -> dict[str, np.ndarray]:
                 summed=summed, normalized=normalized)
 
 
-MAKERS = {"add_norm": make_add_norm}
+def make_qk_norm_rope() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(2)
+    length, hq, hkv, d, pairs, offset, eps, mscale = 5, 4, 2, 128, 32, 3, 1e-6, 1.3465735912322998
+    raw_q = from_float(rng.standard_normal((length, hq, d)))
+    raw_k = from_float(rng.standard_normal((length, hkv, d)))
+    q_weight = from_float(1.0 + 0.1 * rng.standard_normal(d))
+    k_weight = from_float(1.0 + 0.1 * rng.standard_normal(d))
+    cos, sin = rope.angle_table(offset + length, pairs, 1e6)
+    q, k = rope.qk_norm_rope(raw_q, raw_k, q_weight, k_weight, cos, sin, offset, eps, pairs, mscale)
+    fused = from_float(rng.standard_normal((3, (hq + 2 * hkv) * d)))
+    epilogue_offset = 32_000
+    eq, ek = rope.rope_epilogue(fused, hq, hkv, d, q_weight, k_weight, epilogue_offset, 1e6, eps)
+    return dict(raw_q=raw_q, raw_k=raw_k, q_weight=q_weight, k_weight=k_weight, cos=cos, sin=sin,
+                offset=np.int64(offset), eps=np.float32(eps), pairs=np.int64(pairs),
+                mscale=np.float64(mscale), q=q, k=k, fused=fused, hq=np.int64(hq),
+                hkv=np.int64(hkv), epilogue_offset=np.int64(epilogue_offset),
+                epilogue_q=eq, epilogue_k=ek)
+
+
+MAKERS = {"add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope}
 
 
 def main(names: list[str]) -> None:
