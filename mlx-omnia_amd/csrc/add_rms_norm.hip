@@ -5,6 +5,9 @@
 //   s_i = bf16(x_i + b_i)
 //   inv = 1 / sqrt(sum_i s_i^2 / H + eps)          (fp32, IEEE sqrt and divide)
 //   n_i = bf16(w_i * bf16(s_i * inv))
+// The sum of squares is accumulated in fp64 (each square of a bf16 value is exact in
+// fp32) and rounded once to fp32, so it is the correctly rounded fp32 sum whatever the
+// lane order: the result does not depend on how the row is split across lanes.
 //
 // Layout: one wave64 per row. Lane l owns the 16-byte vectors l, l+64, l+128, ...
 // of the row, so every load and store instruction of the wave covers 1 KiB of
@@ -42,7 +45,7 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(
   }
 
   float s[VPL][8];
-  float acc = 0.0f;
+  double acc = 0.0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int v = lane + i * kWave;
@@ -53,12 +56,12 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         s[i][j] = round_bf16(a[j] + b[j]);
-        acc += s[i][j] * s[i][j];
+        acc += static_cast<double>(s[i][j] * s[i][j]);
       }
     }
   }
   acc = group_sum<kWave>(acc);
-  const float inv = 1.0f / sqrtf(acc / hidden + eps);
+  const float inv = 1.0f / sqrtf(static_cast<float>(acc) / hidden + eps);
 
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {

@@ -17,6 +17,8 @@ constexpr int kWave = 64;
 // Native 16-byte vector (clang ext_vector), usable with the nontemporal builtins.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float bf16_lo(uint32_t packed) {
   return __uint_as_float(packed << 16);
@@ -36,10 +38,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float value) {
   return __builtin_bit_cast(uint16_t, narrowed);
 }
 
-// Two fp32 values -> one packed pair, `lo` in the low half (the lower address).
+// Two fp32 values -> one packed bf16 pair (RNE), `lo` in the low half (the lower
+// address): a single v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) |
-         (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  const f32x2 pair = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(pair, bf16x2));
+}
+
+// Rounds two fp32 values to bf16 in one conversion and widens them back.
+__device__ __forceinline__ void round_pair(float& lo, float& hi) {
+  const uint32_t packed = pack_bf16(lo, hi);
+  lo = bf16_lo(packed);
+  hi = bf16_hi(packed);
 }
 
 // fp32 value rounded to bf16 and widened back: one bf16 rounding step.
@@ -66,12 +76,38 @@ __device__ __forceinline__ u32x4 pack8(const float in[8]) {
 
 // Butterfly sum over groups of `width` consecutive lanes (width a power of two <= 64).
 // Every lane of a group ends with the group's total.
-template <int width>
-__device__ __forceinline__ float group_sum(float value) {
+template <int width, typename T>
+__device__ __forceinline__ T group_sum(T value) {
 #pragma unroll
   for (int offset = width / 2; offset > 0; offset >>= 1) {
     value += __shfl_xor(value, offset, kWave);
   }
+  return value;
+}
+
+// Cross-lane moves inside a 16-lane DPP row (no LDS traffic).
+template <int ctrl>
+__device__ __forceinline__ uint32_t dpp(uint32_t value) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_mov_dpp(static_cast<int>(value), ctrl, 0xF, 0xF, false));
+}
+constexpr int kRowRor1 = 0x121, kRowRor2 = 0x122, kRowRor4 = 0x124, kRowRor8 = 0x128;
+
+// Sum over the 16 lanes of each DPP row; every lane ends with the same value (each
+// rotation step adds two operands that the partner lane adds in swapped order).
+__device__ __forceinline__ double row16_sum(double value) {
+#define OMNIA_ROW_STEP(ctrl)                                                          \
+  {                                                                                   \
+    const uint64_t bits = __builtin_bit_cast(uint64_t, value);                        \
+    const uint32_t lo = dpp<ctrl>(static_cast<uint32_t>(bits));                       \
+    const uint32_t hi = dpp<ctrl>(static_cast<uint32_t>(bits >> 32));                 \
+    value += __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);      \
+  }
+  OMNIA_ROW_STEP(kRowRor8)
+  OMNIA_ROW_STEP(kRowRor4)
+  OMNIA_ROW_STEP(kRowRor2)
+  OMNIA_ROW_STEP(kRowRor1)
+#undef OMNIA_ROW_STEP
   return value;
 }
 

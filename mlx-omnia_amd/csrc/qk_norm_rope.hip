@@ -2,7 +2,7 @@
 //
 // Arithmetic (core/kernels/qkv_rope/qk_norm_rope.py:21-24,120-140,295-308; the norm
 // rounds as mx.fast.rms_norm does):
-//   inv  = 1 / sqrt(sum_d x_d^2 / D + eps)
+//   inv  = 1 / sqrt(sum_d x_d^2 / D + eps)   (sum in fp64, rounded once to fp32)
 //   n_d  = bf16(w_d * bf16(x_d * inv))
 //   for p < P:  a = bf16(n_p * bf16(mscale)),  b = bf16(n_{p+P} * bf16(mscale))
 //               out_p     = bf16(a * cos_p - b * sin_p)
@@ -16,20 +16,28 @@
 // correctly rounded for all practical purposes (the reference's Metal code uses
 // fast::cos/sin, which no other machine reproduces bit for bit).
 //
-// Layout (wave64): a head of D bf16 is D/8 lanes x one 16-byte vector, so a wave holds
-// 64/(D/8) heads (4 at D=128). The rotary partner of element p is element p+P, which
-// sits on lane `lane ^ (P/8)` of the same head group: one cross-lane exchange of four
-// packed dwords. One workgroup is one token: the token's cos/sin row (2P floats) is
-// staged once in LDS and read by all its heads. Input is token-major with a row stride
-// (so q and k can be read straight out of a fused qkv projection); output is head-major
-// [heads, T, D], the layout attention consumes (qk_norm_rope.py:163-175).
+// Layout (wave64): a head of D bf16 is G = D/8 lanes x one 16-byte vector, so one
+// wave instruction covers a "slot" of 64/G heads (4 at D=128). A wave owns a few slots
+// (`slots_per_wave`, 2 for prefill) of the q heads or of the k heads of one token, so
+// its norm weight, input row and output base are wave-uniform; it issues all its head
+// loads before any arithmetic and loads its eight (cos, sin) pairs once (L2-resident:
+// every wave of a token reads the same 512-byte row). There is no LDS and no barrier:
+// measured on MI355X, a per-token workgroup that stages the row in LDS behind a
+// barrier runs slower than these independent waves, and so do waves owning a whole
+// token (fewer, longer waves leave HBM idle in the ramp and the tail).
+// The rotary partner of element p is element p+P, on lane `lane ^ (P/8)` of the same
+// head group: one cross-lane exchange of four packed dwords. The per-head sum of
+// squares is a butterfly inside the G-lane group. No LDS and no barrier.
+// Input is token-major with a row stride (so q and k can be read straight out of a
+// fused qkv projection); output is head-major [heads, T, D], the layout attention
+// consumes (qk_norm_rope.py:163-175).
 #include "common.hpp"
 #include "host.hpp"
 
 namespace omnia {
 namespace {
 
-constexpr int kMaxPairs = 128;  // P <= D/2 <= 128
+constexpr int kWavesPerBlock = 4;
 
 struct RopeArgs {
   const uint16_t* queries_in;
@@ -48,128 +56,261 @@ struct RopeArgs {
   int query_heads;
   int kv_heads;
   int pairs;             // P
+  int q_parts;           // waves per token on the q heads
+  int k_parts;           // waves per token on the k heads
   float eps;
   float mscale;
   float log2_base;
 };
 
-template <int D, bool TABLE>
-__global__ __launch_bounds__(1024) void qk_norm_rope_kernel(RopeArgs a) {
-  constexpr int G = D / 8;            // lanes per head
-  __shared__ float cos_row[kMaxPairs];
-  __shared__ float sin_row[kMaxPairs];
+// cos/sin of the in-kernel angle for pair `pair` at `position` (epilogue.py:57-63),
+// evaluated in fp64 and rounded once to fp32.
+__device__ __forceinline__ void derived_angle(int pair, int pairs, int64_t position,
+                                              float log2_base, float& c, float& s) {
+  const float d = static_cast<float>(pair) / static_cast<float>(pairs);
+  const float exponent = -d * log2_base;
+  const float frequency = static_cast<float>(exp2(static_cast<double>(exponent)));
+  const float angle = static_cast<float>(position) * frequency;
+  double sd, cd;
+  sincos(static_cast<double>(angle), &sd, &cd);
+  c = static_cast<float>(cd);
+  s = static_cast<float>(sd);
+}
 
-  const int64_t t = blockIdx.x;
-  const int64_t position = a.offset + t;
-  const int lane_in_head = threadIdx.x % G;
-  const int group = threadIdx.x / G;
-  const int groups = blockDim.x / G;
-  const int heads = a.query_heads + a.kv_heads;
-  const int pair_lanes = a.pairs / 8;  // lanes holding the first rotary half
-
-  // Stage this token's cos/sin row.
-  if constexpr (TABLE) {
-    const int chunks = a.pairs / 4;  // 16-byte chunks per half-row
-    if (threadIdx.x < 2 * chunks) {
-      const bool is_sin = threadIdx.x >= chunks;
-      const int c = is_sin ? threadIdx.x - chunks : threadIdx.x;
-      const float* src = (is_sin ? a.sin_table : a.cos_table) + position * a.table_stride;
-      const f32x4 v = *reinterpret_cast<const f32x4*>(src + 4 * c);
-      *reinterpret_cast<f32x4*>((is_sin ? sin_row : cos_row) + 4 * c) = v;
-    }
+// Sum over the G lanes of each head group.
+template <int G>
+__device__ __forceinline__ double head_sum(double value) {
+  if constexpr (G == 16) {
+    return row16_sum(value);
   } else {
-    if (threadIdx.x < a.pairs) {
-      const float d = static_cast<float>(threadIdx.x) / static_cast<float>(a.pairs);
-      const float exponent = -d * a.log2_base;
-      const float frequency = static_cast<float>(exp2(static_cast<double>(exponent)));
-      const float angle = static_cast<float>(position) * frequency;
-      double s, c;
-      sincos(static_cast<double>(angle), &s, &c);
-      cos_row[threadIdx.x] = static_cast<float>(c);
-      sin_row[threadIdx.x] = static_cast<float>(s);
-    }
+    return group_sum<G>(value);
   }
-  __syncthreads();
+}
 
-  const float rounded_mscale = round_bf16(a.mscale);
-  for (int head = group; head < heads; head += groups) {
-    const bool is_query = head < a.query_heads;
-    const int kv = head - a.query_heads;
-    const uint16_t* in = is_query ? a.queries_in + t * a.query_stride + head * D
-                                  : a.keys_in + t * a.key_stride + kv * D;
-    const uint16_t* weight = is_query ? a.query_weight : a.key_weight;
-    uint16_t* out = is_query ? a.queries_out + (head * a.length + t) * D
-                             : a.keys_out + (kv * a.length + t) * D;
+// The partner half of each rotary pair, `pair_lanes` lanes away inside the head.
+template <int G, bool FULL>
+__device__ __forceinline__ uint32_t partner(uint32_t value, int pair_lanes) {
+  if constexpr (G == 16 && FULL) {
+    return dpp<kRowRor8>(value);  // pair_lanes == 8: the other half of the DPP row
+  } else {
+    return static_cast<uint32_t>(__shfl_xor(static_cast<int>(value), pair_lanes, kWave));
+  }
+}
 
-    float x[8], w[8];
-    unpack8(load_nt(reinterpret_cast<const u32x4*>(in) + lane_in_head), x);
-    unpack8(*(reinterpret_cast<const u32x4*>(weight) + lane_in_head), w);
+// SPW: slots per wave. FULL: 2P == D (every lane rotates). SCALED: mscale != 1 (the
+// bf16 pre-scale round trip is applied; at mscale == 1 it is the identity and is
+// skipped). EXACT: both head counts are multiples of the heads per slot, so no lane of
+// any slot is idle.
+template <int D, int SPW, bool TABLE, bool FULL, bool SCALED, bool EXACT>
+__global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_kernel(RopeArgs a) {
+  constexpr int G = D / 8;          // lanes per head
+  constexpr int kHeadsPerSlot = kWave / G;
+  const int lane = threadIdx.x % kWave;
+  const int parts = a.q_parts + a.k_parts;
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
+  const int64_t t = unit / parts;
+  if (t >= a.length) return;  // whole wave leaves together; no barrier follows
+  const int part = static_cast<int>(unit - t * parts);
+  const bool is_query = part < a.q_parts;  // wave-uniform
+  const int heads = is_query ? a.query_heads : a.kv_heads;
+  const int slots = (heads + kHeadsPerSlot - 1) / kHeadsPerSlot;
+  const int slot_begin = (is_query ? part : part - a.q_parts) * SPW;
+  const int slot_end = min(slots, slot_begin + SPW);
+  const int64_t position = a.offset + t;
+  const int g = lane % G;               // lane within its head
+  const int head_in_slot = lane / G;
+  const int pair_lanes = a.pairs / 8;   // lanes holding the first rotary half
+  const bool rotary = FULL || g < 2 * pair_lanes;
+  const bool first_half = g < pair_lanes;
+  const int base = rotary ? (first_half ? g : g - pair_lanes) * 8 : 0;
 
-    float sumsq = 0.0f;
+  // This lane's eight (cos, sin) pairs. With the sine negated on first-half lanes, both
+  // halves rotate as own * cos + partner * sin:
+  //   first half:  a*cos - b*sin   (own = a, partner = b)
+  //   second half: a*sin + b*cos = b*cos + a*sin   (own = b, partner = a)
+  // which are the reference's expressions term for term (negation and the order of
+  // the two addends do not change an IEEE result).
+  float c[8], s[8];
+  if constexpr (TABLE) {
+    f32x4 c0 = {}, c1 = {}, s0 = {}, s1 = {};
+    if (rotary) {
+      const float* crow = a.cos_table + position * a.table_stride + base;
+      const float* srow = a.sin_table + position * a.table_stride + base;
+      c0 = *reinterpret_cast<const f32x4*>(crow);
+      c1 = *reinterpret_cast<const f32x4*>(crow + 4);
+      s0 = *reinterpret_cast<const f32x4*>(srow);
+      s1 = *reinterpret_cast<const f32x4*>(srow + 4);
+    }
+    c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w;
+    c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+    s[0] = s0.x; s[1] = s0.y; s[2] = s0.z; s[3] = s0.w;
+    s[4] = s1.x; s[5] = s1.y; s[6] = s1.z; s[7] = s1.w;
+  } else {
+    // Lane i derives pairs i and i+64; lanes then fetch the pairs they rotate.
+    float cl = 0.0f, sl = 0.0f, ch = 0.0f, sh = 0.0f;
+    if (lane < a.pairs) derived_angle(lane, a.pairs, position, a.log2_base, cl, sl);
+    if (D == 256 && lane + kWave < a.pairs) {
+      derived_angle(lane + kWave, a.pairs, position, a.log2_base, ch, sh);
+    }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sumsq += x[j] * x[j];
-    sumsq = group_sum<G>(sumsq);
-    const float inv = 1.0f / sqrtf(sumsq / static_cast<float>(D) + a.eps);
-
-    float n[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) n[j] = round_bf16(w[j] * round_bf16(x[j] * inv));
-
-    // Partner lane holds the other half of each pair.
-    const u32x4 mine = pack8(n);
-    u32x4 theirs;
-    theirs.x = __shfl_xor(mine.x, pair_lanes, kWave);
-    theirs.y = __shfl_xor(mine.y, pair_lanes, kWave);
-    theirs.z = __shfl_xor(mine.z, pair_lanes, kWave);
-    theirs.w = __shfl_xor(mine.w, pair_lanes, kWave);
-    float other[8];
-    unpack8(theirs, other);
-
-    float o[8];
-    if (lane_in_head < 2 * pair_lanes) {
-      const bool first_half = lane_in_head < pair_lanes;
-      const int base = (first_half ? lane_in_head : lane_in_head - pair_lanes) * 8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float first = round_bf16((first_half ? n[j] : other[j]) * rounded_mscale);
-        const float second = round_bf16((first_half ? other[j] : n[j]) * rounded_mscale);
-        const float c = cos_row[base + j];
-        const float s = sin_row[base + j];
-        o[j] = first_half ? first * c - second * s : first * s + second * c;
+    for (int j = 0; j < 8; ++j) {
+      const int pair = base + j;
+      const float lo_c = __shfl(cl, pair % kWave, kWave);
+      const float lo_s = __shfl(sl, pair % kWave, kWave);
+      if (D == 256) {
+        const float hi_c = __shfl(ch, pair % kWave, kWave);
+        const float hi_s = __shfl(sh, pair % kWave, kWave);
+        c[j] = pair < kWave ? lo_c : hi_c;
+        s[j] = pair < kWave ? lo_s : hi_s;
+      } else {
+        c[j] = lo_c;
+        s[j] = lo_s;
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = n[j];
     }
-    store_nt(reinterpret_cast<u32x4*>(out) + lane_in_head, pack8(o));
+  }
+  float w[8];
+  unpack8(*(reinterpret_cast<const u32x4*>(is_query ? a.query_weight : a.key_weight) + g), w);
+
+  // Head loads go out after the table row and weight loads: vector-memory results are
+  // counted in issue order, so the first slot's arithmetic then waits only for the
+  // row, the weight and its own head, while the later heads are still in flight.
+  const uint16_t* in = (is_query ? a.queries_in + t * a.query_stride
+                                 : a.keys_in + t * a.key_stride) + head_in_slot * D + g * 8;
+  u32x4 raw[SPW];
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const int slot = slot_begin + i;
+    raw[i] = u32x4{0u, 0u, 0u, 0u};
+    if (slot < slot_end && (EXACT || slot * kHeadsPerSlot + head_in_slot < heads)) {
+      raw[i] = load_nt(reinterpret_cast<const u32x4*>(in + slot * kHeadsPerSlot * D));
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s[j] = first_half ? -s[j] : s[j];
+
+  uint16_t* out = (is_query ? a.queries_out : a.keys_out) + (head_in_slot * a.length + t) * D + g * 8;
+  const int64_t out_slot = static_cast<int64_t>(kHeadsPerSlot) * a.length * D;
+
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const int slot = slot_begin + i;
+    if (slot >= slot_end) break;  // uniform across the wave
+    float x[8];
+    unpack8(raw[i], x);
+    double sumsq = 0.0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sumsq += static_cast<double>(x[j] * x[j]);
+    sumsq = head_sum<G>(sumsq);
+    const float inv =
+        1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(D) + a.eps);
+
+    // n = bf16(w * bf16(x * inv)), two elements per conversion.
+    float n[8];
+    uint32_t packed[4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      float lo = x[j] * inv, hi = x[j + 1] * inv;
+      round_pair(lo, hi);
+      packed[j / 2] = pack_bf16(w[j] * lo, w[j + 1] * hi);
+      n[j] = bf16_lo(packed[j / 2]);
+      n[j + 1] = bf16_hi(packed[j / 2]);
+    }
+    float other[8];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      const uint32_t theirs = partner<G, FULL>(packed[j / 2], pair_lanes);
+      other[j] = bf16_lo(theirs);
+      other[j + 1] = bf16_hi(theirs);
+    }
+    float own[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) own[j] = n[j];
+    if constexpr (SCALED) {
+      const float mscale = round_bf16(a.mscale);
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        own[j] *= mscale; own[j + 1] *= mscale;
+        other[j] *= mscale; other[j + 1] *= mscale;
+        round_pair(own[j], own[j + 1]);
+        round_pair(other[j], other[j + 1]);
+      }
+    }
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float rotated = own[j] * c[j] + other[j] * s[j];
+      o[j] = FULL ? rotated : (rotary ? rotated : n[j]);
+    }
+    if (EXACT || slot * kHeadsPerSlot + head_in_slot < heads) {
+      store_nt(reinterpret_cast<u32x4*>(out + slot * out_slot), pack8(o));
+    }
   }
 }
 
-// One workgroup per token: enough lanes for every head (looping beyond 1024) and at
-// least kMaxPairs, so the in-kernel angle derivation has a lane per pair.
-int block_threads(int heads, int lanes_per_head) {
-  int threads = heads * lanes_per_head;
-  threads = (threads + kWave - 1) / kWave * kWave;
-  if (threads < kMaxPairs) threads = kMaxPairs;
-  return threads > 1024 ? 1024 : threads;
+template <int D, int SPW, bool TABLE, bool FULL, bool SCALED>
+void launch_exact(const RopeArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  constexpr int kHeadsPerSlot = kWave / (D / 8);
+  if (a.query_heads % kHeadsPerSlot == 0 && a.kv_heads % kHeadsPerSlot == 0) {
+    qk_norm_rope_kernel<D, SPW, TABLE, FULL, SCALED, true><<<grid, block, 0, stream>>>(a);
+  } else {
+    qk_norm_rope_kernel<D, SPW, TABLE, FULL, SCALED, false><<<grid, block, 0, stream>>>(a);
+  }
 }
 
+template <int D, int SPW, bool TABLE>
+void launch_variant(const RopeArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  const bool full = 2 * a.pairs == D;
+  const bool scaled = a.mscale != 1.0f;
+  if (!TABLE || (full && !scaled)) {
+    launch_exact<D, SPW, TABLE, true, false>(a, grid, block, stream);
+  } else if (full) {
+    launch_exact<D, SPW, TABLE, true, true>(a, grid, block, stream);
+  } else if (!scaled) {
+    launch_exact<D, SPW, TABLE, false, false>(a, grid, block, stream);
+  } else {
+    launch_exact<D, SPW, TABLE, false, true>(a, grid, block, stream);
+  }
+}
+
+template <int D, bool TABLE>
+void launch_spw(const RopeArgs& a, int spw, dim3 grid, dim3 block, hipStream_t stream) {
+  switch (spw) {
+    case 1: launch_variant<D, 1, TABLE>(a, grid, block, stream); break;
+    case 2: launch_variant<D, 2, TABLE>(a, grid, block, stream); break;
+    default: launch_variant<D, 4, TABLE>(a, grid, block, stream); break;
+  }
+}
+
+// Slots per wave: measured on MI355X at the prefill shape (q [4096,32,128], k
+// [4096,8,128]), two slots per wave beat one (more per-wave overhead) and four or
+// eight (fewer waves in flight during ramp and tail); short segments drop to one so the
+// grid still covers the chip.
+int slots_per_wave(int64_t length, int q_slots, int k_slots) {
+  int spw = 2;
+  constexpr int64_t kTargetWaves = 8192;
+  if (length * ((q_slots + 1) / 2 + (k_slots + 1) / 2) < kTargetWaves) spw = 1;
+  return spw;
+}
+
+// `spw` <= 0 picks the slots per wave; the sweep harness passes 1, 2 or 4 explicitly.
 template <bool TABLE>
-int32_t launch(const RopeArgs& a, int head_dim, hipStream_t stream, const char* name) {
-  const int heads = a.query_heads + a.kv_heads;
-  const dim3 grid(static_cast<unsigned>(a.length));
+int32_t launch(RopeArgs a, int head_dim, hipStream_t stream, const char* name, int spw = 0) {
+  const int heads_per_slot = kWave / (head_dim / 8);
+  const int q_slots = (a.query_heads + heads_per_slot - 1) / heads_per_slot;
+  const int k_slots = (a.kv_heads + heads_per_slot - 1) / heads_per_slot;
+  if (spw <= 0) spw = slots_per_wave(a.length, q_slots, k_slots);
+  spw = spw >= 4 ? 4 : spw;
+  a.q_parts = (q_slots + spw - 1) / spw;
+  a.k_parts = (k_slots + spw - 1) / spw;
+  const int64_t waves = a.length * (a.q_parts + a.k_parts);
+  const dim3 grid(static_cast<unsigned>((waves + kWavesPerBlock - 1) / kWavesPerBlock));
+  const dim3 block(kWavesPerBlock * kWave);
   switch (head_dim) {
-    case 64:
-      qk_norm_rope_kernel<64, TABLE><<<grid, block_threads(heads, 8), 0, stream>>>(a);
-      break;
-    case 128:
-      qk_norm_rope_kernel<128, TABLE><<<grid, block_threads(heads, 16), 0, stream>>>(a);
-      break;
-    case 256:
-      qk_norm_rope_kernel<256, TABLE><<<grid, block_threads(heads, 32), 0, stream>>>(a);
-      break;
-    default:
-      return fail(-EINVAL, std::string(name) + ": head_dim must be 64, 128 or 256");
+    case 64: launch_spw<64, TABLE>(a, spw, grid, block, stream); break;
+    case 128: launch_spw<128, TABLE>(a, spw, grid, block, stream); break;
+    case 256: launch_spw<256, TABLE>(a, spw, grid, block, stream); break;
+    default: return fail(-EINVAL, std::string(name) + ": head_dim must be 64, 128 or 256");
   }
   return launched(name);
 }
@@ -225,7 +366,7 @@ extern "C" int32_t omnia_qk_norm_rope(
   RopeArgs a{raw_queries, raw_keys, query_weight, key_weight, cos_table, sin_table,
              queries, keys, length, query_stride, key_stride, table_stride, offset,
              static_cast<int>(query_heads), static_cast<int>(kv_heads),
-             static_cast<int>(rotary_pairs), eps, mscale, 0.0f};
+             static_cast<int>(rotary_pairs), 1, 1, eps, mscale, 0.0f};
   return launch<true>(a, static_cast<int>(head_dim), stream, "qk_norm_rope");
 }
 
@@ -255,6 +396,6 @@ extern "C" int32_t omnia_rope_epilogue(const uint16_t* fused, int64_t fused_stri
   RopeArgs a{fused, fused + query_heads * head_dim, query_weight, key_weight, nullptr,
              nullptr, queries, keys, length, fused_stride, fused_stride, 0, offset,
              static_cast<int>(query_heads), static_cast<int>(kv_heads),
-             static_cast<int>(head_dim / 2), eps, 1.0f, log2_base};
+             static_cast<int>(head_dim / 2), 1, 1, eps, 1.0f, log2_base};
   return launch<false>(a, static_cast<int>(head_dim), stream, "rope_epilogue");
 }

@@ -81,6 +81,8 @@ def _token_stride(t: torch.Tensor, name: str) -> int:
     (a contiguous tensor, or a column slice of wider rows such as a fused qkv)."""
     _require(t.dtype == BF16, f"{name}: expected bfloat16")
     _require(t.dim() == 3, f"{name}: expected [T, H, D]")
+    if t.numel() == 0:
+        return t.shape[1] * t.shape[2]
     _require(t.stride(2) == 1 and t.stride(1) == t.shape[2], f"{name}: heads must be packed")
     return t.stride(0) if t.shape[0] > 1 else t.shape[1] * t.shape[2]
 

@@ -8,9 +8,10 @@ core/kernels/add_norm/rows.py:65-79 copies:
     inv = 1 / sqrt(sum_i s_i^2 / H + eps)
     n_i = R(w_i * R(s_i * inv))
 
-The sum of squares is taken in float64 and rounded to float32 once (an fp32 accumulation
-whose order the reference leaves free); every later step is float32, operation for
-operation.
+The sum of squares is taken in float64 and rounded to float32 once: the correctly
+rounded fp32 sum, one admissible result of the fp32 accumulation whose order the
+reference leaves free (and the one the HIP kernels produce, since they accumulate the
+exact bf16 squares in fp64). Every later step is float32, operation for operation.
 """
 
 from __future__ import annotations
