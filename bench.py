@@ -185,6 +185,33 @@ def workloads() -> list[Workload]:
             offset=a["offset"], log2_base=math.log2(1e6), eps=1e-6,
             queries=a["oq"], keys=a["ok"]),
     ))
+    # embedding gather + cos/sin atlas rows.
+    def setup_embed(device, copies, vocab=151936, hidden=2560, batch=8, length=2048):
+        rng = np.random.default_rng(4)
+        table = _to_bf16_device(_normal(rng, (vocab, hidden), 0.02), device)
+        cos, sin = make_tables(device)
+        sets = []
+        for _ in range(copies):
+            sets.append(dict(
+                table=table, cos=cos, sin=sin,
+                ids=torch.from_numpy(rng.integers(0, vocab, (batch, length), dtype=np.int32)).to(device),
+                out=torch.empty((batch, length, hidden), dtype=torch.bfloat16, device=device),
+                fo=torch.empty((length, pairs), dtype=torch.float32, device=device),
+                so=torch.empty((length, pairs), dtype=torch.float32, device=device),
+            ))
+        return sets
+
+    out.append(Workload(
+        name="embed_atlas",
+        kernel="embed_atlas_kernel",
+        description="table [151936,2560] bf16 ~N(0,0.02), ids [8,2048] int32 uniform, "
+                    "cos/sin atlases [40960,64] fp32 theta=1e6, positions 0..2047",
+        bytes_per_launch=8 * 2048 * 4 + 2 * 8 * 2048 * 2560 * 2 + 2 * 2048 * 2 * pairs * 4,
+        setup=setup_embed,
+        launch=lambda a: ops.embed_atlas(
+            a["ids"], a["table"], a["cos"], a["sin"], position=0, n_positions=2048,
+            hidden_out=a["out"], full_out=a["fo"], sliding_out=a["so"]),
+    ))
     return out
 
 

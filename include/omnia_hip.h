@@ -91,6 +91,25 @@ int32_t omnia_rope_epilogue(const uint16_t* fused, int64_t fused_stride,
                             int64_t head_dim, float log2_base, float eps,
                             hipStream_t stream);
 
+/* Embedding gather + RoPE angle-atlas rows, pure copies:
+ *   hidden_out [n_tokens, hidden] bf16:  row i = embedding[tokens[i]]
+ *     (embedding [vocab, hidden]; an id outside [0, vocab) gives a zero row);
+ *   full_out [n_positions, full_width] fp32:  row j = full_atlas[position + j]
+ *   sliding_out [n_positions, sliding_width] fp32: row j = sliding_atlas[position + j]
+ * A zero width skips that atlas (its pointers may be NULL).
+ * Replaces: core/kernels/embed/atlas.py:23-69,111-135
+ * (`decode_embedding_rope_atlas_bf16`, AtlasEmbed.__call__), generalised from one token
+ * to a segment sharing positions position .. position+n_positions-1; Core chain
+ * core/kernels/embed/default.py:35-42.
+ * hidden: multiple of 8, at most 8192; atlas widths multiples of 4. */
+int32_t omnia_embed_atlas(const int32_t* tokens, int64_t n_tokens,
+                          const uint16_t* embedding, int64_t vocab, int64_t hidden,
+                          const float* full_atlas, int64_t full_rows, int64_t full_width,
+                          const float* sliding_atlas, int64_t sliding_rows,
+                          int64_t sliding_width, int64_t position, int64_t n_positions,
+                          uint16_t* hidden_out, float* full_out, float* sliding_out,
+                          hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -172,3 +172,51 @@ def rope_epilogue(
         float(log2_base), float(eps), _stream(fused),
     )
     return queries, keys
+
+
+def embed_atlas(
+    tokens: torch.Tensor,
+    embedding: torch.Tensor,
+    full_atlas: torch.Tensor | None,
+    sliding_atlas: torch.Tensor | None,
+    *,
+    position: int,
+    n_positions: int,
+    hidden_out: torch.Tensor | None = None,
+    full_out: torch.Tensor | None = None,
+    sliding_out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor | None, torch.Tensor | None]:
+    """Gather `embedding[tokens]` ([*tokens.shape, H] bf16) and copy atlas rows
+    position .. position+n_positions-1 ([n_positions, W] fp32); see `omnia_embed_atlas`.
+    An atlas passed as None is skipped and its output is None."""
+    _require(tokens.dtype == torch.int32 and tokens.is_contiguous(), "tokens: int32, contiguous")
+    _require(embedding.dim() == 2, "embedding: expected [vocab, hidden]")
+    _dense(embedding, BF16, "embedding")
+    vocab, hidden = embedding.shape
+    atlases = []
+    for atlas, name in ((full_atlas, "full_atlas"), (sliding_atlas, "sliding_atlas")):
+        if atlas is None:
+            atlases.append((None, 0, 0))
+            continue
+        rows_view = atlas.reshape(-1, atlas.shape[-1])
+        _dense(rows_view, F32, name)
+        atlases.append((rows_view, rows_view.shape[0], rows_view.shape[1]))
+    present = [t for t in (tokens, embedding, *(a for a, _, _ in atlases if a is not None))]
+    _require(on_rocm(*present), "embed_atlas: tensors must share one ROCm device")
+    n_tokens = tokens.numel()
+    hidden_out = _out(hidden_out, embedding, (*tokens.shape, hidden), BF16, "hidden_out")
+    outs = []
+    for (atlas, _, width), given, name in zip(atlases, (full_out, sliding_out), ("full_out", "sliding_out")):
+        outs.append(None if atlas is None else _out(given, embedding, (n_positions, width), F32, name))
+    (full, full_rows, full_width), (sliding, sliding_rows, sliding_width) = atlases
+    call(
+        "omnia_embed_atlas",
+        tokens.data_ptr(), n_tokens, embedding.data_ptr(), vocab, hidden,
+        full.data_ptr() if full is not None else None, full_rows, full_width,
+        sliding.data_ptr() if sliding is not None else None, sliding_rows, sliding_width,
+        int(position), int(n_positions), hidden_out.data_ptr(),
+        outs[0].data_ptr() if outs[0] is not None else None,
+        outs[1].data_ptr() if outs[1] is not None else None,
+        _stream(embedding),
+    )
+    return hidden_out, outs[0], outs[1]

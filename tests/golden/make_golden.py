@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent.parent))
 
-from oracle import add_norm, rope  # noqa: E402
+from oracle import add_norm, embed, rope  # noqa: E402
 from oracle.bf16 import from_float  # noqa: E402
 
 
@@ -51,7 +51,19 @@ def make_qk_norm_rope() -> dict[str, np.ndarray]:
                 epilogue_q=eq, epilogue_k=ek)
 
 
-MAKERS = {"add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope}
+def make_embed() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(3)
+    vocab, hidden, length, position = 300, 256, 12, 7
+    embedding = from_float(0.02 * rng.standard_normal((vocab, hidden)))
+    tokens = rng.integers(0, vocab, size=(2, length), dtype=np.int32)
+    full, sliding = rope.angle_table(40, 8, 1e6)
+    out, full_out, sliding_out = embed.embed_atlas(tokens, embedding, full, sliding, position, length)
+    return dict(embedding=embedding, tokens=tokens, full=full, sliding=sliding,
+                position=np.int64(position), hidden=out, full_out=full_out,
+                sliding_out=sliding_out)
+
+
+MAKERS = {"add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed}
 
 
 def main(names: list[str]) -> None:
