@@ -185,6 +185,45 @@ def workloads() -> list[Workload]:
             offset=a["offset"], log2_base=math.log2(1e6), eps=1e-6,
             queries=a["oq"], keys=a["ok"]),
     ))
+    # SwiGLU over [8192, 9728] and the DeltaNet gate-softplus over [8192, 32].
+    def setup_swiglu(device, copies, rows=8192, inner=9728):
+        rng = np.random.default_rng(5)
+        first = dict(
+            g=_to_bf16_device(_normal(rng, (rows, inner)), device),
+            u=_to_bf16_device(_normal(rng, (rows, inner)), device),
+            y=torch.empty((rows, inner), dtype=torch.bfloat16, device=device),
+        )
+        return _copies(first, copies)
+
+    out.append(Workload(
+        name="swiglu",
+        kernel="swiglu_flat_kernel",
+        description="gate, up bf16 [8192, 9728] ~N(0,1) -> silu(gate) * up bf16",
+        bytes_per_launch=3 * 8192 * 9728 * 2,
+        setup=setup_swiglu,
+        launch=lambda a: ops.swiglu(a["g"], a["u"], out=a["y"]),
+    ))
+
+    def setup_softplus(device, copies, rows=8192, heads=32):
+        rng = np.random.default_rng(6)
+        first = dict(
+            a=_to_bf16_device(_normal(rng, (rows, heads)), device),
+            a_log=torch.from_numpy(rng.uniform(0, 2.7, heads).astype(np.float32)).to(device),
+            dt_bias=torch.from_numpy((0.5 * rng.standard_normal(heads)).astype(np.float32)).to(device),
+            g=torch.empty((rows, heads), dtype=torch.float32, device=device),
+        )
+        return _copies(first, copies)
+
+    out.append(Workload(
+        name="gate_softplus",
+        kernel="gate_softplus_kernel",
+        description="a bf16 [8192, 32] ~N(0,1), A_log ~U(0,2.7), dt_bias ~N(0,0.5) fp32 [32] "
+                    "-> -exp(A_log) * softplus(a + dt_bias) fp32",
+        bytes_per_launch=8192 * 32 * 2 + 2 * 32 * 4 + 8192 * 32 * 4,
+        setup=setup_softplus,
+        launch=lambda a: ops.gate_softplus(a["a"], a["a_log"], a["dt_bias"], out=a["g"]),
+    ))
+
     # embedding gather + cos/sin atlas rows.
     def setup_embed(device, copies, vocab=151936, hidden=2560, batch=8, length=2048):
         rng = np.random.default_rng(4)
@@ -248,8 +287,14 @@ def time_workload(w: Workload, steps: int, warmup: int, device, graph_mode: bool
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
-        for i in range(warmup):
+        # Warm up for `warmup` launches and at least ~25 ms, so clocks have ramped and
+        # every rotation buffer has been touched before timing.
+        began, i = time.perf_counter(), 0
+        while i < max(warmup, copies) or time.perf_counter() - began < 0.025:
             w.launch(sets[i % copies])
+            i += 1
+            if i % 64 == 0:
+                torch.cuda.synchronize(device)
         torch.cuda.synchronize(device)
         if graph_mode:
             graph = torch.cuda.CUDAGraph()

@@ -110,6 +110,28 @@ int32_t omnia_embed_atlas(const int32_t* tokens, int64_t n_tokens,
                           uint16_t* hidden_out, float* full_out, float* sliding_out,
                           hipStream_t stream);
 
+/* SwiGLU activation of blocked gate/up rows:
+ *   out[r, i] = bf16(bf16(g * bf16(sigmoid(g))) * u),  g = gate[r, i], u = up[r, i]
+ * gate, up [rows, inner] bf16 with row strides (elements) gate_stride, up_stride, e.g.
+ * two tensors, or the halves of a fused [rows, 2*inner] projection; out contiguous
+ * [rows, inner]. The sigmoid is the correctly rounded bf16 value.
+ * Replaces the Core chain core/layers.py:249-250,284-287 (`swish`, `SwiGLU`,
+ * SwitchGLU.activate) and core/kernels/gate_up/default.py:71-81 (the routed epilogue).
+ * inner and both strides: multiples of 8. */
+int32_t omnia_swiglu(const uint16_t* gate, int64_t gate_stride, const uint16_t* up,
+                     int64_t up_stride, uint16_t* out, int64_t rows, int64_t inner,
+                     hipStream_t stream);
+
+/* DeltaNet gate: out[r, h] = -exp(A_log[h]) * softplus(f32(a[r, h]) + dt_bias[h]), fp32,
+ * softplus(x) = mx.logaddexp(x, 0) = max(x,0) + log1p(exp(-|x|)) with its inf/NaN arms,
+ * each fp32 step correctly rounded. a [rows, heads] bf16 (row stride a_stride),
+ * A_log and dt_bias [heads] fp32, out contiguous [rows, heads] fp32.
+ * Replaces: models/qwen3_5/layers/deltanet.py:222-224 (also models/qwen3_next/layers/
+ * deltanet.py:122-123); softplus lowering as core/kernels/qmv/softplus.py:64-76. */
+int32_t omnia_gate_softplus(const uint16_t* a, int64_t a_stride, const float* a_log,
+                            const float* dt_bias, float* out, int64_t rows, int64_t heads,
+                            hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,241 @@
+// Gated activations: SwiGLU and the DeltaNet gate-softplus.
+//
+// SwiGLU (core/layers.py:249-250,284-287 `gate * mx.sigmoid(gate) * up`, three bf16
+// ops, each rounding its result):
+//   s = bf16(sigmoid(g)),  t = bf16(g * s),  y = bf16(t * u)
+// s is the correctly rounded bf16 of the sigmoid of the bf16 input. It is evaluated in
+// fp32 from the hardware 2^x with the exponent split into a high part and its exact
+// residual (error <= ~5 fp32 ulp); when that value lies within 16 fp32 ulp of a bf16
+// rounding midpoint (about one element in 2000), or |g| > 80, the sigmoid is
+// recomputed in fp64 and rounded straight from fp64, behind one branch per vector and
+// out of line, so the common path stays at the streaming-copy speed. g * s and t * u are products of
+// two bf16 values, exact in fp32, so y is fully determined: the kernel is bit-exact
+// against any correctly rounded restatement of the chain.
+//
+// Gate-softplus (models/qwen3_5/layers/deltanet.py:222-224):
+//   dt = f32(a) + dt_bias;  g = -exp(A_log) * softplus(dt)       all fp32
+// with softplus = mx.logaddexp(dt, 0) = max + log1p(exp(min - max)) and its inf/NaN
+// arms (the lowering core/kernels/qmv/softplus.py:64-76 restates). Each fp32 step is
+// evaluated in fp64 and rounded once, so it is correctly rounded; the data (a [T, 32]
+// bf16) is small and the extra fp64 work is hidden behind memory latency.
+//
+// Layout: 16-byte vectors of 8 bf16; SwiGLU streams the flat array (or row-strided
+// views, e.g. the two halves of a fused [T, 2I] projection) with one vector per lane,
+// the pattern measured fastest for a streaming copy on MI355X.
+#include "common.hpp"
+#include "host.hpp"
+
+namespace omnia {
+namespace {
+
+constexpr int kBlock = 256;
+
+// fp64 -> bf16 bits, round to nearest even, for values in the normal bf16 range; zero,
+// subnormals, infinities and NaN go through fp32 (a double rounding is possible only in
+// the subnormal tail, reached for sigmoid arguments below about -87).
+__device__ __forceinline__ uint32_t f64_to_bf16(double value) {
+  const uint64_t bits = __builtin_bit_cast(uint64_t, value);
+  const uint32_t sign = static_cast<uint32_t>(bits >> 48) & 0x8000u;
+  const int exponent = static_cast<int>((bits >> 52) & 0x7FF) - 1023;
+  if (exponent < -126 || exponent > 127) return f32_to_bf16(static_cast<float>(value));
+  const uint64_t mantissa = bits & ((uint64_t{1} << 52) - 1);
+  const uint64_t rest = mantissa & ((uint64_t{1} << 45) - 1);
+  constexpr uint64_t kHalf = uint64_t{1} << 44;
+  uint32_t magnitude = (static_cast<uint32_t>(exponent + 127) << 7) |
+                       static_cast<uint32_t>(mantissa >> 45);
+  if (rest > kHalf || (rest == kHalf && (magnitude & 1u))) ++magnitude;
+  return sign | magnitude;
+}
+
+// sigmoid(g) in fp32 from the hardware 2^x, the exponent split into a high part and
+// its exact residual: within about 5 fp32 ulp of the true value. `hard` is set when
+// that is not enough to decide the bf16 rounding: the value lies within 16 fp32 ulp of
+// a bf16 rounding midpoint, or |g| > 80 (or g is NaN).
+__device__ __forceinline__ float sigmoid_fast(float g, bool& hard) {
+  constexpr float kLog2e = 1.44269502162933349609375f;       // fp32(log2 e)
+  constexpr float kLog2eLo = 1.925963033500011079101241e-8f;  // log2 e - kLog2e
+  constexpr float kLn2 = 0.693147180559945309417232f;
+  const float a = fabsf(g);
+  const float xh = -a * kLog2e;
+  const float xl = __builtin_fmaf(-a, kLog2eLo, __builtin_fmaf(-a, kLog2e, -xh));
+  const float p = __builtin_amdgcn_exp2f(xh);
+  const float e = __builtin_fmaf(p, xl * kLn2, p);              // exp(-|g|)
+  const float s = (g >= 0.0f ? 1.0f : e) * __builtin_amdgcn_rcpf(1.0f + e);
+  const uint32_t low = __float_as_uint(s) & 0xFFFFu;
+  hard = !(a <= 80.0f) || low - 0x7FF0u <= 0x20u;
+  return s;
+}
+
+// The correctly rounded bf16 of sigmoid(g) (as fp32), from fp64.
+__device__ __attribute__((noinline)) float sigmoid_exact(float g) {
+  const double ed = exp(-static_cast<double>(fabsf(g)));
+  const double sd = (g >= 0.0f ? 1.0 : ed) / (1.0 + ed);
+  return bf16_to_f32(static_cast<uint16_t>(f64_to_bf16(sd)));
+}
+
+__device__ __forceinline__ u32x4 swiglu8(const u32x4& gate, const u32x4& up) {
+  float g[8], u[8], s[8], y[8];
+  unpack8(gate, g);
+  unpack8(up, u);
+  uint32_t hard_mask = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    bool hard;
+    s[j] = sigmoid_fast(g[j], hard);
+    hard_mask |= static_cast<uint32_t>(hard) << j;
+  }
+  // About one element in 2000 needs the fp64 evaluation; one branch per vector.
+  if (hard_mask != 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (hard_mask & (1u << j)) s[j] = sigmoid_exact(g[j]);  // already a bf16 value
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    round_pair(s[j], s[j + 1]);
+    float t0 = g[j] * s[j], t1 = g[j + 1] * s[j + 1];
+    round_pair(t0, t1);
+    y[j] = t0 * u[j];
+    y[j + 1] = t1 * u[j + 1];
+  }
+  return pack8(y);
+}
+
+// Contiguous gate, up and out: one vector per lane over the flat array.
+__global__ __launch_bounds__(kBlock) void swiglu_flat_kernel(const u32x4* __restrict__ gate,
+                                                             const u32x4* __restrict__ up,
+                                                             u32x4* __restrict__ out,
+                                                             int64_t vectors) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= vectors) return;
+  const u32x4 g = load_nt(gate + i);
+  const u32x4 u = load_nt(up + i);
+  store_nt(out + i, swiglu8(g, u));
+}
+
+// Row-strided gate and up (e.g. halves of a fused projection), contiguous out.
+__global__ __launch_bounds__(kBlock) void swiglu_rows_kernel(const uint16_t* __restrict__ gate,
+                                                             int64_t gate_stride,
+                                                             const uint16_t* __restrict__ up,
+                                                             int64_t up_stride,
+                                                             uint16_t* __restrict__ out,
+                                                             int64_t rows, uint32_t row_vectors) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= rows * row_vectors) return;
+  const int64_t r = i / row_vectors;
+  const int64_t c = (i - r * row_vectors) * 8;
+  const u32x4 g = load_nt(reinterpret_cast<const u32x4*>(gate + r * gate_stride + c));
+  const u32x4 u = load_nt(reinterpret_cast<const u32x4*>(up + r * up_stride + c));
+  store_nt(reinterpret_cast<u32x4*>(out + r * row_vectors * 8 + c), swiglu8(g, u));
+}
+
+// softplus(dt) as mx.logaddexp(dt, 0): max + log1p(exp(min - max)), each fp32 step
+// correctly rounded (evaluated in fp64, rounded once).
+__device__ __forceinline__ float softplus_f32(float dt) {
+  const float maxval = dt > 0.0f ? dt : 0.0f;
+  const float minval = dt > 0.0f ? 0.0f : dt;
+  if (minval == -__builtin_huge_valf() || maxval == __builtin_huge_valf()) return maxval;
+  const float r1 = static_cast<float>(exp(static_cast<double>(minval - maxval)));
+  const float r2 = static_cast<float>(log1p(static_cast<double>(r1)));
+  return maxval + r2;
+}
+
+__device__ __forceinline__ float gate_softplus1(float a, float a_log, float dt_bias) {
+  const float dt = a + dt_bias;
+  const float decay = -static_cast<float>(exp(static_cast<double>(a_log)));
+  return decay * softplus_f32(dt);
+}
+
+// Even head count, 4-byte aligned rows: one pair of heads per lane. The tensor is small
+// (1.5 MB at the config) and each element carries three fp64 transcendentals, so the
+// grid is spread wide rather than vectorised deep.
+__global__ __launch_bounds__(kBlock) void gate_softplus_kernel(
+    const uint16_t* __restrict__ a, int64_t a_stride, const float* __restrict__ a_log,
+    const float* __restrict__ dt_bias, float* __restrict__ out, int64_t rows, int heads) {
+  const int head_pairs = heads / 2;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= rows * head_pairs) return;
+  const int64_t r = i / head_pairs;
+  const int h = static_cast<int>(i - r * head_pairs) * 2;
+  const uint32_t x = *reinterpret_cast<const uint32_t*>(a + r * a_stride + h);
+  const f32x2 la = *reinterpret_cast<const f32x2*>(a_log + h);
+  const f32x2 bb = *reinterpret_cast<const f32x2*>(dt_bias + h);
+  const f32x2 o = {gate_softplus1(bf16_lo(x), la.x, bb.x), gate_softplus1(bf16_hi(x), la.y, bb.y)};
+  *reinterpret_cast<f32x2*>(out + r * heads + h) = o;
+}
+
+// Any head count or alignment: one element per lane.
+__global__ __launch_bounds__(kBlock) void gate_softplus_scalar_kernel(
+    const uint16_t* __restrict__ a, int64_t a_stride, const float* __restrict__ a_log,
+    const float* __restrict__ dt_bias, float* __restrict__ out, int64_t rows, int heads) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= rows * heads) return;
+  const int64_t r = i / heads;
+  const int h = static_cast<int>(i - r * heads);
+  out[i] = gate_softplus1(bf16_to_f32(a[r * a_stride + h]), a_log[h], dt_bias[h]);
+}
+
+unsigned blocks_for(int64_t items) {
+  return static_cast<unsigned>((items + kBlock - 1) / kBlock);
+}
+
+}  // namespace
+}  // namespace omnia
+
+extern "C" int32_t omnia_swiglu(const uint16_t* gate, int64_t gate_stride, const uint16_t* up,
+                                int64_t up_stride, uint16_t* out, int64_t rows,
+                                int64_t inner, hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(rows >= 0 && inner > 0 && inner % 8 == 0,
+                "swiglu: inner must be a positive multiple of 8");
+  OMNIA_REQUIRE(gate_stride >= inner && up_stride >= inner && gate_stride % 8 == 0 &&
+                    up_stride % 8 == 0,
+                "swiglu: row strides must be >= inner and multiples of 8");
+  OMNIA_REQUIRE(rows * (inner / 8) < (int64_t{1} << 40), "swiglu: too large");
+  if (rows == 0) return 0;
+  OMNIA_REQUIRE(gate && up && out, "swiglu: null pointer");
+  OMNIA_REQUIRE(aligned16(gate) && aligned16(up) && aligned16(out),
+                "swiglu: pointers must be 16-byte aligned");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  const int64_t vectors = rows * (inner / 8);
+  OMNIA_REQUIRE(vectors / kBlock < (int64_t{1} << 31), "swiglu: grid too large");
+  if (gate_stride == inner && up_stride == inner) {
+    swiglu_flat_kernel<<<blocks_for(vectors), kBlock, 0, stream>>>(
+        reinterpret_cast<const u32x4*>(gate), reinterpret_cast<const u32x4*>(up),
+        reinterpret_cast<u32x4*>(out), vectors);
+  } else {
+    OMNIA_REQUIRE(inner / 8 < (int64_t{1} << 31), "swiglu: rows too wide");
+    swiglu_rows_kernel<<<blocks_for(vectors), kBlock, 0, stream>>>(
+        gate, gate_stride, up, up_stride, out, rows, static_cast<uint32_t>(inner / 8));
+  }
+  return launched("swiglu");
+}
+
+extern "C" int32_t omnia_gate_softplus(const uint16_t* a, int64_t a_stride, const float* a_log,
+                                       const float* dt_bias, float* out, int64_t rows,
+                                       int64_t heads, hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(rows >= 0 && heads > 0 && heads <= (int64_t{1} << 20),
+                "gate_softplus: bad heads");
+  OMNIA_REQUIRE(a_stride >= heads, "gate_softplus: row stride smaller than heads");
+  OMNIA_REQUIRE(rows * heads < (int64_t{1} << 40), "gate_softplus: too large");
+  if (rows == 0) return 0;
+  OMNIA_REQUIRE(a && a_log && dt_bias && out, "gate_softplus: null pointer");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  const auto aligned = [](const void* p, uintptr_t n) {
+    return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0;
+  };
+  const bool paired = heads % 2 == 0 && a_stride % 2 == 0 && aligned(a, 4) &&
+                      aligned(a_log, 8) && aligned(dt_bias, 8) && aligned(out, 8);
+  if (paired) {
+    gate_softplus_kernel<<<blocks_for(rows * heads / 2), kBlock, 0, stream>>>(
+        a, a_stride, a_log, dt_bias, out, rows, static_cast<int>(heads));
+  } else {
+    gate_softplus_scalar_kernel<<<blocks_for(rows * heads), kBlock, 0, stream>>>(
+        a, a_stride, a_log, dt_bias, out, rows, static_cast<int>(heads));
+  }
+  return launched("gate_softplus");
+}

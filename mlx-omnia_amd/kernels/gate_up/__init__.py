@@ -1,0 +1,36 @@
+"""The gate/up activation: one facade, two bindings (`HipSwiGLU` ahead of the Core
+chain `DefaultGateUpActivation`), resolved by the declaration (activation, layout,
+clamp) with the reference's first-build-wins rule."""
+
+from __future__ import annotations
+
+import torch
+
+from ..resolve import resolve
+from .default import DefaultGateUpActivation, swiglu_core
+from .hip import HipSwiGLU, applies
+from .kernel import Activation, GateUpActivationStrategy, Layout, split
+
+__all__ = [
+    "DefaultGateUpActivation",
+    "GateUpActivation",
+    "GateUpActivationStrategy",
+    "HipSwiGLU",
+    "applies",
+    "split",
+    "swiglu_core",
+]
+
+_STRATEGIES = (HipSwiGLU, DefaultGateUpActivation)
+
+
+class GateUpActivation(GateUpActivationStrategy):
+    def __init__(self, *, activation: Activation = "swiglu", layout: Layout = "blocked",
+                 limit: float | None = None, reference: bool = False) -> None:
+        self.strategy: GateUpActivationStrategy = resolve(
+            (DefaultGateUpActivation,) if reference else _STRATEGIES,
+            activation=activation, layout=layout, limit=limit,
+        )
+
+    def __call__(self, gate_up: torch.Tensor, up: torch.Tensor | None = None) -> torch.Tensor:
+        return self.strategy(gate_up, up)

@@ -34,6 +34,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "omnia_rope_epilogue": (
         _I32, [_P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _F32, _F32, _P]
     ),
+    "omnia_swiglu": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _P]),
+    "omnia_gate_softplus": (_I32, [_P, _I64, _P, _P, _P, _I64, _I64, _P]),
     "omnia_embed_atlas": (
         _I32,
         [_P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P],

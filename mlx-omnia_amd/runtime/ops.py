@@ -220,3 +220,50 @@ def embed_atlas(
         _stream(embedding),
     )
     return hidden_out, outs[0], outs[1]
+
+
+def _row_stride(t: torch.Tensor, name: str) -> int:
+    """Row stride of a [rows, width] bf16 view with unit inner stride."""
+    _require(t.dim() == 2 and t.dtype == BF16, f"{name}: expected bf16 [rows, width]")
+    if t.shape[0] <= 1:
+        return t.shape[1]
+    _require(t.stride(1) == 1, f"{name}: inner axis must be contiguous")
+    return t.stride(0)
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """`bf16(bf16(g * bf16(sigmoid(g))) * u)` over [..., inner]; see `omnia_swiglu`.
+
+    gate and up may be row-strided views (e.g. the halves of a fused [T, 2I] projection)
+    as long as all leading axes flatten into one row axis."""
+    _require(gate.shape == up.shape, "swiglu: gate and up shapes differ")
+    inner = gate.shape[-1]
+    g2 = gate.reshape(-1, inner) if gate.is_contiguous() else gate
+    u2 = up.reshape(-1, inner) if up.is_contiguous() else up
+    if g2.dim() != 2 or u2.dim() != 2:
+        g2, u2 = gate.reshape(-1, inner), up.reshape(-1, inner)
+    _require(on_rocm(g2, u2), "swiglu: tensors must share one ROCm device")
+    gs, us = _row_stride(g2, "gate"), _row_stride(u2, "up")
+    out = _out(out, gate, gate.shape, BF16, "out")
+    call("omnia_swiglu", g2.data_ptr(), gs, u2.data_ptr(), us, out.data_ptr(),
+         g2.shape[0], inner, _stream(gate))
+    return out
+
+
+def gate_softplus(a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor, *,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """`-exp(A_log) * softplus(f32(a) + dt_bias)` over [..., heads] -> fp32; see
+    `omnia_gate_softplus`."""
+    heads = a.shape[-1]
+    a2 = a.reshape(-1, heads) if a.is_contiguous() else a
+    _require(a2.dim() == 2 and a2.dtype == BF16, "gate_softplus: a must be bf16 [rows, heads]")
+    _require(a_log.shape == (heads,) and dt_bias.shape == (heads,), "gate_softplus: [heads] params")
+    _dense(a_log, F32, "A_log")
+    _dense(dt_bias, F32, "dt_bias")
+    _require(on_rocm(a2, a_log, dt_bias), "gate_softplus: tensors must share one ROCm device")
+    stride = heads if a2.shape[0] <= 1 else a2.stride(0)
+    _require(a2.stride(-1) == 1, "gate_softplus: heads axis must be contiguous")
+    out = _out(out, a, a.shape, F32, "out")
+    call("omnia_gate_softplus", a2.data_ptr(), stride, a_log.data_ptr(), dt_bias.data_ptr(),
+         out.data_ptr(), a2.shape[0], heads, _stream(a))
+    return out

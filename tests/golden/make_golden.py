@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent.parent))
 
-from oracle import add_norm, embed, rope  # noqa: E402
+from oracle import activations, add_norm, embed, rope  # noqa: E402
 from oracle.bf16 import from_float  # noqa: E402
 
 
@@ -63,7 +63,19 @@ def make_embed() -> dict[str, np.ndarray]:
                 sliding_out=sliding_out)
 
 
-MAKERS = {"add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed}
+def make_activations() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(4)
+    gate = from_float(3 * rng.standard_normal((16, 256)))
+    up = from_float(rng.standard_normal((16, 256)))
+    a = from_float(rng.standard_normal((16, 32)))
+    a_log = rng.uniform(0, 2.7, 32).astype(np.float32)
+    dt_bias = (0.5 * rng.standard_normal(32)).astype(np.float32)
+    return dict(gate=gate, up=up, swiglu=activations.swiglu(gate, up), a=a, a_log=a_log,
+                dt_bias=dt_bias, gate_softplus=activations.gate_softplus(a, a_log, dt_bias))
+
+
+MAKERS = {"add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed,
+          "activations": make_activations}
 
 
 def main(names: list[str]) -> None:
