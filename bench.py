@@ -224,6 +224,36 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.gate_softplus(a["a"], a["a_log"], a["dt_bias"], out=a["g"]),
     ))
 
+    # residual add + RMSNorm + router projection + softmax top-8 (Qwen3-30B-A3B).
+    def setup_router(device, copies, rows=4096, hidden=2048, experts=128, k=8):
+        rng = np.random.default_rng(7)
+        first = dict(
+            x=_to_bf16_device(_normal(rng, (rows, hidden)), device),
+            r=_to_bf16_device(_normal(rng, (rows, hidden)), device),
+            w=_to_bf16_device(_normal(rng, (hidden,), 0.1, 1.0), device),
+            gate=_to_bf16_device(_normal(rng, (experts, hidden), 0.02), device),
+            s=torch.empty((rows, hidden), dtype=torch.bfloat16, device=device),
+            n=torch.empty((rows, hidden), dtype=torch.bfloat16, device=device),
+            idx=torch.empty((rows, k), dtype=torch.int32, device=device),
+            wts=torch.empty((rows, k), dtype=torch.float32, device=device),
+        )
+        sets = _copies(first, copies)
+        for entry in sets:
+            entry["gate"], entry["w"] = first["gate"], first["w"]
+        return sets
+
+    out.append(Workload(
+        name="residual_rms_router",
+        kernel="residual_rms_router_kernel",
+        description="x, residual bf16 [4096, 2048] ~N(0,1), norm weight 1+N(0,0.1), router "
+                    "[128, 2048] ~N(0,0.02) -> summed, normed, top-8 indices + fp32 weights",
+        bytes_per_launch=4 * 4096 * 2048 * 2 + 2048 * 2 + 128 * 2048 * 2 + 2 * 4096 * 8 * 4,
+        setup=setup_router,
+        launch=lambda a: ops.residual_rms_router(
+            a["x"], a["r"], a["w"], a["gate"], k=8, eps=1e-6, summed=a["s"],
+            normalized=a["n"], indices=a["idx"], weights=a["wts"]),
+    ))
+
     # embedding gather + cos/sin atlas rows.
     def setup_embed(device, copies, vocab=151936, hidden=2560, batch=8, length=2048):
         rng = np.random.default_rng(4)

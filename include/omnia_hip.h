@@ -132,6 +132,42 @@ int32_t omnia_gate_softplus(const uint16_t* a, int64_t a_stride, const float* a_
                             const float* dt_bias, float* out, int64_t rows, int64_t heads,
                             hipStream_t stream);
 
+/* Softmax -> top-k -> renormalise over given router logits, one row per token:
+ *   indices[r, :k] = the k largest bf16 logits of row r in descending order, an exact
+ *                    tie going to the lower expert index (int32);
+ *   weights[r, :k] = softmax(logits[r])[indices] / sum of the same (fp32).
+ * logits [rows, experts] bf16 with row stride `stride`; experts <= 256, k <= 64.
+ * Replaces: core/kernels/route/softmax_topk.py:20-75,215-230 (`moe_softmax_topk`,
+ * SoftmaxTopkRoute.__call__) and the Core chain core/kernels/route/default.py:44-69 /
+ * models/qwen3/layers/moe.py:34-42, served for many rows at once, with the
+ * lowest-index tie rule of core/kernels/route/ordinal.py:1-27 (the reference's softmax
+ * path breaks ties toward the higher index). */
+int32_t omnia_softmax_topk(const uint16_t* logits, int64_t stride, int64_t rows,
+                           int64_t experts, int64_t k, int32_t* indices, float* weights,
+                           hipStream_t stream);
+
+/* Residual add + RMSNorm + router projection + softmax top-k, fused:
+ *   summed, normalized [rows, hidden] bf16 exactly as omnia_add_rms_norm;
+ *   logits [rows, experts] = bf16(normalized x router_weight^T), the correctly rounded
+ *     dot products (matrix-core accumulation, with an fp64 recomputation wherever the
+ *     fp32 accumulation error could change the rounding), written only when `logits`
+ *     is not NULL;
+ *   indices [rows, k] int32, weights [rows, k] fp32 exactly as omnia_softmax_topk
+ *     applied to those logits.
+ * x, branch [rows, hidden] bf16; norm_weight [hidden] bf16; router_weight
+ * [experts, hidden] bf16. (hidden, experts) in {(2048, 128), (2048, 256), (4096, 128)};
+ * k <= 64.
+ * Replaces: core/kernels/route/residual.py:117-299 (`residual_rms_router`, the
+ * one-token residual join with the router gemv fused), generalised to many tokens and
+ * to softmax routing; the Core chain is add_norm/default.py:28-29 followed by
+ * route/default.py:44-69. */
+int32_t omnia_residual_rms_router(const uint16_t* x, const uint16_t* branch,
+                                  const uint16_t* norm_weight, const uint16_t* router_weight,
+                                  int64_t rows, int64_t hidden, int64_t experts, int64_t k,
+                                  float eps, uint16_t* summed, uint16_t* normalized,
+                                  uint16_t* logits, int32_t* indices, float* weights,
+                                  hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

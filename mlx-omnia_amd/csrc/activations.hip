@@ -30,23 +30,6 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// fp64 -> bf16 bits, round to nearest even, for values in the normal bf16 range; zero,
-// subnormals, infinities and NaN go through fp32 (a double rounding is possible only in
-// the subnormal tail, reached for sigmoid arguments below about -87).
-__device__ __forceinline__ uint32_t f64_to_bf16(double value) {
-  const uint64_t bits = __builtin_bit_cast(uint64_t, value);
-  const uint32_t sign = static_cast<uint32_t>(bits >> 48) & 0x8000u;
-  const int exponent = static_cast<int>((bits >> 52) & 0x7FF) - 1023;
-  if (exponent < -126 || exponent > 127) return f32_to_bf16(static_cast<float>(value));
-  const uint64_t mantissa = bits & ((uint64_t{1} << 52) - 1);
-  const uint64_t rest = mantissa & ((uint64_t{1} << 45) - 1);
-  constexpr uint64_t kHalf = uint64_t{1} << 44;
-  uint32_t magnitude = (static_cast<uint32_t>(exponent + 127) << 7) |
-                       static_cast<uint32_t>(mantissa >> 45);
-  if (rest > kHalf || (rest == kHalf && (magnitude & 1u))) ++magnitude;
-  return sign | magnitude;
-}
-
 // sigmoid(g) in fp32 from the hardware 2^x, the exponent split into a high part and
 // its exact residual: within about 5 fp32 ulp of the true value. `hard` is set when
 // that is not enough to decide the bf16 rounding: the value lies within 16 fp32 ulp of

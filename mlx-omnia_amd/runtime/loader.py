@@ -36,6 +36,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "omnia_swiglu": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _P]),
     "omnia_gate_softplus": (_I32, [_P, _I64, _P, _P, _P, _I64, _I64, _P]),
+    "omnia_softmax_topk": (_I32, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "omnia_residual_rms_router": (
+        _I32,
+        [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _P, _P, _P, _P],
+    ),
     "omnia_embed_atlas": (
         _I32,
         [_P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P],

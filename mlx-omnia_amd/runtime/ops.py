@@ -267,3 +267,66 @@ def gate_softplus(a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor, *
     call("omnia_gate_softplus", a2.data_ptr(), stride, a_log.data_ptr(), dt_bias.data_ptr(),
          out.data_ptr(), a2.shape[0], heads, _stream(a))
     return out
+
+
+def softmax_topk(logits: torch.Tensor, k: int, *, indices: torch.Tensor | None = None,
+                 weights: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Top-k of bf16 router logits [..., E] (lowest index on ties) and the renormalised
+    softmax weights; see `omnia_softmax_topk`. Returns int32 and fp32 [..., k]."""
+    experts = logits.shape[-1]
+    rows2 = logits.reshape(-1, experts) if logits.is_contiguous() else logits
+    _require(rows2.dim() == 2 and rows2.dtype == BF16 and rows2.stride(-1) == 1,
+             "softmax_topk: logits must be bf16 [rows, experts] with unit inner stride")
+    _require(on_rocm(rows2), "softmax_topk: logits must be on a ROCm device")
+    stride = experts if rows2.shape[0] <= 1 else rows2.stride(0)
+    shape = (*logits.shape[:-1], k)
+    indices = _out(indices, logits, shape, torch.int32, "indices")
+    weights = _out(weights, logits, shape, F32, "weights")
+    call("omnia_softmax_topk", rows2.data_ptr(), stride, rows2.shape[0], experts, int(k),
+         indices.data_ptr(), weights.data_ptr(), _stream(logits))
+    return indices, weights
+
+
+def residual_rms_router(
+    x: torch.Tensor,
+    branch: torch.Tensor,
+    norm_weight: torch.Tensor,
+    router_weight: torch.Tensor,
+    *,
+    k: int,
+    eps: float,
+    emit_logits: bool = False,
+    summed: torch.Tensor | None = None,
+    normalized: torch.Tensor | None = None,
+    logits: torch.Tensor | None = None,
+    indices: torch.Tensor | None = None,
+    weights: torch.Tensor | None = None,
+):
+    """Fused residual add + RMSNorm + router projection + top-k; see
+    `omnia_residual_rms_router`. Returns (summed, normalized, logits or None, indices,
+    weights)."""
+    hidden = norm_weight.numel()
+    experts = router_weight.shape[0]
+    _require(x.shape == branch.shape and x.shape[-1] == hidden, "residual_rms_router: shape mismatch")
+    _require(router_weight.shape == (experts, hidden), "residual_rms_router: router weight shape")
+    for t, name in ((x, "x"), (branch, "branch"), (norm_weight, "norm_weight"),
+                    (router_weight, "router_weight")):
+        _dense(t, BF16, name)
+    _require(on_rocm(x, branch, norm_weight, router_weight),
+             "residual_rms_router: tensors must share one ROCm device")
+    rows = x.numel() // hidden
+    lead = x.shape[:-1]
+    summed = _out(summed, x, x.shape, BF16, "summed")
+    normalized = _out(normalized, x, x.shape, BF16, "normalized")
+    if emit_logits or logits is not None:
+        logits = _out(logits, x, (*lead, experts), BF16, "logits")
+    indices = _out(indices, x, (*lead, k), torch.int32, "indices")
+    weights = _out(weights, x, (*lead, k), F32, "weights")
+    call(
+        "omnia_residual_rms_router",
+        x.data_ptr(), branch.data_ptr(), norm_weight.data_ptr(), router_weight.data_ptr(),
+        rows, hidden, experts, int(k), float(eps), summed.data_ptr(), normalized.data_ptr(),
+        logits.data_ptr() if logits is not None else None, indices.data_ptr(),
+        weights.data_ptr(), _stream(x),
+    )
+    return summed, normalized, logits, indices, weights

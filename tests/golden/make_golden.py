@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent.parent))
 
-from oracle import activations, add_norm, embed, rope  # noqa: E402
+from oracle import activations, add_norm, embed, rope, route  # noqa: E402
 from oracle.bf16 import from_float  # noqa: E402
 
 
@@ -74,8 +74,18 @@ def make_activations() -> dict[str, np.ndarray]:
                 dt_bias=dt_bias, gate_softplus=activations.gate_softplus(a, a_log, dt_bias))
 
 
+def make_route() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(5)
+    logits = from_float(rng.standard_normal((24, 128)))
+    values = np.arange(128, dtype=np.float64) * -0.5
+    values[[3, 11, 35, 67, 99, 120]] = values[3]
+    logits[0] = from_float(values)
+    indices, weights = route.softmax_topk(logits, 8)
+    return dict(logits=logits, k=np.int64(8), indices=indices, weights=weights)
+
+
 MAKERS = {"add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed,
-          "activations": make_activations}
+          "activations": make_activations, "route": make_route}
 
 
 def main(names: list[str]) -> None:

@@ -1,0 +1,113 @@
+"""HIP routing kernels against the oracle.
+
+softmax_topk: indices bit-exact (ties to the lowest index), weights within rtol 1e-5.
+residual_rms_router at the config (x, residual [4096, 2048] ~N(0,1), norm weight
+1 + N(0, 0.1), router [128, 2048] ~N(0, 0.02), k = 8):
+  - summed bit-exact, normalized within the bf16 bar;
+  - logits (when emitted) bit-exact with the oracle's correctly rounded dot products:
+    the kernel refines every logit whose fp32 matrix-core value could round otherwise;
+  - indices bit-exact with the full oracle chain, with and without emitted logits (only
+    the decisive logits are refined then); weights within rtol 1e-5;
+  - exact ties forced through the fused projection (duplicated router rows give equal
+    logits whatever the accumulation order) resolve to the lowest index.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from mlx_omnia_amd.kernels.leaf import RMSNormLeaf
+from mlx_omnia_amd.kernels.route import HipResidualRouter, HipSoftmaxTopkRoute, ResidualRouter, Route, Routing
+from mlx_omnia_amd.runtime import ops
+from oracle import route
+from oracle.bf16 import from_float, ulp_distance
+from util import assert_bf16_close, bits_of, to_device
+
+pytestmark = pytest.mark.gpu
+
+KAT_EXPECTED = [0, 1, 2, 3, 11, 35, 67, 99]
+
+
+def _tied(experts):
+    values = np.arange(experts, dtype=np.float64) * -0.5
+    values[[3, 11, 35, 67, 99, 120]] = values[3]
+    return from_float(values)[None, :]
+
+
+@pytest.mark.parametrize("experts,k", [(128, 8), (256, 8), (64, 4), (100, 16), (32, 32)])
+def test_softmax_topk_matches_oracle(experts, k):
+    rng = np.random.default_rng(experts + k)
+    logits = from_float(rng.standard_normal((1000, experts)))
+    logits[:10] = from_float(rng.integers(-3, 3, (10, experts)) * 0.5)  # heavy ties
+    idx, w = ops.softmax_topk(to_device(logits), k)
+    want_idx, want_w = route.softmax_topk(logits, k)
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(w.cpu().numpy(), want_w, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("experts", [128, 256])
+def test_softmax_topk_tie_fixture_via_facade(experts):
+    facade = Route(None, experts=experts, k=8)
+    assert isinstance(facade.strategy, HipSoftmaxTopkRoute)
+    idx, w = facade.rows(to_device(_tied(experts)))
+    assert idx.cpu().numpy()[0].tolist() == KAT_EXPECTED
+    assert abs(float(w.sum()) - 1.0) < 1e-6
+
+
+def _router_inputs(rows, hidden, experts, seed):
+    rng = np.random.default_rng(seed)
+    return (
+        from_float(rng.standard_normal((rows, hidden), dtype=np.float32)),
+        from_float(rng.standard_normal((rows, hidden), dtype=np.float32)),
+        from_float(1.0 + 0.1 * rng.standard_normal(hidden)),
+        from_float(0.02 * rng.standard_normal((experts, hidden), dtype=np.float32)),
+    )
+
+
+@pytest.mark.parametrize("rows,hidden,experts,k", [
+    (4096, 2048, 128, 8), (1, 2048, 128, 8), (37, 2048, 128, 8), (300, 4096, 128, 8), (50, 2048, 256, 16),
+])
+def test_residual_router_matches_oracle(rows, hidden, experts, k):
+    print(f"residual_rms_router rows={rows} hidden={hidden} experts={experts} k={k}", flush=True)
+    x, r, w, gate = _router_inputs(rows, hidden, experts, seed=rows + hidden + experts)
+    s, n, logits, idx, wts = ops.residual_rms_router(
+        to_device(x), to_device(r), to_device(w), to_device(gate), k=k, eps=1e-6, emit_logits=True)
+    torch.cuda.synchronize()
+    want_s, want_n, want_logits, want_idx, want_w = route.residual_rms_router(x, r, w, gate, 1e-6, k)
+    assert np.array_equal(bits_of(s), want_s)
+    assert_bf16_close(bits_of(n), want_n)
+    # Emitted logits are the correctly rounded dot products, bit for bit.
+    assert np.array_equal(bits_of(logits), want_logits)
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(wts.cpu().numpy(), want_w, rtol=1e-5, atol=1e-7)
+    # Without emitted logits only the decisive ones are refined: same selection.
+    _, _, none, idx2, wts2 = ops.residual_rms_router(
+        to_device(x), to_device(r), to_device(w), to_device(gate), k=k, eps=1e-6)
+    assert none is None
+    assert np.array_equal(idx2.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(wts2.cpu().numpy(), want_w, rtol=1e-5, atol=1e-7)
+
+
+def test_residual_router_forced_ties_and_facade():
+    rows, hidden, experts = 64, 2048, 128
+    x, r, w, gate = _router_inputs(rows, hidden, experts, seed=9)
+    # Equal router rows give equal logits: experts 3, 11, 35, 67, 99, 120 tie with 3.
+    # Positive inputs and a positive offset on those rows put the group on top.
+    rng = np.random.default_rng(10)
+    x = from_float(np.abs(rng.standard_normal((rows, hidden))) + 1.0)
+    r = from_float(0.01 * rng.standard_normal((rows, hidden)))
+    base = 0.02 * rng.standard_normal(hidden)
+    gate = from_float(np.tile(0.02 * rng.standard_normal(hidden), (experts, 1)) * 0.1)
+    gate[[3, 11, 35, 67, 99, 120]] = from_float(base + 0.05)
+    router = ResidualRouter(RMSNormLeaf(to_device(w), 1e-6), to_device(gate), routing=Routing(experts=experts, k=4))
+    assert isinstance(router.strategy, HipResidualRouter)
+    _, _, idx, _ = router(to_device(x), to_device(r))
+    got = idx.cpu().numpy()
+    assert (got == np.array([3, 11, 35, 67])).all(axis=-1).all()
+
+
+def test_golden_fixture():
+    golden = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "route.npz")
+    idx, w = ops.softmax_topk(to_device(golden["logits"]), int(golden["k"]))
+    assert np.array_equal(idx.cpu().numpy(), golden["indices"])
+    np.testing.assert_allclose(w.cpu().numpy(), golden["weights"], rtol=1e-5, atol=1e-7)
