@@ -59,6 +59,7 @@ class Workload:
     setup: Callable[[object, int], list]   # (device, copies) -> per-copy argument sets
     launch: Callable[[object], None]
     details: dict = field(default_factory=dict)
+    default: bool = True             # False: run only when named by --only
 
 
 def _normal(rng: np.random.Generator, shape, scale=1.0, shift=0.0) -> np.ndarray:
@@ -281,6 +282,22 @@ def workloads() -> list[Workload]:
             a["ids"], a["table"], a["cos"], a["sin"], position=0, n_positions=2048,
             hidden_out=a["out"], full_out=a["fo"], sliding_out=a["so"]),
     ))
+    # Not a product kernel: a plain device-to-device copy of known size, the scale for
+    # the FETCH_SIZE / WRITE_SIZE counters (run with --only copy_calibration).
+    def setup_copy(device, copies, elements=64 * 2**20):
+        first = dict(src=torch.ones(elements, dtype=torch.bfloat16, device=device),
+                     dst=torch.empty(elements, dtype=torch.bfloat16, device=device))
+        return _copies(first, copies)
+
+    out.append(Workload(
+        name="copy_calibration",
+        kernel="copy",
+        description="torch copy_ of 128 MiB bf16 (64 Mi elements): 128 MiB read + 128 MiB written",
+        bytes_per_launch=2 * 64 * 2**20 * 2,
+        setup=setup_copy,
+        launch=lambda a: a["dst"].copy_(a["src"]),
+        default=False,
+    ))
     return out
 
 
@@ -299,6 +316,8 @@ def _bound_launch(w: Workload, argset):
         w.launch(argset)
     finally:
         ops.call = original
+    if not recorded:  # not a C-ABI workload (the copy calibration)
+        return lambda: (w.launch(argset), 0)[1]
     (name, args), = recorded
     fn = getattr(loader.library(), name)
 
@@ -425,7 +444,8 @@ def main() -> int:
         print("bench.py: no ROCm device visible", file=sys.stderr)
         return 1
     device = torch.device("cuda:0")
-    selected = [w for w in workloads() if not args.only or w.name in args.only.split(",")]
+    only = [n for n in args.only.split(",") if n]
+    selected = [w for w in workloads() if ((w.name in only) if only else w.default)]
     results = {}
     for w in selected:
         print(f"[bench] {w.name}: {w.description}", file=sys.stderr, flush=True)
