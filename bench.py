@@ -301,6 +301,25 @@ def workloads() -> list[Workload]:
     return out
 
 
+def copy_ceiling(moved: int) -> Workload:
+    """A plain device-to-device copy (torch `copy_`) that reads and writes `moved` / 2 bytes:
+    what the same HBM traffic costs with no arithmetic, the practical ceiling at that size."""
+    import torch
+
+    elements = max(8, (moved // 2) // 2 // 8 * 8)
+
+    def setup(device, copies):
+        first = dict(src=torch.ones(elements, dtype=torch.bfloat16, device=device),
+                     dst=torch.empty(elements, dtype=torch.bfloat16, device=device))
+        return _copies(first, copies)
+
+    return Workload(
+        name="copy_ceiling", kernel="copy",
+        description=f"torch copy_ of {elements * 2} bytes ({elements * 4} bytes moved)",
+        bytes_per_launch=elements * 4, setup=setup,
+        launch=lambda a: a["dst"].copy_(a["src"]), default=False)
+
+
 def _bound_launch(w: Workload, argset):
     """The workload's single C-ABI call for one argument set, arguments bound once.
 
@@ -428,6 +447,8 @@ def main() -> int:
     parser.add_argument("--only", default="", help="comma-separated workload names")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--graph", action="store_true", help="also time a captured HIP graph")
+    parser.add_argument("--ceiling", action="store_true",
+                        help="also time a plain device copy moving each workload's bytes")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not run "
@@ -458,6 +479,12 @@ def main() -> int:
         r = results[w.name]
         print(f"[bench] {w.name}: {r['us']} us  {r['GBps']} GB/s  ({100 * r['frac']:.1f}% of peak)",
               file=sys.stderr, flush=True)
+        if args.ceiling:
+            ceiling = time_workload(copy_ceiling(w.bytes_per_launch), args.steps, args.warmup,
+                                    device, False)
+            r["copy_ceiling"] = {k: ceiling[k] for k in ("us", "GBps", "frac", "workload")}
+            print(f"[bench] {w.name}: plain copy of the same bytes {ceiling['us']} us "
+                  f"{ceiling['GBps']} GB/s", file=sys.stderr, flush=True)
 
     head = results.get(HEADLINE) or next(iter(results.values()))
     head_name = HEADLINE if HEADLINE in results else next(iter(results))
