@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 1
+#define OMNIA_ABI_VERSION 2
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -146,6 +146,20 @@ int32_t omnia_softmax_topk(const uint16_t* logits, int64_t stride, int64_t rows,
                            int64_t experts, int64_t k, int32_t* indices, float* weights,
                            hipStream_t stream);
 
+/* Bytes of the packed router weight for [experts, hidden] (experts a multiple of 16,
+ * hidden of 32), or -EINVAL. Pure; touches no device. */
+int64_t omnia_router_pack_bytes(int64_t experts, int64_t hidden);
+
+/* Repacks a router weight [experts, hidden] bf16 for omnia_residual_rms_router, into a
+ * caller-allocated buffer of omnia_router_pack_bytes(experts, hidden) bytes: the weight
+ * in 1 KiB blocks of 16 experts x 32 columns in the matrix-core operand order, followed
+ * by experts fp32 row norms (rounded up). Run once per weight, when the strategy is
+ * built, as the reference's strategies take their weights at build
+ * (core/kernels/route/residual.py:206-299 holds the gate for the dispatch); no
+ * reference function is replaced. */
+int32_t omnia_pack_router_weight(const uint16_t* router_weight, int64_t experts,
+                                 int64_t hidden, void* packed, hipStream_t stream);
+
 /* Residual add + RMSNorm + router projection + softmax top-k, fused:
  *   summed, normalized [rows, hidden] bf16 exactly as omnia_add_rms_norm;
  *   logits [rows, experts] = bf16(normalized x router_weight^T), the correctly rounded
@@ -154,15 +168,15 @@ int32_t omnia_softmax_topk(const uint16_t* logits, int64_t stride, int64_t rows,
  *     is not NULL;
  *   indices [rows, k] int32, weights [rows, k] fp32 exactly as omnia_softmax_topk
  *     applied to those logits.
- * x, branch [rows, hidden] bf16; norm_weight [hidden] bf16; router_weight
- * [experts, hidden] bf16. (hidden, experts) in {(2048, 128), (2048, 256), (4096, 128)};
- * k <= 64.
+ * x, branch [rows, hidden] bf16; norm_weight [hidden] bf16; packed_router: the router
+ * weight [experts, hidden] bf16 as omnia_pack_router_weight wrote it.
+ * hidden in {2048, 4096}, experts in {128, 256}; k <= 64.
  * Replaces: core/kernels/route/residual.py:117-299 (`residual_rms_router`, the
  * one-token residual join with the router gemv fused), generalised to many tokens and
  * to softmax routing; the Core chain is add_norm/default.py:28-29 followed by
  * route/default.py:44-69. */
 int32_t omnia_residual_rms_router(const uint16_t* x, const uint16_t* branch,
-                                  const uint16_t* norm_weight, const uint16_t* router_weight,
+                                  const uint16_t* norm_weight, const void* packed_router,
                                   int64_t rows, int64_t hidden, int64_t experts, int64_t k,
                                   float eps, uint16_t* summed, uint16_t* normalized,
                                   uint16_t* logits, int32_t* indices, float* weights,

@@ -16,27 +16,31 @@
 // max extract the winners.
 //
 // Fused kernel (core/kernels/route/residual.py:117-299 is the one-token precedent;
-// config: x, residual [4096, 2048], router [128, 2048], k = 8): a workgroup of 8 waves
-// owns 16 tokens; a workgroup is 16 waves.
+// config: x, residual [4096, 2048], router [128, 2048], k = 8): a workgroup of 16
+// waves owns 16 tokens.
 //   1. residual add + RMSNorm, one row per wave (arithmetic of add_rms_norm.hip),
-//      writing summed and normalized and keeping the bf16 normalized tile in LDS;
-//   2. logits[16, E] = tile [16, H] x W^T on v_mfma_f32_16x16x32_bf16 (fp32
-//      accumulation), each wave owning one 16-expert tile over a slice of H (E = 128:
-//      two halves), W streamed from L2 (every workgroup reads all of it; 512 KB at the
-//      config). A second MFMA accumulates A = |tile| x |W|^T, the sum of the products'
-//      magnitudes. The slices' partial sums meet in LDS;
-//   3. per token: the bf16 rounding of each logit, made exact. Each MFMA forms the
-//      sum of its 32 products (at most 31 roundings, any order) and adds it to the
-//      accumulator (one more); adding the slices' partials costs one more, so the fp32
-//      logit L is within delta = 97 * 2^-23 * A (1% slack for the rounding of A itself)
-//      of the exact dot product, each rounding counted at a full ulp. When [L - delta, L + delta]
-//      rounds to one bf16 value, that value is the correctly rounded logit; otherwise
-//      the logit is recomputed as an fp64 dot product from the LDS tile and W (the
-//      products of two bf16 values are exact in fp32) and rounded once. Recomputed
-//      are the unsure logits whose upper bound could reach the top k (all of them when
-//      the logits are written out), so the selection, the weights and any emitted
-//      logit equal those of the correctly rounded logits. Then the selection and the
-//      weights above.
+//      writing summed and normalized, keeping the bf16 normalized tile [16, H] in LDS
+//      and the Euclidean norm of each normalized row;
+//   2. logits[16, E] = tile x W^T on v_mfma_f32_16x16x32_bf16, each wave owning one
+//      16-expert tile over a slice of H (E = 128: two halves). W is read in the packed
+//      layout omnia_pack_router_weight writes: the 16 x 32 B-operand block of one MFMA
+//      is 1 KiB in lane order, so each load instruction of a wave reads 1 KiB of
+//      contiguous memory (eight whole cache lines) and a wave's walk over its slice is
+//      one contiguous stream. Each MFMA sums its 32 products with a zero accumulator;
+//      the step results are added with ordinary fp32 adds, and the slices' partials
+//      meet in LDS;
+//   3. per token: the bf16 rounding of each logit, made exact. With A = ||n|| ||W_e||
+//      (Cauchy-Schwarz: A >= sum |n_k W_ek|), the fp32 logit L is within
+//      delta = (62 + steps + slices - 1) * 2^-24 * A (+1% and a tiny absolute floor)
+//      of the exact dot product, plus an absolute floor for subnormal flushes: each MFMA's internal sum of 32 products carries at most
+//      31 roundings, each counted at a full ulp, and each fp32 add of a step result or
+//      of a slice partial one half-ulp rounding. When [L - delta, L + delta] rounds to
+//      one bf16 value, that value is the correctly rounded logit; otherwise the logit is
+//      recomputed as an fp64 dot product from the LDS tile and W (the products of two
+//      bf16 values are exact in fp32) and rounded once. Recomputed are the unsure
+//      logits whose upper bound could reach the top k (all of them when the logits are
+//      written out), so the selection, the weights and any emitted logit equal those of
+//      the correctly rounded logits. Then the selection and the weights above.
 #include "common.hpp"
 #include "host.hpp"
 
@@ -156,23 +160,87 @@ __global__ __launch_bounds__(256) void softmax_topk_kernel(const uint16_t* __res
   write_winners(chosen, k, lane, indices + row * k, weights + row * k);
 }
 
+// ---- packed router weight --------------------------------------------------------
+//
+// Layout written by omnia_pack_router_weight for W [E, H] bf16 (E a multiple of 16, H of
+// 32): blocks of 16 experts x 32 k of 1 KiB each; block (tile, step) starts at element
+// (tile * H / 32 + step) * 512 and holds, at l * 8 + j, W[tile * 16 + l % 16]
+// [step * 32 + (l / 16) * 8 + j] for l < 64, j < 8: lane l's B operand of
+// v_mfma_f32_16x16x32_bf16. After the E * H values: E fp32 row norms ||W_e||_2, each
+// rounded up (an upper bound of the exact norm).
+
+__host__ __device__ constexpr int64_t packed_weight_elements(int64_t experts, int64_t hidden) {
+  return experts * hidden;
+}
+
+// Element offset of W[e][h0 .. h0 + 8) in the packed layout (h0 a multiple of 8).
+__device__ __forceinline__ int64_t packed_offset(int e, int h0, int hidden) {
+  const int step = h0 / 32, quad = (h0 % 32) / 8;
+  return (static_cast<int64_t>(e / 16) * (hidden / 32) + step) * 512 + (quad * 16 + e % 16) * 8;
+}
+
+// The next fp32 value above a finite non-negative x (x itself if x is +inf).
+__device__ __forceinline__ float bump_up(float x) {
+  return x < __builtin_inff() ? __uint_as_float(__float_as_uint(x) + 1u) : x;
+}
+
+// Upper bound, in fp32, of sqrt(sum), sum >= 0 given in fp64.
+__device__ __forceinline__ float norm_upper(double sum) {
+  return bump_up(static_cast<float>(sqrt(sum) * (1.0 + 0x1p-40)));
+}
+
+constexpr int kPackBlock = 256;
+
+// Blocks [0, chunk_blocks) move one 16-byte chunk per thread; the rest compute one row
+// norm per wave.
+__global__ __launch_bounds__(kPackBlock) void pack_router_kernel(const u32x4* __restrict__ w,
+                                                                 u32x4* __restrict__ packed,
+                                                                 float* __restrict__ norms,
+                                                                 int experts, int hidden,
+                                                                 int chunk_blocks) {
+  const int chunks = experts * hidden / 8;
+  if (static_cast<int>(blockIdx.x) < chunk_blocks) {
+    const int o = blockIdx.x * kPackBlock + threadIdx.x;
+    if (o >= chunks) return;
+    const int block = o / 64, l = o % 64;
+    const int tile = block / (hidden / 32), step = block % (hidden / 32);
+    const int64_t src = (static_cast<int64_t>(tile * 16 + l % 16) * hidden + step * 32 + (l / 16) * 8) / 8;
+    packed[o] = w[src];
+    return;
+  }
+  const int lane = threadIdx.x % kWave;
+  const int e = (blockIdx.x - chunk_blocks) * (kPackBlock / kWave) + threadIdx.x / kWave;
+  if (e >= experts) return;  // whole wave
+  double sum = 0.0;
+  for (int c = lane; c < hidden / 8; c += kWave) {
+    float v[8];
+    unpack8(w[static_cast<int64_t>(e) * (hidden / 8) + c], v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const double d = v[j];  // squared in fp64: no overflow for any finite bf16
+      sum = __builtin_fma(d, d, sum);
+    }
+  }
+  sum = group_sum<kWave>(sum);
+  if (lane == 0) norms[e] = norm_upper(sum);
+}
+
 // ---- fused residual add + RMSNorm + router projection + top-k ---------------------
 
-// Bound on |fp32 MFMA logit - exact dot product| per unit of sum |n_k * W_ek|.
-constexpr float kDeltaPerMagnitude = 97.0f * 1.01f / 8388608.0f;
-
-// Correctly rounded bf16 bits of sum_k n_k * W_k over one row pair, by one wave: the
-// products of two bf16 values are exact in fp32 and are summed in fp64.
+// Correctly rounded bf16 bits of sum_k n_k * W_ek for one expert, by one wave, from the
+// LDS row and the packed weight: the products of two bf16 values are exact in fp32 and
+// are summed in fp64.
 template <int VPL>
-__device__ __forceinline__ uint32_t exact_logit(const uint16_t* n_row, const uint16_t* w_row,
-                                                int lane) {
+__device__ __forceinline__ uint32_t exact_logit(const uint16_t* n_row, const uint16_t* packed,
+                                                int e, int lane) {
+  constexpr int H = 512 * VPL;
   double acc = 0.0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const int v = lane + i * kWave;
+    const int h0 = (lane + i * kWave) * 8;
     float n[8], w[8];
-    unpack8(*reinterpret_cast<const u32x4*>(n_row + v * 8), n);
-    unpack8(*reinterpret_cast<const u32x4*>(w_row + v * 8), w);
+    unpack8(*reinterpret_cast<const u32x4*>(n_row + h0), n);
+    unpack8(*reinterpret_cast<const u32x4*>(packed + packed_offset(e, h0, H)), w);
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc += static_cast<double>(n[j] * w[j]);
   }
@@ -184,7 +252,8 @@ struct RouterArgs {
   const u32x4* x;
   const u32x4* branch;
   const u32x4* norm_weight;
-  const uint16_t* router_weight;  // [E, H]
+  const uint16_t* packed;         // packed W, then the E row norms
+  const float* weight_norms;
   u32x4* summed;
   u32x4* normalized;
   uint16_t* logits;               // [T, E] bf16, optional
@@ -195,156 +264,156 @@ struct RouterArgs {
   float eps;
 };
 
-// VPL: 16-byte vectors per lane per row (H = 512 * VPL). E: experts, a multiple of 16
-// with E / 16 dividing the 16 waves; the waves split H into 16 / (E / 16) slices.
+template <int VPL, int E>
+struct FusedShape {
+  static constexpr int H = 512 * VPL;
+  static constexpr int kTiles = E / 16;             // 16-expert MFMA tiles
+  static constexpr int kSlices = kWaves / kTiles;   // waves sharing one tile, over H
+  static constexpr int kSlice = H / kSlices;
+  static constexpr int kSteps = kSlice / 32;        // MFMAs per wave
+  static constexpr int kRowPitch = H + 8;           // bf16; the pad staggers LDS banks
+  static constexpr size_t kLds = static_cast<size_t>(kTileTokens) * kRowPitch * 2 +
+                                 static_cast<size_t>(kTileTokens) * E * 4 + kTileTokens * 4;
+  // |L - exact| <= kDelta * A + kFloor (see the file comment): 31 full-ulp roundings
+  // inside each MFMA (62 half-ulps), one half-ulp per step add and per slice add; 1%
+  // covers the rounding of A, delta and L +- delta. The floor covers products that
+  // leave the fp32 normal range.
+  static constexpr float kDelta = (62.0f + kSteps + kSlices - 1) * 1.01f / 16777216.0f;
+  static_assert(H <= 8192, "the absolute floor assumes H <= 2^13");
+  static_assert(E % 16 == 0 && kWaves % kTiles == 0 && kSlice % 256 == 0, "shape");
+};
+// Absolute part of the bound, per unit of ||n|| + ||W_e|| + 1: an MFMA that flushed
+// subnormal bf16 inputs or fp32 products would lose at most H * 2^-126 times those.
+constexpr float kDeltaFloor = 0x1p-113f;
+
 template <int VPL, int E>
 __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArgs a) {
-  constexpr int H = 512 * VPL;
-  constexpr int kTiles = E / 16;
-  constexpr int kSlices = kWaves / kTiles;
-  constexpr int kSlice = H / kSlices;
-  constexpr int kRowPitch = H + 8;  // bf16 elements; the pad staggers LDS banks per row
-  constexpr int kRowsPerWave = kTileTokens / kWaves;
-  constexpr int TPW = 1;
+  using S = FusedShape<VPL, E>;
+  constexpr int H = S::H, kTiles = S::kTiles, kSlices = S::kSlices, kSlice = S::kSlice;
+  constexpr int kRowPitch = S::kRowPitch;
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* tile = reinterpret_cast<uint16_t*>(smem);
-  // Logits and magnitudes [token][expert]; the slices' partials are added in turn.
-  float* logit_tile = reinterpret_cast<float*>(smem + kTileTokens * kRowPitch * 2);
-  float* magnitude_tile = logit_tile + kTileTokens * E;
+  float* logit_tile = reinterpret_cast<float*>(smem + kTileTokens * kRowPitch * 2);  // [token][expert]
+  float* row_norm = logit_tile + kTileTokens * E;                                      // ||n_t||, rounded up
 
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * kTileTokens;
 
-  // Phase 1: residual add + RMSNorm, rows wave and wave + 8.
+  // Phase 1: residual add + RMSNorm of row `wave`.
   {
-    u32x4 xv[kRowsPerWave][VPL], bv[kRowsPerWave][VPL], wv[VPL];
+    const int r = wave;
+    const int64_t t = first + r;
+    u32x4 xv[VPL], bv[VPL];
 #pragma unroll
-    for (int rr = 0; rr < kRowsPerWave; ++rr) {
-      const int64_t t = first + wave + rr * kWaves;
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        xv[rr][i] = u32x4{0u, 0u, 0u, 0u};
-        bv[rr][i] = u32x4{0u, 0u, 0u, 0u};
-        if (t < a.rows) {
-          xv[rr][i] = load_nt(a.x + t * (H / 8) + lane + i * kWave);
-          bv[rr][i] = load_nt(a.branch + t * (H / 8) + lane + i * kWave);
-        }
+    for (int i = 0; i < VPL; ++i) {
+      xv[i] = u32x4{0u, 0u, 0u, 0u};
+      bv[i] = u32x4{0u, 0u, 0u, 0u};
+      if (t < a.rows) {
+        xv[i] = load_nt(a.x + t * (H / 8) + lane + i * kWave);
+        bv[i] = load_nt(a.branch + t * (H / 8) + lane + i * kWave);
       }
     }
+    // s = bf16(x + b) is formed twice (for the sum of squares, then for the outputs)
+    // rather than kept: at H = 4096 the rows alone fill half the register budget.
+    double sumsq = 0.0;
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) wv[i] = a.norm_weight[lane + i * kWave];
+    for (int i = 0; i < VPL; ++i) {
+      float xf[8], bf[8];
+      unpack8(xv[i], xf);
+      unpack8(bv[i], bf);
 #pragma unroll
-    for (int rr = 0; rr < kRowsPerWave; ++rr) {
-      const int r = wave + rr * kWaves;
-      const int64_t t = first + r;
-      float s[VPL][8];
-      double sumsq = 0.0;
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        float xf[8], bf[8];
-        unpack8(xv[rr][i], xf);
-        unpack8(bv[rr][i], bf);
-#pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-          s[i][j] = xf[j] + bf[j];
-          s[i][j + 1] = xf[j + 1] + bf[j + 1];
-          round_pair(s[i][j], s[i][j + 1]);
-          sumsq += static_cast<double>(s[i][j] * s[i][j]);
-          sumsq += static_cast<double>(s[i][j + 1] * s[i][j + 1]);
-        }
-      }
-      sumsq = group_sum<kWave>(sumsq);
-      const float inv = 1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(H) + a.eps);
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        float w[8], n[8];
-        unpack8(wv[i], w);
-#pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-          float lo = s[i][j] * inv, hi = s[i][j + 1] * inv;
-          round_pair(lo, hi);
-          n[j] = w[j] * lo;
-          n[j + 1] = w[j + 1] * hi;
-        }
-        const u32x4 packed = pack8(n);
-        const int v = lane + i * kWave;
-        *reinterpret_cast<u32x4*>(tile + r * kRowPitch + v * 8) =
-            t < a.rows ? packed : u32x4{0u, 0u, 0u, 0u};
-        if (t < a.rows) {
-          store_nt(a.summed + t * (H / 8) + v, pack8(s[i]));
-          store_nt(a.normalized + t * (H / 8) + v, packed);
-        }
+      for (int j = 0; j < 8; j += 2) {
+        float lo = xf[j] + bf[j], hi = xf[j + 1] + bf[j + 1];
+        round_pair(lo, hi);
+        sumsq += static_cast<double>(lo * lo);
+        sumsq += static_cast<double>(hi * hi);
       }
     }
+    sumsq = group_sum<kWave>(sumsq);
+    const float inv = 1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(H) + a.eps);
+    double nsq = 0.0;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float xf[8], bf[8], w[8], s[8], n[8];
+      unpack8(xv[i], xf);
+      unpack8(bv[i], bf);
+      unpack8(a.norm_weight[lane + i * kWave], w);  // L2-resident, shared by every row
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        s[j] = xf[j] + bf[j];
+        s[j + 1] = xf[j + 1] + bf[j + 1];
+        round_pair(s[j], s[j + 1]);
+        float lo = s[j] * inv, hi = s[j + 1] * inv;
+        round_pair(lo, hi);
+        n[j] = w[j] * lo;
+        n[j + 1] = w[j + 1] * hi;
+        round_pair(n[j], n[j + 1]);
+        const double n0 = n[j], n1 = n[j + 1];  // squared in fp64: no overflow
+        nsq = __builtin_fma(n0, n0, nsq);
+        nsq = __builtin_fma(n1, n1, nsq);
+      }
+      const u32x4 packed = pack8(n);
+      const int v = lane + i * kWave;
+      *reinterpret_cast<u32x4*>(tile + r * kRowPitch + v * 8) =
+          t < a.rows ? packed : u32x4{0u, 0u, 0u, 0u};
+      if (t < a.rows) {
+        store_nt(a.summed + t * (H / 8) + v, pack8(s));
+        store_nt(a.normalized + t * (H / 8) + v, packed);
+      }
+    }
+    nsq = group_sum<kWave>(nsq);
+    if (lane == 0) row_norm[r] = t < a.rows ? norm_upper(nsq) : 0.0f;
   }
   __syncthreads();
 
-  // Phase 2: logits = tile x W^T and magnitudes = |tile| x |W|^T. Lane l feeds row
-  // (token) l % 16 of A and column (expert) l % 16 of B, both over
-  // k = (l / 16) * 8 .. + 8 of each 32-wide step.
-  f32x4 acc[TPW], mag[TPW];
-#pragma unroll
-  for (int j = 0; j < TPW; ++j) {
-    acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    mag[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
+  // Phase 2: logits = tile x W^T. Lane l feeds row (token) l % 16 of A and column
+  // (expert) l % 16 of B, both over k = (l / 16) * 8 .. + 8 of each 32-wide step.
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   {
-    constexpr uint32_t kAbs = 0x7FFF7FFFu;
-    const int quad = lane / 16;
+    const f32x4 zero = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int expert_tile = wave % kTiles;
     const int slice = wave / kTiles;
-    const uint16_t* arow = tile + (lane % 16) * kRowPitch + slice * kSlice + quad * 8;
-    const uint16_t* brow[TPW];
-#pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      brow[j] = a.router_weight + static_cast<int64_t>(expert_tile * 16 + lane % 16) * H +
-                slice * kSlice + quad * 8;
-    }
-    // Each workgroup starts its walk over k at a different 256-wide block, so the
-    // workgroups of an XCD do not all read the same W lines (the same L2 channels) at
-    // once. The accumulation order changes per workgroup; the error bound does not.
+    const uint16_t* arow = tile + (lane % 16) * kRowPitch + slice * kSlice + (lane / 16) * 8;
+    const uint16_t* brow =
+        a.packed + (static_cast<int64_t>(expert_tile) * (H / 32) + slice * (kSlice / 32)) * 512 +
+        lane * 8;
+    // Each workgroup starts its walk at a different block of kUnroll steps, so the
+    // workgroups of an XCD do not all read the same W lines at once. The order of the
+    // step adds changes per workgroup; the error bound does not.
     constexpr int kUnroll = 8;
-    constexpr int kSteps = kSlice / (32 * kUnroll);
-    const int start = static_cast<int>(blockIdx.x % kSteps);
-    u32x4 next[kUnroll][TPW];
+    constexpr int kOuter = kSlice / (32 * kUnroll);
+    const int start = static_cast<int>(blockIdx.x % kOuter);
+    u32x4 next[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-#pragma unroll
-      for (int j = 0; j < TPW; ++j) {
-        next[u][j] = *reinterpret_cast<const u32x4*>(brow[j] + start * 32 * kUnroll + u * 32);
-      }
+      next[u] = *reinterpret_cast<const u32x4*>(brow + (start * kUnroll + u) * 512);
     }
-    for (int step = 0; step < kSteps; ++step) {
-      const int k0 = ((start + step) % kSteps) * 32 * kUnroll;
-      const int k1 = ((start + step + 1) % kSteps) * 32 * kUnroll;
-      u32x4 b[kUnroll][TPW];
+    for (int step = 0; step < kOuter; ++step) {
+      const int s0 = (start + step) % kOuter;
+      const int s1 = (start + step + 1) % kOuter;
+      u32x4 b[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-#pragma unroll
-        for (int j = 0; j < TPW; ++j) {
-          b[u][j] = next[u][j];
-          if (step + 1 < kSteps) {
-            next[u][j] = *reinterpret_cast<const u32x4*>(brow[j] + k1 + u * 32);
-          }
+        b[u] = next[u];
+        if (step + 1 < kOuter) {
+          next[u] = *reinterpret_cast<const u32x4*>(brow + (s1 * kUnroll + u) * 512);
         }
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        const u32x4 av = *reinterpret_cast<const u32x4*>(arow + k0 + u * 32);
-        const u32x4 aabs = av & kAbs;
-#pragma unroll
-        for (int j = 0; j < TPW; ++j) {
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, b[u][j]), acc[j], 0, 0, 0);
-          mag[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8, aabs), __builtin_bit_cast(bf16x8, b[u][j] & kAbs),
-              mag[j], 0, 0, 0);
-        }
+        const u32x4 av = *reinterpret_cast<const u32x4*>(arow + (s0 * kUnroll + u) * 32);
+        const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, b[u]), zero, 0, 0, 0);
+        acc[0] = acc[0] + part[0];
+        acc[1] = acc[1] + part[1];
+        acc[2] = acc[2] + part[2];
+        acc[3] = acc[3] + part[3];
       }
     }
   }
-  // D layout: lane l holds column (expert) l % 16, rows (tokens) (l / 16) * 4 + i.
+  // D layout: lane l holds column (expert) l % 16, rows (tokens) (l / 16) * 4 + i. The
+  // slices add their partials in turn.
   {
     const int e = (wave % kTiles) * 16 + lane % 16;
     const int slice = wave / kTiles;
@@ -354,94 +423,90 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int at = ((lane / 16) * 4 + i) * E + e;
-          logit_tile[at] = turn == 0 ? acc[0][i] : logit_tile[at] + acc[0][i];
-          magnitude_tile[at] = turn == 0 ? mag[0][i] : magnitude_tile[at] + mag[0][i];
+          logit_tile[at] = turn == 0 ? acc[i] : logit_tile[at] + acc[i];
         }
       }
       __syncthreads();
     }
   }
 
-  // Phase 3: exact bf16 logits where they decide anything, then the selection; two
-  // tokens per wave.
+  // Phase 3: exact bf16 logits where they decide anything, then the selection; one
+  // token per wave.
+  const int r = wave;
+  const int64_t t = first + r;
+  if (t >= a.rows) return;  // wave-uniform; no barrier follows
   const bool emit = a.logits != nullptr;
-#pragma unroll 1
-  for (int rr = 0; rr < kRowsPerWave; ++rr) {
-    const int r = wave * kRowsPerWave + rr;
-    const int64_t t = first + r;
-    if (t >= a.rows) break;  // wave-uniform
-    constexpr int V = E / kWave;
-    uint32_t bits[V], lower[V], upper[V];
-    bool unsure[V];
+  constexpr int V = E / kWave;
+  const float n_norm = row_norm[r];
+  uint32_t bits[V], lower[V], upper[V];
+  bool unsure[V];
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-      const int e = lane + v * kWave;
-      const float logit = logit_tile[r * E + e];
-      const float delta = kDeltaPerMagnitude * magnitude_tile[r * E + e];
-      const uint32_t lo = f32_to_bf16(logit - delta);
-      const uint32_t hi = f32_to_bf16(logit + delta);
-      bits[v] = lo;
-      unsure[v] = lo != hi;
-      lower[v] = route_key(lo, e);
-      upper[v] = route_key(hi, e);
-    }
-    // Select on the lower bounds. A certain logit's lower bound is its value; an
-    // unsure logit whose upper bound stays below the k-th selected key cannot be
-    // selected. If every selected logit is certain and no unsure one can reach the
-    // k-th, this selection is final.
-    uint32_t chosen;
-    uint32_t keys[V];
-#pragma unroll
-    for (int v = 0; v < V; ++v) keys[v] = lower[v];
-    const uint32_t threshold = select_topk<V>(keys, a.k, lane, chosen);
-    const uint16_t* n_row = tile + r * kRowPitch;
-    bool refined = false;
-#pragma unroll
-    for (int v = 0; v < V; ++v) {
-      const bool need = unsure[v] && (emit || upper[v] >= threshold);
-      uint64_t pending = __ballot(need);
-      refined = refined || pending != 0;
-      while (pending != 0) {  // wave-uniform loop
-        const int src = __ffsll(static_cast<unsigned long long>(pending)) - 1;
-        pending &= pending - 1;
-        const int e = src + v * kWave;
-        const uint32_t exact =
-            exact_logit<VPL>(n_row, a.router_weight + static_cast<int64_t>(e) * H, lane);
-        if (lane == src) bits[v] = exact;
-      }
-    }
-    if (refined) {
-#pragma unroll
-      for (int v = 0; v < V; ++v) keys[v] = route_key(bits[v], lane + v * kWave);
-      select_topk<V>(keys, a.k, lane, chosen);
-    }
-    if (emit) {
-#pragma unroll
-      for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
-    }
-    write_winners(chosen, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
+  for (int v = 0; v < V; ++v) {
+    const int e = lane + v * kWave;
+    const float logit = logit_tile[r * E + e];
+    const float w_norm = a.weight_norms[e];
+    const float delta = S::kDelta * (n_norm * w_norm) + kDeltaFloor * (n_norm + w_norm + 1.0f);
+    const uint32_t lo = f32_to_bf16(logit - delta);
+    const uint32_t hi = f32_to_bf16(logit + delta);
+    bits[v] = lo;
+    unsure[v] = lo != hi;
+    lower[v] = route_key(lo, e);
+    upper[v] = route_key(hi, e);
   }
+  // Select on the lower bounds. A certain logit's lower bound is its value; an unsure
+  // logit whose upper bound stays below the k-th selected key cannot be selected. If
+  // every selected logit is certain and no unsure one can reach the k-th, this
+  // selection is final.
+  uint32_t chosen;
+  uint32_t keys[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) keys[v] = lower[v];
+  const uint32_t threshold = select_topk<V>(keys, a.k, lane, chosen);
+  const uint16_t* n_row = tile + r * kRowPitch;
+  bool refined = false;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const bool need = unsure[v] && (emit || upper[v] >= threshold);
+    uint64_t pending = __ballot(need);
+    refined = refined || pending != 0;
+    while (pending != 0) {  // wave-uniform loop
+      const int src = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+      pending &= pending - 1;
+      const uint32_t exact = exact_logit<VPL>(n_row, a.packed, src + v * kWave, lane);
+      if (lane == src) bits[v] = exact;
+    }
+  }
+  if (refined) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) keys[v] = route_key(bits[v], lane + v * kWave);
+    select_topk<V>(keys, a.k, lane, chosen);
+  }
+  if (emit) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
+  }
+  write_winners(chosen, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
 }
 
 template <int VPL, int E>
 int32_t launch_fused(const RouterArgs& a, hipStream_t stream) {
-  constexpr int H = 512 * VPL;
-  const size_t lds = static_cast<size_t>(kTileTokens) * (H + 8) * 2 +
-                     static_cast<size_t>(kTileTokens) * E * 4 * 2;
-  static bool configured = false;  // the attribute is per kernel, set once per process
-  if (!configured) {
-    const hipError_t status = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&residual_rms_router_kernel<VPL, E>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (status != hipSuccess) {
-      return fail(-1, std::string("residual_rms_router: LDS attribute: ") +
-                          hipGetErrorString(status));
-    }
-    configured = true;
+  constexpr size_t lds = FusedShape<VPL, E>::kLds;
+  // The attribute belongs to the kernel on the current device; set it on each call
+  // (a cheap host-side call) rather than caching per process.
+  const hipError_t status = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&residual_rms_router_kernel<VPL, E>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  if (status != hipSuccess) {
+    return fail(-1, std::string("residual_rms_router: LDS attribute: ") + hipGetErrorString(status));
   }
   const dim3 grid(static_cast<unsigned>((a.rows + kTileTokens - 1) / kTileTokens));
   residual_rms_router_kernel<VPL, E><<<grid, kThreads, lds, stream>>>(a);
   return launched("residual_rms_router");
+}
+
+bool fused_shape(int64_t hidden, int64_t experts) {
+  return (hidden == 2048 && (experts == 128 || experts == 256)) ||
+         (hidden == 4096 && (experts == 128 || experts == 256));
 }
 
 }  // namespace
@@ -470,34 +535,65 @@ extern "C" int32_t omnia_softmax_topk(const uint16_t* logits, int64_t stride, in
   return launched("softmax_topk");
 }
 
+extern "C" int64_t omnia_router_pack_bytes(int64_t experts, int64_t hidden) {
+  using namespace omnia;
+  OMNIA_REQUIRE(experts > 0 && experts % 16 == 0 && experts <= 4096 && hidden > 0 &&
+                    hidden % 32 == 0 && hidden <= 65536,
+                "router_pack_bytes: experts must be a multiple of 16, hidden of 32");
+  return packed_weight_elements(experts, hidden) * 2 + experts * 4;
+}
+
+extern "C" int32_t omnia_pack_router_weight(const uint16_t* router_weight, int64_t experts,
+                                            int64_t hidden, void* packed,
+                                            hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(experts > 0 && experts % 16 == 0 && experts <= 4096 && hidden > 0 &&
+                    hidden % 32 == 0 && hidden <= 65536,
+                "pack_router_weight: experts must be a multiple of 16, hidden of 32");
+  OMNIA_REQUIRE(router_weight && packed, "pack_router_weight: null pointer");
+  OMNIA_REQUIRE(aligned16(router_weight) && aligned16(packed),
+                "pack_router_weight: pointers must be 16-byte aligned");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  const int chunks = static_cast<int>(experts * hidden / 8);
+  const int chunk_blocks = (chunks + kPackBlock - 1) / kPackBlock;
+  const int norm_blocks = static_cast<int>((experts + kPackBlock / kWave - 1) / (kPackBlock / kWave));
+  uint16_t* base = static_cast<uint16_t*>(packed);
+  pack_router_kernel<<<chunk_blocks + norm_blocks, kPackBlock, 0, stream>>>(
+      reinterpret_cast<const u32x4*>(router_weight), reinterpret_cast<u32x4*>(base),
+      reinterpret_cast<float*>(base + packed_weight_elements(experts, hidden)),
+      static_cast<int>(experts), static_cast<int>(hidden), chunk_blocks);
+  return launched("pack_router_weight");
+}
+
 extern "C" int32_t omnia_residual_rms_router(
     const uint16_t* x, const uint16_t* branch, const uint16_t* norm_weight,
-    const uint16_t* router_weight, int64_t rows, int64_t hidden, int64_t experts, int64_t k,
+    const void* packed_router, int64_t rows, int64_t hidden, int64_t experts, int64_t k,
     float eps, uint16_t* summed, uint16_t* normalized, uint16_t* logits, int32_t* indices,
     float* weights, hipStream_t stream) {
   using namespace omnia;
   OMNIA_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), "residual_rms_router: bad row count");
-  OMNIA_REQUIRE((hidden == 2048 && (experts == 128 || experts == 256)) ||
-                    (hidden == 4096 && experts == 128),
-                "residual_rms_router: (hidden, experts) must be (2048, 128), (2048, 256) "
-                "or (4096, 128)");
+  OMNIA_REQUIRE(fused_shape(hidden, experts),
+                "residual_rms_router: hidden must be 2048 or 4096 and experts 128 or 256");
   OMNIA_REQUIRE(k > 0 && k <= experts && k <= kMaxTopK,
                 "residual_rms_router: k must be in [1, min(experts, 64)]");
   if (rows == 0) return 0;
-  OMNIA_REQUIRE(x && branch && norm_weight && router_weight && summed && normalized &&
+  OMNIA_REQUIRE(x && branch && norm_weight && packed_router && summed && normalized &&
                     indices && weights,
                 "residual_rms_router: null pointer");
   OMNIA_REQUIRE(aligned16(x) && aligned16(branch) && aligned16(norm_weight) &&
-                    aligned16(router_weight) && aligned16(summed) && aligned16(normalized),
+                    aligned16(packed_router) && aligned16(summed) && aligned16(normalized),
                 "residual_rms_router: pointers must be 16-byte aligned");
   int32_t rc = check_device();
   if (rc != 0) return rc;
+  const uint16_t* packed = static_cast<const uint16_t*>(packed_router);
   RouterArgs a{reinterpret_cast<const u32x4*>(x), reinterpret_cast<const u32x4*>(branch),
-               reinterpret_cast<const u32x4*>(norm_weight), router_weight,
+               reinterpret_cast<const u32x4*>(norm_weight), packed,
+               reinterpret_cast<const float*>(packed + packed_weight_elements(experts, hidden)),
                reinterpret_cast<u32x4*>(summed), reinterpret_cast<u32x4*>(normalized),
                logits, indices, weights, rows, static_cast<int>(k), eps};
   if (hidden == 2048) {
     return experts == 128 ? launch_fused<4, 128>(a, stream) : launch_fused<4, 256>(a, stream);
   }
-  return launch_fused<8, 128>(a, stream);
+  return experts == 128 ? launch_fused<8, 128>(a, stream) : launch_fused<8, 256>(a, stream);
 }

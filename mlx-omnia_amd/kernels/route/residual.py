@@ -5,10 +5,11 @@ gemv (sigmoid scoring, ordinal keys) as machinery beside the routing strategies.
 same fusion is a facade of its own, declared by the norm leaf (`.weight`, `.eps`), the
 router gate [experts, hidden] and a `Routing`, and called as
 `(x, projected) -> (summed, normalized, indices, weights)`. `HipResidualRouter` serves
-softmax routing at (hidden, experts) of (2048, 128), (2048, 256) or (4096, 128) in one
-dispatch
-(`omnia_residual_rms_router`, csrc/router.hip); `DefaultResidualRouter` is the Core chain
-(the residual join, the gate matmul, the routing chain).
+softmax routing at hidden 2048 or 4096 and 128 or 256 experts in one dispatch
+(`omnia_residual_rms_router`, csrc/router.hip); it repacks the gate once when it is
+built (`omnia_pack_router_weight`), as the reference's strategies take their weights at
+build. `DefaultResidualRouter` is the Core chain (the residual join, the gate matmul,
+the routing chain).
 """
 
 from __future__ import annotations
@@ -32,7 +33,7 @@ class ResidualRouterStrategy(Protocol):
 
 
 def residual_router_applies(hidden: int, experts: int, k: int) -> bool:
-    return (hidden, experts) in ((2048, 128), (2048, 256), (4096, 128)) and 0 < k <= 64
+    return hidden in (2048, 4096) and experts in (128, 256) and 0 < k <= 64
 
 
 @dataclass(frozen=True)
@@ -55,7 +56,7 @@ class DefaultResidualRouter(ResidualRouterStrategy):
 class HipResidualRouter(ResidualRouterStrategy):
     norm_weight: torch.Tensor
     eps: float
-    gate: torch.Tensor
+    gate: ops.PackedRouterWeight
     routing: Routing
 
     @classmethod
@@ -69,7 +70,8 @@ class HipResidualRouter(ResidualRouterStrategy):
             return None
         if not hip_device(weight, gate):
             return None
-        return cls(weight.contiguous(), float(leaf.eps), gate.contiguous(), routing)
+        return cls(weight.contiguous(), float(leaf.eps), ops.pack_router_weight(gate.contiguous()),
+                   routing)
 
     def __call__(self, x, projected):
         summed, normalized, _, indices, weights = ops.residual_rms_router(

@@ -9,9 +9,11 @@ fit.
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
-from .loader import call
+from .loader import call, last_error, library
 
 BF16 = torch.bfloat16
 F32 = torch.float32
@@ -287,11 +289,36 @@ def softmax_topk(logits: torch.Tensor, k: int, *, indices: torch.Tensor | None =
     return indices, weights
 
 
+@dataclass(frozen=True)
+class PackedRouterWeight:
+    """A router weight [experts, hidden] bf16 in the layout `omnia_pack_router_weight`
+    writes (matrix-core operand blocks, then the fp32 row norms), on one device."""
+
+    buffer: torch.Tensor  # uint8 [omnia_router_pack_bytes(experts, hidden)]
+    experts: int
+    hidden: int
+
+
+def pack_router_weight(router_weight: torch.Tensor) -> PackedRouterWeight:
+    """Repacks a router weight once, for `residual_rms_router`."""
+    _dense(router_weight, BF16, "router_weight")
+    _require(router_weight.dim() == 2, "pack_router_weight: router weight must be 2-D")
+    _require(on_rocm(router_weight), "pack_router_weight: router weight must be on a ROCm device")
+    experts, hidden = router_weight.shape
+    nbytes = library().omnia_router_pack_bytes(experts, hidden)
+    if nbytes < 0:
+        raise ValueError(f"omnia_router_pack_bytes: {last_error()} (code {nbytes})")
+    buffer = torch.empty(nbytes, dtype=torch.uint8, device=router_weight.device)
+    call("omnia_pack_router_weight", router_weight.data_ptr(), experts, hidden,
+         buffer.data_ptr(), _stream(router_weight))
+    return PackedRouterWeight(buffer, int(experts), int(hidden))
+
+
 def residual_rms_router(
     x: torch.Tensor,
     branch: torch.Tensor,
     norm_weight: torch.Tensor,
-    router_weight: torch.Tensor,
+    router: torch.Tensor | PackedRouterWeight,
     *,
     k: int,
     eps: float,
@@ -303,16 +330,20 @@ def residual_rms_router(
     weights: torch.Tensor | None = None,
 ):
     """Fused residual add + RMSNorm + router projection + top-k; see
-    `omnia_residual_rms_router`. Returns (summed, normalized, logits or None, indices,
-    weights)."""
+    `omnia_residual_rms_router`. `router` is a packed weight (`pack_router_weight`, what a
+    strategy holds) or the [experts, hidden] bf16 weight itself, then packed for this call.
+    Returns (summed, normalized, logits or None, indices, weights)."""
     hidden = norm_weight.numel()
-    experts = router_weight.shape[0]
+    if not isinstance(router, PackedRouterWeight):
+        _require(router.dim() == 2 and router.shape[-1] == hidden,
+                 "residual_rms_router: router weight shape")
+        router = pack_router_weight(router)
+    experts = router.experts
+    _require(router.hidden == hidden, "residual_rms_router: router weight shape")
     _require(x.shape == branch.shape and x.shape[-1] == hidden, "residual_rms_router: shape mismatch")
-    _require(router_weight.shape == (experts, hidden), "residual_rms_router: router weight shape")
-    for t, name in ((x, "x"), (branch, "branch"), (norm_weight, "norm_weight"),
-                    (router_weight, "router_weight")):
+    for t, name in ((x, "x"), (branch, "branch"), (norm_weight, "norm_weight")):
         _dense(t, BF16, name)
-    _require(on_rocm(x, branch, norm_weight, router_weight),
+    _require(on_rocm(x, branch, norm_weight, router.buffer),
              "residual_rms_router: tensors must share one ROCm device")
     rows = x.numel() // hidden
     lead = x.shape[:-1]
@@ -324,7 +355,7 @@ def residual_rms_router(
     weights = _out(weights, x, (*lead, k), F32, "weights")
     call(
         "omnia_residual_rms_router",
-        x.data_ptr(), branch.data_ptr(), norm_weight.data_ptr(), router_weight.data_ptr(),
+        x.data_ptr(), branch.data_ptr(), norm_weight.data_ptr(), router.buffer.data_ptr(),
         rows, hidden, experts, int(k), float(eps), summed.data_ptr(), normalized.data_ptr(),
         logits.data_ptr() if logits is not None else None, indices.data_ptr(),
         weights.data_ptr(), _stream(x),

@@ -55,3 +55,9 @@ def test_argument_errors_come_back_as_codes(lib):
     assert rc == -22
     assert "hidden" in lib_module.last_error()
     assert lib.omnia_add_rms_norm(None, None, None, None, None, 0, 2560, 1e-6, None) == 0
+
+
+def test_router_pack_size_is_pure(lib):
+    assert lib.omnia_router_pack_bytes(128, 2048) == 128 * 2048 * 2 + 128 * 4
+    assert lib.omnia_router_pack_bytes(100, 2048) == -22
+    assert lib.omnia_router_pack_bytes(128, 2000) == -22

@@ -20,7 +20,7 @@ from mlx_omnia_amd.kernels.leaf import RMSNormLeaf
 from mlx_omnia_amd.kernels.route import HipResidualRouter, HipSoftmaxTopkRoute, ResidualRouter, Route, Routing
 from mlx_omnia_amd.runtime import ops
 from oracle import route
-from oracle.bf16 import from_float, ulp_distance
+from oracle.bf16 import to_f32, from_float, ulp_distance
 from util import assert_bf16_close, bits_of, to_device
 
 pytestmark = pytest.mark.gpu
@@ -66,6 +66,7 @@ def _router_inputs(rows, hidden, experts, seed):
 
 @pytest.mark.parametrize("rows,hidden,experts,k", [
     (4096, 2048, 128, 8), (1, 2048, 128, 8), (37, 2048, 128, 8), (300, 4096, 128, 8), (50, 2048, 256, 16),
+    (20, 4096, 256, 8),
 ])
 def test_residual_router_matches_oracle(rows, hidden, experts, k):
     print(f"residual_rms_router rows={rows} hidden={hidden} experts={experts} k={k}", flush=True)
@@ -86,6 +87,27 @@ def test_residual_router_matches_oracle(rows, hidden, experts, k):
     assert none is None
     assert np.array_equal(idx2.cpu().numpy(), want_idx)
     np.testing.assert_allclose(wts2.cpu().numpy(), want_w, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("experts,hidden", [(128, 2048), (256, 4096), (32, 96)])
+def test_pack_router_weight_layout_and_norms(experts, hidden):
+    rng = np.random.default_rng(experts + hidden)
+    gate = from_float(0.02 * rng.standard_normal((experts, hidden), dtype=np.float32))
+    gate[0, :5] = from_float(np.array([0.0, -0.0, 1e-38, 3e38, -2.5], dtype=np.float32))
+    packed = ops.pack_router_weight(to_device(gate))
+    torch.cuda.synchronize()
+    raw = packed.buffer.cpu().numpy()
+    body = raw[: experts * hidden * 2].view(np.uint16).reshape(experts // 16, hidden // 32, 64, 8)
+    lane = np.arange(64)
+    for tile in range(experts // 16):
+        for step in range(hidden // 32):
+            rows = tile * 16 + lane % 16
+            cols = step * 32 + (lane // 16)[:, None] * 8 + np.arange(8)[None, :]
+            assert np.array_equal(body[tile, step], gate[rows[:, None], cols])
+    norms = raw[experts * hidden * 2 :].view(np.float32)
+    exact = np.sqrt((to_f32(gate).astype(np.float64) ** 2).sum(axis=1))
+    assert np.all(norms.astype(np.float64) >= exact)
+    assert np.allclose(norms, exact, rtol=1e-6)
 
 
 def test_residual_router_forced_ties_and_facade():
