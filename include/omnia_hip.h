@@ -152,8 +152,9 @@ int64_t omnia_router_pack_bytes(int64_t experts, int64_t hidden);
 
 /* Repacks a router weight [experts, hidden] bf16 for omnia_residual_rms_router, into a
  * caller-allocated buffer of omnia_router_pack_bytes(experts, hidden) bytes: the weight
- * in 1 KiB blocks of 16 experts x 32 columns in the matrix-core operand order, followed
- * by experts fp32 row norms (rounded up). Run once per weight, when the strategy is
+ * in 1 KiB blocks of 16 experts x 32 columns in the matrix-core operand order, then
+ * experts fp32 row norms (rounded up), then the weight row-major (read to recompute
+ * single logits exactly). Run once per weight, when the strategy is
  * built, as the reference's strategies take their weights at build
  * (core/kernels/route/residual.py:206-299 holds the gate for the dispatch); no
  * reference function is replaced. */

@@ -167,16 +167,20 @@ __global__ __launch_bounds__(256) void softmax_topk_kernel(const uint16_t* __res
 // (tile * H / 32 + step) * 512 and holds, at l * 8 + j, W[tile * 16 + l % 16]
 // [step * 32 + (l / 16) * 8 + j] for l < 64, j < 8: lane l's B operand of
 // v_mfma_f32_16x16x32_bf16. After the E * H values: E fp32 row norms ||W_e||_2, each
-// rounded up (an upper bound of the exact norm).
+// rounded up (an upper bound of the exact norm); then W again, row-major, for the
+// exact recomputation of single logits (a row is 4 KiB of contiguous memory there,
+// where the operand blocks would scatter it over 256 cache lines).
 
 __host__ __device__ constexpr int64_t packed_weight_elements(int64_t experts, int64_t hidden) {
   return experts * hidden;
 }
-
-// Element offset of W[e][h0 .. h0 + 8) in the packed layout (h0 a multiple of 8).
-__device__ __forceinline__ int64_t packed_offset(int e, int h0, int hidden) {
-  const int step = h0 / 32, quad = (h0 % 32) / 8;
-  return (static_cast<int64_t>(e / 16) * (hidden / 32) + step) * 512 + (quad * 16 + e % 16) * 8;
+// Element offset of the row-major copy: after the blocks and the norms (2 bf16 slots
+// per fp32 norm).
+__host__ __device__ constexpr int64_t packed_rows_offset(int64_t experts, int64_t hidden) {
+  return experts * hidden + 2 * experts;
+}
+__host__ __device__ constexpr int64_t packed_bytes(int64_t experts, int64_t hidden) {
+  return (packed_rows_offset(experts, hidden) + experts * hidden) * 2;
 }
 
 // The next fp32 value above a finite non-negative x (x itself if x is +inf).
@@ -196,6 +200,7 @@ constexpr int kPackBlock = 256;
 __global__ __launch_bounds__(kPackBlock) void pack_router_kernel(const u32x4* __restrict__ w,
                                                                  u32x4* __restrict__ packed,
                                                                  float* __restrict__ norms,
+                                                                 u32x4* __restrict__ rows,
                                                                  int experts, int hidden,
                                                                  int chunk_blocks) {
   const int chunks = experts * hidden / 8;
@@ -206,6 +211,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_router_kernel(const u32x4* __
     const int tile = block / (hidden / 32), step = block % (hidden / 32);
     const int64_t src = (static_cast<int64_t>(tile * 16 + l % 16) * hidden + step * 32 + (l / 16) * 8) / 8;
     packed[o] = w[src];
+    rows[o] = w[o];
     return;
   }
   const int lane = threadIdx.x % kWave;
@@ -228,19 +234,18 @@ __global__ __launch_bounds__(kPackBlock) void pack_router_kernel(const u32x4* __
 // ---- fused residual add + RMSNorm + router projection + top-k ---------------------
 
 // Correctly rounded bf16 bits of sum_k n_k * W_ek for one expert, by one wave, from the
-// LDS row and the packed weight: the products of two bf16 values are exact in fp32 and
-// are summed in fp64.
+// LDS row and the expert's row of W: the products of two bf16 values are exact in fp32
+// and are summed in fp64.
 template <int VPL>
-__device__ __forceinline__ uint32_t exact_logit(const uint16_t* n_row, const uint16_t* packed,
-                                                int e, int lane) {
-  constexpr int H = 512 * VPL;
+__device__ __forceinline__ uint32_t exact_logit(const uint16_t* n_row, const uint16_t* w_row,
+                                                int lane) {
   double acc = 0.0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int h0 = (lane + i * kWave) * 8;
     float n[8], w[8];
     unpack8(*reinterpret_cast<const u32x4*>(n_row + h0), n);
-    unpack8(*reinterpret_cast<const u32x4*>(packed + packed_offset(e, h0, H)), w);
+    unpack8(*reinterpret_cast<const u32x4*>(w_row + h0), w);
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc += static_cast<double>(n[j] * w[j]);
   }
@@ -252,8 +257,9 @@ struct RouterArgs {
   const u32x4* x;
   const u32x4* branch;
   const u32x4* norm_weight;
-  const uint16_t* packed;         // packed W, then the E row norms
-  const float* weight_norms;
+  const uint16_t* packed;         // W in operand blocks
+  const float* weight_norms;      // ||W_e||, rounded up
+  const uint16_t* weight_rows;    // W row-major
   u32x4* summed;
   u32x4* normalized;
   uint16_t* logits;               // [T, E] bf16, optional
@@ -299,6 +305,10 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * kTileTokens;
+  constexpr int V = E / kWave;  // experts per lane in phase 3
+  float weight_norm[V];         // loaded now, used in phase 3
+#pragma unroll
+  for (int v = 0; v < V; ++v) weight_norm[v] = a.weight_norms[lane + v * kWave];
 
   // Phase 1: residual add + RMSNorm of row `wave`.
   {
@@ -436,7 +446,6 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   const int64_t t = first + r;
   if (t >= a.rows) return;  // wave-uniform; no barrier follows
   const bool emit = a.logits != nullptr;
-  constexpr int V = E / kWave;
   const float n_norm = row_norm[r];
   uint32_t bits[V], lower[V], upper[V];
   bool unsure[V];
@@ -444,7 +453,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   for (int v = 0; v < V; ++v) {
     const int e = lane + v * kWave;
     const float logit = logit_tile[r * E + e];
-    const float w_norm = a.weight_norms[e];
+    const float w_norm = weight_norm[v];
     const float delta = S::kDelta * (n_norm * w_norm) + kDeltaFloor * (n_norm + w_norm + 1.0f);
     const uint32_t lo = f32_to_bf16(logit - delta);
     const uint32_t hi = f32_to_bf16(logit + delta);
@@ -472,7 +481,8 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
     while (pending != 0) {  // wave-uniform loop
       const int src = __ffsll(static_cast<unsigned long long>(pending)) - 1;
       pending &= pending - 1;
-      const uint32_t exact = exact_logit<VPL>(n_row, a.packed, src + v * kWave, lane);
+      const uint32_t exact = exact_logit<VPL>(
+          n_row, a.weight_rows + static_cast<int64_t>(src + v * kWave) * H, lane);
       if (lane == src) bits[v] = exact;
     }
   }
@@ -540,7 +550,7 @@ extern "C" int64_t omnia_router_pack_bytes(int64_t experts, int64_t hidden) {
   OMNIA_REQUIRE(experts > 0 && experts % 16 == 0 && experts <= 4096 && hidden > 0 &&
                     hidden % 32 == 0 && hidden <= 65536,
                 "router_pack_bytes: experts must be a multiple of 16, hidden of 32");
-  return packed_weight_elements(experts, hidden) * 2 + experts * 4;
+  return packed_bytes(experts, hidden);
 }
 
 extern "C" int32_t omnia_pack_router_weight(const uint16_t* router_weight, int64_t experts,
@@ -562,6 +572,7 @@ extern "C" int32_t omnia_pack_router_weight(const uint16_t* router_weight, int64
   pack_router_kernel<<<chunk_blocks + norm_blocks, kPackBlock, 0, stream>>>(
       reinterpret_cast<const u32x4*>(router_weight), reinterpret_cast<u32x4*>(base),
       reinterpret_cast<float*>(base + packed_weight_elements(experts, hidden)),
+      reinterpret_cast<u32x4*>(base + packed_rows_offset(experts, hidden)),
       static_cast<int>(experts), static_cast<int>(hidden), chunk_blocks);
   return launched("pack_router_weight");
 }
@@ -590,6 +601,7 @@ extern "C" int32_t omnia_residual_rms_router(
   RouterArgs a{reinterpret_cast<const u32x4*>(x), reinterpret_cast<const u32x4*>(branch),
                reinterpret_cast<const u32x4*>(norm_weight), packed,
                reinterpret_cast<const float*>(packed + packed_weight_elements(experts, hidden)),
+               packed + packed_rows_offset(experts, hidden),
                reinterpret_cast<u32x4*>(summed), reinterpret_cast<u32x4*>(normalized),
                logits, indices, weights, rows, static_cast<int>(k), eps};
   if (hidden == 2048) {

@@ -58,6 +58,6 @@ def test_argument_errors_come_back_as_codes(lib):
 
 
 def test_router_pack_size_is_pure(lib):
-    assert lib.omnia_router_pack_bytes(128, 2048) == 128 * 2048 * 2 + 128 * 4
+    assert lib.omnia_router_pack_bytes(128, 2048) == 2 * 128 * 2048 * 2 + 128 * 4
     assert lib.omnia_router_pack_bytes(100, 2048) == -22
     assert lib.omnia_router_pack_bytes(128, 2000) == -22

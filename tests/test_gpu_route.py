@@ -104,7 +104,9 @@ def test_pack_router_weight_layout_and_norms(experts, hidden):
             rows = tile * 16 + lane % 16
             cols = step * 32 + (lane // 16)[:, None] * 8 + np.arange(8)[None, :]
             assert np.array_equal(body[tile, step], gate[rows[:, None], cols])
-    norms = raw[experts * hidden * 2 :].view(np.float32)
+    norms = raw[experts * hidden * 2 : experts * hidden * 2 + experts * 4].view(np.float32)
+    rows = raw[experts * hidden * 2 + experts * 4 :].view(np.uint16).reshape(experts, hidden)
+    assert np.array_equal(rows, gate)
     exact = np.sqrt((to_f32(gate).astype(np.float64) ** 2).sum(axis=1))
     assert np.all(norms.astype(np.float64) >= exact)
     assert np.allclose(norms, exact, rtol=1e-6)
