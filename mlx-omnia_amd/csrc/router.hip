@@ -70,36 +70,69 @@ __device__ __forceinline__ uint32_t route_key(uint32_t logit_bits, int expert) {
 
 __device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
 
-// Maximum over the wave, returned as a wave-uniform value: DPP steps inside each
-// 16-lane row (quad swaps, half-row and row mirrors), then the four row results read
-// into scalar registers. No LDS round trips on the dependency chain.
+// Cross-row steps of a wave reduction (gfx950): with the same value in both operands,
+// v_permlane16_swap hands each lane the value of the same column in the paired 16-lane
+// row (rows 0-1, 2-3), v_permlane32_swap that of the other 32-lane half; the two
+// returned dwords are then {own, partner} in some order, the same pair on both lanes.
+__device__ __forceinline__ void row_pair(uint32_t v, uint32_t& a, uint32_t& b) {
+  const auto swapped = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  a = swapped[0];
+  b = swapped[1];
+}
+__device__ __forceinline__ void half_pair(uint32_t v, uint32_t& a, uint32_t& b) {
+  const auto swapped = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  a = swapped[0];
+  b = swapped[1];
+}
+
+constexpr int kQuadSwap1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kQuadSwap2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+// Maximum over the wave, left in every lane: DPP steps inside each 16-lane row (quad
+// swaps, half-row and row mirrors), then the two cross-row swaps. Everything stays in
+// vector registers; no LDS and no scalar round trip on the dependency chain.
 __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
-  constexpr int kQuadSwap1 = 0xB1;        // quad_perm [1, 0, 3, 2]
-  constexpr int kQuadSwap2 = 0x4E;        // quad_perm [2, 3, 0, 1]
-  constexpr int kRowHalfMirror = 0x141;
-  constexpr int kRowMirror = 0x140;
   v = umax(v, dpp<kQuadSwap1>(v));
   v = umax(v, dpp<kQuadSwap2>(v));
   v = umax(v, dpp<kRowHalfMirror>(v));
   v = umax(v, dpp<kRowMirror>(v));
-  const uint32_t r0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0));
-  const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16));
-  const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
-  const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 48));
-  return umax(umax(r0, r1), umax(r2, r3));
+  uint32_t a, b;
+  row_pair(v, a, b);
+  v = umax(a, b);
+  half_pair(v, a, b);
+  return umax(a, b);
 }
 
-// Sum over the wave (same DPP pattern), wave-uniform result.
+// Sum over the wave, the same in every lane (each step adds the same two operands on
+// both lanes of a pair, so every lane computes the identical fp32 result).
 __device__ __forceinline__ float wave_sum(float v) {
-  constexpr int kQuadSwap1 = 0xB1, kQuadSwap2 = 0x4E, kRowHalfMirror = 0x141, kRowMirror = 0x140;
   v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
   v += __uint_as_float(dpp<kQuadSwap2>(__float_as_uint(v)));
   v += __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
   v += __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
-         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)) +
-         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
-         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  uint32_t a, b;
+  row_pair(__float_as_uint(v), a, b);
+  v = __uint_as_float(a) + __uint_as_float(b);
+  half_pair(__float_as_uint(v), a, b);
+  return __uint_as_float(a) + __uint_as_float(b);
+}
+
+// fp64 sum over the wave, the same in every lane.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v = row16_sum(v);
+  uint32_t lo_a, lo_b, hi_a, hi_b;
+  const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+  row_pair(static_cast<uint32_t>(bits), lo_a, lo_b);
+  row_pair(static_cast<uint32_t>(bits >> 32), hi_a, hi_b);
+  v = __builtin_bit_cast(double, (static_cast<uint64_t>(hi_a) << 32) | lo_a) +
+      __builtin_bit_cast(double, (static_cast<uint64_t>(hi_b) << 32) | lo_b);
+  const uint64_t bits2 = __builtin_bit_cast(uint64_t, v);
+  half_pair(static_cast<uint32_t>(bits2), lo_a, lo_b);
+  half_pair(static_cast<uint32_t>(bits2 >> 32), hi_a, hi_b);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi_a) << 32) | lo_a) +
+         __builtin_bit_cast(double, (static_cast<uint64_t>(hi_b) << 32) | lo_b);
 }
 
 // Extracts the top k of the wave's keys (V per lane; a taken key becomes 0, below
@@ -233,24 +266,38 @@ __global__ __launch_bounds__(kPackBlock) void pack_router_kernel(const u32x4* __
 
 // ---- fused residual add + RMSNorm + router projection + top-k ---------------------
 
-// Correctly rounded bf16 bits of sum_k n_k * W_ek for one expert, by one wave, from the
-// LDS row and the expert's row of W: the products of two bf16 values are exact in fp32
-// and are summed in fp64.
+// Correctly rounded bf16 bits of two logits sum_k n_k * W_ek at once, by one wave, from
+// normalized rows in LDS and experts' rows of W (the second pair may repeat the first):
+// the products of two bf16 values are exact in fp32 and are summed in fp64. Both rows'
+// loads are in flight together.
 template <int VPL>
-__device__ __forceinline__ uint32_t exact_logit(const uint16_t* n_row, const uint16_t* w_row,
-                                                int lane) {
-  double acc = 0.0;
+__device__ __forceinline__ void exact_logits(const uint16_t* n_row0, const uint16_t* n_row1,
+                                             const uint16_t* w_row0, const uint16_t* w_row1,
+                                             int lane, uint32_t& bits0, uint32_t& bits1) {
+  u32x4 w0[VPL], w1[VPL];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int h0 = (lane + i * kWave) * 8;
-    float n[8], w[8];
-    unpack8(*reinterpret_cast<const u32x4*>(n_row + h0), n);
-    unpack8(*reinterpret_cast<const u32x4*>(w_row + h0), w);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc += static_cast<double>(n[j] * w[j]);
+    w0[i] = *reinterpret_cast<const u32x4*>(w_row0 + h0);
+    w1[i] = *reinterpret_cast<const u32x4*>(w_row1 + h0);
   }
-  acc = group_sum<kWave>(acc);
-  return f64_to_bf16(acc);
+  double acc0 = 0.0, acc1 = 0.0;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int h0 = (lane + i * kWave) * 8;
+    float n0[8], n1[8], a[8], b[8];
+    unpack8(*reinterpret_cast<const u32x4*>(n_row0 + h0), n0);
+    unpack8(*reinterpret_cast<const u32x4*>(n_row1 + h0), n1);
+    unpack8(w0[i], a);
+    unpack8(w1[i], b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc0 += static_cast<double>(n0[j] * a[j]);
+      acc1 += static_cast<double>(n1[j] * b[j]);
+    }
+  }
+  bits0 = f64_to_bf16(wave_sum_f64(acc0));
+  bits1 = f64_to_bf16(wave_sum_f64(acc1));
 }
 
 struct RouterArgs {
@@ -278,8 +325,11 @@ struct FusedShape {
   static constexpr int kSlice = H / kSlices;
   static constexpr int kSteps = kSlice / 32;        // MFMAs per wave
   static constexpr int kRowPitch = H + 8;           // bf16; the pad staggers LDS banks
+  // LDS: the normalized tile, the logits [16][E] (reused for the recomputed bits), the
+  // row norms, the task count (padded to 16 bytes) and the task list [16 * E] of uint16.
   static constexpr size_t kLds = static_cast<size_t>(kTileTokens) * kRowPitch * 2 +
-                                 static_cast<size_t>(kTileTokens) * E * 4 + kTileTokens * 4;
+                                 static_cast<size_t>(kTileTokens) * E * 4 + kTileTokens * 4 +
+                                 16 + static_cast<size_t>(kTileTokens) * E * 2;
   // |L - exact| <= kDelta * A + kFloor (see the file comment): 31 full-ulp roundings
   // inside each MFMA (62 half-ulps), one half-ulp per step add and per slice add; 1%
   // covers the rounding of A, delta and L +- delta. The floor covers products that
@@ -301,6 +351,9 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   uint16_t* tile = reinterpret_cast<uint16_t*>(smem);
   float* logit_tile = reinterpret_cast<float*>(smem + kTileTokens * kRowPitch * 2);  // [token][expert]
   float* row_norm = logit_tile + kTileTokens * E;                                      // ||n_t||, rounded up
+  int* task_count = reinterpret_cast<int*>(row_norm + kTileTokens);
+  uint16_t* tasks = reinterpret_cast<uint16_t*>(task_count + 4);                      // token * E + expert
+  if (threadIdx.x == 0) *task_count = 0;  // ordered before phase 3 by the barriers below
 
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
@@ -441,13 +494,15 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   }
 
   // Phase 3: exact bf16 logits where they decide anything, then the selection; one
-  // token per wave.
+  // token per wave. The logits that need an exact recomputation are pooled over the
+  // workgroup and shared out among all its waves, so the workgroup waits for about one
+  // recomputation whichever token needs them.
   const int r = wave;
   const int64_t t = first + r;
-  if (t >= a.rows) return;  // wave-uniform; no barrier follows
+  const bool active = t < a.rows;  // wave-uniform; inactive waves still meet the barriers
   const bool emit = a.logits != nullptr;
   const float n_norm = row_norm[r];
-  uint32_t bits[V], lower[V], upper[V];
+  uint32_t bits[V], upper[V], keys[V];
   bool unsure[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
@@ -459,36 +514,57 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
     const uint32_t hi = f32_to_bf16(logit + delta);
     bits[v] = lo;
     unsure[v] = lo != hi;
-    lower[v] = route_key(lo, e);
+    keys[v] = route_key(lo, e);
     upper[v] = route_key(hi, e);
   }
   // Select on the lower bounds. A certain logit's lower bound is its value; an unsure
   // logit whose upper bound stays below the k-th selected key cannot be selected. If
   // every selected logit is certain and no unsure one can reach the k-th, this
   // selection is final.
-  uint32_t chosen;
-  uint32_t keys[V];
-#pragma unroll
-  for (int v = 0; v < V; ++v) keys[v] = lower[v];
-  const uint32_t threshold = select_topk<V>(keys, a.k, lane, chosen);
-  const uint16_t* n_row = tile + r * kRowPitch;
+  uint32_t chosen = 0;
+  uint32_t threshold = 0xFFFFFFFFu;
+  if (active) threshold = select_topk<V>(keys, a.k, lane, chosen);
+  bool need[V];
   bool refined = false;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
-    const bool need = unsure[v] && (emit || upper[v] >= threshold);
-    uint64_t pending = __ballot(need);
-    refined = refined || pending != 0;
-    while (pending != 0) {  // wave-uniform loop
-      const int src = __ffsll(static_cast<unsigned long long>(pending)) - 1;
-      pending &= pending - 1;
-      const uint32_t exact = exact_logit<VPL>(
-          n_row, a.weight_rows + static_cast<int64_t>(src + v * kWave) * H, lane);
-      if (lane == src) bits[v] = exact;
+    need[v] = active && unsure[v] && (emit || upper[v] >= threshold);
+    const uint64_t mask = __ballot(need[v]);
+    if (mask != 0) {  // wave-uniform
+      refined = true;
+      int base = 0;
+      if (lane == 0) base = atomicAdd(task_count, __popcll(mask));
+      base = __builtin_amdgcn_readfirstlane(base);
+      const int below = __builtin_amdgcn_mbcnt_hi(
+          static_cast<uint32_t>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+      if (need[v]) tasks[base + below] = static_cast<uint16_t>(r * E + lane + v * kWave);
     }
   }
+  __syncthreads();
+  // The recomputations, two per wave per pass; results overwrite the logits in LDS,
+  // which are no longer read.
+  uint32_t* exact_bits = reinterpret_cast<uint32_t*>(logit_tile);
+  const int count = *task_count;
+  for (int i = 2 * wave; i < count; i += 2 * kWaves) {  // wave-uniform
+    const int task0 = tasks[i];
+    const int task1 = i + 1 < count ? tasks[i + 1] : task0;
+    uint32_t exact0, exact1;
+    exact_logits<VPL>(tile + (task0 / E) * kRowPitch, tile + (task1 / E) * kRowPitch,
+                      a.weight_rows + static_cast<int64_t>(task0 % E) * H,
+                      a.weight_rows + static_cast<int64_t>(task1 % E) * H, lane, exact0, exact1);
+    if (lane == 0) {
+      exact_bits[task0] = exact0;
+      exact_bits[task1] = exact1;
+    }
+  }
+  __syncthreads();
+  if (!active) return;  // no barrier follows
   if (refined) {
 #pragma unroll
-    for (int v = 0; v < V; ++v) keys[v] = route_key(bits[v], lane + v * kWave);
+    for (int v = 0; v < V; ++v) {
+      if (need[v]) bits[v] = exact_bits[r * E + lane + v * kWave];
+      keys[v] = route_key(bits[v], lane + v * kWave);
+    }
     select_topk<V>(keys, a.k, lane, chosen);
   }
   if (emit) {
