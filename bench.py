@@ -45,6 +45,7 @@ sys.path.insert(0, str(REPO))
 
 PEAK_GBS = 8000.0
 ROTATE_BYTES = 512 * 2**20
+WARM_SECONDS = float(os.environ.get("OMNIA_BENCH_WARM", "1.0"))  # per workload, before timing
 MAX_COPIES = 64
 METRIC = "achieved HBM GB/s (% of MI355X peak) and µs per fused kernel, 1 GPU"
 HEADLINE = "qk_norm_rope_prefill"
@@ -358,10 +359,11 @@ def time_workload(w: Workload, steps: int, warmup: int, device, graph_mode: bool
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
-        # Warm up for `warmup` launches and at least ~25 ms, so clocks have ramped and
-        # every rotation buffer has been touched before timing.
+        # Warm up for `warmup` launches, two passes over the rotation buffers and at
+        # least WARM_SECONDS, so clocks have ramped and every buffer has been touched
+        # (measured: 25 ms left the rope epilogue ~7% and the headline ~3% slow).
         began, i = time.perf_counter(), 0
-        while i < max(warmup, copies) or time.perf_counter() - began < 0.025:
+        while i < max(warmup, 2 * copies) or time.perf_counter() - began < WARM_SECONDS:
             w.launch(sets[i % copies])
             i += 1
             if i % 64 == 0:

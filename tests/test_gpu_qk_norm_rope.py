@@ -121,7 +121,7 @@ def test_reads_q_and_k_in_place_from_fused_rows_via_facade():
     assert np.array_equal(bits_of(v[0]), want_v)
 
 
-EPILOGUE = [(1, 0), (1, 4095), (64, 137), (4096, 28_301), (3, 32_767)]
+EPILOGUE = [(1, 0), (1, 4095), (64, 137), (4096, 28_301), (3, 32_767), (200, 16_777_000), (512, 9_000_000)]
 
 
 @pytest.mark.parametrize("length,offset", EPILOGUE)
