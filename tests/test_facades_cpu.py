@@ -1,0 +1,218 @@
+"""Facade resolution, HIP predicates and the Core chains of every primitive, on the CPU.
+
+Mirrors the reference's resolution tests (tests/test_kernel_qk_norm_rope.py,
+tests/test_kernel_embedding_rope_atlas.py, tests/test_kernel_moe_route.py,
+tests/test_kernel_gate_softplus.py: "a binding binds only where it computes the declared
+arithmetic"): on CPU tensors every HIP binding declines or hands the call to its Core
+chain, `reference=True` forces the Core chain, and each Core chain agrees with the oracle
+on seeded inputs. The HIP kernels themselves are compared with the oracle in
+tests/test_gpu_*.py.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from mlx_omnia_amd.kernels.embed import DefaultEmbed, Embed, applies as embed_applies
+from mlx_omnia_amd.kernels.gate_softplus import DefaultGateSoftplus, GateSoftplus
+from mlx_omnia_amd.kernels.gate_up import (DefaultGateUpActivation, GateUpActivation, HipSwiGLU,
+                                           applies as swiglu_applies)
+from mlx_omnia_amd.kernels.leaf import RMSNormLeaf
+from mlx_omnia_amd.kernels.qkv_rope import (AngleTable, DefaultQkvRope, QkvRope, qk_norm_rope_applies,
+                                            rope_core, rope_epilogue_applies)
+from mlx_omnia_amd.kernels.route import (DefaultResidualRouter, DefaultRoute, ResidualRouter, Route,
+                                         Routing, residual_router_applies, softmax_topk_applies)
+from oracle import activations as act
+from oracle import embed as oracle_embed
+from oracle import rope as oracle_rope
+from oracle import route as oracle_route
+from oracle.bf16 import from_float, to_f32, ulp_distance
+from util import assert_bf16_close
+
+EPS = 1e-6
+
+
+def cpu(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16)
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+# ---- QK-norm + RoPE ---------------------------------------------------------------
+
+
+def test_rope_predicates():
+    for d, p in ((128, 64), (128, 32), (128, 16), (64, 32), (64, 8), (256, 128), (256, 64)):
+        assert qk_norm_rope_applies(d, p), (d, p)
+    for d, p in ((128, 48), (96, 48), (128, 128), (64, 4), (128, 0), (512, 256)):
+        assert not qk_norm_rope_applies(d, p), (d, p)
+    assert rope_epilogue_applies(128) and rope_epilogue_applies(64) and not rope_epilogue_applies(96)
+
+
+def _qkv_declaration(hq, hkv, d, rng, **extra):
+    qw, kw = from_float(1 + 0.1 * rng.standard_normal(d)), from_float(1 + 0.1 * rng.standard_normal(d))
+    common = dict(heads=hq, kv_heads=hkv, head_dim=d, rope=lambda x, o: rope_core(x, o, base=1e6),
+                  eps=EPS, q_norm=cpu(qw), k_norm=cpu(kw))
+    return qw, kw, dict(common, **extra)
+
+
+def test_qkv_rope_cpu_resolves_to_core_and_matches_epilogue_oracle():
+    hq, hkv, d, length, offset = 4, 2, 128, 7, 1234
+    rng = np.random.default_rng(0)
+    qw, kw, declaration = _qkv_declaration(hq, hkv, d, rng, base=1e6)
+    prologue = QkvRope(lambda x: x, **declaration)
+    assert isinstance(prologue.strategy, DefaultQkvRope)
+    fused = from_float(rng.standard_normal((1, length, (hq + 2 * hkv) * d)))
+    q, k, v = prologue(cpu(fused), offset)
+    want_q, want_k = oracle_rope.rope_epilogue(fused[0], hq, hkv, d, qw, kw, offset, 1e6, EPS)
+    assert_bf16_close(bits(q[0]), want_q)
+    assert_bf16_close(bits(k[0]), want_k)
+    want_v = fused[0, :, (hq + hkv) * d :].reshape(length, hkv, d).transpose(1, 0, 2)
+    assert np.array_equal(bits(v[0]), want_v)
+
+
+def test_qkv_rope_table_declaration_on_cpu_and_reference_flag():
+    rng = np.random.default_rng(1)
+    cos, sin = oracle_rope.angle_table(64, 64, 1e6)
+    table = AngleTable(torch.from_numpy(cos), torch.from_numpy(sin))
+    _, _, declaration = _qkv_declaration(4, 2, 128, rng, angles=table, rotary_pairs=64)
+    assert isinstance(QkvRope(lambda x: x, **declaration).strategy, DefaultQkvRope)
+    assert isinstance(QkvRope(lambda x: x, reference=True, **declaration).strategy, DefaultQkvRope)
+
+
+def test_angle_table_contract_and_atlas_view():
+    cos, sin = oracle_rope.angle_table(32, 8, 1e4)
+    atlas = torch.from_numpy(np.concatenate([cos, sin], axis=-1))
+    table = AngleTable.from_atlas(atlas)
+    assert table.pairs == 8
+    rows = table(5, 3)  # the reference's Angles contract: [length, 2P], cos then sin
+    assert rows.shape == (3, 16)
+    assert np.array_equal(rows.numpy(), atlas[5:8].numpy())
+
+
+# ---- Embedding + atlas --------------------------------------------------------------
+
+
+def test_embed_predicate():
+    assert embed_applies(2560, 64, 64, dtype=torch.bfloat16)
+    assert embed_applies(256, 32, 0, dtype=torch.bfloat16)
+    assert not embed_applies(2562, 64, 64, dtype=torch.bfloat16)
+    assert not embed_applies(2560, 62, 64, dtype=torch.bfloat16)
+    assert not embed_applies(2560, 64, 64, dtype=torch.float32)
+    assert not embed_applies(16384, 64, 64, dtype=torch.bfloat16)
+
+
+def test_embed_cpu_resolves_to_core_and_matches_oracle():
+    rng = np.random.default_rng(2)
+    table = from_float(0.02 * rng.standard_normal((100, 64)))
+    full = rng.standard_normal((1, 1, 20, 8)).astype(np.float32)
+    sliding = rng.standard_normal((1, 1, 20, 16)).astype(np.float32)
+    embed = Embed(cpu(table), full_atlas=torch.from_numpy(full), sliding_atlas=torch.from_numpy(sliding))
+    assert isinstance(embed.strategy, DefaultEmbed)
+    tokens = rng.integers(0, 100, size=(2, 6), dtype=np.int32)
+    h, f, s = embed(torch.from_numpy(tokens), 9)
+    want_h, want_f, want_s = oracle_embed.embed_atlas(tokens, table, full, sliding, 9, 6)
+    assert np.array_equal(bits(h), want_h)
+    assert np.array_equal(f.numpy(), want_f) and np.array_equal(s.numpy(), want_s)
+    h1, f1, s1 = embed(torch.tensor([[7]], dtype=torch.int32), 3)  # one token: flat rows
+    assert h1.shape == (64,) and f1.shape == (8,) and s1.shape == (16,)
+    assert np.array_equal(bits(h1), table[7]) and np.array_equal(f1.numpy(), full[0, 0, 3])
+
+
+# ---- SwiGLU and gate-softplus --------------------------------------------------------
+
+
+def test_swiglu_binding_declares_only_plain_swiglu():
+    assert swiglu_applies(9728) and swiglu_applies(8) and not swiglu_applies(12) and not swiglu_applies(0)
+    assert isinstance(GateUpActivation().strategy, HipSwiGLU)
+    for kw in (dict(activation="swiglu_oai", limit=7.0), dict(limit=7.0), dict(layout="interleaved")):
+        assert isinstance(GateUpActivation(**kw).strategy, DefaultGateUpActivation), kw
+    assert isinstance(GateUpActivation(reference=True).strategy, DefaultGateUpActivation)
+
+
+def test_swiglu_core_chain_on_cpu_tensors_matches_oracle():
+    rng = np.random.default_rng(3)
+    gate_up = from_float(3 * rng.standard_normal((5, 2 * 48)))
+    for activation in (GateUpActivation(), GateUpActivation(reference=True)):
+        y = activation(cpu(gate_up))  # CPU tensors: the HIP binding hands over to Core
+        want = act.swiglu(gate_up[:, :48], gate_up[:, 48:])
+        got = bits(y)
+        # torch's CPU sigmoid is not correctly rounded; the oracle's is: a rare one-ulp
+        # bf16 difference of the sigmoid may carry through the two products.
+        assert ulp_distance(got, want).max() <= 2
+        assert (got == want).mean() > 0.98
+
+
+def test_gate_softplus_cpu_resolves_to_core_and_matches_oracle():
+    rng = np.random.default_rng(4)
+    a = from_float(4 * rng.standard_normal((9, 32)))
+    a_log = rng.uniform(0, 2.7, 32).astype(np.float32)
+    dt_bias = (0.5 * rng.standard_normal(32)).astype(np.float32)
+    gate = GateSoftplus(torch.from_numpy(a_log), torch.from_numpy(dt_bias))
+    assert isinstance(gate.strategy, DefaultGateSoftplus)
+    got = gate(cpu(a)).numpy()
+    want = act.gate_softplus(a, a_log, dt_bias)
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=0)
+
+
+# ---- Routing ------------------------------------------------------------------------
+
+
+def test_route_predicates_and_declines():
+    assert softmax_topk_applies(128, 8) and softmax_topk_applies(256, 64)
+    assert not softmax_topk_applies(257, 8) and not softmax_topk_applies(128, 65)
+    assert residual_router_applies(2048, 128, 8) and residual_router_applies(4096, 256, 8)
+    assert not residual_router_applies(2560, 128, 8) and not residual_router_applies(2048, 64, 8)
+    assert Routing(experts=128, k=8).plain_softmax()
+    for knob in (dict(scoring="sigmoid"), dict(bias=torch.zeros(128)), dict(normalize=False),
+                 dict(scale=2.5), dict(softcap=30.0), dict(shared=True), dict(ties="higher"),
+                 dict(norm_eps=1e-20)):
+        routing = Routing(experts=128, k=8, **knob)
+        assert not routing.plain_softmax(), knob
+        assert isinstance(Route(None, experts=128, k=8, **knob).strategy, DefaultRoute), knob
+
+
+def test_route_core_chain_matches_oracle_and_reference_tie_fixture():
+    rng = np.random.default_rng(5)
+    logits = from_float(rng.standard_normal((50, 128)))
+    logits[:6] = from_float(rng.integers(-2, 3, (6, 128)) * 0.5)  # many exact ties
+    route = Route(None, experts=128, k=8, reference=True)
+    idx, w = route.rows(cpu(logits))
+    want_idx, want_w = oracle_route.softmax_topk(logits, 8)
+    assert np.array_equal(idx.numpy(), want_idx)
+    np.testing.assert_allclose(w.numpy(), want_w, rtol=1e-5, atol=1e-7)
+    # The higher-index rule of the reference's softmax chain, on the tie KAT
+    # (tests/test_kernel_moe_route.py:152-177): indices 0..7 tie with 11, 35, 67, 99.
+    row = np.full((1, 128), from_float(np.array([-1.0]))[0], dtype=np.uint16)
+    row[0, [0, 1, 2, 3, 11, 35, 67, 99, 120, 127]] = from_float(np.array([2.0]))[0]
+    lower, _ = Route(None, experts=128, k=8, reference=True).rows(cpu(row))
+    higher, _ = Route(None, experts=128, k=8, ties="higher").rows(cpu(row))
+    assert lower.numpy()[0].tolist() == [0, 1, 2, 3, 11, 35, 67, 99]
+    assert higher.numpy()[0].tolist() == [127, 120, 99, 67, 35, 11, 3, 2]
+
+
+def test_residual_router_cpu_resolves_to_core_and_matches_oracle():
+    rows, hidden, experts, k = 6, 2048, 128, 8
+    rng = np.random.default_rng(6)
+    x = from_float(rng.standard_normal((rows, hidden)))
+    r = from_float(rng.standard_normal((rows, hidden)))
+    w = from_float(1 + 0.1 * rng.standard_normal(hidden))
+    gate = from_float(0.02 * rng.standard_normal((experts, hidden)))
+    router = ResidualRouter(RMSNormLeaf(cpu(w), EPS), cpu(gate), routing=Routing(experts=experts, k=k))
+    assert isinstance(router.strategy, DefaultResidualRouter)
+    summed, normed, idx, wts = router(cpu(x), cpu(r))
+    want = oracle_route.residual_rms_router(x, r, w, gate, EPS, k)
+    assert np.array_equal(bits(summed), want[0])
+    assert ulp_distance(bits(normed), want[1]).max() <= 1
+    # The Core chain's bf16 matmul rounds its fp32 accumulation, the oracle rounds the
+    # exact dot product: they agree except for logits at a rounding boundary, so the
+    # selections agree wherever the k-th and (k+1)-th logits are apart.
+    logits = to_f32(oracle_route.router_logits(want[1], gate))
+    for t in range(rows):
+        values = np.sort(logits[t])[::-1]
+        if values[k - 1] - values[k] < 2.0**-6:  # a near tie at the cut: either pick is fine
+            continue
+        assert idx.numpy()[t].tolist() == want[3][t].tolist()
+    np.testing.assert_allclose(wts.numpy().sum(axis=-1), 1.0, rtol=1e-5)
