@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(
       }
     }
   }
-  acc = group_sum<kWave>(acc);
+  acc = wave_sum_f64(acc);
   const float inv = 1.0f / sqrtf(static_cast<float>(acc) / hidden + eps);
 
 #pragma unroll

@@ -128,6 +128,43 @@ __device__ __forceinline__ double row16_sum(double value) {
   return value;
 }
 
+// Cross-row steps of a wave reduction (gfx950): with the same value in both operands,
+// v_permlane16_swap hands each lane the value of the same column in the paired 16-lane
+// row (rows 0-1, 2-3), v_permlane32_swap that of the other 32-lane half; the two
+// returned dwords are then {own, partner} in some order, the same pair on both lanes.
+__device__ __forceinline__ void row_pair(uint32_t v, uint32_t& a, uint32_t& b) {
+  const auto swapped = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  a = swapped[0];
+  b = swapped[1];
+}
+__device__ __forceinline__ void half_pair(uint32_t v, uint32_t& a, uint32_t& b) {
+  const auto swapped = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  a = swapped[0];
+  b = swapped[1];
+}
+
+constexpr int kQuadSwap1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kQuadSwap2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+// fp64 sum over the wave, the same in every lane.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v = row16_sum(v);
+  uint32_t lo_a, lo_b, hi_a, hi_b;
+  const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+  row_pair(static_cast<uint32_t>(bits), lo_a, lo_b);
+  row_pair(static_cast<uint32_t>(bits >> 32), hi_a, hi_b);
+  v = __builtin_bit_cast(double, (static_cast<uint64_t>(hi_a) << 32) | lo_a) +
+      __builtin_bit_cast(double, (static_cast<uint64_t>(hi_b) << 32) | lo_b);
+  const uint64_t bits2 = __builtin_bit_cast(uint64_t, v);
+  half_pair(static_cast<uint32_t>(bits2), lo_a, lo_b);
+  half_pair(static_cast<uint32_t>(bits2 >> 32), hi_a, hi_b);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi_a) << 32) | lo_a) +
+         __builtin_bit_cast(double, (static_cast<uint64_t>(hi_b) << 32) | lo_b);
+}
+
+
 template <typename T>
 __device__ __forceinline__ T load_nt(const T* ptr) {
   return __builtin_nontemporal_load(ptr);

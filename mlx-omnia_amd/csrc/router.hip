@@ -70,26 +70,6 @@ __device__ __forceinline__ uint32_t route_key(uint32_t logit_bits, int expert) {
 
 __device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
 
-// Cross-row steps of a wave reduction (gfx950): with the same value in both operands,
-// v_permlane16_swap hands each lane the value of the same column in the paired 16-lane
-// row (rows 0-1, 2-3), v_permlane32_swap that of the other 32-lane half; the two
-// returned dwords are then {own, partner} in some order, the same pair on both lanes.
-__device__ __forceinline__ void row_pair(uint32_t v, uint32_t& a, uint32_t& b) {
-  const auto swapped = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  a = swapped[0];
-  b = swapped[1];
-}
-__device__ __forceinline__ void half_pair(uint32_t v, uint32_t& a, uint32_t& b) {
-  const auto swapped = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  a = swapped[0];
-  b = swapped[1];
-}
-
-constexpr int kQuadSwap1 = 0xB1;  // quad_perm [1, 0, 3, 2]
-constexpr int kQuadSwap2 = 0x4E;  // quad_perm [2, 3, 0, 1]
-constexpr int kRowHalfMirror = 0x141;
-constexpr int kRowMirror = 0x140;
-
 // Maximum over the wave, left in every lane: DPP steps inside each 16-lane row (quad
 // swaps, half-row and row mirrors), then the two cross-row swaps. Everything stays in
 // vector registers; no LDS and no scalar round trip on the dependency chain.
@@ -117,22 +97,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   v = __uint_as_float(a) + __uint_as_float(b);
   half_pair(__float_as_uint(v), a, b);
   return __uint_as_float(a) + __uint_as_float(b);
-}
-
-// fp64 sum over the wave, the same in every lane.
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  v = row16_sum(v);
-  uint32_t lo_a, lo_b, hi_a, hi_b;
-  const uint64_t bits = __builtin_bit_cast(uint64_t, v);
-  row_pair(static_cast<uint32_t>(bits), lo_a, lo_b);
-  row_pair(static_cast<uint32_t>(bits >> 32), hi_a, hi_b);
-  v = __builtin_bit_cast(double, (static_cast<uint64_t>(hi_a) << 32) | lo_a) +
-      __builtin_bit_cast(double, (static_cast<uint64_t>(hi_b) << 32) | lo_b);
-  const uint64_t bits2 = __builtin_bit_cast(uint64_t, v);
-  half_pair(static_cast<uint32_t>(bits2), lo_a, lo_b);
-  half_pair(static_cast<uint32_t>(bits2 >> 32), hi_a, hi_b);
-  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi_a) << 32) | lo_a) +
-         __builtin_bit_cast(double, (static_cast<uint64_t>(hi_b) << 32) | lo_b);
 }
 
 // Extracts the top k of the wave's keys (V per lane; a taken key becomes 0, below
@@ -260,7 +224,7 @@ __global__ __launch_bounds__(kPackBlock) void pack_router_kernel(const u32x4* __
       sum = __builtin_fma(d, d, sum);
     }
   }
-  sum = group_sum<kWave>(sum);
+  sum = wave_sum_f64(sum);
   if (lane == 0) norms[e] = norm_upper(sum);
 }
 
@@ -393,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
         sumsq += static_cast<double>(hi * hi);
       }
     }
-    sumsq = group_sum<kWave>(sumsq);
+    sumsq = wave_sum_f64(sumsq);
     const float inv = 1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(H) + a.eps);
     double nsq = 0.0;
 #pragma unroll
@@ -425,7 +389,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
         store_nt(a.normalized + t * (H / 8) + v, packed);
       }
     }
-    nsq = group_sum<kWave>(nsq);
+    nsq = wave_sum_f64(nsq);
     if (lane == 0) row_norm[r] = t < a.rows ? norm_upper(nsq) : 0.0f;
   }
   __syncthreads();
