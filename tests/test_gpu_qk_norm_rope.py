@@ -56,6 +56,9 @@ CASES = [
     (5, 12, 4, 64, 16, 3, MSCALE, "atlas"),
     (7, 8, 2, 256, 128, 100, 1.0, "separate"),
     (3, 8, 2, 256, 64, 9, 1.0, "separate"),
+    (6, 16, 4, 64, 32, 77, 1.0, "separate"),        # full rotary, 4 lanes per head
+    (4, 20, 4, 64, 32, 5, MSCALE, "atlas"),         # ... head counts not a multiple of 16
+    (9, 6, 2, 256, 128, 31_000, MSCALE, "atlas"),   # full rotary, 16 lanes per head, scaled
     (1, 32, 8, 128, 64, TABLE_ROWS - 1, 1.0, "separate"),
     (0, 32, 8, 128, 64, 0, 1.0, "separate"),
 ]
@@ -140,6 +143,23 @@ def test_epilogue_matches_oracle(length, offset):
     assert_bf16_close(bits_of(q), want_q)
     assert_bf16_close(bits_of(k), want_k)
     assert exact_fraction(bits_of(q), want_q) > 0.99
+
+
+@pytest.mark.parametrize("head_dim,hq,hkv,length,offset", [(64, 20, 4, 33, 901), (256, 8, 2, 17, 12_345)])
+def test_epilogue_other_head_dims(head_dim, hq, hkv, length, offset):
+    print(f"rope_epilogue D={head_dim} hq={hq} hkv={hkv} T={length}", flush=True)
+    rng = np.random.default_rng(head_dim + length)
+    fused = from_float(rng.standard_normal((length, (hq + 2 * hkv) * head_dim)))
+    qw = from_float(1 + 0.1 * rng.standard_normal(head_dim))
+    kw = from_float(1 + 0.1 * rng.standard_normal(head_dim))
+    q, k = ops.rope_epilogue(
+        to_device(fused), to_device(qw), to_device(kw), query_heads=hq, kv_heads=hkv,
+        head_dim=head_dim, offset=offset, log2_base=math.log2(1e6), eps=EPS,
+    )
+    torch.cuda.synchronize()
+    want_q, want_k = rope.rope_epilogue(fused, hq, hkv, head_dim, qw, kw, offset, 1e6, EPS)
+    assert_bf16_close(bits_of(q), want_q)
+    assert_bf16_close(bits_of(k), want_k)
 
 
 def test_epilogue_facade_resolution_and_segment():
