@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 2
+#define OMNIA_ABI_VERSION 3
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -182,6 +182,34 @@ int32_t omnia_residual_rms_router(const uint16_t* x, const uint16_t* branch,
                                   float eps, uint16_t* summed, uint16_t* normalized,
                                   uint16_t* logits, int32_t* indices, float* weights,
                                   hipStream_t stream);
+
+/* Routed expert gate/up projection of one token, dense bf16 weights, "blocked" layout
+ * (gate and up block-concatenated on the output axis and left un-activated):
+ *   out[j, n] = bf16(sum_h x[h] * weight[chosen[j], n, h])   j < k, n < rows (= 2 * inner)
+ * with fp32 accumulation. x [hidden] bf16; weight [experts, rows, hidden] bf16; chosen
+ * [k] int32 (an id outside [0, experts) gives a zero row); out [k, rows] bf16.
+ * Replaces: core/kernels/gate_up/dense.py:30-119 (`moe_dense_gate_up`,
+ * DenseGateUp.__call__ at :104-119); Core chain core/kernels/gate_up/default.py:59-66.
+ * hidden: multiple of 8, at most 8192. */
+int32_t omnia_moe_gate_up(const uint16_t* x, const uint16_t* weight, int64_t experts,
+                          int64_t rows, int64_t hidden, const int32_t* chosen, int64_t k,
+                          uint16_t* out, hipStream_t stream);
+
+/* Routed expert down projection of one token with the SwiGLU and the combine fused:
+ *   a[j, i] = g / (1 + exp(-g)) * u          fp32; g = act[j, i], u = act[j, inner + i]
+ *   d[j, n] = bf16(fp32(sum_i a[j, i] * weight[chosen[j], n, i]) * weights[j])
+ *   out[n]  = bf16(bf16(sum_j d[j, n]) + residual[n])     (residual NULL: no add)
+ * act [k, 2 * inner] bf16 (omnia_moe_gate_up's output); weight [experts, hidden, inner]
+ * bf16; chosen [k] int32 (an id outside [0, experts) contributes zero); weights [k] fp32;
+ * out [hidden] bf16.
+ * Replaces: core/kernels/down_combine/dense.py:21-109 (`moe_dense_down` and the
+ * `routed.sum(axis=0) + residual` of DenseDownCombine.__call__ at :91-109); Core chain
+ * core/kernels/down_combine/default.py:43-58.
+ * inner: multiple of 8, at most 2048; 1 <= k <= 16. */
+int32_t omnia_moe_down_combine(const uint16_t* act, const uint16_t* weight, int64_t experts,
+                               int64_t hidden, int64_t inner, const int32_t* chosen,
+                               const float* weights, int64_t k, const uint16_t* residual,
+                               uint16_t* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,123 @@
+"""The routed down/combine primitive of a one-token step, `GateUp`'s sibling:
+(act, chosen [n], weights [n], residual [hidden]) -> [hidden], each activation row
+down-projected by its expert, routing-weighted, summed and residual-added.
+
+Mirrors core/kernels/down_combine/__init__.py and kernel.py (`DownCombine`,
+`DownCombineStrategy`, `Layout`).
+
+- `HipDenseDownCombine` (`omnia_moe_down_combine`, csrc/moe.hip) serves what the
+  reference's `DenseDownCombine` serves (core/kernels/down_combine/dense.py:69-109): a
+  dense bf16 stack [experts, hidden, inner] under the `blocked` layout (the pair block
+  arrives un-activated and the SwiGLU runs inside the kernel), no bias, no shared
+  expert, at most 16 experts per token. Its arithmetic is the dense binding's: the
+  activation in fp32, bf16(dot * weight) per expert, then the expert sum and the
+  residual add in bf16, all in one dispatch.
+- `DefaultDownCombine` is the Core chain (core/kernels/down_combine/default.py:24-58): the
+  activation in bf16 ops, the gathered matrices times the rows, the routing weights,
+  the sum and the residual in torch ops. It accepts everything.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable, Literal, Protocol, runtime_checkable
+
+import torch
+
+from ...runtime import ops
+from .._device import hip_device
+from ..resolve import resolve
+
+Layout = Literal["interleaved", "blocked"]
+MAX_SLOTS = 16
+
+__all__ = ["DefaultDownCombine", "DownCombine", "DownCombineStrategy", "HipDenseDownCombine",
+           "Layout", "dense_down_applies"]
+
+
+@runtime_checkable
+class DownCombineStrategy(Protocol):
+    def __call__(self, act: torch.Tensor, chosen: torch.Tensor, weights: torch.Tensor,
+                 residual: torch.Tensor) -> torch.Tensor: ...
+
+
+def dense_down_applies(inner: int) -> bool:
+    """The lane's slice of the activation stays in registers: inner / 8 vectors over 32
+    lanes, at most 8 each."""
+    return 0 < inner <= 2048 and inner % 8 == 0
+
+
+@dataclass(frozen=True)
+class DefaultDownCombine(DownCombineStrategy):
+    weight: torch.Tensor
+    bias: torch.Tensor | None
+    shared: Callable[[torch.Tensor], torch.Tensor] | None
+    layout: Layout
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, bias, shared, layout) -> "DefaultDownCombine":
+        return cls(leaf.weight, bias, shared, layout)
+
+    def __call__(self, act, chosen, weights, residual):
+        rows = act.reshape(chosen.shape[0], -1)
+        if self.layout == "blocked":
+            gate, up = torch.chunk(rows, 2, dim=-1)
+            rows = gate * torch.sigmoid(gate) * up
+        routed = chosen if self.shared is None else chosen[:-1]
+        k = routed.shape[0]
+        matrices = self.weight[routed.long()]
+        down = (matrices.float() @ rows[:k].float()[..., None]).squeeze(-1).to(rows.dtype)
+        if self.bias is not None:
+            down = down + self.bias[routed.long()]
+        out = (down * weights[:k, None]).sum(dim=0)
+        if self.shared is not None:
+            out = out + weights[-1] * self.shared(rows[-1][None]).reshape(-1)
+        return out + residual
+
+
+@dataclass(frozen=True)
+class HipDenseDownCombine(DownCombineStrategy):
+    weight: torch.Tensor
+    fallback: DefaultDownCombine
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, bias, shared, layout) -> "HipDenseDownCombine | None":
+        weight = leaf.weight
+        if layout != "blocked" or bias is not None or shared is not None:
+            return None
+        if weight.dtype != torch.bfloat16 or weight.dim() != 3:
+            return None
+        if tuple(weight.shape[1:]) != (hidden, inner) or not dense_down_applies(inner):
+            return None
+        if not hip_device(weight):
+            return None
+        return cls(weight.contiguous(), DefaultDownCombine(weight, bias, shared, layout))
+
+    def __call__(self, act, chosen, weights, residual):
+        k = chosen.numel()
+        if k == 0 or k > MAX_SLOTS:  # one wave per expert in a workgroup
+            return self.fallback(act, chosen, weights, residual)
+        device = self.weight.device
+        return ops.moe_down_combine(
+            act.reshape(k, -1).to(torch.bfloat16).contiguous(), self.weight,
+            chosen.to(device=device, dtype=torch.int32).contiguous().reshape(-1),
+            weights.to(device=device, dtype=torch.float32).contiguous().reshape(-1),
+            None if residual is None else residual.reshape(-1).to(torch.bfloat16).contiguous(),
+        )
+
+
+_STRATEGIES = (HipDenseDownCombine, DefaultDownCombine)
+
+
+class DownCombine(DownCombineStrategy):
+    """Resolves the strategy at construction and delegates; itself a DownCombineStrategy."""
+
+    def __init__(self, leaf, *, hidden: int, inner: int, bias: torch.Tensor | None = None,
+                 shared=None, layout: Layout = "interleaved", reference: bool = False) -> None:
+        self.strategy: DownCombineStrategy = resolve(
+            (DefaultDownCombine,) if reference else _STRATEGIES, leaf, hidden=hidden,
+            inner=inner, bias=bias, shared=shared, layout=layout,
+        )
+
+    def __call__(self, act, chosen, weights, residual):
+        return self.strategy(act, chosen, weights, residual)

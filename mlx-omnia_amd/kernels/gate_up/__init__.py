@@ -1,6 +1,7 @@
-"""The gate/up activation: one facade, two bindings (`HipSwiGLU` ahead of the Core
-chain `DefaultGateUpActivation`), resolved by the declaration (activation, layout,
-clamp) with the reference's first-build-wins rule."""
+"""Gate/up: the activation facade (`GateUpActivation`: `HipSwiGLU` ahead of the Core
+chain `DefaultGateUpActivation`) and the routed projection of a one-token step
+(`GateUp` in routed.py: `HipDenseGateUp` ahead of `DefaultGateUp`), each resolved by its
+declaration with the reference's first-build-wins rule."""
 
 from __future__ import annotations
 
@@ -10,9 +11,17 @@ from ..resolve import resolve
 from .default import DefaultGateUpActivation, swiglu_core
 from .hip import HipSwiGLU, applies
 from .kernel import Activation, GateUpActivationStrategy, Layout, split
+from .routed import (DefaultGateUp, GateUp, GateUpStrategy, HipDenseGateUp, OrdinalRouting,
+                     dense_gate_up_applies)
 
 __all__ = [
+    "DefaultGateUp",
     "DefaultGateUpActivation",
+    "GateUp",
+    "GateUpStrategy",
+    "HipDenseGateUp",
+    "OrdinalRouting",
+    "dense_gate_up_applies",
     "GateUpActivation",
     "GateUpActivationStrategy",
     "HipSwiGLU",

@@ -1,0 +1,137 @@
+"""The routed gate/up primitive of a one-token step: (row [hidden], chosen [k]) ->
+[k, inner] (the activation) or [k, 2 * inner] (the un-activated pair block, `blocked`).
+
+Mirrors core/kernels/gate_up/__init__.py and kernel.py (`GateUp`, `GateUpStrategy`,
+`Layout`, `OrdinalRouting`): a block declares the expert leaf and the epilogue
+(activation, clamp, projection bias, layout, ordinal routing, a shared expert), and the
+first strategy whose `build` accepts the declaration serves it.
+
+- `HipDenseGateUp` (`omnia_moe_gate_up`, csrc/moe.hip) serves what the reference's
+  `DenseGateUp` serves (core/kernels/gate_up/dense.py:75-119): a dense bf16 stack
+  [experts, 2 * inner, hidden], the `blocked` layout (gate and up block-concatenated,
+  handed on un-activated), silu, no clamp, bias, routing or shared expert.
+- `DefaultGateUp` is the Core chain (core/kernels/gate_up/default.py:31-81): the gathered
+  matrices times the row, then the declared epilogue in bf16 ops. It accepts everything.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable, Literal, Protocol, runtime_checkable
+
+import torch
+
+from ...runtime import ops
+from .._device import hip_device
+from ..resolve import resolve
+
+Activation = Literal["silu", "swiglu_oai"]
+Layout = Literal["interleaved", "blocked"]
+
+
+@dataclass(frozen=True)
+class OrdinalRouting:
+    """The second argument carries the router's ordinal keys [experts] (ascending =
+    better); the strategy keeps the `top_k` best, equal keys to the lower index
+    (core/kernels/gate_up/kernel.py:23-36)."""
+
+    top_k: int
+
+    def indices(self, keys: torch.Tensor) -> torch.Tensor:
+        return torch.sort(keys.to(torch.int64), stable=True).indices[: self.top_k].to(torch.int32)
+
+
+@runtime_checkable
+class GateUpStrategy(Protocol):
+    def __call__(self, row: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor: ...
+
+
+def dense_gate_up_applies(hidden: int) -> bool:
+    """A row is hidden / 8 16-byte vectors, at most 16 per lane."""
+    return 0 < hidden <= 8192 and hidden % 8 == 0
+
+
+@dataclass(frozen=True)
+class DefaultGateUp(GateUpStrategy):
+    weight: torch.Tensor
+    activation: Activation
+    limit: float | None
+    bias: torch.Tensor | None
+    layout: Layout
+    routing: OrdinalRouting | None
+    shared: Callable[[torch.Tensor], torch.Tensor] | None
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, activation, limit, bias, layout, routing,
+              shared) -> "DefaultGateUp":
+        assert shared is None or routing is None
+        return cls(leaf.weight, activation, limit, bias, layout, routing, shared)
+
+    def __call__(self, row: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor:
+        if self.routing is not None:
+            chosen = self.routing.indices(chosen)
+        routed = chosen if self.shared is None else chosen[:-1]
+        matrices = self.weight[routed.long()]
+        fused = (matrices.float() @ row.reshape(-1).float()).to(row.dtype)
+        if self.bias is not None:
+            fused = fused + self.bias[routed.long()]
+        if self.shared is not None:
+            fused = torch.cat([fused, self.shared(row.reshape(1, -1)).reshape(1, -1)], dim=0)
+        if self.layout == "blocked":
+            return fused
+        pairs = fused.reshape(fused.shape[0], -1, 2)
+        gate, up = pairs[..., 0], pairs[..., 1]
+        if self.activation == "swiglu_oai":
+            assert self.limit is not None
+            gate = torch.clamp(gate, max=self.limit)
+            up = torch.clamp(up, -self.limit, self.limit)
+            return gate * torch.sigmoid(1.702 * gate) * (up + 1)
+        if self.limit is not None:
+            gate = torch.clamp(gate, max=self.limit)
+            up = torch.clamp(up, -self.limit, self.limit)
+        return gate * torch.sigmoid(gate) * up
+
+
+@dataclass(frozen=True)
+class HipDenseGateUp(GateUpStrategy):
+    weight: torch.Tensor
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, activation, limit, bias, layout, routing,
+              shared) -> "HipDenseGateUp | None":
+        weight = leaf.weight
+        if shared is not None or routing is not None or bias is not None or limit is not None:
+            return None
+        if layout != "blocked" or activation != "silu":
+            return None
+        if weight.dtype != torch.bfloat16 or weight.dim() != 3:
+            return None
+        if tuple(weight.shape[1:]) != (2 * inner, hidden) or not dense_gate_up_applies(hidden):
+            return None
+        if not hip_device(weight):
+            return None
+        return cls(weight.contiguous())
+
+    def __call__(self, row: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor:
+        ids = chosen.to(device=self.weight.device, dtype=torch.int32).contiguous().reshape(-1)
+        return ops.moe_gate_up(row.reshape(-1).contiguous(), self.weight, ids)
+
+
+_STRATEGIES = (HipDenseGateUp, DefaultGateUp)
+
+
+class GateUp(GateUpStrategy):
+    """Resolves the strategy at construction and delegates; itself a GateUpStrategy."""
+
+    def __init__(self, leaf, *, hidden: int, inner: int, activation: Activation = "silu",
+                 limit: float | None = None, bias: torch.Tensor | None = None,
+                 layout: Layout = "interleaved", routing: OrdinalRouting | None = None,
+                 shared=None, reference: bool = False) -> None:
+        self.strategy: GateUpStrategy = resolve(
+            (DefaultGateUp,) if reference else _STRATEGIES, leaf, hidden=hidden, inner=inner,
+            activation=activation, limit=limit, bias=bias, layout=layout, routing=routing,
+            shared=shared,
+        )
+
+    def __call__(self, row: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor:
+        return self.strategy(row, chosen)

@@ -15,3 +15,11 @@ import torch
 class RMSNormLeaf:
     weight: torch.Tensor
     eps: float = 1e-6
+
+
+@dataclass
+class SwitchLinearLeaf:
+    """A stack of expert matrices, one per row: weight [experts, out, in], the layout of
+    the reference's `SwitchLinear` leaf (core/layers.py:140-154)."""
+
+    weight: torch.Tensor

@@ -361,3 +361,62 @@ def residual_rms_router(
         weights.data_ptr(), _stream(x),
     )
     return summed, normalized, logits, indices, weights
+
+
+def moe_gate_up(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    chosen: torch.Tensor,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One token's routed gate/up projection; see `omnia_moe_gate_up`. x [hidden] bf16,
+    weight [experts, 2 * inner, hidden] bf16, chosen [k] int32 -> [k, 2 * inner] bf16."""
+    _require(x.dim() == 1 or x.numel() == x.shape[-1], "moe_gate_up: x must be one row")
+    _require(weight.dim() == 3 and weight.shape[-1] == x.shape[-1], "moe_gate_up: weight shape")
+    _dense(x, BF16, "x")
+    _dense(weight, BF16, "weight")
+    _require(chosen.dtype == torch.int32 and chosen.is_contiguous() and chosen.dim() == 1,
+             "moe_gate_up: chosen must be contiguous int32 [k]")
+    _require(on_rocm(x, weight, chosen), "moe_gate_up: tensors must share one ROCm device")
+    experts, rows, hidden = weight.shape
+    k = chosen.numel()
+    out = _out(out, x, (k, rows), BF16, "out")
+    call("omnia_moe_gate_up", x.data_ptr(), weight.data_ptr(), experts, rows, hidden,
+         chosen.data_ptr(), k, out.data_ptr(), _stream(x))
+    return out
+
+
+def moe_down_combine(
+    act: torch.Tensor,
+    weight: torch.Tensor,
+    chosen: torch.Tensor,
+    weights: torch.Tensor,
+    residual: torch.Tensor | None = None,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One token's routed down projection with the SwiGLU, the routing weights, the expert
+    sum and the residual; see `omnia_moe_down_combine`. act [k, 2 * inner] bf16, weight
+    [experts, hidden, inner] bf16, chosen [k] int32, weights [k] fp32, residual [hidden]
+    bf16 or None -> [hidden] bf16."""
+    _require(weight.dim() == 3, "moe_down_combine: weight must be [experts, hidden, inner]")
+    experts, hidden, inner = weight.shape
+    k = chosen.numel()
+    _require(act.shape == (k, 2 * inner), "moe_down_combine: act must be [k, 2 * inner]")
+    _dense(act, BF16, "act")
+    _dense(weight, BF16, "weight")
+    _require(chosen.dtype == torch.int32 and chosen.is_contiguous(), "moe_down_combine: chosen int32")
+    _require(weights.dtype == F32 and weights.is_contiguous() and weights.numel() == k,
+             "moe_down_combine: weights must be contiguous fp32 [k]")
+    tensors = [act, weight, chosen, weights]
+    if residual is not None:
+        _require(residual.numel() == hidden and residual.dtype == BF16 and residual.is_contiguous(),
+                 "moe_down_combine: residual must be contiguous bf16 [hidden]")
+        tensors.append(residual)
+    _require(on_rocm(*tensors), "moe_down_combine: tensors must share one ROCm device")
+    out = _out(out, act, (hidden,), BF16, "out")
+    call("omnia_moe_down_combine", act.data_ptr(), weight.data_ptr(), experts, hidden, inner,
+         chosen.data_ptr(), weights.data_ptr(), k,
+         residual.data_ptr() if residual is not None else None, out.data_ptr(), _stream(act))
+    return out

@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent.parent))
 
-from oracle import activations, add_norm, embed, rope, route  # noqa: E402
+from oracle import activations, add_norm, embed, moe, rope, route  # noqa: E402
 from oracle.bf16 import from_float  # noqa: E402
 
 
@@ -84,8 +84,23 @@ def make_route() -> dict[str, np.ndarray]:
     return dict(logits=logits, k=np.int64(8), indices=indices, weights=weights)
 
 
+def make_moe() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(6)
+    experts, hidden, inner, k = 4, 128, 32, 3
+    x = from_float(rng.standard_normal(hidden))
+    gate_up_weight = from_float(0.05 * rng.standard_normal((experts, 2 * inner, hidden)))
+    down_weight = from_float(0.05 * rng.standard_normal((experts, hidden, inner)))
+    chosen = np.array([3, 0, 2], dtype=np.int32)
+    weights = np.array([0.5, 0.3, 0.2], dtype=np.float32)
+    residual = from_float(rng.standard_normal(hidden))
+    act = moe.gate_up(x, gate_up_weight, chosen)
+    out = moe.down_combine(act, down_weight, chosen, weights, residual)
+    return dict(x=x, gate_up_weight=gate_up_weight, down_weight=down_weight, chosen=chosen,
+                weights=weights, residual=residual, act=act, out=out)
+
+
 MAKERS = {"add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed,
-          "activations": make_activations, "route": make_route}
+          "activations": make_activations, "route": make_route, "moe": make_moe}
 
 
 def main(names: list[str]) -> None:
