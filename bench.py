@@ -286,6 +286,58 @@ def workloads() -> list[Workload]:
             a["ids"], a["table"], a["cos"], a["sin"], position=0, n_positions=2048,
             hidden_out=a["out"], full_out=a["fo"], sliding_out=a["so"]),
     ))
+    # Next after the path: the routed expert MLP of a one-token step at Qwen3-30B-A3B's
+    # shape (hidden 2048, moe inner 768, 128 experts, top-8), dense bf16 weights, the
+    # "blocked" gate||up layout. The weight stacks are shared parameters (805 MB and
+    # 403 MB); each argument set routes to its own random experts.
+    moe_e, moe_h, moe_i, moe_k = 128, 2048, 768, 8
+    moe_stacks = {}
+
+    def moe_weights(device):
+        if not moe_stacks:
+            gen = torch.Generator(device=device).manual_seed(8)
+            for name, shape in (("gate_up", (moe_e, 2 * moe_i, moe_h)), ("down", (moe_e, moe_h, moe_i))):
+                stack = torch.empty(shape, dtype=torch.bfloat16, device=device)
+                for e in range(moe_e):  # one expert at a time: bounded fp32 scratch
+                    stack[e] = (0.02 * torch.randn(shape[1:], generator=gen, device=device)).to(torch.bfloat16)
+                moe_stacks[name] = stack
+        return moe_stacks
+
+    def setup_moe(device, copies, down=False):
+        rng = np.random.default_rng(9)
+        stacks = moe_weights(device)
+        sets = []
+        for _ in range(copies):
+            chosen = torch.from_numpy(rng.choice(moe_e, size=moe_k, replace=False).astype(np.int32)).to(device)
+            entry = dict(gu=stacks["gate_up"], dn=stacks["down"], ids=chosen,
+                         x=_to_bf16_device(_normal(rng, (moe_h,)), device),
+                         act=_to_bf16_device(_normal(rng, (moe_k, 2 * moe_i)), device),
+                         w=torch.from_numpy(rng.dirichlet(np.ones(moe_k)).astype(np.float32)).to(device),
+                         r=_to_bf16_device(_normal(rng, (moe_h,)), device))
+            entry["y"] = torch.empty((moe_k, 2 * moe_i), dtype=torch.bfloat16, device=device)
+            entry["o"] = torch.empty((moe_h,), dtype=torch.bfloat16, device=device)
+            sets.append(entry)
+        return sets
+
+    out.append(Workload(
+        name="moe_gate_up_decode",
+        kernel="moe_gate_up_kernel",
+        description="x [2048] bf16 x 8 of 128 experts' [1536, 2048] bf16 gate||up stacks "
+                    "(Qwen3-30B-A3B, T=1) -> [8, 1536] bf16",
+        bytes_per_launch=moe_k * 2 * moe_i * moe_h * 2 + moe_h * 2 + moe_k * 4 + moe_k * 2 * moe_i * 2,
+        setup=setup_moe,
+        launch=lambda a: ops.moe_gate_up(a["x"], a["gu"], a["ids"], out=a["y"]),
+    ))
+    out.append(Workload(
+        name="moe_down_combine_decode",
+        kernel="moe_down_kernel",
+        description="silu(gate)*up of [8, 1536] x 8 of 128 experts' [2048, 768] bf16 down "
+                    "stacks, routing weights, expert sum, residual (Qwen3-30B-A3B, T=1)",
+        bytes_per_launch=moe_k * moe_h * moe_i * 2 + moe_k * 2 * moe_i * 2 + moe_k * 8 + 2 * moe_h * 2,
+        setup=lambda device, copies: setup_moe(device, copies, down=True),
+        launch=lambda a: ops.moe_down_combine(a["act"], a["dn"], a["ids"], a["w"], a["r"], out=a["o"]),
+    ))
+
     # Not a product kernel: a plain device-to-device copy of known size, the scale for
     # the FETCH_SIZE / WRITE_SIZE counters (run with --only copy_calibration).
     def setup_copy(device, copies, elements=64 * 2**20):

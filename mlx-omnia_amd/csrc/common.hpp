@@ -130,8 +130,9 @@ __device__ __forceinline__ double row16_sum(double value) {
 
 // Cross-row steps of a wave reduction (gfx950): with the same value in both operands,
 // v_permlane16_swap hands each lane the value of the same column in the paired 16-lane
-// row (rows 0-1, 2-3), v_permlane32_swap that of the other 32-lane half; the two
-// returned dwords are then {own, partner} in some order, the same pair on both lanes.
+// row (rows 0-1, 2-3), v_permlane32_swap that of the other 32-lane half. Both lanes of a
+// pair get the same two dwords: the first from the lower lane (row 0 or 2, half 0), the
+// second from the upper one (checked on MI355X with a one-wave probe of lane ids).
 __device__ __forceinline__ void row_pair(uint32_t v, uint32_t& a, uint32_t& b) {
   const auto swapped = __builtin_amdgcn_permlane16_swap(v, v, false, false);
   a = swapped[0];

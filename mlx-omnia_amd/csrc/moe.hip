@@ -150,20 +150,20 @@ __global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a)
   const bool valid = expert >= 0 && expert < a.experts;  // wave-uniform
   const float scale = a.weights[slot];
 
-  // This lane's slice of the activation: elements (hl + 32 i) * 8 + j of I.
-  float act[VPL][8];
+  // The lane's slice of the pair block (elements (hl + 32 i) * 8 + j of I) is loaded
+  // first, then the first group of weight rows; the activation is computed while the
+  // weight loads are in flight (vector-memory results are counted in issue order, so the
+  // wait for the block leaves the weight loads outstanding).
+  u32x4 gate_raw[VPL], up_raw[VPL];
   {
     const uint16_t* gate = a.act + static_cast<int64_t>(slot) * 2 * a.inner;
     const uint16_t* up = gate + a.inner;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int v = hl + i * 32;
-      float g[8], u[8];
       const bool in = v < a.vecs;
-      unpack8(in ? *reinterpret_cast<const u32x4*>(gate + v * 8) : u32x4{0u, 0u, 0u, 0u}, g);
-      unpack8(in ? *reinterpret_cast<const u32x4*>(up + v * 8) : u32x4{0u, 0u, 0u, 0u}, u);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) act[i][j] = g[j] / (1.0f + expf(-g[j])) * u[j];
+      gate_raw[i] = in ? *reinterpret_cast<const u32x4*>(gate + v * 8) : u32x4{0u, 0u, 0u, 0u};
+      up_raw[i] = in ? *reinterpret_cast<const u32x4*>(up + v * 8) : u32x4{0u, 0u, 0u, 0u};
     }
   }
   const u32x4* w = reinterpret_cast<const u32x4*>(a.w) +
@@ -171,9 +171,7 @@ __global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a)
   // Row pairs in flight together: all four while the vectors fit the 128-register
   // budget of a 16-wave workgroup.
   constexpr int kGroup = VPL <= 4 ? 4 : (VPL <= 6 ? 2 : 1);
-#pragma unroll
-  for (int p0 = 0; p0 < kDownRows / 2; p0 += kGroup) {
-    u32x4 wv[kGroup][VPL];
+  auto load_group = [&](int p0, u32x4 (&wv)[kGroup][VPL]) {
 #pragma unroll
     for (int p = 0; p < kGroup; ++p) {
       const int n = row_base + (p0 + p) * 2 + half;
@@ -184,6 +182,34 @@ __global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a)
         if (valid && n < a.hidden && v < a.vecs) wv[p][i] = load_nt(w + static_cast<int64_t>(n) * a.vecs + v);
       }
     }
+  };
+  u32x4 wv[kGroup][VPL];
+  load_group(0, wv);
+  // Both halves of the wave hold the same slice; each computes half of it (flat
+  // elements [half * 4 VPL, (half + 1) * 4 VPL)) and the halves swap results.
+  float act[VPL][8];
+  {
+    float g[VPL * 8], u[VPL * 8];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      unpack8(gate_raw[i], g + i * 8);
+      unpack8(up_raw[i], u + i * 8);
+    }
+    constexpr int kHalf = VPL * 4;
+#pragma unroll
+    for (int f = 0; f < kHalf; ++f) {
+      const float gf = half ? g[f + kHalf] : g[f];
+      const float uf = half ? u[f + kHalf] : u[f];
+      const float mine = gf / (1.0f + expf(-gf)) * uf;
+      uint32_t lower, upper;  // the lower half's value and the upper half's
+      half_pair(__float_as_uint(mine), lower, upper);
+      act[f / 8][f % 8] = __uint_as_float(lower);
+      act[(f + kHalf) / 8][(f + kHalf) % 8] = __uint_as_float(upper);
+    }
+  }
+#pragma unroll
+  for (int p0 = 0; p0 < kDownRows / 2; p0 += kGroup) {
+    if (p0 > 0) load_group(p0, wv);
 #pragma unroll
     for (int p = 0; p < kGroup; ++p) {
       float acc = 0.0f;
