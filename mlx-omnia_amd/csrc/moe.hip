@@ -20,9 +20,10 @@
 // wave reduction in vector registers (DPP and permlane swaps).
 // down: a workgroup owns kDownRows output rows and has one wave per chosen expert; the
 // wave computes its expert's activation once (the lane's slice of I, kept in registers)
-// and reuses it for all the rows: half-waves take one row each (32 lanes x 16-byte
-// vectors over I), reduce it, scale and round it, and leave it in LDS; after a barrier
-// one lane per row adds the experts in order and the residual.
+// and reuses it for all the rows. Lanes l and l + 32 own the same slice of I, so each
+// evaluates half of its elements and the two swap results. Half-waves then take one row
+// each (32 lanes x 16-byte vectors over I), reduce it, scale and round it, and leave it
+// in LDS; after a barrier one lane per row adds the experts in order and the residual.
 #include "common.hpp"
 #include "host.hpp"
 

@@ -72,7 +72,7 @@ class DefaultDownCombine(DownCombineStrategy):
         out = (down * weights[:k, None]).sum(dim=0)
         if self.shared is not None:
             out = out + weights[-1] * self.shared(rows[-1][None]).reshape(-1)
-        return out + residual
+        return out if residual is None else out + residual
 
 
 @dataclass(frozen=True)

@@ -216,3 +216,84 @@ def test_residual_router_cpu_resolves_to_core_and_matches_oracle():
             continue
         assert idx.numpy()[t].tolist() == want[3][t].tolist()
     np.testing.assert_allclose(wts.numpy().sum(axis=-1), 1.0, rtol=1e-5)
+
+
+# ---- routed expert gate/up and down/combine ---------------------------------------
+
+
+def test_moe_predicates():
+    from mlx_omnia_amd.kernels.down_combine import dense_down_applies
+    from mlx_omnia_amd.kernels.gate_up import dense_gate_up_applies
+
+    for h in (8, 520, 2048, 4096, 8192):
+        assert dense_gate_up_applies(h), h
+    for h in (0, 4, 100, 8200, 16384):
+        assert not dense_gate_up_applies(h), h
+    for i in (8, 72, 768, 1792, 2048):
+        assert dense_down_applies(i), i
+    for i in (0, 12, 2056, 4096):
+        assert not dense_down_applies(i), i
+
+
+def test_moe_cpu_resolves_to_core_and_matches_oracle():
+    from mlx_omnia_amd.kernels.down_combine import (DefaultDownCombine, DownCombine,
+                                                    HipDenseDownCombine)
+    from mlx_omnia_amd.kernels.gate_up import DefaultGateUp, GateUp, HipDenseGateUp
+    from mlx_omnia_amd.kernels.leaf import SwitchLinearLeaf
+    from oracle import moe as oracle_moe
+
+    experts, hidden, inner = 6, 64, 24
+    rng = np.random.default_rng(11)
+    gu = from_float(0.05 * rng.standard_normal((experts, 2 * inner, hidden)))
+    dn = from_float(0.05 * rng.standard_normal((experts, hidden, inner)))
+    x = from_float(rng.standard_normal(hidden))
+    chosen = np.array([4, 1, 5], dtype=np.int32)
+    weights = np.array([0.5, 0.3, 0.2], dtype=np.float32)
+    residual = from_float(rng.standard_normal(hidden))
+    gate_up = GateUp(SwitchLinearLeaf(cpu(gu)), hidden=hidden, inner=inner, layout="blocked")
+    down = DownCombine(SwitchLinearLeaf(cpu(dn)), hidden=hidden, inner=inner, layout="blocked")
+    assert isinstance(gate_up.strategy, DefaultGateUp)
+    assert isinstance(down.strategy, DefaultDownCombine)
+    assert not isinstance(gate_up.strategy, HipDenseGateUp)
+    assert not isinstance(down.strategy, HipDenseDownCombine)
+    ids = torch.from_numpy(chosen)
+    act = gate_up(cpu(x), ids)
+    assert act.shape == (3, 2 * inner)
+    # The Core chain's float32 matmul rounds once to bf16 like the oracle's float64 dot.
+    assert ulp_distance(bits(act), oracle_moe.gate_up(x, gu, chosen)).max() <= 1
+    out = down(act, ids, torch.from_numpy(weights), cpu(residual))
+    # The Core chain runs the SwiGLU in bf16 ops (core/kernels/down_combine/default.py:43-58):
+    # the dense binding's fp32 activation is the oracle's, so only the north-star bar holds.
+    # fp32 routing weights promote the chain's sum to fp32, as mlx promotes it.
+    assert out.dtype == torch.float32
+    assert_bf16_close(bits(out.to(torch.bfloat16)), oracle_moe.down_combine(bits(act), dn, chosen, weights, residual),
+                      min_exact=0.5)
+    no_residual = down(act, ids, torch.from_numpy(weights), None)
+    assert no_residual.shape == (hidden,)
+
+
+def test_moe_hip_bindings_decline_other_declarations():
+    from mlx_omnia_amd.kernels.down_combine import HipDenseDownCombine
+    from mlx_omnia_amd.kernels.gate_up import HipDenseGateUp, OrdinalRouting
+    from mlx_omnia_amd.kernels.leaf import SwitchLinearLeaf
+
+    leaf = SwitchLinearLeaf(torch.zeros((4, 48, 64), dtype=torch.bfloat16))
+    base = dict(hidden=64, inner=24, activation="silu", limit=None, bias=None, layout="blocked",
+                routing=None, shared=None)
+    assert HipDenseGateUp.build(leaf, **base) is None  # CPU tensors
+    for change in (dict(layout="interleaved"), dict(activation="swiglu_oai"), dict(limit=7.0),
+                   dict(routing=OrdinalRouting(2)), dict(bias=torch.zeros(4, 48)),
+                   dict(inner=32)):
+        assert HipDenseGateUp.build(leaf, **dict(base, **change)) is None, change
+    down_leaf = SwitchLinearLeaf(torch.zeros((4, 64, 24), dtype=torch.bfloat16))
+    dbase = dict(hidden=64, inner=24, bias=None, shared=None, layout="blocked")
+    assert HipDenseDownCombine.build(down_leaf, **dbase) is None
+    for change in (dict(layout="interleaved"), dict(bias=torch.zeros(4, 64)), dict(hidden=32)):
+        assert HipDenseDownCombine.build(down_leaf, **dict(dbase, **change)) is None, change
+
+
+def test_ordinal_routing_keeps_the_best_keys_lowest_index_first():
+    from mlx_omnia_amd.kernels.gate_up import OrdinalRouting
+
+    keys = torch.tensor([5, 2, 9, 2, 0, 7], dtype=torch.int32)
+    assert OrdinalRouting(3).indices(keys).tolist() == [4, 1, 3]
