@@ -338,6 +338,45 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.moe_down_combine(a["act"], a["dn"], a["ids"], a["w"], a["r"], out=a["o"]),
     ))
 
+    # Next after the routed MLP: the dense SwiGLU MLP of a one-token step at Qwen3-4B's
+    # shape (hidden 2560, inner 9728: config 4's inner dimension), bf16 weights, gate rows
+    # first. Each argument set holds its own weights, as each layer of a model does.
+    mlp_h, mlp_i = 2560, 9728
+
+    def setup_mlp(device, copies, down=False):
+        rng = np.random.default_rng(10)
+        gen = torch.Generator(device=device).manual_seed(11)
+        sets = []
+        for _ in range(copies):
+            shape = (mlp_h, mlp_i) if down else (2 * mlp_i, mlp_h)
+            weight = (torch.randn(shape, generator=gen, device=device) / np.sqrt(shape[1])).to(torch.bfloat16)
+            entry = dict(w=weight, x=_to_bf16_device(_normal(rng, (mlp_h,)), device),
+                         act=_to_bf16_device(_normal(rng, (mlp_i,)), device),
+                         r=_to_bf16_device(_normal(rng, (mlp_h,)), device))
+            entry["y"] = torch.empty((mlp_i,), dtype=torch.bfloat16, device=device)
+            entry["o"] = torch.empty((mlp_h,), dtype=torch.bfloat16, device=device)
+            sets.append(entry)
+        return sets
+
+    out.append(Workload(
+        name="dense_mlp_gate_up_decode",
+        kernel="dense_gate_up_swiglu_kernel",
+        description="x [2560] bf16 x fused gate||up [19456, 2560] bf16 -> bf16 SwiGLU [9728] "
+                    "(Qwen3-4B MLP, T=1)",
+        bytes_per_launch=2 * mlp_i * mlp_h * 2 + mlp_h * 2 + mlp_i * 2,
+        setup=setup_mlp,
+        launch=lambda a: ops.dense_gate_up_swiglu(a["x"], a["w"], out=a["y"]),
+    ))
+    out.append(Workload(
+        name="dense_mlp_down_decode",
+        kernel="dense_down_residual_kernel",
+        description="act [9728] bf16 x down [2560, 9728] bf16 + residual [2560] -> [2560] bf16 "
+                    "(Qwen3-4B MLP, T=1)",
+        bytes_per_launch=mlp_h * mlp_i * 2 + mlp_i * 2 + 2 * mlp_h * 2,
+        setup=lambda device, copies: setup_mlp(device, copies, down=True),
+        launch=lambda a: ops.dense_down_residual(a["act"], a["w"], a["r"], out=a["o"]),
+    ))
+
     # Not a product kernel: a plain device-to-device copy of known size, the scale for
     # the FETCH_SIZE / WRITE_SIZE counters (run with --only copy_calibration).
     def setup_copy(device, copies, elements=64 * 2**20):

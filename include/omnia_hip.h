@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 3
+#define OMNIA_ABI_VERSION 4
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -210,6 +210,31 @@ int32_t omnia_moe_down_combine(const uint16_t* act, const uint16_t* weight, int6
                                int64_t hidden, int64_t inner, const int32_t* chosen,
                                const float* weights, int64_t k, const uint16_t* residual,
                                uint16_t* out, hipStream_t stream);
+
+/* Dense SwiGLU MLP of one token, first half: the fused gate||up projection with the
+ * SwiGLU applied in bf16 steps,
+ *   g = bf16(sum_h x[h] * fused[n, h]),  u = bf16(sum_h x[h] * fused[inner + n, h])   fp32 sums
+ *   e = bf16(exp(|g|)), den = bf16(1 + e), y = bf16(1 / den), sig = g < 0 ? y : bf16(1 - y)
+ *   activated[n] = bf16(bf16(g * sig) * u)
+ * x [hidden] bf16; fused_weight [2 * inner, hidden] bf16 (gate rows first); activated
+ * [inner] bf16.
+ * Replaces: core/kernels/mlp/dense.py:34-97,185-199 (`dense_gate_up_swiglu`, the first
+ * dispatch of DenseMlp.__call__ at :244-246); Core chain core/kernels/mlp/default.py:28-29
+ * through SwiGLU.__call__ at core/layers.py:270-272.
+ * hidden: multiple of 8, at most 8192. */
+int32_t omnia_dense_gate_up_swiglu(const uint16_t* x, const uint16_t* fused_weight,
+                                   int64_t hidden, int64_t inner, uint16_t* activated,
+                                   hipStream_t stream);
+
+/* Dense SwiGLU MLP of one token, second half: the down projection with the residual,
+ *   out[n] = bf16(residual[n] + bf16(sum_i activated[i] * down[n, i]))   fp32 sum
+ * activated [inner] bf16; down_weight [hidden, inner] bf16; residual, out [hidden] bf16.
+ * Replaces: core/kernels/mlp/dense.py:100-147,202-218 (`dense_down_residual`, the second
+ * dispatch of DenseMlp.__call__ at :246); Core chain core/kernels/mlp/default.py:28-29.
+ * inner: multiple of 8. */
+int32_t omnia_dense_down_residual(const uint16_t* activated, const uint16_t* down_weight,
+                                  const uint16_t* residual, int64_t hidden, int64_t inner,
+                                  uint16_t* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

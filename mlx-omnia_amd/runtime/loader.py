@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libomnia_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -47,6 +47,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "omnia_moe_down_combine": (
         _I32, [_P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P]
     ),
+    "omnia_dense_gate_up_swiglu": (_I32, [_P, _P, _I64, _I64, _P, _P]),
+    "omnia_dense_down_residual": (_I32, [_P, _P, _P, _I64, _I64, _P, _P]),
     "omnia_embed_atlas": (
         _I32,
         [_P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P],

@@ -420,3 +420,51 @@ def moe_down_combine(
          chosen.data_ptr(), weights.data_ptr(), k,
          residual.data_ptr() if residual is not None else None, out.data_ptr(), _stream(act))
     return out
+
+
+def dense_gate_up_swiglu(
+    x: torch.Tensor,
+    fused_weight: torch.Tensor,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One token through the fused gate||up weight with the bf16 SwiGLU applied; see
+    `omnia_dense_gate_up_swiglu`. x [hidden] bf16, fused_weight [2 * inner, hidden] bf16
+    (gate rows first) -> [inner] bf16."""
+    _require(x.dim() == 1 or x.numel() == x.shape[-1], "dense_gate_up_swiglu: x must be one row")
+    _require(fused_weight.dim() == 2 and fused_weight.shape[0] % 2 == 0
+             and fused_weight.shape[1] == x.shape[-1],
+             "dense_gate_up_swiglu: fused_weight must be [2 * inner, hidden]")
+    _dense(x, BF16, "x")
+    _dense(fused_weight, BF16, "fused_weight")
+    _require(on_rocm(x, fused_weight), "dense_gate_up_swiglu: tensors must share one ROCm device")
+    rows, hidden = fused_weight.shape
+    out = _out(out, x, (rows // 2,), BF16, "out")
+    call("omnia_dense_gate_up_swiglu", x.data_ptr(), fused_weight.data_ptr(), hidden, rows // 2,
+         out.data_ptr(), _stream(x))
+    return out
+
+
+def dense_down_residual(
+    activated: torch.Tensor,
+    down_weight: torch.Tensor,
+    residual: torch.Tensor,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The activation down-projected with the residual added; see
+    `omnia_dense_down_residual`. activated [inner] bf16, down_weight [hidden, inner] bf16,
+    residual [hidden] bf16 -> [hidden] bf16."""
+    _require(down_weight.dim() == 2, "dense_down_residual: down_weight must be [hidden, inner]")
+    hidden, inner = down_weight.shape
+    _require(activated.numel() == inner, "dense_down_residual: activated must hold inner values")
+    _require(residual.numel() == hidden, "dense_down_residual: residual must hold hidden values")
+    _dense(activated, BF16, "activated")
+    _dense(down_weight, BF16, "down_weight")
+    _dense(residual, BF16, "residual")
+    _require(on_rocm(activated, down_weight, residual),
+             "dense_down_residual: tensors must share one ROCm device")
+    out = _out(out, activated, (hidden,), BF16, "out")
+    call("omnia_dense_down_residual", activated.data_ptr(), down_weight.data_ptr(),
+         residual.data_ptr(), hidden, inner, out.data_ptr(), _stream(activated))
+    return out

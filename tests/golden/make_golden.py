@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent.parent))
 
-from oracle import activations, add_norm, embed, moe, rope, route  # noqa: E402
+from oracle import activations, add_norm, embed, mlp, moe, rope, route  # noqa: E402
 from oracle.bf16 import from_float  # noqa: E402
 
 
@@ -99,8 +99,21 @@ def make_moe() -> dict[str, np.ndarray]:
                 weights=weights, residual=residual, act=act, out=out)
 
 
+def make_mlp() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(7)
+    hidden, inner = 128, 192
+    x = from_float(rng.standard_normal(hidden))
+    fused_weight = from_float(0.1 * rng.standard_normal((2 * inner, hidden)))
+    down_weight = from_float(0.05 * rng.standard_normal((hidden, inner)))
+    residual = from_float(rng.standard_normal(hidden))
+    act = mlp.gate_up_swiglu(x, fused_weight)
+    out = mlp.down_residual(act, down_weight, residual)
+    return dict(x=x, fused_weight=fused_weight, down_weight=down_weight, residual=residual,
+                act=act, out=out)
+
+
 MAKERS = {"add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed,
-          "activations": make_activations, "route": make_route, "moe": make_moe}
+          "activations": make_activations, "route": make_route, "moe": make_moe, "mlp": make_mlp}
 
 
 def main(names: list[str]) -> None:

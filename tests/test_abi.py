@@ -55,6 +55,12 @@ def test_argument_errors_come_back_as_codes(lib):
     assert rc == -22
     assert "hidden" in lib_module.last_error()
     assert lib.omnia_add_rms_norm(None, None, None, None, None, 0, 2560, 1e-6, None) == 0
+    assert lib.omnia_dense_gate_up_swiglu(None, None, 12, 8, None, None) == -22
+    assert "hidden" in lib_module.last_error()
+    assert lib.omnia_dense_gate_up_swiglu(None, None, 8200, 8, None, None) == -22
+    assert lib.omnia_dense_down_residual(None, None, None, 8, 12, None, None) == -22
+    assert "inner" in lib_module.last_error()
+    assert lib.omnia_moe_down_combine(None, None, 4, 8, 2056, None, None, 1, None, None, None) == -22
 
 
 def test_router_pack_size_is_pure(lib):

@@ -297,3 +297,63 @@ def test_ordinal_routing_keeps_the_best_keys_lowest_index_first():
 
     keys = torch.tensor([5, 2, 9, 2, 0, 7], dtype=torch.int32)
     assert OrdinalRouting(3).indices(keys).tolist() == [4, 1, 3]
+
+
+# ---- dense SwiGLU MLP ---------------------------------------------------------------
+
+
+def test_mlp_predicates():
+    from mlx_omnia_amd.kernels.mlp import dense_down_residual_applies, dense_gate_up_swiglu_applies
+
+    assert dense_gate_up_swiglu_applies(2560, 9728) and dense_gate_up_swiglu_applies(8192, 8)
+    assert not dense_gate_up_swiglu_applies(8200, 64) and not dense_gate_up_swiglu_applies(100, 64)
+    assert dense_down_residual_applies(2560, 9728) and dense_down_residual_applies(16, 25600)
+    assert not dense_down_residual_applies(2560, 100)
+
+
+def test_mlp_cpu_resolves_to_core_and_matches_oracle():
+    from mlx_omnia_amd.kernels.leaf import SwiGLU
+    from mlx_omnia_amd.kernels.mlp import DefaultMlp, HipDenseMlp, Mlp
+    from oracle import mlp as oracle_mlp
+
+    hidden, inner = 128, 256
+    rng = np.random.default_rng(12)
+    fused = from_float(0.1 * rng.standard_normal((2 * inner, hidden)))
+    down = from_float(0.05 * rng.standard_normal((hidden, inner)))
+    leaf = SwiGLU(hidden, inner).to(torch.bfloat16)
+    with torch.no_grad():
+        leaf.gate_up_proj.weight.copy_(cpu(fused))
+        leaf.down_proj.weight.copy_(cpu(down))
+    mlp = Mlp(leaf, hidden=hidden, inner=inner)
+    assert isinstance(mlp.strategy, DefaultMlp)
+    assert HipDenseMlp.build(leaf, hidden=hidden, inner=inner, activation="silu") is None  # CPU
+    assert isinstance(Mlp(leaf, hidden=hidden, inner=inner, activation="gelu_tanh").strategy, DefaultMlp)
+    x = from_float(rng.standard_normal(hidden))
+    residual = from_float(rng.standard_normal(hidden))
+    with torch.no_grad():
+        out = mlp(cpu(x), cpu(residual))
+    # The Core chain rounds at the op boundaries of torch's bf16 ops (silu in one op, not
+    # the kernel's bf16 steps): the same MLP, not the same bits (the reference's own
+    # facade test, tests/test_kernel_dense_mlp.py:104-122, bounds it at 2^-5).
+    want = to_f32(oracle_mlp.mlp(x, fused, down, residual))
+    got = out.float().numpy()
+    assert np.abs(got - want).max() / np.abs(want).max() < 2.0**-5
+
+
+def test_mlp_hip_binding_declines_other_leaves():
+    from mlx_omnia_amd.kernels.leaf import SwiGLU
+    from mlx_omnia_amd.kernels.mlp import HipDenseMlp
+
+    leaf = SwiGLU(64, 32)  # fp32 weights
+    assert HipDenseMlp.build(leaf, hidden=64, inner=32, activation="silu") is None
+    leaf = leaf.to(torch.bfloat16)
+    assert HipDenseMlp.build(leaf, hidden=64, inner=32, activation="gelu_tanh") is None
+    assert HipDenseMlp.build(leaf, hidden=64, inner=16, activation="silu") is None  # shape
+
+    class Quantized(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate_up_proj = torch.nn.Identity()
+            self.down_proj = torch.nn.Identity()
+
+    assert HipDenseMlp.build(Quantized(), hidden=64, inner=32, activation="silu") is None
