@@ -377,6 +377,55 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.dense_down_residual(a["act"], a["w"], a["r"], out=a["o"]),
     ))
 
+    # Decode attention over a KV cache at Qwen3-4B's geometry (32 query heads over 8 kv
+    # heads, head_dim 128, full rotary): the step at position 32767 of a 32768-row fixed
+    # cache (134 MB of keys and values read) and at position 4095 of a 4096-row one.
+    att_h, att_kv, att_d, att_p = 32, 8, 128, 64
+
+    def setup_attention(device, copies, rows):
+        rng = np.random.default_rng(12)
+        gen = torch.Generator(device=device).manual_seed(13)
+        inv = np.exp(-np.log(1e6) * np.arange(att_p) / att_p)
+        theta = np.arange(rows)[:, None] * inv[None, :]
+        atlas = torch.from_numpy(np.concatenate([np.cos(theta), np.sin(theta)], axis=1).astype(np.float32)).to(device)
+        position = torch.tensor([rows - 1], dtype=torch.int32, device=device)
+        workspace = torch.empty(ops.attention_workspace_bytes(att_h, att_kv, att_d, rows),
+                                dtype=torch.uint8, device=device)
+        sets = []
+        for _ in range(copies):
+            shape = (att_kv, rows, att_d)
+            entry = dict(kc=torch.randn(shape, generator=gen, device=device).to(torch.bfloat16),
+                         vc=torch.randn(shape, generator=gen, device=device).to(torch.bfloat16),
+                         q=_to_bf16_device(_normal(rng, (att_h * att_d,)), device),
+                         k=_to_bf16_device(_normal(rng, (att_kv * att_d,)), device),
+                         v=_to_bf16_device(_normal(rng, (att_kv * att_d,)), device),
+                         qw=_to_bf16_device(_normal(rng, (att_d,), 0.1, 1.0), device),
+                         kw=_to_bf16_device(_normal(rng, (att_d,), 0.1, 1.0), device),
+                         atlas=atlas, pos=position, ws=workspace, rows=rows)
+            entry["o"] = torch.empty((att_h, att_d), dtype=torch.bfloat16, device=device)
+            sets.append(entry)
+        return sets
+
+    def attention_bytes(rows):
+        # K and V rows attended (the written row included), q/k/v in, context out, the new
+        # K/V row written, norm weights and the angle row.
+        return (2 * att_kv * rows * att_d * 2 + (att_h + 2 * att_kv) * att_d * 2
+                + att_h * att_d * 2 + 2 * att_kv * att_d * 2 + 2 * att_d * 2 + 2 * att_p * 4)
+
+    for rows, tag in ((32768, "32k"), (4096, "4k")):
+        out.append(Workload(
+            name=f"attention_decode_{tag}",
+            kernel="attention_split_kernel",
+            description=f"decode step: q [32x128], k, v [8x128] bf16, norm + rope + cache write, "
+                        f"attention over {rows} cached rows [8, {rows}, 128] bf16 (Qwen3-4B geometry)",
+            bytes_per_launch=attention_bytes(rows),
+            setup=lambda device, copies, rows=rows: setup_attention(device, copies, rows),
+            launch=lambda a: ops.attention_decode(
+                a["q"], a["k"], a["v"], a["qw"], a["kw"], a["atlas"], a["kc"], a["vc"], a["pos"],
+                heads=att_h, kv_heads=att_kv, max_rows=a["rows"], scale=att_d ** -0.5, eps=1e-6,
+                workspace=a["ws"], out=a["o"]),
+        ))
+
     # Not a product kernel: a plain device-to-device copy of known size, the scale for
     # the FETCH_SIZE / WRITE_SIZE counters (run with --only copy_calibration).
     def setup_copy(device, copies, elements=64 * 2**20):

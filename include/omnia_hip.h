@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 4
+#define OMNIA_ABI_VERSION 5
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -235,6 +235,43 @@ int32_t omnia_dense_gate_up_swiglu(const uint16_t* x, const uint16_t* fused_weig
 int32_t omnia_dense_down_residual(const uint16_t* activated, const uint16_t* down_weight,
                                   const uint16_t* residual, int64_t hidden, int64_t inner,
                                   uint16_t* out, hipStream_t stream);
+
+/* Workspace bytes omnia_attention_decode needs for a cache of `capacity` rows (the
+ * per-chunk softmax states of a long cache). Pure; touches no device. -EINVAL for a
+ * geometry the kernel does not serve. */
+int64_t omnia_attention_workspace_bytes(int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                        int64_t capacity);
+
+/* One decode step of an attention layer over a KV cache, fused:
+ *   per head: n = bf16(w * bf16(x * inv)), inv = 1 / sqrt(sum x^2 / 128 + eps)
+ *   a, b = bf16(n_p * bf16(mscale)), bf16(n_{p+P} * bf16(mscale))       p < P = rotary_pairs
+ *   q_p = bf16(a cos - b sin), q_{p+P} = bf16(a sin + b cos), q_d = n_d for d >= 2P
+ *   (the same for the key row; cos || sin from row `position` of `angles` [angle_rows, 2P])
+ *   the new key and value rows written into the caches, then for every query head h
+ *   out[h] = bf16(sum_r softmax_r(scale * q_h . k_r) v_r) over the attended rows of kv
+ *   head h / (heads / kv_heads), softmax and sums in fp32.
+ * raw_queries [heads, 128], raw_keys / raw_values [kv_heads, 128], query_weight /
+ * key_weight [128] bf16; key_cache / value_cache [kv_heads, capacity, 128] bf16, written
+ * in place; position: one device int32, read and not advanced. window 0 (fixed cache):
+ * write row p, attend rows [0, p]; window == capacity (ring): write row p % window, attend
+ * rows [0, min(p + 1, window)). max_rows: an upper bound on the attended rows (sizes the
+ * grid; the host's position + 1, or capacity under graph capture). workspace: at least
+ * omnia_attention_workspace_bytes(heads, kv_heads, 128, capacity) bytes, 16-byte
+ * aligned (unused when max_rows <= 128). out [heads, 128] bf16.
+ * Replaces: core/kernels/attention/full.py:133-471,557-629 (`full_fused_attention`,
+ * FullAttentionStep at :632-740) and sliding.py:136-430,504-580 (`sliding_fused_attention`
+ * over a RingKVCache, SlidingAttentionStep at :583-691); Core chain
+ * core/kernels/attention/default.py:114-156.
+ * head_dim 128; heads / kv_heads in {1, 2, 4, 8}; rotary_pairs in {8, 16, 32, 64}. */
+int32_t omnia_attention_decode(const uint16_t* raw_queries, const uint16_t* raw_keys,
+                               const uint16_t* raw_values, const uint16_t* query_weight,
+                               const uint16_t* key_weight, const float* angles,
+                               int64_t angle_rows, int64_t rotary_pairs, float mscale,
+                               uint16_t* key_cache, uint16_t* value_cache, int64_t capacity,
+                               int64_t window, const int32_t* position, int64_t max_rows,
+                               int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
+                               float eps, void* workspace, int64_t workspace_bytes,
+                               uint16_t* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

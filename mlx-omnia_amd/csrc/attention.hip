@@ -1,0 +1,457 @@
+// One decode step of an attention layer over a KV cache: per-head RMSNorm of the new
+// query and key rows, the half-split rotation, the write of the new key/value row into
+// the cache, and the attention of every query head over the cache rows written so far.
+//
+// Arithmetic (core/kernels/attention/full.py:133-471, sliding.py:136-430 for the ring;
+// the Core chain core/kernels/attention/default.py:114-156):
+//   n      = bf16(w * bf16(x * inv)), inv = 1 / sqrt(sum x^2 / 128 + eps)   per head
+//   a, b   = bf16(n_p * bf16(mscale)), bf16(n_{p+P} * bf16(mscale))         p < P
+//   q_p    = bf16(a cos - b sin), q_{p+P} = bf16(a sin + b cos), the tail n_d (d >= 2P)
+//   the same for the new key row; the value row is stored as given;
+//   s_r    = scale * (q . k_r),  o = sum_r softmax(s)_r v_r  over the attended rows,
+//   scores, softmax and accumulators in fp32; the context rounds to bf16 once.
+//
+// Cache geometry. key_cache / value_cache are [kv_heads, capacity, 128] bf16. The step's
+// position p is read on the device (so a captured graph replays it), and decides:
+//   fixed cache (window 0):  write row p, attend rows [0, p]
+//   ring (window = capacity): write row p % window, attend rows [0, min(p + 1, window))
+// `max_rows` bounds the attended rows; it sizes the grid.
+//
+// Layout. A workgroup (4 waves) owns one kv head and one chunk of cache rows, a multiple
+// of 128; all `gqa` query heads of that kv head attend through it, so every key and value
+// byte is read once per step. A wave walks blocks of 32 rows: lane c of each 16-lane DPP
+// row holds elements [8c, 8c + 8) of a head (one 16-byte load), and the wave's four DPP
+// rows take rows 4j + 0..3, so one load instruction reads 1 KiB of contiguous cache.
+// Scores are packed bf16 dot products (v_dot2_f32_bf16) summed across the DPP row; each
+// DPP row keeps its own online softmax (running max, sum and its slice of the context).
+// The four DPP rows merge through permlane swaps, the four waves through LDS. With one
+// chunk the workgroup writes the context; with several it writes (max, sum, context) to
+// the workspace and a second kernel merges the chunks of each query head.
+//
+// The chunk holding the write row computes the new key row itself and reads that row
+// from LDS, never from the cache line it has just written.
+#include "common.hpp"
+#include "host.hpp"
+
+namespace omnia {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kWaves = 4;
+constexpr int kBlockRows = 32;                        // rows per wave iteration
+constexpr int kChunkUnit = kWaves * kBlockRows;       // a chunk is a multiple of 128 rows
+constexpr int kPartial = kD + 2;                      // context slice, max, sum
+constexpr int kTargetGroups = 512;                    // workgroups a long cache is split into
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+  const uint16_t* raw_q;      // [heads, 128]
+  const uint16_t* raw_k;      // [kv_heads, 128]
+  const uint16_t* raw_v;      // [kv_heads, 128]
+  const uint16_t* q_weight;   // [128]
+  const uint16_t* k_weight;   // [128]
+  const float* angles;        // [angle_rows, 2 * pairs]: cos || sin per position
+  uint16_t* k_cache;          // [kv_heads, capacity, 128]
+  uint16_t* v_cache;
+  const int32_t* position;
+  float* partial;             // [kv_heads, splits, gqa, kPartial]
+  uint16_t* out;              // [heads, 128]
+  int angle_rows;
+  int pairs;
+  float mscale;
+  int capacity;
+  int window;                 // 0: fixed cache
+  int max_rows;
+  int kv_heads;
+  float scale_log2;           // scale * log2(e)
+  float eps;
+  int chunk;                  // rows per workgroup
+  int splits;                 // chunks per kv head
+};
+
+struct StepRows {
+  int position;
+  int write;                  // the row the new key/value land in, or -1
+  int count;                  // rows [0, count) are attended
+};
+
+__device__ __forceinline__ StepRows step_rows(const AttnArgs& a) {
+  StepRows r;
+  r.position = *a.position;
+  if (r.position < 0) {
+    r.write = -1;
+    r.count = 0;
+  } else if (a.window > 0) {
+    r.write = r.position % a.window;
+    r.count = min(r.position + 1, a.window);
+  } else {
+    r.write = r.position < a.capacity ? r.position : -1;
+    r.count = min(r.position + 1, a.capacity);
+  }
+  r.count = min(r.count, a.max_rows);
+  if (r.write >= r.count) r.write = -1;
+  return r;
+}
+
+__device__ __forceinline__ float row16_fsum(float v) {
+  v += __uint_as_float(dpp<kRowRor8>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowRor4>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowRor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowRor1>(__float_as_uint(v)));
+  return v;
+}
+
+// Merge two online-softmax states (running max m, sum l, context slice o). Both lanes of
+// a swap pair call it with the same (lower, upper) order, so they end bit-identical.
+template <int N>
+__device__ __forceinline__ void merge_state(float& m, float& l, float (&o)[N], float m2,
+                                            float l2, const float (&o2)[N]) {
+  const float mx = fmaxf(m, m2);
+  const float f1 = m == mx ? 1.0f : exp2f(m - mx);
+  const float f2 = m2 == mx ? 1.0f : exp2f(m2 - mx);
+  m = mx;
+  l = l * f1 + l2 * f2;
+#pragma unroll
+  for (int e = 0; e < N; ++e) o[e] = o[e] * f1 + o2[e] * f2;
+}
+
+// RMSNorm + rotation of one 128-wide head row by a 16-lane DPP row: lane c holds elements
+// [8c, 8c + 8). Returns the bf16 result (already rounded) in `out`. Every lane of the row
+// must call it (the rotation partner comes by a lane shuffle).
+__device__ __forceinline__ void norm_rope_row(const uint16_t* raw, const uint16_t* weight,
+                                              const float* angle_row, int pairs, bool scaled,
+                                              float mscale_bf, float eps, int c, float out[8]) {
+  float x[8], w[8];
+  unpack8(*reinterpret_cast<const u32x4*>(raw + 8 * c), x);
+  unpack8(*reinterpret_cast<const u32x4*>(weight + 8 * c), w);
+  double sumsq = 0.0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sumsq += static_cast<double>(x[j] * x[j]);
+  sumsq = row16_sum(sumsq);
+  const float inv = 1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(kD) + eps);
+  float n[8];
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    float a0 = x[j] * inv, a1 = x[j + 1] * inv;
+    round_pair(a0, a1);
+    n[j] = w[j] * a0;
+    n[j + 1] = w[j + 1] * a1;
+    round_pair(n[j], n[j + 1]);
+  }
+  const int lanes = pairs / 8;        // lanes per rotated half (a power of two <= 8)
+  const bool rotated = c < 2 * lanes;
+  if (scaled && rotated) {
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      n[j] *= mscale_bf;
+      n[j + 1] *= mscale_bf;
+      round_pair(n[j], n[j + 1]);
+    }
+  }
+  float partner[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) partner[j] = __shfl_xor(n[j], lanes, kWave);
+  if (!rotated) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] = n[j];
+    return;
+  }
+  const bool first_half = c < lanes;
+  const int p0 = 8 * (first_half ? c : c - lanes);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float cs = angle_row[p0 + j];
+    const float sn = angle_row[pairs + p0 + j];
+    // a: the first-half value of the pair, b: the second-half one.
+    const float av = first_half ? n[j] : partner[j];
+    const float bv = first_half ? partner[j] : n[j];
+    out[j] = first_half ? av * cs - bv * sn : av * sn + bv * cs;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) round_pair(out[j], out[j + 1]);
+}
+
+// Eight bf16 products of a lane's slices, accumulated in fp32 by four v_dot2 steps. The
+// whole 16-byte vector is reinterpreted at once: a bit cast of one ext-vector element
+// (`k.y`) is compiled by this toolchain as a cast of element 0.
+__device__ __forceinline__ float dot8_bf16(const u32x4& k, const u32x4& q) {
+  const bf16x8 kb = __builtin_bit_cast(bf16x8, k);
+  const bf16x8 qb = __builtin_bit_cast(bf16x8, q);
+  float acc = 0.0f;
+  acc = __builtin_amdgcn_fdot2_f32_bf16(kb.s01, qb.s01, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(kb.s23, qb.s23, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(kb.s45, qb.s45, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(kb.s67, qb.s67, acc, false);
+  return acc;
+}
+
+template <int GQA, bool SCALED>
+__global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArgs a) {
+  __shared__ u32x4 q_lds[GQA][16];      // the roped queries, bf16 pairs
+  __shared__ u32x4 kv_lds[2][16];       // the new key and value rows
+  __shared__ float merge_lds[kWaves][GQA][kPartial];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int drow = lane / 16;           // DPP row of the lane
+  const int c = lane % 16;              // 8-element slice of a head
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const StepRows rows = step_rows(a);
+  const int c0 = split * a.chunk;
+  if (c0 >= rows.count) return;         // whole workgroup, before any barrier
+  const int c1 = min(c0 + a.chunk, rows.count);
+  const bool writer = rows.write >= c0 && rows.write < c1;
+
+  // Prologue: item i = wave * 4 + drow; items [0, GQA) are the query heads, GQA the new
+  // key row, GQA + 1 the new value row (both only in the chunk holding the write row).
+  {
+    const int item = wave * 4 + drow;
+    const int arow = min(rows.position, a.angle_rows - 1);
+    const float* angle_row = a.angles + static_cast<int64_t>(arow) * 2 * a.pairs;
+    const float mscale_bf = round_bf16(a.mscale);
+    if (item < GQA || (item == GQA && writer)) {
+      const bool is_q = item < GQA;
+      const uint16_t* raw = is_q ? a.raw_q + static_cast<int64_t>(kvh * GQA + item) * kD
+                                 : a.raw_k + static_cast<int64_t>(kvh) * kD;
+      float r[8];
+      norm_rope_row(raw, is_q ? a.q_weight : a.k_weight, angle_row, a.pairs, SCALED,
+                    mscale_bf, a.eps, c, r);
+      const u32x4 packed = pack8(r);
+      if (is_q) {
+        q_lds[item][c] = packed;
+      } else {
+        kv_lds[0][c] = packed;
+        *reinterpret_cast<u32x4*>(a.k_cache + (static_cast<int64_t>(kvh) * a.capacity + rows.write) * kD + 8 * c) = packed;
+      }
+    } else if (item == GQA + 1 && writer) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(a.raw_v + static_cast<int64_t>(kvh) * kD + 8 * c);
+      kv_lds[1][c] = v;
+      *reinterpret_cast<u32x4*>(a.v_cache + (static_cast<int64_t>(kvh) * a.capacity + rows.write) * kD + 8 * c) = v;
+    }
+  }
+  __syncthreads();
+
+  u32x4 q[GQA];
+#pragma unroll
+  for (int g = 0; g < GQA; ++g) q[g] = q_lds[g][c];
+
+  float m[GQA], l[GQA], o[GQA][8];
+#pragma unroll
+  for (int g = 0; g < GQA; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+  }
+
+  const int64_t head_base = static_cast<int64_t>(kvh) * a.capacity;
+  for (int b0 = c0 + wave * kBlockRows; b0 < c1; b0 += kWaves * kBlockRows) {
+    u32x4 kv[8], vv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = b0 + 4 * j + drow;
+      kv[j] = vv[j] = u32x4{0u, 0u, 0u, 0u};
+      if (r < c1) {
+        if (r == rows.write) {
+          kv[j] = kv_lds[0][c];
+          vv[j] = kv_lds[1][c];
+        } else {
+          const int64_t off = (head_base + r) * kD + 8 * c;
+          kv[j] = load_nt(reinterpret_cast<const u32x4*>(a.k_cache + off));
+          vv[j] = load_nt(reinterpret_cast<const u32x4*>(a.v_cache + off));
+        }
+      }
+    }
+    float vf[8][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) unpack8(vv[j], vf[j]);
+#pragma unroll
+    for (int g = 0; g < GQA; ++g) {
+      float s[8];
+      float block_max = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float dot = row16_fsum(dot8_bf16(kv[j], q[g]));
+        s[j] = b0 + 4 * j + drow < c1 ? dot * a.scale_log2 : -INFINITY;
+        block_max = fmaxf(block_max, s[j]);
+      }
+      const float mx = fmaxf(m[g], block_max);
+      const float f = m[g] == mx ? 1.0f : exp2f(m[g] - mx);
+      m[g] = mx;
+      l[g] *= f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] *= f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = s[j] == -INFINITY ? 0.0f : exp2f(s[j] - mx);
+        l[g] += p;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] = __builtin_fmaf(p, vf[j][e], o[g][e]);
+      }
+    }
+  }
+
+  // Merge the four DPP rows of the wave (rows 0-1 and 2-3, then the halves).
+#pragma unroll
+  for (int g = 0; g < GQA; ++g) {
+#pragma unroll
+    for (int step = 0; step < 2; ++step) {
+      uint32_t lo, hi;
+      float m2, l2, o2[8], mlo, llo, olo[8];
+      if (step == 0) row_pair(__float_as_uint(m[g]), lo, hi); else half_pair(__float_as_uint(m[g]), lo, hi);
+      mlo = __uint_as_float(lo); m2 = __uint_as_float(hi);
+      if (step == 0) row_pair(__float_as_uint(l[g]), lo, hi); else half_pair(__float_as_uint(l[g]), lo, hi);
+      llo = __uint_as_float(lo); l2 = __uint_as_float(hi);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (step == 0) row_pair(__float_as_uint(o[g][e]), lo, hi); else half_pair(__float_as_uint(o[g][e]), lo, hi);
+        olo[e] = __uint_as_float(lo);
+        o2[e] = __uint_as_float(hi);
+      }
+      merge_state(mlo, llo, olo, m2, l2, o2);
+      m[g] = mlo;
+      l[g] = llo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] = olo[e];
+    }
+    if (drow == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) merge_lds[wave][g][8 * c + e] = o[g][e];
+      if (c == 0) {
+        merge_lds[wave][g][kD] = m[g];
+        merge_lds[wave][g][kD + 1] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Merge the four waves (in wave order) and emit: thread t serves elements of the heads.
+  for (int idx = threadIdx.x; idx < GQA * kD; idx += kWaves * kWave) {
+    const int g = idx / kD;
+    const int e = idx % kD;
+    float mm = merge_lds[0][g][kD], ll = merge_lds[0][g][kD + 1];
+    float oo[1] = {merge_lds[0][g][e]};
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      const float o2[1] = {merge_lds[w][g][e]};
+      merge_state(mm, ll, oo, merge_lds[w][g][kD], merge_lds[w][g][kD + 1], o2);
+    }
+    if (a.splits == 1) {
+      const float value = ll == 0.0f ? oo[0] : oo[0] / ll;
+      a.out[static_cast<int64_t>(kvh * GQA + g) * kD + e] = f32_to_bf16(value);
+    } else {
+      float* slot = a.partial + ((static_cast<int64_t>(kvh) * a.splits + split) * GQA + g) * kPartial;
+      slot[e] = oo[0];
+      if (e == 0) {
+        slot[kD] = mm;
+        slot[kD + 1] = ll;
+      }
+    }
+  }
+}
+
+// One wave per query head: merge the chunks' states in chunk order, then normalise.
+template <int GQA>
+__global__ __launch_bounds__(kWave) void attention_combine_kernel(AttnArgs a) {
+  const int head = blockIdx.x;
+  const int kvh = head / GQA;
+  const int g = head % GQA;
+  const int lane = threadIdx.x;
+  const StepRows rows = step_rows(a);
+  const int used = min(a.splits, (rows.count + a.chunk - 1) / a.chunk);
+  float m = -INFINITY, l = 0.0f, o[2] = {0.0f, 0.0f};
+  for (int s = 0; s < used; ++s) {
+    const float* slot = a.partial + ((static_cast<int64_t>(kvh) * a.splits + s) * GQA + g) * kPartial;
+    const float o2[2] = {slot[2 * lane], slot[2 * lane + 1]};
+    merge_state(m, l, o, slot[kD], slot[kD + 1], o2);
+  }
+  float v0 = l == 0.0f ? o[0] : o[0] / l;
+  float v1 = l == 0.0f ? o[1] : o[1] / l;
+  reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(head) * kD)[lane] = pack_bf16(v0, v1);
+}
+
+int chunk_rows(int max_rows, int kv_heads) {
+  const int per_head = (kTargetGroups + kv_heads - 1) / kv_heads;
+  int chunk = (max_rows + per_head - 1) / per_head;
+  chunk = (chunk + kChunkUnit - 1) / kChunkUnit * kChunkUnit;
+  return chunk < kChunkUnit ? kChunkUnit : chunk;
+}
+
+template <int GQA>
+void launch(const AttnArgs& a, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(a.splits), static_cast<unsigned>(a.kv_heads));
+  if (a.mscale != 1.0f) {
+    attention_split_kernel<GQA, true><<<grid, kWaves * kWave, 0, stream>>>(a);
+  } else {
+    attention_split_kernel<GQA, false><<<grid, kWaves * kWave, 0, stream>>>(a);
+  }
+  if (a.splits > 1) {
+    attention_combine_kernel<GQA><<<dim3(static_cast<unsigned>(a.kv_heads * GQA)), kWave, 0, stream>>>(a);
+  }
+}
+
+}  // namespace
+}  // namespace omnia
+
+extern "C" int64_t omnia_attention_workspace_bytes(int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                                   int64_t capacity) {
+  using namespace omnia;
+  if (heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || head_dim != kD || capacity <= 0) {
+    return -EINVAL;
+  }
+  const int64_t splits = (capacity + kChunkUnit - 1) / kChunkUnit;
+  return kv_heads * splits * (heads / kv_heads) * kPartial * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int32_t omnia_attention_decode(
+    const uint16_t* raw_queries, const uint16_t* raw_keys, const uint16_t* raw_values,
+    const uint16_t* query_weight, const uint16_t* key_weight, const float* angles,
+    int64_t angle_rows, int64_t rotary_pairs, float mscale, uint16_t* key_cache,
+    uint16_t* value_cache, int64_t capacity, int64_t window, const int32_t* position,
+    int64_t max_rows, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale, float eps,
+    void* workspace, int64_t workspace_bytes, uint16_t* out, hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(head_dim == kD, "attention_decode: head_dim must be 128");
+  OMNIA_REQUIRE(kv_heads > 0 && heads > 0 && heads % kv_heads == 0,
+                "attention_decode: heads must be a positive multiple of kv_heads");
+  const int64_t gqa = heads / kv_heads;
+  OMNIA_REQUIRE(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8,
+                "attention_decode: heads / kv_heads must be 1, 2, 4 or 8");
+  OMNIA_REQUIRE(kv_heads <= 65535, "attention_decode: too many kv heads");
+  OMNIA_REQUIRE(rotary_pairs == 8 || rotary_pairs == 16 || rotary_pairs == 32 || rotary_pairs == 64,
+                "attention_decode: rotary_pairs must be 8, 16, 32 or 64");
+  OMNIA_REQUIRE(capacity > 0 && capacity < (int64_t{1} << 30), "attention_decode: bad capacity");
+  OMNIA_REQUIRE(window == 0 || window == capacity,
+                "attention_decode: a ring's window must be its capacity (0: fixed cache)");
+  OMNIA_REQUIRE(max_rows > 0 && max_rows <= capacity, "attention_decode: max_rows must be in [1, capacity]");
+  OMNIA_REQUIRE(angle_rows > 0 && angle_rows < (int64_t{1} << 30), "attention_decode: bad angle_rows");
+  OMNIA_REQUIRE(raw_queries && raw_keys && raw_values && query_weight && key_weight && angles &&
+                key_cache && value_cache && position && out, "attention_decode: null pointer");
+  OMNIA_REQUIRE(aligned16(raw_queries) && aligned16(raw_keys) && aligned16(raw_values) &&
+                aligned16(query_weight) && aligned16(key_weight) && aligned16(key_cache) &&
+                aligned16(value_cache) && aligned16(out),
+                "attention_decode: bf16 rows must be 16-byte aligned");
+  const int chunk = chunk_rows(static_cast<int>(max_rows), static_cast<int>(kv_heads));
+  const int splits = static_cast<int>((max_rows + chunk - 1) / chunk);
+  if (splits > 1) {
+    const int64_t need = kv_heads * splits * gqa * kPartial * static_cast<int64_t>(sizeof(float));
+    OMNIA_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+                  "attention_decode: workspace smaller than omnia_attention_workspace_bytes()");
+    OMNIA_REQUIRE(aligned16(workspace), "attention_decode: workspace must be 16-byte aligned");
+  }
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  AttnArgs a{raw_queries, raw_keys, raw_values, query_weight, key_weight, angles, key_cache,
+             value_cache, position, static_cast<float*>(workspace), out,
+             static_cast<int>(angle_rows), static_cast<int>(rotary_pairs), mscale,
+             static_cast<int>(capacity), static_cast<int>(window), static_cast<int>(max_rows),
+             static_cast<int>(kv_heads), scale * kLog2e, eps, chunk, splits};
+  switch (gqa) {
+    case 1: launch<1>(a, stream); break;
+    case 2: launch<2>(a, stream); break;
+    case 4: launch<4>(a, stream); break;
+    default: launch<8>(a, stream); break;
+  }
+  return launched("attention_decode");
+}

@@ -47,7 +47,6 @@
 namespace omnia {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kTileTokens = 16;   // MFMA M
 constexpr int kWaves = 16;        // one row per wave in phases 1 and 3

@@ -1,0 +1,218 @@
+"""The T=1 attention step over a KV cache: raw q/k/v projections in, context out.
+
+Mirrors core/kernels/attention/__init__.py and kernel.py (`AttentionStep`,
+`AttentionStepStrategy`): the declaration carries the cache, the head geometry, the norm
+gains, the rotary geometry (an angle table) and the sink logits; the first strategy
+whose `build` accepts it serves the layer.
+
+- `HipAttentionStep` (`omnia_attention_decode`, csrc/attention.hip) serves what the
+  reference's `FullAttentionStep` (a fixed cache, core/kernels/attention/full.py:632-740)
+  and `SlidingAttentionStep` (a ring, sliding.py:583-691) serve: bf16, head_dim 128,
+  q/k norm gains, a rotary table, no sinks; one fused step that writes the new K/V row
+  into the cache and reads the position on the device. A prefill (T != 1) goes to the
+  Core chain, as in the reference.
+- `DefaultAttentionStep` is the Core chain (core/kernels/attention/default.py:85-156): the
+  norms, the rotation, `cache.update_and_fetch` and attention in torch ops (fp32). It
+  accepts everything, sinks included.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Protocol, runtime_checkable
+
+import torch
+
+from ...runtime import ops
+from .._device import hip_device
+from ..qkv_rope.kernel import AngleTable
+from ..resolve import resolve
+from .cache import FixedKVCache, RingKVCache
+
+__all__ = ["AttentionStep", "AttentionStepStrategy", "DefaultAttentionStep", "FixedKVCache",
+           "HipAttentionStep", "RingKVCache", "attention_step_applies"]
+
+HEAD_DIM = 128
+
+
+@runtime_checkable
+class AttentionStepStrategy(Protocol):
+    def __call__(self, raw_queries: torch.Tensor, raw_keys: torch.Tensor,
+                 raw_values: torch.Tensor, mask=None) -> torch.Tensor: ...
+
+
+def attention_step_applies(heads: int, kv_heads: int, head_dim: int, rotary_pairs: int) -> bool:
+    """head_dim 128 (a 16-lane row holds a head); grouped queries 1, 2, 4 or 8 per kv head;
+    the rotated half a power-of-two number of 8-element lane slices."""
+    if head_dim != HEAD_DIM or kv_heads <= 0 or heads % kv_heads != 0:
+        return False
+    return heads // kv_heads in (1, 2, 4, 8) and rotary_pairs in (8, 16, 32, 64)
+
+
+def _split_heads(raw: torch.Tensor, count: int, head_dim: int) -> torch.Tensor:
+    """[1, T, count * D] -> [1, count, T, D] (default.py:28-31)."""
+    return raw.reshape(1, raw.shape[1], count, head_dim).transpose(1, 2)
+
+
+def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """bf16(w * bf16(x * inv)), inv in fp32 (the fused kernels' rounding points)."""
+    xf = x.float()
+    inv = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (weight.float() * (xf * inv).to(x.dtype).float()).to(x.dtype)
+
+
+def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pairs: int,
+            mscale: float) -> torch.Tensor:
+    """Half-split rotation of the first 2P dims with the folded mscale; tail untouched."""
+    factor = torch.tensor(mscale, dtype=x.dtype).float()
+    a = (x[..., :pairs].float() * factor).to(x.dtype).float()
+    b = (x[..., pairs : 2 * pairs].float() * factor).to(x.dtype).float()
+    rotated = torch.cat([a * cos - b * sin, a * sin + b * cos], dim=-1).to(x.dtype)
+    return torch.cat([rotated, x[..., 2 * pairs :]], dim=-1)
+
+
+@dataclass(frozen=True)
+class DefaultAttentionStep(AttentionStepStrategy):
+    cache: FixedKVCache
+    heads: int
+    kv_heads: int
+    head_dim: int
+    scale: float
+    query_weight: torch.Tensor | None
+    key_weight: torch.Tensor | None
+    eps: float
+    rotary_pairs: int
+    mscale: float
+    angles: AngleTable | None
+    base: float
+    sinks: torch.Tensor | None
+
+    @classmethod
+    def build(cls, cache, *, heads, kv_heads, head_dim, scale, dtype, query_weight, key_weight,
+              eps, rotary_pairs, mscale, angles, base, sinks) -> "DefaultAttentionStep":
+        return cls(cache, heads, kv_heads, head_dim, scale, query_weight, key_weight, eps,
+                   rotary_pairs, mscale, angles, base, sinks)
+
+    def _angles(self, offset: int, length: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+        pairs = self.rotary_pairs
+        if self.angles is not None:
+            row = self.angles(offset, length).to(device=device, dtype=torch.float32)
+            return row[:, :pairs], row[:, pairs : 2 * pairs]
+        index = torch.arange(pairs, dtype=torch.float64, device=device)
+        positions = torch.arange(offset, offset + length, dtype=torch.float64, device=device)
+        theta = positions[:, None] * torch.exp(-torch.log(torch.tensor(self.base, dtype=torch.float64)) * index / pairs)
+        return torch.cos(theta).float(), torch.sin(theta).float()
+
+    def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
+        position = self.cache.offset
+        length = raw_queries.shape[1]
+        q = _split_heads(raw_queries, self.heads, self.head_dim)
+        k = _split_heads(raw_keys, self.kv_heads, self.head_dim)
+        v = _split_heads(raw_values, self.kv_heads, self.head_dim)
+        if self.query_weight is not None:
+            q = _rms_norm(q, self.query_weight, self.eps)
+        if self.key_weight is not None:
+            k = _rms_norm(k, self.key_weight, self.eps)
+        if self.rotary_pairs:
+            cos, sin = self._angles(position, length, q.device)
+            q = _rotate(q, cos, sin, self.rotary_pairs, self.mscale)
+            k = _rotate(k, cos, sin, self.rotary_pairs, self.mscale)
+        keys, values = self.cache.update_and_fetch(k, v)
+        gqa = self.heads // self.kv_heads
+        kf = keys.float().repeat_interleave(gqa, dim=1)
+        vf = values.float().repeat_interleave(gqa, dim=1)
+        scores = (q.float() @ kf.transpose(-1, -2).contiguous()) * self.scale
+        if mask is not None and not isinstance(mask, str):
+            scores = scores + mask.float()
+        if self.sinks is not None:
+            sink = self.sinks.float().reshape(1, -1, 1, 1).expand(*scores.shape[:-1], 1)
+            probs = torch.softmax(torch.cat([sink, scores], dim=-1), dim=-1)[..., 1:]
+        else:
+            probs = torch.softmax(scores, dim=-1)
+        return (probs @ vf).to(raw_queries.dtype)
+
+
+@dataclass(frozen=True)
+class HipAttentionStep(AttentionStepStrategy):
+    cache: FixedKVCache
+    heads: int
+    kv_heads: int
+    scale: float
+    eps: float
+    mscale: float
+    query_weight: torch.Tensor
+    key_weight: torch.Tensor
+    atlas: torch.Tensor
+    workspace: torch.Tensor
+    fallback: DefaultAttentionStep
+
+    @classmethod
+    def build(cls, cache, *, heads, kv_heads, head_dim, scale, dtype, query_weight, key_weight,
+              eps, rotary_pairs, mscale, angles, base, sinks) -> "HipAttentionStep | None":
+        if not isinstance(cache, FixedKVCache) or sinks is not None:
+            return None
+        if not isinstance(angles, AngleTable) or angles.pairs != rotary_pairs:
+            return None
+        if query_weight is None or key_weight is None:
+            return None
+        if dtype != torch.bfloat16 or not attention_step_applies(heads, kv_heads, head_dim, rotary_pairs):
+            return None
+        keys, values = cache.fetch()
+        if keys.dtype != torch.bfloat16 or keys.shape[1] != kv_heads or keys.shape[3] != head_dim:
+            return None
+        if not (keys.is_contiguous() and values.is_contiguous()):
+            return None
+        if query_weight.dtype != torch.bfloat16 or key_weight.dtype != torch.bfloat16:
+            return None
+        if not hip_device(keys, values, query_weight, key_weight, angles.cos, angles.sin):
+            return None
+        atlas = torch.cat([angles.cos, angles.sin], dim=-1).to(torch.float32).contiguous()
+        nbytes = ops.attention_workspace_bytes(heads, kv_heads, head_dim, keys.shape[2])
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=keys.device)
+        fallback = DefaultAttentionStep.build(
+            cache, heads=heads, kv_heads=kv_heads, head_dim=head_dim, scale=scale, dtype=dtype,
+            query_weight=query_weight, key_weight=key_weight, eps=eps, rotary_pairs=rotary_pairs,
+            mscale=mscale, angles=angles, base=base, sinks=sinks)
+        return cls(cache, heads, kv_heads, scale, eps, mscale, query_weight.contiguous(),
+                   key_weight.contiguous(), atlas, workspace, fallback)
+
+    def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
+        if raw_queries.shape[1] != 1:
+            return self.fallback(raw_queries, raw_keys, raw_values, mask)
+        cache = self.cache
+        if cache.window == 0 and cache.offset >= cache.capacity:
+            raise ValueError(f"cache of {cache.capacity} rows is full")
+        if cache.offset >= self.atlas.shape[0]:
+            raise ValueError(f"position {cache.offset} is past the angle table's {self.atlas.shape[0]} rows")
+        keys, values = cache.fetch()
+        max_rows = min(cache.offset + 1, cache.capacity)
+        out = ops.attention_decode(
+            raw_queries.contiguous(), raw_keys.contiguous(), raw_values.contiguous(),
+            self.query_weight, self.key_weight, self.atlas, keys, values, cache.position,
+            heads=self.heads, kv_heads=self.kv_heads, max_rows=max_rows, scale=self.scale,
+            eps=self.eps, mscale=self.mscale, window=cache.window, workspace=self.workspace)
+        cache.advance()
+        return out.reshape(1, self.heads, 1, HEAD_DIM)
+
+
+_STRATEGIES = (HipAttentionStep, DefaultAttentionStep)
+
+
+class AttentionStep(AttentionStepStrategy):
+    """Resolves the strategy at construction and delegates; bound to one cache."""
+
+    def __init__(self, cache, *, heads: int, kv_heads: int, head_dim: int, scale: float,
+                 dtype: torch.dtype, query_weight: torch.Tensor | None = None,
+                 key_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                 rotary_pairs: int = 0, mscale: float = 1.0, angles: AngleTable | None = None,
+                 base: float = 0.0, sinks: torch.Tensor | None = None,
+                 reference: bool = False) -> None:
+        self.strategy: AttentionStepStrategy = resolve(
+            (DefaultAttentionStep,) if reference else _STRATEGIES, cache, heads=heads,
+            kv_heads=kv_heads, head_dim=head_dim, scale=scale, dtype=dtype,
+            query_weight=query_weight, key_weight=key_weight, eps=eps,
+            rotary_pairs=rotary_pairs, mscale=mscale, angles=angles, base=base, sinks=sinks,
+        )
+
+    def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
+        return self.strategy(raw_queries, raw_keys, raw_values, mask)

@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent.parent))
 
-from oracle import activations, add_norm, embed, mlp, moe, rope, route  # noqa: E402
+from oracle import activations, add_norm, attention, embed, mlp, moe, rope, route  # noqa: E402
 from oracle.bf16 import from_float  # noqa: E402
 
 
@@ -112,7 +112,28 @@ def make_mlp() -> dict[str, np.ndarray]:
                 act=act, out=out)
 
 
-MAKERS = {"add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed,
+def make_attention() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(8)
+    heads, kv_heads, capacity, pairs, position = 4, 2, 40, 32, 23
+    cos, sin = rope.angle_table(capacity, pairs, 10000.0)
+    angles = np.concatenate([cos, sin], axis=1).astype(np.float32)
+    raw_q = from_float(rng.standard_normal(heads * 128))
+    raw_k = from_float(rng.standard_normal(kv_heads * 128))
+    raw_v = from_float(rng.standard_normal(kv_heads * 128))
+    q_weight = from_float(1 + 0.1 * rng.standard_normal(128))
+    k_weight = from_float(1 + 0.1 * rng.standard_normal(128))
+    k_cache = from_float(rng.standard_normal((kv_heads, capacity, 128)))
+    v_cache = from_float(rng.standard_normal((kv_heads, capacity, 128)))
+    out, new_keys, new_values = attention.decode_step(
+        raw_q, raw_k, raw_v, q_weight, k_weight, angles[position], k_cache, v_cache, position,
+        window=0, scale=128 ** -0.5, eps=1e-6, pairs=pairs)
+    return dict(raw_q=raw_q, raw_k=raw_k, raw_v=raw_v, q_weight=q_weight, k_weight=k_weight,
+                angles=angles, k_cache=k_cache, v_cache=v_cache,
+                position=np.array([position], dtype=np.int32), out=out,
+                key_row=new_keys[:, position], value_row=new_values[:, position])
+
+
+MAKERS = {"attention": make_attention, "add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed,
           "activations": make_activations, "route": make_route, "moe": make_moe, "mlp": make_mlp}
 
 

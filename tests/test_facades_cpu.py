@@ -357,3 +357,63 @@ def test_mlp_hip_binding_declines_other_leaves():
             self.down_proj = torch.nn.Identity()
 
     assert HipDenseMlp.build(Quantized(), hidden=64, inner=32, activation="silu") is None
+
+
+# ---- decode attention step ----------------------------------------------------------
+
+
+def test_attention_predicates_and_declines():
+    from mlx_omnia_amd.kernels.attention import (AttentionStep, DefaultAttentionStep, FixedKVCache,
+                                                 HipAttentionStep, attention_step_applies)
+    from mlx_omnia_amd.kernels.qkv_rope import AngleTable
+
+    assert attention_step_applies(32, 8, 128, 64) and attention_step_applies(16, 16, 128, 8)
+    assert not attention_step_applies(32, 8, 64, 32)      # head_dim
+    assert not attention_step_applies(48, 3, 128, 64)     # gqa 16
+    assert not attention_step_applies(32, 8, 128, 4)      # pairs
+    assert not attention_step_applies(30, 8, 128, 64)     # not grouped evenly
+    cache = FixedKVCache.empty(2, 16, 128)
+    table = AngleTable.from_atlas(torch.zeros(64, 128))
+    weight = torch.ones(128, dtype=torch.bfloat16)
+    common = dict(heads=8, kv_heads=2, head_dim=128, scale=0.1, dtype=torch.bfloat16,
+                  query_weight=weight, key_weight=weight, eps=1e-6, rotary_pairs=64, mscale=1.0,
+                  angles=table, base=0.0, sinks=None)
+    assert HipAttentionStep.build(cache, **common) is None           # CPU tensors
+    assert HipAttentionStep.build(cache, **dict(common, sinks=torch.zeros(8))) is None
+    assert HipAttentionStep.build(cache, **dict(common, angles=None)) is None
+    assert HipAttentionStep.build(cache, **dict(common, query_weight=None)) is None
+    assert isinstance(AttentionStep(cache, **{k: v for k, v in common.items()}).strategy,
+                      DefaultAttentionStep)
+
+
+def test_attention_core_chain_matches_oracle_on_cpu():
+    from mlx_omnia_amd.kernels.attention import AttentionStep, FixedKVCache, RingKVCache
+    from mlx_omnia_amd.kernels.qkv_rope import AngleTable
+    from oracle import attention as attn
+    from oracle.rope import angle_table
+
+    heads, kv_heads, pairs, d = 8, 2, 32, 128
+    rng = np.random.default_rng(13)
+    cos, sin = angle_table(64, pairs, 10000.0)
+    atlas = np.concatenate([cos, sin], axis=1)
+    table = AngleTable.from_atlas(torch.from_numpy(atlas))
+    qw = from_float(1 + 0.1 * rng.standard_normal(d))
+    kw = from_float(1 + 0.1 * rng.standard_normal(d))
+    for cache, window in ((FixedKVCache.empty(kv_heads, 24, d), 0), (RingKVCache.empty(kv_heads, 8, d), 8)):
+        step = AttentionStep(cache, heads=heads, kv_heads=kv_heads, head_dim=d, scale=d ** -0.5,
+                             dtype=torch.bfloat16, query_weight=cpu(qw), key_weight=cpu(kw),
+                             rotary_pairs=pairs, angles=table)
+        rows = cache.keys.shape[2]
+        keys = np.zeros((kv_heads, rows, d), np.uint16)
+        values = np.zeros_like(keys)
+        for position in range(12):
+            q, k, v = (from_float(rng.standard_normal(n * d)) for n in (heads, kv_heads, kv_heads))
+            got = bits(step(*(cpu(x).reshape(1, 1, -1) for x in (q, k, v))).reshape(heads, d))
+            want, keys, values = attn.decode_step(q, k, v, qw, kw, atlas[position], keys, values,
+                                                  position, window=window, scale=d ** -0.5,
+                                                  eps=1e-6, pairs=pairs)
+            # The chain's norm sums in fp32 (the oracle in fp64) and its softmax is torch's:
+            # the same step at the north-star bar.
+            assert_bf16_close(got, want, min_exact=0.9)
+            keys, values = bits(cache.keys[0]), bits(cache.values[0])
+        assert cache.offset == 12
