@@ -42,6 +42,7 @@ constexpr int kBlockRows = 32;                        // rows per wave iteration
 constexpr int kChunkUnit = kWaves * kBlockRows;       // a chunk is a multiple of 128 rows
 constexpr int kPartial = kD + 2;                      // context slice, max, sum
 constexpr int kTargetGroups = 512;                    // workgroups a long cache is split into
+constexpr int kMaxSplits = 1024;                      // chunks per kv head at most
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -101,14 +102,40 @@ __device__ __forceinline__ float row16_fsum(float v) {
   return v;
 }
 
+__device__ __forceinline__ float row16_fmax(float v) {
+  v = fmaxf(v, __uint_as_float(dpp<kRowRor8>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp<kRowRor4>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp<kRowRor2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp<kRowRor1>(__float_as_uint(v))));
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_fmax(v);
+  uint32_t lo, hi;
+  row_pair(__float_as_uint(v), lo, hi);
+  v = fmaxf(__uint_as_float(lo), __uint_as_float(hi));
+  half_pair(__float_as_uint(v), lo, hi);
+  return fmaxf(__uint_as_float(lo), __uint_as_float(hi));
+}
+
+__device__ __forceinline__ float wave_total(float v) {
+  v = row16_fsum(v);
+  uint32_t lo, hi;
+  row_pair(__float_as_uint(v), lo, hi);
+  v = __uint_as_float(lo) + __uint_as_float(hi);
+  half_pair(__float_as_uint(v), lo, hi);
+  return __uint_as_float(lo) + __uint_as_float(hi);
+}
+
 // Merge two online-softmax states (running max m, sum l, context slice o). Both lanes of
 // a swap pair call it with the same (lower, upper) order, so they end bit-identical.
 template <int N>
 __device__ __forceinline__ void merge_state(float& m, float& l, float (&o)[N], float m2,
                                             float l2, const float (&o2)[N]) {
   const float mx = fmaxf(m, m2);
-  const float f1 = m == mx ? 1.0f : exp2f(m - mx);
-  const float f2 = m2 == mx ? 1.0f : exp2f(m2 - mx);
+  const float f1 = m == mx ? 1.0f : __builtin_amdgcn_exp2f(m - mx);
+  const float f2 = m2 == mx ? 1.0f : __builtin_amdgcn_exp2f(m2 - mx);
   m = mx;
   l = l * f1 + l2 * f2;
 #pragma unroll
@@ -185,7 +212,76 @@ __device__ __forceinline__ float dot8_bf16(const u32x4& k, const u32x4& q) {
   return acc;
 }
 
-template <int GQA, bool SCALED>
+// Loads the 16-byte slices of block rows b0 + 4j + drow (j < 8) below c1; zeros elsewhere.
+__device__ __forceinline__ void load_block(const AttnArgs& a, int64_t head_base, int b0, int c1,
+                                           int drow, int c, u32x4 (&k)[8], u32x4 (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = b0 + 4 * j + drow;
+    k[j] = v[j] = u32x4{0u, 0u, 0u, 0u};
+    if (r < c1) {
+      const int64_t off = (head_base + r) * kD + 8 * c;
+      k[j] = load_nt(reinterpret_cast<const u32x4*>(a.k_cache + off));
+      v[j] = load_nt(reinterpret_cast<const u32x4*>(a.v_cache + off));
+    }
+  }
+}
+
+// One block of 32 cache rows into the lane's online-softmax states: lane (drow, c) holds
+// rows first + 4j (j < 8) of the block, slice c. MASKED: rows at or past c1 drop out
+// (score -inf, value zero); a block wholly below c1 skips those selects.
+template <int GQA, bool MASKED>
+__device__ __forceinline__ void consume_block(const u32x4 (&kb)[8], u32x4 (&vb)[8],
+                                              const u32x4 (&q)[GQA], float (&m)[GQA],
+                                              float (&l)[GQA], float (&o)[GQA][8],
+                                              float scale_log2, int first, int c1) {
+  if constexpr (MASKED) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (first + 4 * j >= c1) vb[j] = u32x4{0u, 0u, 0u, 0u};  // never-written rows
+    }
+  }
+  // Scores of every head first, then the softmax update per head, then the values: one
+  // row's slice is unpacked at a time and feeds all heads.
+  float p[GQA][8];
+#pragma unroll
+  for (int g = 0; g < GQA; ++g) {
+    float block_max = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[g][j] = row16_fsum(dot8_bf16(kb[j], q[g])) * scale_log2;
+      if constexpr (MASKED) p[g][j] = first + 4 * j < c1 ? p[g][j] : -INFINITY;
+      block_max = fmaxf(block_max, p[g][j]);
+    }
+    const float mx = fmaxf(m[g], block_max);
+    const float f = m[g] == mx ? 1.0f : __builtin_amdgcn_exp2f(m[g] - mx);
+    m[g] = mx;
+    l[g] *= f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] *= f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (MASKED) {
+        p[g][j] = p[g][j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(p[g][j] - mx);
+      } else {
+        p[g][j] = __builtin_amdgcn_exp2f(p[g][j] - mx);
+      }
+      l[g] += p[g][j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float vf[8];
+    unpack8(vb[j], vf);
+#pragma unroll
+    for (int g = 0; g < GQA; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] = __builtin_fmaf(p[g][j], vf[e], o[g][e]);
+    }
+  }
+}
+
+template <int GQA, bool SCALED, bool PREFETCH = (GQA <= 4)>
 __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArgs a) {
   __shared__ u32x4 q_lds[GQA][16];      // the roped queries, bf16 pairs
   __shared__ u32x4 kv_lds[2][16];       // the new key and value rows
@@ -197,8 +293,18 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   const int c = lane % 16;              // 8-element slice of a head
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
-  const StepRows rows = step_rows(a);
   const int c0 = split * a.chunk;
+  const int64_t head_base = static_cast<int64_t>(kvh) * a.capacity;
+
+  // The wave's first block of cache rows goes out before anything else, bounded by the
+  // host's max_rows (rows there are allocated even when not yet written): rows past the
+  // attended count are masked below, their value slices zeroed. (The write row is read
+  // stale here and replaced from LDS before use.)
+  u32x4 kcur[8], vcur[8];
+  int b0 = c0 + wave * kBlockRows;
+  load_block(a, head_base, b0, min(c0 + a.chunk, a.max_rows), drow, c, kcur, vcur);
+
+  const StepRows rows = step_rows(a);
   if (c0 >= rows.count) return;         // whole workgroup, before any barrier
   const int c1 = min(c0 + a.chunk, rows.count);
   const bool writer = rows.write >= c0 && rows.write < c1;
@@ -245,50 +351,42 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
     for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
   }
 
-  const int64_t head_base = static_cast<int64_t>(kvh) * a.capacity;
-  for (int b0 = c0 + wave * kBlockRows; b0 < c1; b0 += kWaves * kBlockRows) {
-    u32x4 kv[8], vv[8];
+  // Blocks of the wave: b0, b0 + 128, ... With PREFETCH (the register budget allows a
+  // second buffer) the next block's loads are issued before the current one is consumed,
+  // the two buffers taking turns. Only the chunk's last, partial block runs the masked
+  // form.
+  constexpr int kStride = kWaves * kBlockRows;
+  auto run = [&](u32x4 (&kb)[8], u32x4 (&vb)[8]) {
+    if (writer && rows.write >= b0 && rows.write < b0 + kBlockRows) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = b0 + 4 * j + drow;
-      kv[j] = vv[j] = u32x4{0u, 0u, 0u, 0u};
-      if (r < c1) {
-        if (r == rows.write) {
-          kv[j] = kv_lds[0][c];
-          vv[j] = kv_lds[1][c];
-        } else {
-          const int64_t off = (head_base + r) * kD + 8 * c;
-          kv[j] = load_nt(reinterpret_cast<const u32x4*>(a.k_cache + off));
-          vv[j] = load_nt(reinterpret_cast<const u32x4*>(a.v_cache + off));
+      for (int j = 0; j < 8; ++j) {
+        if (b0 + 4 * j + drow == rows.write) {
+          kb[j] = kv_lds[0][c];
+          vb[j] = kv_lds[1][c];
         }
       }
     }
-    float vf[8][8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) unpack8(vv[j], vf[j]);
-#pragma unroll
-    for (int g = 0; g < GQA; ++g) {
-      float s[8];
-      float block_max = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float dot = row16_fsum(dot8_bf16(kv[j], q[g]));
-        s[j] = b0 + 4 * j + drow < c1 ? dot * a.scale_log2 : -INFINITY;
-        block_max = fmaxf(block_max, s[j]);
-      }
-      const float mx = fmaxf(m[g], block_max);
-      const float f = m[g] == mx ? 1.0f : exp2f(m[g] - mx);
-      m[g] = mx;
-      l[g] *= f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] *= f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float p = s[j] == -INFINITY ? 0.0f : exp2f(s[j] - mx);
-        l[g] += p;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] = __builtin_fmaf(p, vf[j][e], o[g][e]);
-      }
+    if (b0 + kBlockRows <= c1) {
+      consume_block<GQA, false>(kb, vb, q, m, l, o, a.scale_log2, b0 + drow, c1);
+    } else {
+      consume_block<GQA, true>(kb, vb, q, m, l, o, a.scale_log2, b0 + drow, c1);
+    }
+  };
+  if constexpr (PREFETCH) {
+    u32x4 knext[8], vnext[8];
+    while (b0 < c1) {
+      load_block(a, head_base, b0 + kStride, c1, drow, c, knext, vnext);
+      run(kcur, vcur);
+      b0 += kStride;
+      if (b0 >= c1) break;
+      load_block(a, head_base, b0 + kStride, c1, drow, c, kcur, vcur);
+      run(knext, vnext);
+      b0 += kStride;
+    }
+  } else {
+    for (; b0 < c1; b0 += kStride) {
+      run(kcur, vcur);
+      load_block(a, head_base, b0 + kStride, c1, drow, c, kcur, vcur);
     }
   }
 
@@ -351,29 +449,72 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   }
 }
 
-// One wave per query head: merge the chunks' states in chunk order, then normalise.
+// One workgroup per query head merges the chunks' states. Pass 1: every thread reads the
+// maxima of some chunks; the global max M gives each chunk its weight 2^(m - M), kept in
+// LDS with the weighted sum. Pass 2: wave w accumulates chunks w, w + 4, ... for its
+// lane's two context elements (independent loads, all in flight), and wave 0 adds the four
+// partial sums in order and normalises.
 template <int GQA>
-__global__ __launch_bounds__(kWave) void attention_combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kWaves * kWave) void attention_combine_kernel(AttnArgs a) {
+  __shared__ float weight[kMaxSplits];
+  __shared__ float reduce[kWaves];
+  __shared__ float2 partial_out[kWaves][kWave];
   const int head = blockIdx.x;
   const int kvh = head / GQA;
   const int g = head % GQA;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
   const StepRows rows = step_rows(a);
   const int used = min(a.splits, (rows.count + a.chunk - 1) / a.chunk);
-  float m = -INFINITY, l = 0.0f, o[2] = {0.0f, 0.0f};
-  for (int s = 0; s < used; ++s) {
-    const float* slot = a.partial + ((static_cast<int64_t>(kvh) * a.splits + s) * GQA + g) * kPartial;
-    const float o2[2] = {slot[2 * lane], slot[2 * lane + 1]};
-    merge_state(m, l, o, slot[kD], slot[kD + 1], o2);
+  const float* base = a.partial + (static_cast<int64_t>(kvh) * a.splits * GQA + g) * kPartial;
+  const int64_t stride = static_cast<int64_t>(GQA) * kPartial;  // between chunks
+
+  float local = -INFINITY;
+  for (int s = threadIdx.x; s < used; s += kWaves * kWave) local = fmaxf(local, base[s * stride + kD]);
+  local = wave_max(local);
+  if (lane == 0) reduce[wave] = local;
+  __syncthreads();
+  const float top = fmaxf(fmaxf(reduce[0], reduce[1]), fmaxf(reduce[2], reduce[3]));
+  __syncthreads();
+  float sum = 0.0f;
+  for (int s = threadIdx.x; s < used; s += kWaves * kWave) {
+    const float m = base[s * stride + kD];
+    const float w = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - top);
+    weight[s] = w;
+    sum += base[s * stride + kD + 1] * w;
   }
-  float v0 = l == 0.0f ? o[0] : o[0] / l;
-  float v1 = l == 0.0f ? o[1] : o[1] / l;
-  reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(head) * kD)[lane] = pack_bf16(v0, v1);
+  sum = wave_total(sum);
+  if (lane == 0) reduce[wave] = sum;
+  __syncthreads();
+  const float total = (reduce[0] + reduce[1]) + (reduce[2] + reduce[3]);
+
+  float2 acc = {0.0f, 0.0f};
+#pragma unroll 4
+  for (int s = wave; s < used; s += kWaves) {
+    const float2 o = *reinterpret_cast<const float2*>(base + s * stride + 2 * lane);
+    const float w = weight[s];
+    acc.x = __builtin_fmaf(w, o.x, acc.x);
+    acc.y = __builtin_fmaf(w, o.y, acc.y);
+  }
+  partial_out[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    float2 o = partial_out[0][lane];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      o.x += partial_out[w][lane].x;
+      o.y += partial_out[w][lane].y;
+    }
+    const float v0 = total == 0.0f ? o.x : o.x / total;
+    const float v1 = total == 0.0f ? o.y : o.y / total;
+    reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(head) * kD)[lane] = pack_bf16(v0, v1);
+  }
 }
 
 int chunk_rows(int max_rows, int kv_heads) {
   const int per_head = (kTargetGroups + kv_heads - 1) / kv_heads;
   int chunk = (max_rows + per_head - 1) / per_head;
+  chunk = max(chunk, (max_rows + kMaxSplits - 1) / kMaxSplits);  // the combine's LDS
   chunk = (chunk + kChunkUnit - 1) / kChunkUnit * kChunkUnit;
   return chunk < kChunkUnit ? kChunkUnit : chunk;
 }
@@ -387,7 +528,7 @@ void launch(const AttnArgs& a, hipStream_t stream) {
     attention_split_kernel<GQA, false><<<grid, kWaves * kWave, 0, stream>>>(a);
   }
   if (a.splits > 1) {
-    attention_combine_kernel<GQA><<<dim3(static_cast<unsigned>(a.kv_heads * GQA)), kWave, 0, stream>>>(a);
+    attention_combine_kernel<GQA><<<dim3(static_cast<unsigned>(a.kv_heads * GQA)), kWaves * kWave, 0, stream>>>(a);
   }
 }
 

@@ -103,11 +103,14 @@ __device__ __forceinline__ T group_sum(T value) {
   return value;
 }
 
-// Cross-lane moves inside a 16-lane DPP row (no LDS traffic).
+// Cross-lane moves inside a 16-lane DPP row (no LDS traffic). Every control used here
+// (row rotations, mirrors, quad permutations) gives each lane a source inside its row, so
+// bound_ctrl changes nothing; set, it lets the compiler fold the move into the consuming
+// VALU op (v_add_f32_dpp and the like).
 template <int ctrl>
 __device__ __forceinline__ uint32_t dpp(uint32_t value) {
   return static_cast<uint32_t>(
-      __builtin_amdgcn_mov_dpp(static_cast<int>(value), ctrl, 0xF, 0xF, false));
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(value), ctrl, 0xF, 0xF, true));
 }
 constexpr int kRowRor1 = 0x121, kRowRor2 = 0x122, kRowRor4 = 0x124, kRowRor8 = 0x128;
 
