@@ -43,6 +43,7 @@ constexpr int kChunkUnit = kWaves * kBlockRows;       // a chunk is a multiple o
 constexpr int kPartial = kD + 2;                      // context slice, max, sum
 constexpr int kTargetGroups = 512;                    // workgroups a long cache is split into
 constexpr int kMaxSplits = 1024;                      // chunks per kv head at most
+constexpr int kCombineWaves = 16;                     // waves merging one query head
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -449,16 +450,14 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   }
 }
 
-// One workgroup per query head merges the chunks' states. Pass 1: every thread reads the
-// maxima of some chunks; the global max M gives each chunk its weight 2^(m - M), kept in
-// LDS with the weighted sum. Pass 2: wave w accumulates chunks w, w + 4, ... for its
-// lane's two context elements (independent loads, all in flight), and wave 0 adds the four
-// partial sums in order and normalises.
+// One workgroup of kCombineWaves waves per query head merges the chunks' states. Wave w
+// takes chunks w, w + kCombineWaves, ... and merges them online (at the configured sizes a
+// wave has at most four, all loaded at once); wave 0 then merges the waves' states in
+// wave order and normalises.
 template <int GQA>
-__global__ __launch_bounds__(kWaves * kWave) void attention_combine_kernel(AttnArgs a) {
-  __shared__ float weight[kMaxSplits];
-  __shared__ float reduce[kWaves];
-  __shared__ float2 partial_out[kWaves][kWave];
+__global__ __launch_bounds__(kCombineWaves * kWave) void attention_combine_kernel(AttnArgs a) {
+  __shared__ float wave_m[kCombineWaves], wave_l[kCombineWaves];
+  __shared__ float2 wave_o[kCombineWaves][kWave];
   const int head = blockIdx.x;
   const int kvh = head / GQA;
   const int g = head % GQA;
@@ -469,44 +468,30 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_combine_kernel(AttnA
   const float* base = a.partial + (static_cast<int64_t>(kvh) * a.splits * GQA + g) * kPartial;
   const int64_t stride = static_cast<int64_t>(GQA) * kPartial;  // between chunks
 
-  float local = -INFINITY;
-  for (int s = threadIdx.x; s < used; s += kWaves * kWave) local = fmaxf(local, base[s * stride + kD]);
-  local = wave_max(local);
-  if (lane == 0) reduce[wave] = local;
-  __syncthreads();
-  const float top = fmaxf(fmaxf(reduce[0], reduce[1]), fmaxf(reduce[2], reduce[3]));
-  __syncthreads();
-  float sum = 0.0f;
-  for (int s = threadIdx.x; s < used; s += kWaves * kWave) {
-    const float m = base[s * stride + kD];
-    const float w = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - top);
-    weight[s] = w;
-    sum += base[s * stride + kD + 1] * w;
-  }
-  sum = wave_total(sum);
-  if (lane == 0) reduce[wave] = sum;
-  __syncthreads();
-  const float total = (reduce[0] + reduce[1]) + (reduce[2] + reduce[3]);
-
-  float2 acc = {0.0f, 0.0f};
+  float m = -INFINITY, l = 0.0f, o[2] = {0.0f, 0.0f};
 #pragma unroll 4
-  for (int s = wave; s < used; s += kWaves) {
-    const float2 o = *reinterpret_cast<const float2*>(base + s * stride + 2 * lane);
-    const float w = weight[s];
-    acc.x = __builtin_fmaf(w, o.x, acc.x);
-    acc.y = __builtin_fmaf(w, o.y, acc.y);
+  for (int s = wave; s < used; s += kCombineWaves) {
+    const float* slot = base + s * stride;
+    const float2 v = *reinterpret_cast<const float2*>(slot + 2 * lane);
+    const float o2[2] = {v.x, v.y};
+    merge_state(m, l, o, slot[kD], slot[kD + 1], o2);
   }
-  partial_out[wave][lane] = acc;
+  wave_o[wave][lane] = float2{o[0], o[1]};
+  if (lane == 0) {
+    wave_m[wave] = m;
+    wave_l[wave] = l;
+  }
   __syncthreads();
   if (wave == 0) {
-    float2 o = partial_out[0][lane];
+    float mm = wave_m[0], ll = wave_l[0];
+    float oo[2] = {wave_o[0][lane].x, wave_o[0][lane].y};
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) {
-      o.x += partial_out[w][lane].x;
-      o.y += partial_out[w][lane].y;
+    for (int w = 1; w < kCombineWaves; ++w) {
+      const float o2[2] = {wave_o[w][lane].x, wave_o[w][lane].y};
+      merge_state(mm, ll, oo, wave_m[w], wave_l[w], o2);
     }
-    const float v0 = total == 0.0f ? o.x : o.x / total;
-    const float v1 = total == 0.0f ? o.y : o.y / total;
+    const float v0 = ll == 0.0f ? oo[0] : oo[0] / ll;
+    const float v1 = ll == 0.0f ? oo[1] : oo[1] / ll;
     reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(head) * kD)[lane] = pack_bf16(v0, v1);
   }
 }
@@ -514,7 +499,7 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_combine_kernel(AttnA
 int chunk_rows(int max_rows, int kv_heads) {
   const int per_head = (kTargetGroups + kv_heads - 1) / kv_heads;
   int chunk = (max_rows + per_head - 1) / per_head;
-  chunk = max(chunk, (max_rows + kMaxSplits - 1) / kMaxSplits);  // the combine's LDS
+  chunk = max(chunk, (max_rows + kMaxSplits - 1) / kMaxSplits);  // bounds the combine loop
   chunk = (chunk + kChunkUnit - 1) / kChunkUnit * kChunkUnit;
   return chunk < kChunkUnit ? kChunkUnit : chunk;
 }
@@ -528,7 +513,7 @@ void launch(const AttnArgs& a, hipStream_t stream) {
     attention_split_kernel<GQA, false><<<grid, kWaves * kWave, 0, stream>>>(a);
   }
   if (a.splits > 1) {
-    attention_combine_kernel<GQA><<<dim3(static_cast<unsigned>(a.kv_heads * GQA)), kWaves * kWave, 0, stream>>>(a);
+    attention_combine_kernel<GQA><<<dim3(static_cast<unsigned>(a.kv_heads * GQA)), kCombineWaves * kWave, 0, stream>>>(a);
   }
 }
 
