@@ -36,6 +36,7 @@ constexpr int kDownRows = 8;            // down output rows per workgroup
 constexpr int kMaxVectorsPerLane = 16;  // gate_up: hidden <= 8192
 constexpr int kMaxDownVectors = 8;      // down: inner <= 2048 (the activation slice stays in registers)
 constexpr int kMaxSlots = 16;           // chosen experts per token (down: one wave each)
+constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float fsum_row16(float v) {
   v += __uint_as_float(dpp<kRowRor8>(__float_as_uint(v)));
@@ -201,7 +202,9 @@ __global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a)
     for (int f = 0; f < kHalf; ++f) {
       const float gf = half ? g[f + kHalf] : g[f];
       const float uf = half ? u[f + kHalf] : u[f];
-      const float mine = gf / (1.0f + expf(-gf)) * uf;
+      // exp(-g) as v_exp_f32 of -g log2(e), the division as v_rcp_f32: a few ulps in fp32,
+      // far below the bf16 rounding of the projection they feed.
+      const float mine = gf * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gf * kLog2e)) * uf;
       uint32_t lower, upper;  // the lower half's value and the upper half's
       half_pair(__float_as_uint(mine), lower, upper);
       act[f / 8][f % 8] = __uint_as_float(lower);
