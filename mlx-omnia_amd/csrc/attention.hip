@@ -19,14 +19,15 @@
 //
 // Layout. A workgroup (4 waves) owns one kv head and one chunk of cache rows, a multiple
 // of 128; all `gqa` query heads of that kv head attend through it, so every key and value
-// byte is read once per step. A wave walks blocks of 32 rows: lane c of each 16-lane DPP
-// row holds elements [8c, 8c + 8) of a head (one 16-byte load), and the wave's four DPP
-// rows take rows 4j + 0..3, so one load instruction reads 1 KiB of contiguous cache.
-// Scores are packed bf16 dot products (v_dot2_f32_bf16) summed across the DPP row; each
-// DPP row keeps its own online softmax (running max, sum and its slice of the context).
-// The four DPP rows merge through permlane swaps, the four waves through LDS. With one
-// chunk the workgroup writes the context; with several it writes (max, sum, context) to
-// the workspace and a second kernel merges the chunks of each query head.
+// byte is read once per step. A wave walks blocks of 32 rows. Scores come from
+// v_mfma_f32_16x16x32_bf16 (the query heads as M, 16 cache rows as N, four steps over the
+// 128 dimensions); the running max is uniform over the wave, and the weights pass
+// through LDS to the value layout, where lane c of each 16-lane DPP row holds elements
+// [8c, 8c + 8) of a row and the wave's four DPP rows take rows 4j + 0..3 (one load
+// instruction reads 1 KiB of contiguous values). The four DPP rows' context slices add
+// through permlane swaps, the four waves merge through LDS. With one chunk the
+// workgroup writes the context; with several it writes (max, sum, context) to the
+// workspace and a second kernel merges the chunks of each query head.
 //
 // The chunk holding the write row computes the new key row itself and reads that row
 // from LDS, never from the cache line it has just written.
@@ -213,85 +214,154 @@ __device__ __forceinline__ float dot8_bf16(const u32x4& k, const u32x4& q) {
   return acc;
 }
 
-// Loads the 16-byte slices of block rows b0 + 4j + drow (j < 8) below c1; zeros elsewhere.
-__device__ __forceinline__ void load_block(const AttnArgs& a, int64_t head_base, int b0, int c1,
+// A block of 32 cache rows in two layouts. Keys, for the score MFMAs (two 16-row tiles):
+// lane (drow, c) holds row b0 + 16t + c, dimensions 32 kk + 8 drow .. + 8, in k[4t + kk]:
+// the four lanes of a row read 64 contiguous bytes per instruction. (With dimensions
+// 32 drow + 8 kk, 16-byte pieces 64 bytes apart, the step took 38.8 us at 32k rows
+// against 32.9 us.)
+// Values, for the VALU accumulation: row b0 + 4j + drow, dimensions 8c .. + 8, in v[j].
+// Rows at or past `bound` are not loaded (zeros).
+__device__ __forceinline__ void load_block(const AttnArgs& a, int64_t head_base, int b0, int bound,
                                            int drow, int c, u32x4 (&k)[8], u32x4 (&v)[8]) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int r = b0 + 16 * t + c;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      k[4 * t + kk] = u32x4{0u, 0u, 0u, 0u};
+      if (r < bound) {
+        k[4 * t + kk] = load_nt(reinterpret_cast<const u32x4*>(
+            a.k_cache + (head_base + r) * kD + 32 * kk + 8 * drow));
+      }
+    }
+  }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int r = b0 + 4 * j + drow;
-    k[j] = v[j] = u32x4{0u, 0u, 0u, 0u};
-    if (r < c1) {
-      const int64_t off = (head_base + r) * kD + 8 * c;
-      k[j] = load_nt(reinterpret_cast<const u32x4*>(a.k_cache + off));
-      v[j] = load_nt(reinterpret_cast<const u32x4*>(a.v_cache + off));
-    }
+    v[j] = u32x4{0u, 0u, 0u, 0u};
+    if (r < bound) v[j] = load_nt(reinterpret_cast<const u32x4*>(a.v_cache + (head_base + r) * kD + 8 * c));
   }
 }
 
-// One block of 32 cache rows into the lane's online-softmax states: lane (drow, c) holds
-// rows first + 4j (j < 8) of the block, slice c. MASKED: rows at or past c1 drop out
-// (score -inf, value zero); a block wholly below c1 skips those selects.
+// The uniform running max of head h, picked per lane for the heads 4 drow + i it scores.
+template <int GQA>
+__device__ __forceinline__ float head_value(const float (&x)[GQA], int drow, int i) {
+  float out = x[i < GQA ? i : 0];
+#pragma unroll
+  for (int h = 4; h < GQA; h += 4) {
+    if (drow == h / 4) out = x[h + i];
+  }
+  return out;
+}
+
+// One block of 32 rows into the wave's online softmax. Scores: q (A operand: head c,
+// dimensions 32 kk + 8 drow) times the key tile (B operand) on v_mfma_f32_16x16x32_bf16,
+// four steps over the 128 dimensions; the result gives lane (drow, c) the scores of heads
+// 4 drow + i for row c of the tile. The running max is uniform over the wave; the
+// weights p pass through LDS to the value layout, where each lane accumulates its slice.
+// MASKED: rows at or past c1 drop out (score -inf, value zero).
 template <int GQA, bool MASKED>
 __device__ __forceinline__ void consume_block(const u32x4 (&kb)[8], u32x4 (&vb)[8],
-                                              const u32x4 (&q)[GQA], float (&m)[GQA],
-                                              float (&l)[GQA], float (&o)[GQA][8],
-                                              float scale_log2, int first, int c1) {
-  if constexpr (MASKED) {
+                                              const bf16x8 (&qa)[4], float (&m)[GQA],
+                                              float (&lsum)[4], float (&o)[GQA][8],
+                                              float (*p_lds)[4 * ((GQA + 3) / 4)],
+                                              float scale_log2, int b0, int drow, int c, int c1) {
+  constexpr int kPitch = 4 * ((GQA + 3) / 4);
+  float s[2][4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (first + 4 * j >= c1) vb[j] = u32x4{0u, 0u, 0u, 0u};  // never-written rows
+  for (int t = 0; t < 2; ++t) {
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kk], __builtin_bit_cast(bf16x8, kb[4 * t + kk]),
+                                                    acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[t][i] = acc[i] * scale_log2;
+      if constexpr (MASKED) s[t][i] = b0 + 16 * t + c < c1 ? s[t][i] : -INFINITY;
     }
   }
-  // Scores of every head first, then the softmax update per head, then the values: one
-  // row's slice is unpacked at a time and feeds all heads.
-  float p[GQA][8];
+  // Block max per head: over the two tiles in the lane, then over the 16 rows (lanes).
+  float bmax[4];
 #pragma unroll
-  for (int g = 0; g < GQA; ++g) {
-    float block_max = -INFINITY;
+  for (int i = 0; i < 4; ++i) bmax[i] = row16_fmax(fmaxf(s[0][i], s[1][i]));
+  float f[GQA];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      p[g][j] = row16_fsum(dot8_bf16(kb[j], q[g])) * scale_log2;
-      if constexpr (MASKED) p[g][j] = first + 4 * j < c1 ? p[g][j] : -INFINITY;
-      block_max = fmaxf(block_max, p[g][j]);
+  for (int h = 0; h < GQA; ++h) {
+    const float bm = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(bmax[h % 4]), 16 * (h / 4)));
+    const float mx = fmaxf(m[h], bm);
+    f[h] = m[h] == mx ? 1.0f : __builtin_amdgcn_exp2f(m[h] - mx);
+    m[h] = mx;
+  }
+  // Weights of the lane's heads for its two rows; partial sums stay per lane.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float mh = head_value(m, drow, i);
+    const float fh = head_value(f, drow, i);
+    float p0, p1;
+    if constexpr (MASKED) {
+      p0 = s[0][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[0][i] - mh);
+      p1 = s[1][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[1][i] - mh);
+    } else {
+      p0 = __builtin_amdgcn_exp2f(s[0][i] - mh);
+      p1 = __builtin_amdgcn_exp2f(s[1][i] - mh);
     }
-    const float mx = fmaxf(m[g], block_max);
-    const float f = m[g] == mx ? 1.0f : __builtin_amdgcn_exp2f(m[g] - mx);
-    m[g] = mx;
-    l[g] *= f;
+    lsum[i] = lsum[i] * fh + (p0 + p1);
+    s[0][i] = p0;
+    s[1][i] = p1;
+  }
+  if (4 * drow < GQA) {
+    *reinterpret_cast<f32x4*>(&p_lds[c][4 * drow]) = f32x4{s[0][0], s[0][1], s[0][2], s[0][3]};
+    *reinterpret_cast<f32x4*>(&p_lds[16 + c][4 * drow]) = f32x4{s[1][0], s[1][1], s[1][2], s[1][3]};
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // Values: rescale, then add p * v for the lane's rows 4j + drow.
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] *= f;
+  for (int h = 0; h < GQA; ++h) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if constexpr (MASKED) {
-        p[g][j] = p[g][j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(p[g][j] - mx);
-      } else {
-        p[g][j] = __builtin_amdgcn_exp2f(p[g][j] - mx);
-      }
-      l[g] += p[g][j];
-    }
+    for (int e = 0; e < 8; ++e) o[h][e] *= f[h];
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    if constexpr (MASKED) {
+      if (b0 + 4 * j + drow >= c1) vb[j] = u32x4{0u, 0u, 0u, 0u};  // never-written rows
+    }
     float vf[8];
     unpack8(vb[j], vf);
+    float pw[kPitch];
 #pragma unroll
-    for (int g = 0; g < GQA; ++g) {
+    for (int h4 = 0; h4 < kPitch; h4 += 4) {
+      const f32x4 w4 = *reinterpret_cast<const f32x4*>(&p_lds[4 * j + drow][h4]);
+      pw[h4] = w4[0];
+      pw[h4 + 1] = w4[1];
+      pw[h4 + 2] = w4[2];
+      pw[h4 + 3] = w4[3];
+    }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] = __builtin_fmaf(p[g][j], vf[e], o[g][e]);
+    for (int h = 0; h < GQA; ++h) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[h][e] = __builtin_fmaf(pw[h], vf[e], o[h][e]);
     }
   }
+  // The next block overwrites p_lds only after every lane has read this one.
+  __builtin_amdgcn_wave_barrier();
 }
 
 template <int GQA, bool SCALED, bool PREFETCH = (GQA <= 4)>
 __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArgs a) {
+  constexpr int kPitch = 4 * ((GQA + 3) / 4);
   __shared__ u32x4 q_lds[GQA][16];      // the roped queries, bf16 pairs
   __shared__ u32x4 kv_lds[2][16];       // the new key and value rows
   __shared__ float merge_lds[kWaves][GQA][kPartial];
+  __shared__ __align__(16) float p_lds[kWaves][kBlockRows][kPitch];  // a block's weights
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int drow = lane / 16;           // DPP row of the lane
-  const int c = lane % 16;              // 8-element slice of a head
+  const int c = lane % 16;              // tile row (scores) / 8-element slice (values)
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int c0 = split * a.chunk;
@@ -339,18 +409,23 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   }
   __syncthreads();
 
-  u32x4 q[GQA];
+  // The A operand: head c (zero past the group), dimensions 32 kk + 8 drow .. + 8.
+  bf16x8 qa[4];
 #pragma unroll
-  for (int g = 0; g < GQA; ++g) q[g] = q_lds[g][c];
-
-  float m[GQA], l[GQA], o[GQA][8];
-#pragma unroll
-  for (int g = 0; g < GQA; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+  for (int kk = 0; kk < 4; ++kk) {
+    const u32x4 q = c < GQA ? q_lds[c < GQA ? c : 0][4 * kk + drow] : u32x4{0u, 0u, 0u, 0u};
+    qa[kk] = __builtin_bit_cast(bf16x8, q);
   }
+
+  float m[GQA], lsum[4], o[GQA][8];
+#pragma unroll
+  for (int h = 0; h < GQA; ++h) {
+    m[h] = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lsum[i] = 0.0f;
 
   // Blocks of the wave: b0, b0 + 128, ... With PREFETCH (the register budget allows a
   // second buffer) the next block's loads are issued before the current one is consumed,
@@ -360,17 +435,21 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   auto run = [&](u32x4 (&kb)[8], u32x4 (&vb)[8]) {
     if (writer && rows.write >= b0 && rows.write < b0 + kBlockRows) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (b0 + 4 * j + drow == rows.write) {
-          kb[j] = kv_lds[0][c];
-          vb[j] = kv_lds[1][c];
+      for (int t = 0; t < 2; ++t) {
+        if (b0 + 16 * t + c == rows.write) {
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) kb[4 * t + kk] = kv_lds[0][4 * kk + drow];
         }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (b0 + 4 * j + drow == rows.write) vb[j] = kv_lds[1][c];
       }
     }
     if (b0 + kBlockRows <= c1) {
-      consume_block<GQA, false>(kb, vb, q, m, l, o, a.scale_log2, b0 + drow, c1);
+      consume_block<GQA, false>(kb, vb, qa, m, lsum, o, p_lds[wave], a.scale_log2, b0, drow, c, c1);
     } else {
-      consume_block<GQA, true>(kb, vb, q, m, l, o, a.scale_log2, b0 + drow, c1);
+      consume_block<GQA, true>(kb, vb, qa, m, lsum, o, p_lds[wave], a.scale_log2, b0, drow, c, c1);
     }
   };
   if constexpr (PREFETCH) {
@@ -391,35 +470,31 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
     }
   }
 
-  // Merge the four DPP rows of the wave (rows 0-1 and 2-3, then the halves).
+  // The wave's state: the max is uniform already; the sums add over the 16 lanes of each
+  // DPP row (rows of the tiles), the context slices over the four DPP rows.
+  float l[GQA];
 #pragma unroll
-  for (int g = 0; g < GQA; ++g) {
+  for (int i = 0; i < 4; ++i) lsum[i] = row16_fsum(lsum[i]);
 #pragma unroll
-    for (int step = 0; step < 2; ++step) {
+  for (int h = 0; h < GQA; ++h) {
+    l[h] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(lsum[h % 4]), 16 * (h / 4)));
+  }
+#pragma unroll
+  for (int h = 0; h < GQA; ++h) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
       uint32_t lo, hi;
-      float m2, l2, o2[8], mlo, llo, olo[8];
-      if (step == 0) row_pair(__float_as_uint(m[g]), lo, hi); else half_pair(__float_as_uint(m[g]), lo, hi);
-      mlo = __uint_as_float(lo); m2 = __uint_as_float(hi);
-      if (step == 0) row_pair(__float_as_uint(l[g]), lo, hi); else half_pair(__float_as_uint(l[g]), lo, hi);
-      llo = __uint_as_float(lo); l2 = __uint_as_float(hi);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (step == 0) row_pair(__float_as_uint(o[g][e]), lo, hi); else half_pair(__float_as_uint(o[g][e]), lo, hi);
-        olo[e] = __uint_as_float(lo);
-        o2[e] = __uint_as_float(hi);
-      }
-      merge_state(mlo, llo, olo, m2, l2, o2);
-      m[g] = mlo;
-      l[g] = llo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] = olo[e];
+      row_pair(__float_as_uint(o[h][e]), lo, hi);
+      float v = __uint_as_float(lo) + __uint_as_float(hi);
+      half_pair(__float_as_uint(v), lo, hi);
+      o[h][e] = __uint_as_float(lo) + __uint_as_float(hi);
     }
     if (drow == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) merge_lds[wave][g][8 * c + e] = o[g][e];
+      for (int e = 0; e < 8; ++e) merge_lds[wave][h][8 * c + e] = o[h][e];
       if (c == 0) {
-        merge_lds[wave][g][kD] = m[g];
-        merge_lds[wave][g][kD + 1] = l[g];
+        merge_lds[wave][h][kD] = m[h];
+        merge_lds[wave][h][kD + 1] = l[h];
       }
     }
   }
