@@ -45,6 +45,7 @@ constexpr int kPartial = kD + 2;                      // context slice, max, sum
 constexpr int kTargetGroups = 512;                    // workgroups a long cache is split into
 constexpr int kMaxSplits = 1024;                      // chunks per kv head at most
 constexpr int kCombineWaves = 16;                     // waves merging one query head
+constexpr int kKeyPitch = kD + 8;                     // bf16; a key tile row in LDS, padded
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -214,32 +215,20 @@ __device__ __forceinline__ float dot8_bf16(const u32x4& k, const u32x4& q) {
   return acc;
 }
 
-// A block of 32 cache rows in two layouts. Keys, for the score MFMAs (two 16-row tiles):
-// lane (drow, c) holds row b0 + 16t + c, dimensions 32 kk + 8 drow .. + 8, in k[4t + kk]:
-// the four lanes of a row read 64 contiguous bytes per instruction. (With dimensions
-// 32 drow + 8 kk, 16-byte pieces 64 bytes apart, the step took 38.8 us at 32k rows
-// against 32.9 us.)
-// Values, for the VALU accumulation: row b0 + 4j + drow, dimensions 8c .. + 8, in v[j].
-// Rows at or past `bound` are not loaded (zeros).
+// A block of 32 cache rows: lane (drow, c) loads row b0 + 4j + drow, dimensions
+// 8c .. + 8, of the keys (k[j]) and of the values (v[j]), so one load instruction reads
+// 1 KiB of contiguous cache. The keys are turned into the score MFMAs' operand layout
+// through LDS (consume_block). Rows at or past `bound` are not loaded (zeros).
 __device__ __forceinline__ void load_block(const AttnArgs& a, int64_t head_base, int b0, int bound,
                                            int drow, int c, u32x4 (&k)[8], u32x4 (&v)[8]) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int r = b0 + 16 * t + c;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      k[4 * t + kk] = u32x4{0u, 0u, 0u, 0u};
-      if (r < bound) {
-        k[4 * t + kk] = load_nt(reinterpret_cast<const u32x4*>(
-            a.k_cache + (head_base + r) * kD + 32 * kk + 8 * drow));
-      }
-    }
-  }
-#pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int r = b0 + 4 * j + drow;
-    v[j] = u32x4{0u, 0u, 0u, 0u};
-    if (r < bound) v[j] = load_nt(reinterpret_cast<const u32x4*>(a.v_cache + (head_base + r) * kD + 8 * c));
+    k[j] = v[j] = u32x4{0u, 0u, 0u, 0u};
+    if (r < bound) {
+      k[j] = load_nt(reinterpret_cast<const u32x4*>(a.k_cache + (head_base + r) * kD + 8 * c));
+      v[j] = load_nt(reinterpret_cast<const u32x4*>(a.v_cache + (head_base + r) * kD + 8 * c));
+    }
   }
 }
 
@@ -264,17 +253,27 @@ template <int GQA, bool MASKED>
 __device__ __forceinline__ void consume_block(const u32x4 (&kb)[8], u32x4 (&vb)[8],
                                               const bf16x8 (&qa)[4], float (&m)[GQA],
                                               float (&lsum)[4], float (&o)[GQA][8],
-                                              float (*p_lds)[4 * ((GQA + 3) / 4)],
+                                              float (*p_lds)[4 * ((GQA + 3) / 4)], uint16_t* kt_lds,
                                               float scale_log2, int b0, int drow, int c, int c1) {
   constexpr int kPitch = 4 * ((GQA + 3) / 4);
+  // The key block into the wave's LDS tile (rows padded to 272 bytes, so the 16 rows an
+  // operand read touches fall on different banks), read back as the B operand: lane
+  // (drow, c) takes row 16t + c, dimensions 32 kk + 8 drow .. + 8. Loading the operand
+  // layout straight from HBM (16 rows per instruction) measured 32.8 us at 32k rows,
+  // against 32.0 us this way.
+#pragma unroll
+  for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(kt_lds + (4 * j + drow) * kKeyPitch + 8 * c) = kb[j];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float s[2][4];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kk], __builtin_bit_cast(bf16x8, kb[4 * t + kk]),
-                                                    acc, 0, 0, 0);
+      const u32x4 kt = *reinterpret_cast<const u32x4*>(kt_lds + (16 * t + c) * kKeyPitch + 32 * kk + 8 * drow);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kk], __builtin_bit_cast(bf16x8, kt), acc, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -357,6 +356,7 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   __shared__ u32x4 kv_lds[2][16];       // the new key and value rows
   __shared__ float merge_lds[kWaves][GQA][kPartial];
   __shared__ __align__(16) float p_lds[kWaves][kBlockRows][kPitch];  // a block's weights
+  __shared__ __align__(16) uint16_t kt_lds[kWaves][kBlockRows * kKeyPitch];  // a block's keys
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -435,21 +435,17 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   auto run = [&](u32x4 (&kb)[8], u32x4 (&vb)[8]) {
     if (writer && rows.write >= b0 && rows.write < b0 + kBlockRows) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (b0 + 16 * t + c == rows.write) {
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) kb[4 * t + kk] = kv_lds[0][4 * kk + drow];
-        }
-      }
-#pragma unroll
       for (int j = 0; j < 8; ++j) {
-        if (b0 + 4 * j + drow == rows.write) vb[j] = kv_lds[1][c];
+        if (b0 + 4 * j + drow == rows.write) {
+          kb[j] = kv_lds[0][c];
+          vb[j] = kv_lds[1][c];
+        }
       }
     }
     if (b0 + kBlockRows <= c1) {
-      consume_block<GQA, false>(kb, vb, qa, m, lsum, o, p_lds[wave], a.scale_log2, b0, drow, c, c1);
+      consume_block<GQA, false>(kb, vb, qa, m, lsum, o, p_lds[wave], kt_lds[wave], a.scale_log2, b0, drow, c, c1);
     } else {
-      consume_block<GQA, true>(kb, vb, qa, m, lsum, o, p_lds[wave], a.scale_log2, b0, drow, c, c1);
+      consume_block<GQA, true>(kb, vb, qa, m, lsum, o, p_lds[wave], kt_lds[wave], a.scale_log2, b0, drow, c, c1);
     }
   };
   if constexpr (PREFETCH) {
