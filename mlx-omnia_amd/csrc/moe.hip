@@ -32,7 +32,7 @@ namespace {
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kRowsPerWave = 2;         // gate_up rows per wave (4: 10.2 us, 2: 9.6 us, 1: 10.4 us at the config)
-constexpr int kDownRows = 8;            // down output rows per workgroup
+constexpr int kDownRows = 4;            // down output rows per workgroup (8: 7.1 us, 4: 6.9 us, 2: 7.5 us)
 constexpr int kMaxVectorsPerLane = 16;  // gate_up: hidden <= 8192
 constexpr int kMaxDownVectors = 8;      // down: inner <= 2048 (the activation slice stays in registers)
 constexpr int kMaxSlots = 16;           // chosen experts per token (down: one wave each)
@@ -170,9 +170,10 @@ __global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a)
   }
   const u32x4* w = reinterpret_cast<const u32x4*>(a.w) +
                    (valid ? expert : 0) * a.hidden * static_cast<int64_t>(a.vecs);
-  // Row pairs in flight together: all four while the vectors fit the 128-register
-  // budget of a 16-wave workgroup.
-  constexpr int kGroup = VPL <= 4 ? 4 : (VPL <= 6 ? 2 : 1);
+  // Row pairs in flight together: all of the workgroup's while the vectors fit the
+  // 128-register budget of a 16-wave workgroup.
+  constexpr int kGroupWanted = VPL <= 4 ? 4 : (VPL <= 6 ? 2 : 1);
+  constexpr int kGroup = kGroupWanted < kDownRows / 2 ? kGroupWanted : kDownRows / 2;
   auto load_group = [&](int p0, u32x4 (&wv)[kGroup][VPL]) {
 #pragma unroll
     for (int p = 0; p < kGroup; ++p) {
