@@ -146,14 +146,16 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float (&o)[N], f
 }
 
 // RMSNorm + rotation of one 128-wide head row by a 16-lane DPP row: lane c holds elements
-// [8c, 8c + 8). Returns the bf16 result (already rounded) in `out`. Every lane of the row
-// must call it (the rotation partner comes by a lane shuffle).
-__device__ __forceinline__ void norm_rope_row(const uint16_t* raw, const uint16_t* weight,
-                                              const float* angle_row, int pairs, bool scaled,
-                                              float mscale_bf, float eps, int c, float out[8]) {
+// [8c, 8c + 8) (raw, weight: 16-byte slices already loaded; cs, sn: the cosines and sines
+// of the lane's pairs, for rotated lanes). Returns the bf16 result (already rounded) in
+// `out`. Every lane of the row must call it (the rotation partner comes by a lane shuffle).
+__device__ __forceinline__ void norm_rope_row(const u32x4& raw, const u32x4& weight,
+                                              const float (&cs)[8], const float (&sn)[8],
+                                              int pairs, bool scaled, float mscale_bf,
+                                              float eps, int c, float out[8]) {
   float x[8], w[8];
-  unpack8(*reinterpret_cast<const u32x4*>(raw + 8 * c), x);
-  unpack8(*reinterpret_cast<const u32x4*>(weight + 8 * c), w);
+  unpack8(raw, x);
+  unpack8(weight, w);
   double sumsq = 0.0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) sumsq += static_cast<double>(x[j] * x[j]);
@@ -187,32 +189,15 @@ __device__ __forceinline__ void norm_rope_row(const uint16_t* raw, const uint16_
     return;
   }
   const bool first_half = c < lanes;
-  const int p0 = 8 * (first_half ? c : c - lanes);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const float cs = angle_row[p0 + j];
-    const float sn = angle_row[pairs + p0 + j];
     // a: the first-half value of the pair, b: the second-half one.
     const float av = first_half ? n[j] : partner[j];
     const float bv = first_half ? partner[j] : n[j];
-    out[j] = first_half ? av * cs - bv * sn : av * sn + bv * cs;
+    out[j] = first_half ? av * cs[j] - bv * sn[j] : av * sn[j] + bv * cs[j];
   }
 #pragma unroll
   for (int j = 0; j < 8; j += 2) round_pair(out[j], out[j + 1]);
-}
-
-// Eight bf16 products of a lane's slices, accumulated in fp32 by four v_dot2 steps. The
-// whole 16-byte vector is reinterpreted at once: a bit cast of one ext-vector element
-// (`k.y`) is compiled by this toolchain as a cast of element 0.
-__device__ __forceinline__ float dot8_bf16(const u32x4& k, const u32x4& q) {
-  const bf16x8 kb = __builtin_bit_cast(bf16x8, k);
-  const bf16x8 qb = __builtin_bit_cast(bf16x8, q);
-  float acc = 0.0f;
-  acc = __builtin_amdgcn_fdot2_f32_bf16(kb.s01, qb.s01, acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(kb.s23, qb.s23, acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(kb.s45, qb.s45, acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(kb.s67, qb.s67, acc, false);
-  return acc;
 }
 
 // A block of 32 cache rows: lane (drow, c) loads row b0 + 4j + drow, dimensions
@@ -367,45 +352,67 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   const int c0 = split * a.chunk;
   const int64_t head_base = static_cast<int64_t>(kvh) * a.capacity;
 
-  // The wave's first block of cache rows goes out before anything else, bounded by the
-  // host's max_rows (rows there are allocated even when not yet written): rows past the
-  // attended count are masked below, their value slices zeroed. (The write row is read
-  // stale here and replaced from LDS before use.)
-  u32x4 kcur[8], vcur[8];
-  int b0 = c0 + wave * kBlockRows;
-  load_block(a, head_base, b0, min(c0 + a.chunk, a.max_rows), drow, c, kcur, vcur);
-
   const StepRows rows = step_rows(a);
   if (c0 >= rows.count) return;         // whole workgroup, before any barrier
   const int c1 = min(c0 + a.chunk, rows.count);
   const bool writer = rows.write >= c0 && rows.write < c1;
 
-  // Prologue: item i = wave * 4 + drow; items [0, GQA) are the query heads, GQA the new
-  // key row, GQA + 1 the new value row (both only in the chunk holding the write row).
-  {
-    const int item = wave * 4 + drow;
-    const int arow = min(rows.position, a.angle_rows - 1);
-    const float* angle_row = a.angles + static_cast<int64_t>(arow) * 2 * a.pairs;
-    const float mscale_bf = round_bf16(a.mscale);
-    if (item < GQA || (item == GQA && writer)) {
-      const bool is_q = item < GQA;
-      const uint16_t* raw = is_q ? a.raw_q + static_cast<int64_t>(kvh * GQA + item) * kD
-                                 : a.raw_k + static_cast<int64_t>(kvh) * kD;
-      float r[8];
-      norm_rope_row(raw, is_q ? a.q_weight : a.k_weight, angle_row, a.pairs, SCALED,
-                    mscale_bf, a.eps, c, r);
-      const u32x4 packed = pack8(r);
-      if (is_q) {
-        q_lds[item][c] = packed;
-      } else {
-        kv_lds[0][c] = packed;
-        *reinterpret_cast<u32x4*>(a.k_cache + (static_cast<int64_t>(kvh) * a.capacity + rows.write) * kD + 8 * c) = packed;
+  // Prologue inputs first: item i = wave * 4 + drow; items [0, GQA) are the query heads,
+  // GQA the new key row, GQA + 1 the new value row (both only in the chunk holding the
+  // write row). Vector-memory results arrive in issue order, so these go out ahead of the
+  // first block of cache rows and the prologue runs while that block is in flight.
+  const int item = wave * 4 + drow;
+  const bool norm_item = item < GQA || (item == GQA && writer);
+  const bool value_item = item == GQA + 1 && writer;
+  const bool is_q = item < GQA;
+  u32x4 raw = u32x4{0u, 0u, 0u, 0u}, wgt = u32x4{0u, 0u, 0u, 0u};
+  float cs[8], sn[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) cs[j] = sn[j] = 0.0f;
+  if (norm_item) {
+    const uint16_t* row = is_q ? a.raw_q + static_cast<int64_t>(kvh * GQA + item) * kD
+                               : a.raw_k + static_cast<int64_t>(kvh) * kD;
+    raw = *reinterpret_cast<const u32x4*>(row + 8 * c);
+    wgt = *reinterpret_cast<const u32x4*>((is_q ? a.q_weight : a.k_weight) + 8 * c);
+    const int lanes = a.pairs / 8;
+    if (c < 2 * lanes) {
+      const int arow = min(rows.position, a.angle_rows - 1);
+      const float* angle = a.angles + static_cast<int64_t>(arow) * 2 * a.pairs + 8 * (c < lanes ? c : c - lanes);
+      const f32x4 c0v = *reinterpret_cast<const f32x4*>(angle);
+      const f32x4 c1v = *reinterpret_cast<const f32x4*>(angle + 4);
+      const f32x4 s0v = *reinterpret_cast<const f32x4*>(angle + a.pairs);
+      const f32x4 s1v = *reinterpret_cast<const f32x4*>(angle + a.pairs + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        cs[j] = c0v[j];
+        cs[4 + j] = c1v[j];
+        sn[j] = s0v[j];
+        sn[4 + j] = s1v[j];
       }
-    } else if (item == GQA + 1 && writer) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(a.raw_v + static_cast<int64_t>(kvh) * kD + 8 * c);
-      kv_lds[1][c] = v;
-      *reinterpret_cast<u32x4*>(a.v_cache + (static_cast<int64_t>(kvh) * a.capacity + rows.write) * kD + 8 * c) = v;
     }
+  } else if (value_item) {
+    raw = *reinterpret_cast<const u32x4*>(a.raw_v + static_cast<int64_t>(kvh) * kD + 8 * c);
+  }
+
+  // The wave's first block of cache rows. (The write row is read stale here and replaced
+  // from LDS before use.)
+  u32x4 kcur[8], vcur[8];
+  int b0 = c0 + wave * kBlockRows;
+  load_block(a, head_base, b0, c1, drow, c, kcur, vcur);
+
+  if (norm_item) {
+    float r[8];
+    norm_rope_row(raw, wgt, cs, sn, a.pairs, SCALED, round_bf16(a.mscale), a.eps, c, r);
+    const u32x4 packed = pack8(r);
+    if (is_q) {
+      q_lds[item][c] = packed;
+    } else {
+      kv_lds[0][c] = packed;
+      *reinterpret_cast<u32x4*>(a.k_cache + (head_base + rows.write) * kD + 8 * c) = packed;
+    }
+  } else if (value_item) {
+    kv_lds[1][c] = raw;
+    *reinterpret_cast<u32x4*>(a.v_cache + (head_base + rows.write) * kD + 8 * c) = raw;
   }
   __syncthreads();
 
@@ -627,8 +634,8 @@ extern "C" int32_t omnia_attention_decode(
                 key_cache && value_cache && position && out, "attention_decode: null pointer");
   OMNIA_REQUIRE(aligned16(raw_queries) && aligned16(raw_keys) && aligned16(raw_values) &&
                 aligned16(query_weight) && aligned16(key_weight) && aligned16(key_cache) &&
-                aligned16(value_cache) && aligned16(out),
-                "attention_decode: bf16 rows must be 16-byte aligned");
+                aligned16(value_cache) && aligned16(out) && aligned16(angles),
+                "attention_decode: bf16 rows and the angle table must be 16-byte aligned");
   const int chunk = chunk_rows(static_cast<int>(max_rows), static_cast<int>(kv_heads));
   const int splits = static_cast<int>((max_rows + chunk - 1) / chunk);
   if (splits > 1) {
