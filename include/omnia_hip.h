@@ -246,7 +246,8 @@ int64_t omnia_attention_workspace_bytes(int64_t heads, int64_t kv_heads, int64_t
  *   per head: n = bf16(w * bf16(x * inv)), inv = 1 / sqrt(sum x^2 / 128 + eps)
  *   a, b = bf16(n_p * bf16(mscale)), bf16(n_{p+P} * bf16(mscale))       p < P = rotary_pairs
  *   q_p = bf16(a cos - b sin), q_{p+P} = bf16(a sin + b cos), q_d = n_d for d >= 2P
- *   (the same for the key row; cos || sin from row `position` of `angles` [angle_rows, 2P])
+ *   (the same for the key row; cos || sin from row `position` of `angles` [angle_rows, 2P]
+ *   fp32, 16-byte aligned)
  *   the new key and value rows written into the caches, then for every query head h
  *   out[h] = bf16(sum_r softmax_r(scale * q_h . k_r) v_r) over the attended rows of kv
  *   head h / (heads / kv_heads), softmax and sums in fp32.
