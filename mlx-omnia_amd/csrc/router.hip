@@ -326,6 +326,29 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
 #pragma unroll
   for (int v = 0; v < V; ++v) weight_norm[v] = a.weight_norms[lane + v * kWave];
 
+  // The walk of phase 2 over W: wave w owns expert tile w % kTiles over slice w / kTiles
+  // of H, in kOuter blocks of kUnroll steps. Each workgroup starts at a different block,
+  // so the workgroups of an XCD do not all read the same W lines at once (the order of
+  // the step adds changes per workgroup; the error bound does not).
+  constexpr int kUnroll = 8;
+  constexpr int kOuter = kSlice / (32 * kUnroll);
+  const int start = static_cast<int>(blockIdx.x % kOuter);
+  const uint16_t* brow =
+      a.packed + (static_cast<int64_t>(wave % kTiles) * (H / 32) + (wave / kTiles) * (kSlice / 32)) * 512 +
+      lane * 8;
+  u32x4 next[kUnroll];
+  // At H = 2048 the first block's loads go out now, ahead of phase 1, whose row loads
+  // take the HBM stream: the 8 KiB per wave arrive while the CU's L1 is otherwise idle
+  // (23.0 us against 24.4 us at [4096, 2048], E = 128). At H = 4096 the rows leave no
+  // registers for them.
+  constexpr bool kEarlyWalk = VPL <= 4;
+  if constexpr (kEarlyWalk) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      next[u] = *reinterpret_cast<const u32x4*>(brow + (start * kUnroll + u) * 512);
+    }
+  }
+
   // Phase 1: residual add + RMSNorm of row `wave`.
   {
     const int r = wave;
@@ -398,22 +421,13 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   {
     const f32x4 zero = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int expert_tile = wave % kTiles;
     const int slice = wave / kTiles;
     const uint16_t* arow = tile + (lane % 16) * kRowPitch + slice * kSlice + (lane / 16) * 8;
-    const uint16_t* brow =
-        a.packed + (static_cast<int64_t>(expert_tile) * (H / 32) + slice * (kSlice / 32)) * 512 +
-        lane * 8;
-    // Each workgroup starts its walk at a different block of kUnroll steps, so the
-    // workgroups of an XCD do not all read the same W lines at once. The order of the
-    // step adds changes per workgroup; the error bound does not.
-    constexpr int kUnroll = 8;
-    constexpr int kOuter = kSlice / (32 * kUnroll);
-    const int start = static_cast<int>(blockIdx.x % kOuter);
-    u32x4 next[kUnroll];
+    if constexpr (!kEarlyWalk) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      next[u] = *reinterpret_cast<const u32x4*>(brow + (start * kUnroll + u) * 512);
+      for (int u = 0; u < kUnroll; ++u) {
+        next[u] = *reinterpret_cast<const u32x4*>(brow + (start * kUnroll + u) * 512);
+      }
     }
     for (int step = 0; step < kOuter; ++step) {
       const int s0 = (start + step) % kOuter;
