@@ -127,6 +127,13 @@ def test_rows_past_the_position_never_enter_and_every_row_up_to_it_does():
     poisoned_v[:, 121:] = float("nan")
     again, _, _ = case.run(120, kc=poisoned_k, vc=poisoned_v)
     assert np.array_equal(base, again)
+    # A grid sized for the whole cache (as under graph capture) reads rows past the
+    # position before it knows the position; NaN and infinite rows there still drop out.
+    poisoned_k[:, 160:] = float("inf")
+    poisoned_v[:, 180:] = float("-inf")
+    for max_rows in (121, 160, 200):
+        again, _, _ = case.run(120, kc=poisoned_k, vc=poisoned_v, max_rows=max_rows)
+        assert np.array_equal(base, again), max_rows
     for row in (0, 31, 64, 119):
         moved = case.vc.clone()
         moved[:, row] += 4.0

@@ -66,7 +66,7 @@ def _router_inputs(rows, hidden, experts, seed):
 
 @pytest.mark.parametrize("rows,hidden,experts,k", [
     (4096, 2048, 128, 8), (1, 2048, 128, 8), (37, 2048, 128, 8), (300, 4096, 128, 8), (50, 2048, 256, 16),
-    (20, 4096, 256, 8),
+    (20, 4096, 256, 8), (45, 2048, 128, 1), (64, 2048, 128, 40), (19, 4096, 256, 64), (30, 2048, 128, 64),
 ])
 def test_residual_router_matches_oracle(rows, hidden, experts, k):
     print(f"residual_rms_router rows={rows} hidden={hidden} experts={experts} k={k}", flush=True)
