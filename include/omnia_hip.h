@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 5
+#define OMNIA_ABI_VERSION 6
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -210,6 +210,49 @@ int32_t omnia_moe_down_combine(const uint16_t* act, const uint16_t* weight, int6
                                int64_t hidden, int64_t inner, const int32_t* chosen,
                                const float* weights, int64_t k, const uint16_t* residual,
                                uint16_t* out, hipStream_t stream);
+
+/* Routed expert gate/up of one token over an affine-quantized stack (MLX's
+ * QuantizedSwitchLinear, mode "affine"), the interleaved layout, silu fused:
+ *   r = sum over groups of scale * sum_j x[j] q[j] + bias * sum_j x[j]     fp32
+ *   g = bf16(r[2n]), u = bf16(r[2n + 1]); with limit < +inf, g = min(g, limit) and
+ *   u = clip(u, -limit, limit); out[s, n] = bf16(bf16(g * bf16(1 / (1 + exp(-g)))) * u)
+ * x [hidden] bf16; weight [experts, 2 * inner, hidden * bits / 32] uint32 (each row a
+ * little-endian bit stream of bits-wide values); scales, biases [experts, 2 * inner,
+ * hidden / group_size] bf16; chosen [slots] int32; out [slots, inner] bf16. A non-null
+ * shared_weight ([2 * inner, ...], with its own scales, biases, width and group) serves the
+ * last slot, whose index is then not read. An index outside [0, experts) gives zeros.
+ * bits in {2, 3, 4, 5, 6, 8}, groups in {32, 64, 128} dividing hidden; hidden a multiple
+ * of 32, at most 16384; limit >= 0 or +inf (none).
+ * Replaces: core/kernels/gate_up/affine.py:24-191 (`AffineGateUp`, `moe_gateup_act`); Core
+ * chain core/kernels/gate_up/default.py:60-81 over QuantizedSwitchLinear.__call__
+ * (core/layers.py:183-197). */
+int32_t omnia_moe_gate_up_affine(const uint16_t* x, const uint32_t* weight, const uint16_t* scales,
+                                 const uint16_t* biases, int64_t experts, int64_t hidden,
+                                 int64_t inner, int64_t bits, int64_t group_size,
+                                 const int32_t* chosen, int64_t slots, float limit,
+                                 const uint32_t* shared_weight, const uint16_t* shared_scales,
+                                 const uint16_t* shared_biases, int64_t shared_bits,
+                                 int64_t shared_group_size, uint16_t* out, hipStream_t stream);
+
+/* Routed expert down/combine of one token over an affine-quantized stack:
+ *   t[s, n] = sum over groups of scale * sum_i act[s, i] q[i] + bias * sum_i act[s, i]   fp32
+ *   acc[n] = sum over s in order of bf16(bf16(t[s, n]) * weights[s])                      fp32
+ *   out[n] = bf16(bf16(acc[n]) + residual[n])   (no add when residual is null)
+ * act [slots, inner] bf16; weight [experts, hidden, inner * bits / 32] uint32; scales,
+ * biases [experts, hidden, inner / group_size] bf16; chosen [slots] int32; weights [slots]
+ * fp32; residual, out [hidden] bf16. The shared leaf serves the last slot as in
+ * omnia_moe_gate_up_affine.
+ * inner a multiple of 32, at most 1536, divisible by the groups; 1 <= slots <= 16.
+ * Replaces: core/kernels/down_combine/affine.py:17-178 (`AffineDownCombine`,
+ * `moe_down_combine`); Core chain core/kernels/down_combine/default.py:43-58. */
+int32_t omnia_moe_down_combine_affine(const uint16_t* act, const uint32_t* weight,
+                                      const uint16_t* scales, const uint16_t* biases,
+                                      int64_t experts, int64_t hidden, int64_t inner, int64_t bits,
+                                      int64_t group_size, const int32_t* chosen,
+                                      const float* weights, int64_t slots, const uint16_t* residual,
+                                      const uint32_t* shared_weight, const uint16_t* shared_scales,
+                                      const uint16_t* shared_biases, int64_t shared_bits,
+                                      int64_t shared_group_size, uint16_t* out, hipStream_t stream);
 
 /* Dense SwiGLU MLP of one token, first half: the fused gate||up projection with the
  * SwiGLU applied in bf16 steps,

@@ -1,0 +1,473 @@
+// Routed expert MLP of a one-token step over affine-quantized expert stacks (MLX's
+// `QuantizedSwitchLinear`, mode "affine"): gate/up with the SwiGLU applied, then
+// down/combine, the interleaved layout of the reference's affine kernels.
+//
+// Format (core/layers.py:164-197; decoded as core/kernels/shared/affine.py:9-58 reads it):
+// a row is one little-endian bit stream of `bits`-wide values (value j at bit j * bits,
+// straddling two words at 3, 5 and 6 bits), packed in uint32 words; scales and biases are
+// bf16 per group of `group` values; w = scale * q + bias.
+//
+// Arithmetic:
+//   gate_up (core/kernels/gate_up/affine.py:24-95): per row r = sum over groups of
+//     scale * sum_j x_j q_j + bias * sum_j x_j (fp32, any order); rows 2n and 2n + 1 are
+//     the gate and up of output n; g = T(r_gate), u = T(r_up), clamped when a limit is
+//     declared (gate capped above, up clipped both ways);
+//     y = T(T(g * T(1 / (1 + exp(-g)))) * u), each operation in fp32.
+//   down_combine (core/kernels/down_combine/affine.py:17-70): t_e the same dot product over
+//     the activation row of slot e; acc = sum over slots in order of T(fp32(T(t_e) * w_e))
+//     in fp32; y = T(fp32(T(acc) + residual)).
+// With a shared expert declared, the last slot reads the shared leaf, on its own width and
+// group (gate_up/affine.py:36-49, down_combine/affine.py:29-44); its index is not read.
+// An expert id outside [0, experts) gives zero rows.
+//
+// Decoding. A lane takes 32 consecutive values of a row at a time: `bits` words, one
+// quantization group (groups are multiples of 32). For widths up to 6, a value q OR-ed
+// into the bf16 pattern of 128.0 (0x4300) is the bf16 value 128 + q exactly (the bf16 step
+// at 128 is 1), so two values go into one `v_dot2_f32_bf16` against a pair of activations;
+// the 128 * sum(x) this adds comes back out through the bias term:
+// scale * dot + (bias - 128 * scale) * sum(x). At 4 bits a word's pairs are its nibble
+// fields i and i + 4 (mask 0x000F000F), at 2 bits fields i and i + 8, so the activations
+// are paired to match once per lane; at 3, 5 and 6 bits consecutive values pair up. At 8
+// bits the bytes convert to fp32 (exact), whose high halves are their bf16 values.
+//
+// gate_up: a wave owns kPairsPerWave gate/up pairs of one slot (8 consecutive rows of the
+// interleaved matrix) and streams them together; x is read per 32-value chunk from L2.
+// down_combine: a workgroup owns kDownRows output rows with one wave per slot; eight lanes
+// share a row, each taking every eighth chunk of it, all of its weight words loaded before
+// any arithmetic; the slots' terms meet in LDS and are summed in slot order.
+#include "common.hpp"
+#include "host.hpp"
+
+namespace omnia {
+namespace {
+
+constexpr int kChunk = 32;                // values per lane per step (`bits` words)
+constexpr int kPairsPerWave = 4;          // gate_up: gate/up pairs per wave
+constexpr int kGateWaves = 4;             // gate_up: waves per workgroup
+constexpr int kDownRows = 8;              // down: output rows per workgroup
+constexpr int kLanesPerRow = kWave / kDownRows;
+constexpr int kMaxDownSteps = 6;          // down: chunks per lane, inner <= 8 * 6 * 32
+constexpr int kMaxDownSlots = 16;         // down: one wave per slot
+constexpr uint32_t kMagic = 0x43004300u;  // the bf16 pair (128, 128)
+
+struct Leaf {
+  const uint32_t* weight;  // [experts, rows, in * bits / 32], or [rows, ...] when shared
+  const uint16_t* scales;  // [experts, rows, in / group]
+  const uint16_t* biases;
+  int bits;
+  int group;
+};
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                         false);
+}
+
+// Value j of a 32-value chunk held in B words (j is a constant once unrolled).
+template <int B>
+__device__ __forceinline__ uint32_t field(const uint32_t (&w)[B], int j) {
+  const int bit = j * B;
+  const int d = bit >> 5;
+  const int s = bit & 31;
+  uint32_t v = w[d] >> s;
+  if (s + B > 32) v |= w[d + 1] << (32 - s);
+  return v & ((1u << B) - 1u);
+}
+
+// The chunk's B words, nontemporal (each weight byte is read once per step).
+template <int B>
+__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t (&w)[B]) {
+  if constexpr (B == 4 || B == 8) {
+#pragma unroll
+    for (int i = 0; i < B / 4; ++i) {
+      const u32x4 v = load_nt(reinterpret_cast<const u32x4*>(p) + i);
+      w[4 * i] = v.x;
+      w[4 * i + 1] = v.y;
+      w[4 * i + 2] = v.z;
+      w[4 * i + 3] = v.w;
+    }
+  } else if constexpr (B == 2 || B == 6) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int i = 0; i < B / 2; ++i) {
+      const u32x2 v = load_nt(reinterpret_cast<const u32x2*>(p) + i);
+      w[2 * i] = v.x;
+      w[2 * i + 1] = v.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < B; ++i) w[i] = load_nt(p + i);
+  }
+}
+
+// A lane's 32 activations (16 bf16 pairs in memory order) paired the way the B-bit
+// decoder pairs its values, and their fp32 sum.
+template <int B>
+__device__ __forceinline__ float pair_x(const u32x4 (&raw)[4], uint32_t (&xq)[16]) {
+  uint32_t xp[16];
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xp[4 * i] = raw[i].x;
+    xp[4 * i + 1] = raw[i].y;
+    xp[4 * i + 2] = raw[i].z;
+    xp[4 * i + 3] = raw[i].w;
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) sum += bf16_lo(xp[m]) + bf16_hi(xp[m]);
+  constexpr int kSpan = B == 4 ? 8 : B == 2 ? 16 : 0;  // values per word
+  if constexpr (kSpan != 0) {
+    // Word d's pair i is values (kSpan d + i, kSpan d + i + kSpan / 2).
+#pragma unroll
+    for (int d = 0; d < 32 / kSpan; ++d) {
+#pragma unroll
+      for (int i = 0; i < kSpan / 2; ++i) {
+        const uint32_t a = xp[(kSpan * d + i) / 2];
+        const uint32_t b = xp[(kSpan * d + i + kSpan / 2) / 2];
+        xq[kSpan / 2 * d + i] = (i % 2 == 0) ? ((a & 0xFFFFu) | (b << 16)) : ((a >> 16) | (b & 0xFFFF0000u));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 16; ++m) xq[m] = xp[m];
+  }
+  return sum;
+}
+
+// sum_j x_j (q_j + offset) over one chunk; offset is 128 below 8 bits, 0 at 8.
+template <int B>
+__device__ __forceinline__ float chunk_dot(const uint32_t (&w)[B], const uint32_t (&xq)[16]) {
+  float acc = 0.0f;
+  if constexpr (B == 4) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = dot2(((w[d] >> (4 * i)) & 0x000F000Fu) | kMagic, xq[4 * d + i], acc);
+    }
+  } else if constexpr (B == 2) {
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = dot2(((w[d] >> (2 * i)) & 0x00030003u) | kMagic, xq[8 * d + i], acc);
+    }
+  } else if constexpr (B == 8) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float lo = static_cast<float>((w[d] >> (16 * h)) & 0xFFu);
+        const float hi = static_cast<float>((w[d] >> (16 * h + 8)) & 0xFFu);
+        const uint32_t pair = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+        acc = dot2(pair, xq[2 * d + h], acc);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const uint32_t pair = field<B>(w, 2 * p) | (field<B>(w, 2 * p + 1) << 16) | kMagic;
+      acc = dot2(pair, xq[p], acc);
+    }
+  }
+  return acc;
+}
+
+// The chunk's contribution scale * sum(x q) + bias * sum(x), from chunk_dot's value.
+template <int B>
+__device__ __forceinline__ float chunk_term(float dot, float xsum, uint16_t scale_bits, uint16_t bias_bits) {
+  const float s = bf16_to_f32(scale_bits);
+  const float b = bf16_to_f32(bias_bits);
+  const float shifted = B == 8 ? b : b - 128.0f * s;
+  return __builtin_fmaf(s, dot, shifted * xsum);
+}
+
+// Sum over the wave, the same in every lane.
+__device__ __forceinline__ float wave_fsum(float v) {
+  v += __uint_as_float(dpp<kRowRor8>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowRor4>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowRor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowRor1>(__float_as_uint(v)));
+  uint32_t a, b;
+  row_pair(__float_as_uint(v), a, b);
+  v = __uint_as_float(a) + __uint_as_float(b);
+  half_pair(__float_as_uint(v), a, b);
+  return __uint_as_float(a) + __uint_as_float(b);
+}
+
+// Sum over each group of 8 lanes (8k .. 8k + 7), the same in each of them.
+__device__ __forceinline__ float octet_sum(float v) {
+  v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kQuadSwap2>(__float_as_uint(v)));
+  return v + __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
+}
+
+__device__ __forceinline__ bool uses_shared(const Leaf& shared, int slot, int slots) {
+  return shared.weight != nullptr && slot == slots - 1;
+}
+
+// ---- gate_up ------------------------------------------------------------------------
+
+struct GateUpArgs {
+  const uint16_t* x;       // [hidden]
+  Leaf routed;             // [experts, 2 * inner, hidden * bits / 32]
+  Leaf shared;             // [2 * inner, ...]; weight null when none is declared
+  const int32_t* chosen;   // [slots]
+  uint16_t* out;           // [slots, inner]
+  int64_t experts;
+  int hidden;
+  int inner;
+  int slots;
+  float limit;             // +inf: no clamp
+};
+
+template <int B>
+__device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const Leaf& leaf, int64_t row0, int rows,
+                                             int lane, float (&r)[2 * kPairsPerWave]) {
+  const int chunks = a.hidden / kChunk;
+  const int64_t words = static_cast<int64_t>(a.hidden) * B / 32;
+  const int groups = a.hidden / leaf.group;
+  for (int c = lane; c < chunks; c += kWave) {
+    uint32_t w[2 * kPairsPerWave][B];
+    uint16_t sb[2 * kPairsPerWave], bb[2 * kPairsPerWave];
+#pragma unroll
+    for (int i = 0; i < 2 * kPairsPerWave; ++i) {
+      if (i < rows) {
+        const int64_t row = row0 + i;
+        load_words<B>(leaf.weight + row * words + static_cast<int64_t>(c) * B, w[i]);
+        const int64_t g = row * groups + (c * kChunk) / leaf.group;
+        sb[i] = leaf.scales[g];
+        bb[i] = leaf.biases[g];
+      }
+    }
+    u32x4 raw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) raw[i] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[i];
+    uint32_t xq[16];
+    const float xsum = pair_x<B>(raw, xq);
+#pragma unroll
+    for (int i = 0; i < 2 * kPairsPerWave; ++i) {
+      if (i < rows) r[i] += chunk_term<B>(chunk_dot<B>(w[i], xq), xsum, sb[i], bb[i]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(GateUpArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int slot = blockIdx.y;
+  const int pair0 = (blockIdx.x * kGateWaves + threadIdx.x / kWave) * kPairsPerWave;
+  if (pair0 >= a.inner) return;  // whole wave; no barrier follows
+  const int pairs = min(kPairsPerWave, a.inner - pair0);
+  uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + pair0;
+  const bool shared = uses_shared(a.shared, slot, a.slots);
+  const Leaf& leaf = shared ? a.shared : a.routed;
+  int64_t row0 = 2 * static_cast<int64_t>(pair0);
+  if (!shared) {
+    const int expert = a.chosen[slot];
+    if (expert < 0 || expert >= a.experts) {
+      if (lane < pairs) out[lane] = 0;
+      return;
+    }
+    row0 += static_cast<int64_t>(expert) * 2 * a.inner;
+  }
+  float r[2 * kPairsPerWave];
+#pragma unroll
+  for (int i = 0; i < 2 * kPairsPerWave; ++i) r[i] = 0.0f;
+  switch (leaf.bits) {  // wave-uniform
+    case 2: gate_up_rows<2>(a, leaf, row0, 2 * pairs, lane, r); break;
+    case 3: gate_up_rows<3>(a, leaf, row0, 2 * pairs, lane, r); break;
+    case 4: gate_up_rows<4>(a, leaf, row0, 2 * pairs, lane, r); break;
+    case 5: gate_up_rows<5>(a, leaf, row0, 2 * pairs, lane, r); break;
+    case 6: gate_up_rows<6>(a, leaf, row0, 2 * pairs, lane, r); break;
+    default: gate_up_rows<8>(a, leaf, row0, 2 * pairs, lane, r); break;
+  }
+#pragma unroll
+  for (int p = 0; p < kPairsPerWave; ++p) {
+    float g = round_bf16(wave_fsum(r[2 * p]));
+    float u = round_bf16(wave_fsum(r[2 * p + 1]));
+    if (a.limit < __builtin_inff()) {
+      g = fminf(g, a.limit);
+      u = fminf(fmaxf(u, -a.limit), a.limit);
+    }
+    const float den = 1.0f + expf(-g);
+    const float sig = round_bf16(1.0f / den);
+    const float act = round_bf16(g * sig);
+    if (lane == p && p < pairs) out[p] = f32_to_bf16(act * u);
+  }
+}
+
+// ---- down_combine -------------------------------------------------------------------
+
+struct DownArgs {
+  const uint16_t* act;      // [slots, inner]
+  Leaf routed;              // [experts, hidden, inner * bits / 32]
+  Leaf shared;              // [hidden, ...]; weight null when none is declared
+  const int32_t* chosen;    // [slots]
+  const float* weights;     // [slots]
+  const uint16_t* residual; // [hidden] or null
+  uint16_t* out;            // [hidden]
+  int64_t experts;
+  int hidden;
+  int inner;
+  int slots;
+};
+
+// The dot product of the lane's row (lane / 8) over the chunks part, part + 8, ... of
+// the slot's activation row, all weight words in flight before the first multiply.
+template <int B>
+__device__ __forceinline__ float down_row(const DownArgs& a, const Leaf& leaf, int64_t row, int slot,
+                                          int part) {
+  const int chunks = a.inner / kChunk;
+  const int64_t words = static_cast<int64_t>(a.inner) * B / 32;
+  const int groups = a.inner / leaf.group;
+  uint32_t w[kMaxDownSteps][B];
+  uint16_t sb[kMaxDownSteps], bb[kMaxDownSteps];
+#pragma unroll
+  for (int i = 0; i < kMaxDownSteps; ++i) {
+    const int c = part + kLanesPerRow * i;
+    if (c < chunks) {
+      load_words<B>(leaf.weight + row * words + static_cast<int64_t>(c) * B, w[i]);
+      const int64_t g = row * groups + (c * kChunk) / leaf.group;
+      sb[i] = leaf.scales[g];
+      bb[i] = leaf.biases[g];
+    }
+  }
+  const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kMaxDownSteps; ++i) {
+    const int c = part + kLanesPerRow * i;
+    if (c < chunks) {
+      u32x4 raw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) raw[j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
+      uint32_t xq[16];
+      const float xsum = pair_x<B>(raw, xq);
+      acc += chunk_term<B>(chunk_dot<B>(w[i], xq), xsum, sb[i], bb[i]);
+    }
+  }
+  return acc;
+}
+
+__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(DownArgs a) {
+  __shared__ float partial[kMaxDownSlots][kDownRows];
+  const int lane = threadIdx.x % kWave;
+  const int slot = threadIdx.x / kWave;   // one wave per slot
+  const int row_base = blockIdx.x * kDownRows;
+  const int r = lane / kLanesPerRow;
+  const int part = lane % kLanesPerRow;
+  const bool row_valid = row_base + r < a.hidden;
+  const bool shared = uses_shared(a.shared, slot, a.slots);
+  const Leaf& leaf = shared ? a.shared : a.routed;
+  bool valid = true;
+  int64_t row = row_base + r;
+  if (!shared) {
+    const int expert = a.chosen[slot];
+    valid = expert >= 0 && expert < a.experts;
+    row += static_cast<int64_t>(valid ? expert : 0) * a.hidden;
+  }
+  float t = 0.0f;
+  if (valid && row_valid) {  // row_valid is uniform over the lane's octet
+    switch (leaf.bits) {  // wave-uniform
+      case 2: t = down_row<2>(a, leaf, row, slot, part); break;
+      case 3: t = down_row<3>(a, leaf, row, slot, part); break;
+      case 4: t = down_row<4>(a, leaf, row, slot, part); break;
+      case 5: t = down_row<5>(a, leaf, row, slot, part); break;
+      case 6: t = down_row<6>(a, leaf, row, slot, part); break;
+      default: t = down_row<8>(a, leaf, row, slot, part); break;
+    }
+  }
+  t = octet_sum(t);
+  if (part == 0) {
+    partial[slot][r] = valid ? round_bf16(round_bf16(t) * a.weights[slot]) : 0.0f;
+  }
+  __syncthreads();
+  if (threadIdx.x < kDownRows && row_base + static_cast<int>(threadIdx.x) < a.hidden) {
+    const int n = row_base + threadIdx.x;
+    float sum = 0.0f;
+    for (int j = 0; j < a.slots; ++j) sum += partial[j][threadIdx.x];
+    float out = round_bf16(sum);
+    if (a.residual != nullptr) out = out + bf16_to_f32(a.residual[n]);
+    a.out[n] = f32_to_bf16(out);
+  }
+}
+
+bool valid_format(int64_t bits, int64_t group) {
+  return (bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8) &&
+         (group == 32 || group == 64 || group == 128);
+}
+
+}  // namespace
+}  // namespace omnia
+
+extern "C" int32_t omnia_moe_gate_up_affine(
+    const uint16_t* x, const uint32_t* weight, const uint16_t* scales, const uint16_t* biases,
+    int64_t experts, int64_t hidden, int64_t inner, int64_t bits, int64_t group_size,
+    const int32_t* chosen, int64_t slots, float limit, const uint32_t* shared_weight,
+    const uint16_t* shared_scales, const uint16_t* shared_biases, int64_t shared_bits,
+    int64_t shared_group_size, uint16_t* out, hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), "moe_gate_up_affine: bad expert count");
+  OMNIA_REQUIRE(hidden > 0 && hidden % kChunk == 0 && hidden <= 16384,
+                "moe_gate_up_affine: hidden must be a multiple of 32 in [32, 16384]");
+  OMNIA_REQUIRE(inner > 0 && inner < (int64_t{1} << 24), "moe_gate_up_affine: bad inner size");
+  OMNIA_REQUIRE(valid_format(bits, group_size) && hidden % group_size == 0,
+                "moe_gate_up_affine: bits must be 2, 3, 4, 5, 6 or 8 and the group 32, 64 or 128, dividing hidden");
+  OMNIA_REQUIRE(slots >= 0 && slots <= 1024, "moe_gate_up_affine: slots must be in [0, 1024]");
+  OMNIA_REQUIRE(!(limit < 0.0f), "moe_gate_up_affine: the limit must be non-negative (+inf: none)");
+  if (slots == 0) return 0;
+  OMNIA_REQUIRE(x && weight && scales && biases && chosen && out, "moe_gate_up_affine: null pointer");
+  OMNIA_REQUIRE(aligned16(x) && aligned16(weight), "moe_gate_up_affine: x and weight must be 16-byte aligned");
+  if (shared_weight != nullptr) {
+    OMNIA_REQUIRE(shared_scales && shared_biases, "moe_gate_up_affine: shared leaf without scales or biases");
+    OMNIA_REQUIRE(valid_format(shared_bits, shared_group_size) && hidden % shared_group_size == 0,
+                  "moe_gate_up_affine: bad shared width or group");
+    OMNIA_REQUIRE(aligned16(shared_weight), "moe_gate_up_affine: the shared weight must be 16-byte aligned");
+  }
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  GateUpArgs a{x,
+               Leaf{weight, scales, biases, static_cast<int>(bits), static_cast<int>(group_size)},
+               Leaf{shared_weight, shared_scales, shared_biases, static_cast<int>(shared_bits),
+                    static_cast<int>(shared_group_size)},
+               chosen, out, experts, static_cast<int>(hidden), static_cast<int>(inner),
+               static_cast<int>(slots), limit};
+  const int64_t waves = (inner + kPairsPerWave - 1) / kPairsPerWave;
+  const dim3 grid(static_cast<unsigned>((waves + kGateWaves - 1) / kGateWaves), static_cast<unsigned>(slots));
+  moe_gate_up_affine_kernel<<<grid, kGateWaves * kWave, 0, stream>>>(a);
+  return launched("moe_gate_up_affine");
+}
+
+extern "C" int32_t omnia_moe_down_combine_affine(
+    const uint16_t* act, const uint32_t* weight, const uint16_t* scales, const uint16_t* biases,
+    int64_t experts, int64_t hidden, int64_t inner, int64_t bits, int64_t group_size,
+    const int32_t* chosen, const float* weights, int64_t slots, const uint16_t* residual,
+    const uint32_t* shared_weight, const uint16_t* shared_scales, const uint16_t* shared_biases,
+    int64_t shared_bits, int64_t shared_group_size, uint16_t* out, hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), "moe_down_combine_affine: bad expert count");
+  OMNIA_REQUIRE(hidden > 0 && hidden < (int64_t{1} << 24), "moe_down_combine_affine: bad hidden size");
+  OMNIA_REQUIRE(inner > 0 && inner % kChunk == 0 && inner <= kLanesPerRow * kMaxDownSteps * kChunk,
+                "moe_down_combine_affine: inner must be a multiple of 32 in [32, 1536]");
+  OMNIA_REQUIRE(valid_format(bits, group_size) && inner % group_size == 0,
+                "moe_down_combine_affine: bits must be 2, 3, 4, 5, 6 or 8 and the group 32, 64 or 128, dividing inner");
+  OMNIA_REQUIRE(slots > 0 && slots <= kMaxDownSlots, "moe_down_combine_affine: slots must be in [1, 16]");
+  OMNIA_REQUIRE(act && weight && scales && biases && chosen && weights && out,
+                "moe_down_combine_affine: null pointer");
+  OMNIA_REQUIRE(aligned16(act) && aligned16(weight), "moe_down_combine_affine: act and weight must be 16-byte aligned");
+  if (shared_weight != nullptr) {
+    OMNIA_REQUIRE(shared_scales && shared_biases, "moe_down_combine_affine: shared leaf without scales or biases");
+    OMNIA_REQUIRE(valid_format(shared_bits, shared_group_size) && inner % shared_group_size == 0,
+                  "moe_down_combine_affine: bad shared width or group");
+    OMNIA_REQUIRE(aligned16(shared_weight), "moe_down_combine_affine: the shared weight must be 16-byte aligned");
+  }
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  DownArgs a{act,
+             Leaf{weight, scales, biases, static_cast<int>(bits), static_cast<int>(group_size)},
+             Leaf{shared_weight, shared_scales, shared_biases, static_cast<int>(shared_bits),
+                  static_cast<int>(shared_group_size)},
+             chosen, weights, residual, out, experts, static_cast<int>(hidden),
+             static_cast<int>(inner), static_cast<int>(slots)};
+  const dim3 grid(static_cast<unsigned>((hidden + kDownRows - 1) / kDownRows));
+  moe_down_affine_kernel<<<grid, static_cast<unsigned>(slots * kWave), 0, stream>>>(a);
+  return launched("moe_down_combine_affine");
+}

@@ -422,6 +422,132 @@ def moe_down_combine(
     return out
 
 
+AFFINE_BITS = (2, 3, 4, 5, 6, 8)
+AFFINE_GROUPS = (32, 64, 128)
+
+
+@dataclass(frozen=True)
+class AffineLeaf:
+    """One affine-quantized matrix set as the kernels read it: weight [..., rows,
+    features * bits / 32] (int32 or uint32 words, each row a little-endian bit stream),
+    scales and biases [..., rows, features / group] bf16."""
+
+    weight: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+    bits: int
+    group: int
+
+    @property
+    def features(self) -> int:
+        return self.weight.shape[-1] * 32 // self.bits
+
+    def check(self, rows: int, features: int, stacked: bool, name: str) -> None:
+        _require(self.bits in AFFINE_BITS and self.group in AFFINE_GROUPS,
+                 f"{name}: bits must be one of {AFFINE_BITS} and the group one of {AFFINE_GROUPS}")
+        _require(features % self.group == 0, f"{name}: the group must divide {features}")
+        dims = 3 if stacked else 2
+        _require(self.weight.dim() == dims and self.scales.dim() == dims and self.biases.dim() == dims,
+                 f"{name}: expected {dims}-D weight, scales and biases")
+        _require(self.weight.dtype in (torch.int32, torch.uint32), f"{name}: weight must hold 32-bit words")
+        _require(self.weight.is_contiguous() and self.weight.data_ptr() % 16 == 0,
+                 f"{name}: weight must be contiguous and 16-byte aligned")
+        lead = tuple(self.weight.shape[:-2])
+        _require(tuple(self.weight.shape[-2:]) == (rows, features * self.bits // 32),
+                 f"{name}: weight shape {tuple(self.weight.shape)}")
+        for t, part in ((self.scales, "scales"), (self.biases, "biases")):
+            _require(t.dtype == BF16 and t.is_contiguous(), f"{name}: {part} must be contiguous bf16")
+            _require(tuple(t.shape) == lead + (rows, features // self.group),
+                     f"{name}: {part} shape {tuple(t.shape)}")
+
+    def tensors(self) -> list[torch.Tensor]:
+        return [self.weight, self.scales, self.biases]
+
+
+def _shared_args(shared: AffineLeaf | None) -> tuple:
+    if shared is None:
+        return (None, None, None, 0, 0)
+    return (shared.weight.data_ptr(), shared.scales.data_ptr(), shared.biases.data_ptr(),
+            shared.bits, shared.group)
+
+
+def moe_gate_up_affine(
+    x: torch.Tensor,
+    leaf: AffineLeaf,
+    chosen: torch.Tensor,
+    *,
+    limit: float | None = None,
+    shared: AffineLeaf | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One token's routed gate/up over an affine-quantized stack, the interleaved layout,
+    silu fused; see `omnia_moe_gate_up_affine`. x [hidden] bf16, leaf [experts, 2 * inner,
+    ...], chosen [slots] int32 (with `shared`, the last slot is the shared leaf's) ->
+    [slots, inner] bf16."""
+    _require(x.dim() == 1 or x.numel() == x.shape[-1], "moe_gate_up_affine: x must be one row")
+    hidden = x.shape[-1]
+    _dense(x, BF16, "x")
+    _require(leaf.weight.dim() == 3 and leaf.weight.shape[1] % 2 == 0,
+             "moe_gate_up_affine: weight must be [experts, 2 * inner, words]")
+    experts, rows = leaf.weight.shape[0], leaf.weight.shape[1]
+    leaf.check(rows, hidden, True, "moe_gate_up_affine")
+    if shared is not None:
+        shared.check(rows, hidden, False, "moe_gate_up_affine shared")
+    _require(chosen.dtype == torch.int32 and chosen.is_contiguous() and chosen.dim() == 1,
+             "moe_gate_up_affine: chosen must be contiguous int32 [slots]")
+    _require(limit is None or limit >= 0, "moe_gate_up_affine: the limit must be non-negative")
+    tensors = [x, chosen, *leaf.tensors(), *(shared.tensors() if shared is not None else [])]
+    _require(on_rocm(*tensors), "moe_gate_up_affine: tensors must share one ROCm device")
+    slots = chosen.numel()
+    out = _out(out, x, (slots, rows // 2), BF16, "out")
+    call("omnia_moe_gate_up_affine", x.data_ptr(), leaf.weight.data_ptr(), leaf.scales.data_ptr(),
+         leaf.biases.data_ptr(), experts, hidden, rows // 2, leaf.bits, leaf.group,
+         chosen.data_ptr(), slots, float("inf") if limit is None else float(limit),
+         *_shared_args(shared), out.data_ptr(), _stream(x))
+    return out
+
+
+def moe_down_combine_affine(
+    act: torch.Tensor,
+    leaf: AffineLeaf,
+    chosen: torch.Tensor,
+    weights: torch.Tensor,
+    residual: torch.Tensor | None = None,
+    *,
+    shared: AffineLeaf | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One token's routed down projection over an affine-quantized stack, the routing
+    weights, the slot sum and the residual; see `omnia_moe_down_combine_affine`. act
+    [slots, inner] bf16, leaf [experts, hidden, ...], chosen [slots] int32, weights [slots]
+    fp32, residual [hidden] bf16 or None -> [hidden] bf16."""
+    _require(leaf.weight.dim() == 3, "moe_down_combine_affine: weight must be [experts, hidden, words]")
+    experts, hidden = leaf.weight.shape[0], leaf.weight.shape[1]
+    slots = chosen.numel()
+    _require(act.dim() == 2 and act.shape[0] == slots, "moe_down_combine_affine: act must be [slots, inner]")
+    inner = act.shape[1]
+    _dense(act, BF16, "act")
+    leaf.check(hidden, inner, True, "moe_down_combine_affine")
+    if shared is not None:
+        shared.check(hidden, inner, False, "moe_down_combine_affine shared")
+    _require(chosen.dtype == torch.int32 and chosen.is_contiguous(), "moe_down_combine_affine: chosen int32")
+    _require(weights.dtype == F32 and weights.is_contiguous() and weights.numel() == slots,
+             "moe_down_combine_affine: weights must be contiguous fp32 [slots]")
+    tensors = [act, chosen, weights, *leaf.tensors(), *(shared.tensors() if shared is not None else [])]
+    if residual is not None:
+        _require(residual.numel() == hidden and residual.dtype == BF16 and residual.is_contiguous(),
+                 "moe_down_combine_affine: residual must be contiguous bf16 [hidden]")
+        tensors.append(residual)
+    _require(on_rocm(*tensors), "moe_down_combine_affine: tensors must share one ROCm device")
+    out = _out(out, act, (hidden,), BF16, "out")
+    call("omnia_moe_down_combine_affine", act.data_ptr(), leaf.weight.data_ptr(),
+         leaf.scales.data_ptr(), leaf.biases.data_ptr(), experts, hidden, inner, leaf.bits,
+         leaf.group, chosen.data_ptr(), weights.data_ptr(), slots,
+         residual.data_ptr() if residual is not None else None, *_shared_args(shared),
+         out.data_ptr(), _stream(act))
+    return out
+
+
 def dense_gate_up_swiglu(
     x: torch.Tensor,
     fused_weight: torch.Tensor,
