@@ -5,6 +5,13 @@ down-projected by its expert, routing-weighted, summed and residual-added.
 Mirrors core/kernels/down_combine/__init__.py and kernel.py (`DownCombine`,
 `DownCombineStrategy`, `Layout`).
 
+- `HipAffineDownCombine` (`omnia_moe_down_combine_affine`, csrc/moe_affine.hip) serves
+  what the reference's `AffineDownCombine` serves (core/kernels/down_combine/affine.py:
+  97-178): an affine-quantized stack under the `interleaved` layout (the activation rows
+  arrive activated), no bias, a shared expert on the last slot when it is an affine
+  `QuantizedLinearLeaf`, inner a multiple of 32 up to 1536, at most 16 slots (more go to
+  the Core chain). Per slot bf16(bf16(dot) * weight), the slot sum in fp32 in slot
+  order, then the residual add, in one dispatch.
 - `HipDenseDownCombine` (`omnia_moe_down_combine`, csrc/moe.hip) serves what the
   reference's `DenseDownCombine` serves (core/kernels/down_combine/dense.py:69-109): a
   dense bf16 stack [experts, hidden, inner] under the `blocked` layout (the pair block
@@ -13,7 +20,8 @@ Mirrors core/kernels/down_combine/__init__.py and kernel.py (`DownCombine`,
   activation in fp32, bf16(dot * weight) per expert, then the expert sum and the
   residual add in bf16, all in one dispatch.
 - `DefaultDownCombine` is the Core chain (core/kernels/down_combine/default.py:24-58): the
-  activation in bf16 ops, the gathered matrices times the rows, the routing weights,
+  activation in bf16 ops, the gathered matrices (dequantized for a quantized leaf) times
+  the rows with an fp32 sum, the routing weights,
   the sum and the residual in torch ops. It accepts everything.
 """
 
@@ -26,13 +34,15 @@ import torch
 
 from ...runtime import ops
 from .._device import hip_device
+from ..gate_up.routed import affine_leaf
+from ..leaf import QuantizedLinearLeaf, QuantizedSwitchLinearLeaf
 from ..resolve import resolve
 
 Layout = Literal["interleaved", "blocked"]
 MAX_SLOTS = 16
 
-__all__ = ["DefaultDownCombine", "DownCombine", "DownCombineStrategy", "HipDenseDownCombine",
-           "Layout", "dense_down_applies"]
+__all__ = ["DefaultDownCombine", "DownCombine", "DownCombineStrategy", "HipAffineDownCombine",
+           "HipDenseDownCombine", "Layout", "affine_down_applies", "dense_down_applies"]
 
 
 @runtime_checkable
@@ -47,16 +57,22 @@ def dense_down_applies(inner: int) -> bool:
     return 0 < inner <= 2048 and inner % 8 == 0
 
 
+def affine_down_applies(inner: int, group: int, bits: int) -> bool:
+    """Eight lanes share a row, each taking at most six 32-value steps of it."""
+    return (0 < inner <= 1536 and inner % 32 == 0 and group in ops.AFFINE_GROUPS
+            and inner % group == 0 and bits in ops.AFFINE_BITS)
+
+
 @dataclass(frozen=True)
 class DefaultDownCombine(DownCombineStrategy):
-    weight: torch.Tensor
+    leaf: object
     bias: torch.Tensor | None
     shared: Callable[[torch.Tensor], torch.Tensor] | None
     layout: Layout
 
     @classmethod
     def build(cls, leaf, *, hidden, inner, bias, shared, layout) -> "DefaultDownCombine":
-        return cls(leaf.weight, bias, shared, layout)
+        return cls(leaf, bias, shared, layout)
 
     def __call__(self, act, chosen, weights, residual):
         rows = act.reshape(chosen.shape[0], -1)
@@ -65,8 +81,8 @@ class DefaultDownCombine(DownCombineStrategy):
             rows = gate * torch.sigmoid(gate) * up
         routed = chosen if self.shared is None else chosen[:-1]
         k = routed.shape[0]
-        matrices = self.weight[routed.long()]
-        down = (matrices.float() @ rows[:k].float()[..., None]).squeeze(-1).to(rows.dtype)
+        matrices = self.leaf.matrices(routed)
+        down = (matrices @ rows[:k].float()[..., None]).squeeze(-1).to(rows.dtype)
         if self.bias is not None:
             down = down + self.bias[routed.long()]
         out = (down * weights[:k, None]).sum(dim=0)
@@ -91,7 +107,7 @@ class HipDenseDownCombine(DownCombineStrategy):
             return None
         if not hip_device(weight):
             return None
-        return cls(weight.contiguous(), DefaultDownCombine(weight, bias, shared, layout))
+        return cls(weight.contiguous(), DefaultDownCombine(leaf, bias, shared, layout))
 
     def __call__(self, act, chosen, weights, residual):
         k = chosen.numel()
@@ -106,7 +122,48 @@ class HipDenseDownCombine(DownCombineStrategy):
         )
 
 
-_STRATEGIES = (HipDenseDownCombine, DefaultDownCombine)
+@dataclass(frozen=True)
+class HipAffineDownCombine(DownCombineStrategy):
+    leaf: "ops.AffineLeaf"
+    shared: "ops.AffineLeaf | None"
+    fallback: DefaultDownCombine
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, bias, shared, layout) -> "HipAffineDownCombine | None":
+        if layout != "interleaved" or bias is not None:
+            return None
+        if not isinstance(leaf, QuantizedSwitchLinearLeaf):
+            return None
+        if not affine_down_applies(inner, leaf.group_size, leaf.bits):
+            return None
+        view = affine_leaf(leaf, hidden, inner, stacked=True)
+        if view is None:
+            return None
+        spare = None
+        if shared is not None:
+            if not isinstance(shared, QuantizedLinearLeaf) or not affine_down_applies(
+                    inner, shared.group_size, shared.bits):
+                return None
+            spare = affine_leaf(shared, hidden, inner, stacked=False)
+            if spare is None or spare.weight.device != view.weight.device:
+                return None
+        return cls(view, spare, DefaultDownCombine(leaf, bias, shared, layout))
+
+    def __call__(self, act, chosen, weights, residual):
+        slots = chosen.numel()
+        if slots == 0 or slots > MAX_SLOTS:  # one wave per slot in a workgroup
+            return self.fallback(act, chosen, weights, residual)
+        device = self.leaf.weight.device
+        return ops.moe_down_combine_affine(
+            act.reshape(slots, -1).to(torch.bfloat16).contiguous(), self.leaf,
+            chosen.to(device=device, dtype=torch.int32).contiguous().reshape(-1),
+            weights.to(device=device, dtype=torch.float32).contiguous().reshape(-1),
+            None if residual is None else residual.reshape(-1).to(torch.bfloat16).contiguous(),
+            shared=self.shared,
+        )
+
+
+_STRATEGIES = (HipAffineDownCombine, HipDenseDownCombine, DefaultDownCombine)
 
 
 class DownCombine(DownCombineStrategy):

@@ -1,7 +1,8 @@
 """Gate/up: the activation facade (`GateUpActivation`: `HipSwiGLU` ahead of the Core
 chain `DefaultGateUpActivation`) and the routed projection of a one-token step
-(`GateUp` in routed.py: `HipDenseGateUp` ahead of `DefaultGateUp`), each resolved by its
-declaration with the reference's first-build-wins rule."""
+(`GateUp` in routed.py: `HipAffineGateUp` and `HipDenseGateUp` ahead of
+`DefaultGateUp`), each resolved by its declaration with the reference's
+first-build-wins rule."""
 
 from __future__ import annotations
 
@@ -11,16 +12,18 @@ from ..resolve import resolve
 from .default import DefaultGateUpActivation, swiglu_core
 from .hip import HipSwiGLU, applies
 from .kernel import Activation, GateUpActivationStrategy, Layout, split
-from .routed import (DefaultGateUp, GateUp, GateUpStrategy, HipDenseGateUp, OrdinalRouting,
-                     dense_gate_up_applies)
+from .routed import (DefaultGateUp, GateUp, GateUpStrategy, HipAffineGateUp, HipDenseGateUp,
+                     OrdinalRouting, affine_gate_up_applies, dense_gate_up_applies)
 
 __all__ = [
     "DefaultGateUp",
     "DefaultGateUpActivation",
     "GateUp",
     "GateUpStrategy",
+    "HipAffineGateUp",
     "HipDenseGateUp",
     "OrdinalRouting",
+    "affine_gate_up_applies",
     "dense_gate_up_applies",
     "GateUpActivation",
     "GateUpActivationStrategy",

@@ -6,12 +6,19 @@ Mirrors core/kernels/gate_up/__init__.py and kernel.py (`GateUp`, `GateUpStrateg
 (activation, clamp, projection bias, layout, ordinal routing, a shared expert), and the
 first strategy whose `build` accepts the declaration serves it.
 
+- `HipAffineGateUp` (`omnia_moe_gate_up_affine`, csrc/moe_affine.hip) serves what the
+  reference's `AffineGateUp` serves (core/kernels/gate_up/affine.py:105-191): an
+  affine-quantized stack (`QuantizedSwitchLinearLeaf`, 2, 3, 4, 5, 6 or 8 bits, groups of
+  32, 64 or 128) under the `interleaved` layout, silu with the optional clamp, no bias
+  or ordinal routing, and a shared expert on the last slot when it is an affine
+  `QuantizedLinearLeaf` of its own width and group.
 - `HipDenseGateUp` (`omnia_moe_gate_up`, csrc/moe.hip) serves what the reference's
   `DenseGateUp` serves (core/kernels/gate_up/dense.py:75-119): a dense bf16 stack
   [experts, 2 * inner, hidden], the `blocked` layout (gate and up block-concatenated,
   handed on un-activated), silu, no clamp, bias, routing or shared expert.
 - `DefaultGateUp` is the Core chain (core/kernels/gate_up/default.py:31-81): the gathered
-  matrices times the row, then the declared epilogue in bf16 ops. It accepts everything.
+  matrices (dequantized for a quantized leaf) times the row with an fp32 sum, then the
+  declared epilogue in bf16 ops. It accepts everything.
 """
 
 from __future__ import annotations
@@ -23,6 +30,7 @@ import torch
 
 from ...runtime import ops
 from .._device import hip_device
+from ..leaf import QuantizedLinearLeaf, QuantizedSwitchLinearLeaf
 from ..resolve import resolve
 
 Activation = Literal["silu", "swiglu_oai"]
@@ -51,9 +59,34 @@ def dense_gate_up_applies(hidden: int) -> bool:
     return 0 < hidden <= 8192 and hidden % 8 == 0
 
 
+def affine_gate_up_applies(hidden: int, group: int, bits: int) -> bool:
+    """32 values per lane step, inside one quantization group."""
+    return (0 < hidden <= 16384 and hidden % 32 == 0 and group in ops.AFFINE_GROUPS
+            and hidden % group == 0 and bits in ops.AFFINE_BITS)
+
+
+def affine_leaf(leaf, rows: int, features: int, stacked: bool) -> "ops.AffineLeaf | None":
+    """The kernels' view of an affine leaf whose tensors they can read as they are, or None."""
+    wanted = QuantizedSwitchLinearLeaf if stacked else QuantizedLinearLeaf
+    if not isinstance(leaf, wanted) or leaf.mode != "affine" or leaf.biases is None:
+        return None
+    if leaf.bits not in ops.AFFINE_BITS or leaf.group_size not in ops.AFFINE_GROUPS:
+        return None
+    if features % leaf.group_size != 0:
+        return None
+    view = ops.AffineLeaf(leaf.weight, leaf.scales, leaf.biases, leaf.bits, leaf.group_size)
+    try:
+        view.check(rows, features, stacked, "affine leaf")
+    except ValueError:
+        return None
+    if not all(hip_device(t) for t in view.tensors()):
+        return None
+    return view
+
+
 @dataclass(frozen=True)
 class DefaultGateUp(GateUpStrategy):
-    weight: torch.Tensor
+    leaf: object
     activation: Activation
     limit: float | None
     bias: torch.Tensor | None
@@ -65,14 +98,14 @@ class DefaultGateUp(GateUpStrategy):
     def build(cls, leaf, *, hidden, inner, activation, limit, bias, layout, routing,
               shared) -> "DefaultGateUp":
         assert shared is None or routing is None
-        return cls(leaf.weight, activation, limit, bias, layout, routing, shared)
+        return cls(leaf, activation, limit, bias, layout, routing, shared)
 
     def __call__(self, row: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor:
         if self.routing is not None:
             chosen = self.routing.indices(chosen)
         routed = chosen if self.shared is None else chosen[:-1]
-        matrices = self.weight[routed.long()]
-        fused = (matrices.float() @ row.reshape(-1).float()).to(row.dtype)
+        matrices = self.leaf.matrices(routed)
+        fused = (matrices @ row.reshape(-1).float()).to(row.dtype)
         if self.bias is not None:
             fused = fused + self.bias[routed.long()]
         if self.shared is not None:
@@ -117,7 +150,42 @@ class HipDenseGateUp(GateUpStrategy):
         return ops.moe_gate_up(row.reshape(-1).contiguous(), self.weight, ids)
 
 
-_STRATEGIES = (HipDenseGateUp, DefaultGateUp)
+@dataclass(frozen=True)
+class HipAffineGateUp(GateUpStrategy):
+    leaf: "ops.AffineLeaf"
+    limit: float | None
+    shared: "ops.AffineLeaf | None"
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, activation, limit, bias, layout, routing,
+              shared) -> "HipAffineGateUp | None":
+        if layout != "interleaved" or routing is not None:
+            return None
+        if activation != "silu" or bias is not None or (limit is not None and not limit >= 0):
+            return None
+        if not isinstance(leaf, QuantizedSwitchLinearLeaf):
+            return None
+        if not affine_gate_up_applies(hidden, leaf.group_size, leaf.bits):
+            return None
+        view = affine_leaf(leaf, 2 * inner, hidden, stacked=True)
+        if view is None:
+            return None
+        spare = None
+        if shared is not None:
+            if not isinstance(shared, QuantizedLinearLeaf):
+                return None
+            spare = affine_leaf(shared, 2 * inner, hidden, stacked=False)
+            if spare is None or spare.weight.device != view.weight.device:
+                return None
+        return cls(view, limit, spare)
+
+    def __call__(self, row: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor:
+        ids = chosen.to(device=self.leaf.weight.device, dtype=torch.int32).contiguous().reshape(-1)
+        return ops.moe_gate_up_affine(row.reshape(-1).contiguous(), self.leaf, ids,
+                                      limit=self.limit, shared=self.shared)
+
+
+_STRATEGIES = (HipAffineGateUp, HipDenseGateUp, DefaultGateUp)
 
 
 class GateUp(GateUpStrategy):

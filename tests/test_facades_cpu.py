@@ -292,6 +292,92 @@ def test_moe_hip_bindings_decline_other_declarations():
         assert HipDenseDownCombine.build(down_leaf, **dict(dbase, **change)) is None, change
 
 
+@pytest.mark.parametrize("width", (2, 3, 4, 5, 6, 8))
+def test_torch_bit_stream_decoder_matches_the_oracle(width):
+    from mlx_omnia_amd.kernels.leaf import unpack_words
+    from oracle import affine
+
+    rng = np.random.default_rng(width)
+    words = rng.integers(0, 1 << 32, size=(3, 5, 4 * width), dtype=np.uint64).astype(np.uint32)
+    got = unpack_words(torch.from_numpy(words.view(np.int32)), width)
+    assert np.array_equal(got.numpy(), affine.unpack(words, width))
+
+
+def _affine_leaves(rng, experts, rows, features, bits, group):
+    from mlx_omnia_amd.kernels.leaf import QuantizedLinearLeaf, QuantizedSwitchLinearLeaf
+    from oracle import affine
+
+    words = rng.integers(0, 1 << 32, size=(experts, rows, features * bits // 32), dtype=np.uint64)
+    words = words.astype(np.uint32)
+    scale = 4.0 / ((1 << bits) * np.sqrt(features))
+    s = from_float(scale * (0.5 + rng.random((experts, rows, features // group))))
+    b = from_float(-to_f32(s) * ((1 << bits) - 1) / 2)
+    stack = affine.Stack(words, s, b, group, bits)
+    leaf = QuantizedSwitchLinearLeaf(torch.from_numpy(words.view(np.int32)), cpu(s), cpu(b), group, bits)
+    single = QuantizedLinearLeaf(leaf.weight[0], leaf.scales[0], leaf.biases[0], group, bits)
+    return stack, leaf, single
+
+
+@pytest.mark.parametrize("width", (3, 4, 8))
+def test_affine_moe_cpu_resolves_to_core_and_matches_oracle(width):
+    from mlx_omnia_amd.kernels.down_combine import DefaultDownCombine, DownCombine, HipAffineDownCombine
+    from mlx_omnia_amd.kernels.gate_up import DefaultGateUp, GateUp, HipAffineGateUp
+    from oracle import affine
+
+    experts, hidden, inner = 5, 128, 64
+    rng = np.random.default_rng(width)
+    gstack, gleaf, _ = _affine_leaves(rng, experts, 2 * inner, hidden, width, 32)
+    dstack, dleaf, _ = _affine_leaves(rng, experts, hidden, inner, width, 64)
+    gate_up = GateUp(gleaf, hidden=hidden, inner=inner)
+    down = DownCombine(dleaf, hidden=hidden, inner=inner)
+    assert isinstance(gate_up.strategy, DefaultGateUp) and isinstance(down.strategy, DefaultDownCombine)
+    assert HipAffineGateUp.build(gleaf, hidden=hidden, inner=inner, activation="silu", limit=None,
+                                 bias=None, layout="interleaved", routing=None, shared=None) is None
+    assert HipAffineDownCombine.build(dleaf, hidden=hidden, inner=inner, bias=None, shared=None,
+                                      layout="interleaved") is None
+    x = from_float(rng.standard_normal(hidden))
+    chosen = np.array([4, 0, 2], dtype=np.int32)
+    act_core = gate_up(cpu(x), torch.from_numpy(chosen))
+    # The Core chain's sigmoid is torch's, its dot an fp32 sum: one ulp from the oracle.
+    want_act = affine.gate_up(x, gstack, chosen)
+    assert ulp_distance(bits(act_core), want_act).max() <= 1
+    weights = to_f32(from_float(np.array([0.5, 0.3, 0.2])))
+    residual = from_float(rng.standard_normal(hidden))
+    out = down(act_core, torch.from_numpy(chosen), torch.from_numpy(weights).to(torch.bfloat16),
+               cpu(residual))
+    # The Core chain rounds the weighted rows and their sum at other points than the kernel.
+    assert_bf16_close(bits(out), affine.down_combine(bits(act_core), dstack, chosen, weights, residual),
+                      min_exact=0.8)
+
+
+def test_affine_core_chain_serves_the_shared_slot_and_the_clamp():
+    from mlx_omnia_amd.kernels.gate_up import GateUp
+    from oracle import affine
+
+    experts, hidden, inner = 4, 64, 32
+    rng = np.random.default_rng(12)
+    gstack, gleaf, _ = _affine_leaves(rng, experts, 2 * inner, hidden, 4, 32)
+    sstack, _, shared = _affine_leaves(rng, 1, 2 * inner, hidden, 2, 64)
+    x = from_float(2 * rng.standard_normal(hidden))
+    gate_up = GateUp(gleaf, hidden=hidden, inner=inner, limit=0.5, shared=shared)
+    got = gate_up(cpu(x), torch.tensor([3, 1, 7], dtype=torch.int32))
+    want = affine.gate_up(x, gstack, [3, 1, 7], limit=0.5,
+                          shared=affine.Stack(sstack.weight[0], sstack.scales[0], sstack.biases[0], 64, 2))
+    assert ulp_distance(bits(got), want).max() <= 1
+
+
+def test_affine_bindings_decline_other_declarations():
+    from mlx_omnia_amd.kernels.down_combine import affine_down_applies
+    from mlx_omnia_amd.kernels.gate_up import affine_gate_up_applies
+
+    assert affine_gate_up_applies(2048, 64, 4) and affine_gate_up_applies(96, 32, 3)
+    for args in ((2048, 16, 4), (2048, 64, 7), (1000, 32, 4), (2048 + 64, 128, 4), (32768, 32, 4)):
+        assert not affine_gate_up_applies(*args), args
+    assert affine_down_applies(768, 64, 4) and affine_down_applies(1536, 128, 8)
+    for args in ((2048, 64, 4), (768, 48, 4), (100, 32, 2), (768, 64, 1)):
+        assert not affine_down_applies(*args), args
+
+
 def test_ordinal_routing_keeps_the_best_keys_lowest_index_first():
     from mlx_omnia_amd.kernels.gate_up import OrdinalRouting
 

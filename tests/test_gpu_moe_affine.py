@@ -186,3 +186,67 @@ def test_shape_checks_raise_before_launch():
     act = to_device(from_float(rng.standard_normal((2, 2048))))
     with pytest.raises(ValueError):                           # inner past the kernel's 1536
         ops.moe_down_combine_affine(act, dleaf, _ids([0, 1]), f32_to_device(np.ones(2, np.float32)))
+
+
+def test_facades_resolve_to_the_affine_bindings_and_agree_with_the_core_chain():
+    from mlx_omnia_amd.kernels.down_combine import (DefaultDownCombine, DownCombine,
+                                                    HipAffineDownCombine)
+    from mlx_omnia_amd.kernels.gate_up import DefaultGateUp, GateUp, HipAffineGateUp
+    from mlx_omnia_amd.kernels.leaf import QuantizedLinearLeaf, QuantizedSwitchLinearLeaf
+
+    print("moe affine facades", flush=True)
+    rng = np.random.default_rng(120)
+    gstack, g = _leaf(rng, (EXPERTS,), 2 * INNER, HIDDEN, 4, 64)
+    dstack, d = _leaf(rng, (EXPERTS,), HIDDEN, INNER, 4, 64)
+    sstack, s = _leaf(rng, (), 2 * INNER, HIDDEN, 8, 128)
+    sdstack, sd = _leaf(rng, (), HIDDEN, INNER, 8, 128)
+    gleaf = QuantizedSwitchLinearLeaf(g.weight, g.scales, g.biases, 64, 4)
+    dleaf = QuantizedSwitchLinearLeaf(d.weight, d.scales, d.biases, 64, 4)
+    shared_gate = QuantizedLinearLeaf(s.weight, s.scales, s.biases, 128, 8)
+    shared_down = QuantizedLinearLeaf(sd.weight, sd.scales, sd.biases, 128, 8)
+    gate_up = GateUp(gleaf, hidden=HIDDEN, inner=INNER, shared=shared_gate)
+    down = DownCombine(dleaf, hidden=HIDDEN, inner=INNER, shared=shared_down)
+    assert isinstance(gate_up.strategy, HipAffineGateUp)
+    assert isinstance(down.strategy, HipAffineDownCombine)
+    core_gate_up = GateUp(gleaf, hidden=HIDDEN, inner=INNER, shared=shared_gate, reference=True)
+    core_down = DownCombine(dleaf, hidden=HIDDEN, inner=INNER, shared=shared_down, reference=True)
+    assert isinstance(core_gate_up.strategy, DefaultGateUp)
+    assert isinstance(core_down.strategy, DefaultDownCombine)
+    # A layout or a mode the kernels do not decode goes to the Core chain.
+    assert isinstance(GateUp(gleaf, hidden=HIDDEN, inner=INNER, layout="blocked").strategy, DefaultGateUp)
+    mx = QuantizedSwitchLinearLeaf(g.weight, g.scales, None, 64, 4, mode="mxfp4")
+    assert isinstance(GateUp(mx, hidden=HIDDEN, inner=INNER).strategy, DefaultGateUp)
+
+    x = from_float(rng.standard_normal(HIDDEN))
+    chosen = torch.tensor([2, 7, 0, 0], dtype=torch.int32, device="cuda")
+    act = gate_up(to_device(x), chosen)
+    want_act = affine.gate_up(x, gstack, [2, 7, 0, 0], shared=sstack)
+    assert_bf16_close(bits_of(act), want_act, min_exact=0.99)
+    assert_bf16_close(bits_of(core_gate_up(to_device(x), chosen)), want_act, min_exact=0.97)
+
+    weights = torch.tensor([0.4, 0.3, 0.2, 0.1], dtype=torch.bfloat16, device="cuda")
+    residual = from_float(rng.standard_normal(HIDDEN))
+    out = down(act, chosen, weights, to_device(residual))
+    want = affine.down_combine(bits_of(act), dstack, [2, 7, 0, 0], weights.float().cpu().numpy(),
+                               residual, shared=sdstack)
+    assert_bf16_close(bits_of(out), want, min_exact=0.99)
+    core = core_down(act, chosen, weights, to_device(residual))
+    assert_bf16_close(bits_of(core), want, min_exact=0.8)
+
+
+def test_down_facade_hands_more_than_16_slots_to_the_core_chain():
+    from mlx_omnia_amd.kernels.down_combine import DownCombine, HipAffineDownCombine
+    from mlx_omnia_amd.kernels.leaf import QuantizedSwitchLinearLeaf
+
+    rng = np.random.default_rng(130)
+    dstack, d = _leaf(rng, (EXPERTS,), HIDDEN, INNER, 4, 32)
+    down = DownCombine(QuantizedSwitchLinearLeaf(d.weight, d.scales, d.biases, 32, 4), hidden=HIDDEN,
+                       inner=INNER)
+    assert isinstance(down.strategy, HipAffineDownCombine)
+    chosen = list(rng.integers(0, EXPERTS, size=20))
+    act = from_float(rng.standard_normal((20, INNER)))
+    weights = np.full(20, 0.05, dtype=np.float32)
+    out = down(to_device(act), torch.tensor(chosen, dtype=torch.int32, device="cuda"),
+               f32_to_device(weights), None)
+    want = affine.down_combine(act, dstack, chosen, weights, None)
+    assert_bf16_close(bits_of(out.to(torch.bfloat16)), want, min_exact=0.5)
