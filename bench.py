@@ -338,6 +338,67 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.moe_down_combine(a["act"], a["dn"], a["ids"], a["w"], a["r"], out=a["o"]),
     ))
 
+    # The same routed MLP over 4-bit affine stacks, groups of 64 (the common MLX
+    # quantization of Qwen3-30B-A3B): random words, scales of a checkpoint's size and
+    # centring biases, gate/up rows interleaved. A 4-bit layer's stacks (226 MB + 113 MB)
+    # fit in the 256 MB Infinity Cache, so the copies cycle over four layers' stacks.
+    aff_bits, aff_group, aff_layers = 4, 64, 4
+    affine_stacks: list = []
+
+    def affine_weights(device):
+        if not affine_stacks:
+            gen = torch.Generator(device=device).manual_seed(10)
+            for _ in range(aff_layers):
+                layer = {}
+                for name, rows, features in (("gate_up", 2 * moe_i, moe_h), ("down", moe_h, moe_i)):
+                    words = torch.randint(-2**31, 2**31, (moe_e, rows, features * aff_bits // 32),
+                                          generator=gen, device=device, dtype=torch.int32)
+                    scale = 4.0 / ((1 << aff_bits) * features ** 0.5)
+                    groups = (moe_e, rows, features // aff_group)
+                    scales = (scale * (0.5 + torch.rand(groups, generator=gen, device=device))).to(torch.bfloat16)
+                    biases = (-scales.float() * ((1 << aff_bits) - 1) / 2).to(torch.bfloat16)
+                    layer[name] = ops.AffineLeaf(words, scales, biases, aff_bits, aff_group)
+                affine_stacks.append(layer)
+        return affine_stacks
+
+    def setup_moe_affine(device, copies):
+        rng = np.random.default_rng(11)
+        layers = affine_weights(device)
+        sets = []
+        for i in range(copies):
+            stacks = layers[i % aff_layers]
+            chosen = torch.from_numpy(rng.choice(moe_e, size=moe_k, replace=False).astype(np.int32)).to(device)
+            sets.append(dict(gu=stacks["gate_up"], dn=stacks["down"], ids=chosen,
+                             x=_to_bf16_device(_normal(rng, (moe_h,)), device),
+                             act=_to_bf16_device(_normal(rng, (moe_k, moe_i)), device),
+                             w=torch.from_numpy(rng.dirichlet(np.ones(moe_k)).astype(np.float32)).to(device),
+                             r=_to_bf16_device(_normal(rng, (moe_h,)), device),
+                             y=torch.empty((moe_k, moe_i), dtype=torch.bfloat16, device=device),
+                             o=torch.empty((moe_h,), dtype=torch.bfloat16, device=device)))
+        return sets
+
+    def affine_row_bytes(features):
+        return features * aff_bits // 8 + 2 * 2 * (features // aff_group)
+
+    out.append(Workload(
+        name="moe_affine_gate_up_decode",
+        kernel="moe_gate_up_affine_kernel",
+        description="x [2048] bf16 x 8 of 128 experts' 4-bit affine (group 64) interleaved "
+                    "gate||up stacks [1536, 2048] -> silu(gate)*up [8, 768] bf16 (Qwen3-30B-A3B, T=1)",
+        bytes_per_launch=moe_k * 2 * moe_i * affine_row_bytes(moe_h) + moe_h * 2 + moe_k * 4 + moe_k * moe_i * 2,
+        setup=setup_moe_affine,
+        launch=lambda a: ops.moe_gate_up_affine(a["x"], a["gu"], a["ids"], out=a["y"]),
+    ))
+    out.append(Workload(
+        name="moe_affine_down_combine_decode",
+        kernel="moe_down_affine_kernel",
+        description="activation [8, 768] x 8 of 128 experts' 4-bit affine (group 64) down "
+                    "stacks [2048, 768], routing weights, slot sum, residual (Qwen3-30B-A3B, T=1)",
+        bytes_per_launch=moe_k * moe_h * affine_row_bytes(moe_i) + moe_k * moe_i * 2 + moe_k * 8 + 2 * moe_h * 2,
+        setup=setup_moe_affine,
+        launch=lambda a: ops.moe_down_combine_affine(a["act"], a["dn"], a["ids"], a["w"], a["r"], out=a["o"]),
+    ))
+
     # Next after the routed MLP: the dense SwiGLU MLP of a one-token step at Qwen3-4B's
     # shape (hidden 2560, inner 9728: config 4's inner dimension), bf16 weights, gate rows
     # first. Each argument set holds its own weights, as each layer of a model does.

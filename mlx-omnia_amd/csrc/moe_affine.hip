@@ -30,11 +30,16 @@
 // are paired to match once per lane; at 3, 5 and 6 bits consecutive values pair up. At 8
 // bits the bytes convert to fp32 (exact), whose high halves are their bf16 values.
 //
-// gate_up: a wave owns kPairsPerWave gate/up pairs of one slot (8 consecutive rows of the
-// interleaved matrix) and streams them together; x is read per 32-value chunk from L2.
-// down_combine: a workgroup owns kDownRows output rows with one wave per slot; eight lanes
-// share a row, each taking every eighth chunk of it, all of its weight words loaded before
-// any arithmetic; the slots' terms meet in LDS and are summed in slot order.
+// gate_up: a wave owns kPairsPerWave gate/up pairs of one slot (consecutive rows of the
+// interleaved matrix) and streams them together; x is read per 32-value chunk from L2, and
+// lane p runs pair p's activation. down_combine: a workgroup owns kDownRows output rows
+// with one wave per slot; kLanesPerRow lanes share a row, each taking every kLanesPerRow-th
+// chunk of it, all of its weight words loaded before any arithmetic; the slots' terms meet
+// in LDS and are summed in slot order.
+// Measured at Qwen3-30B-A3B's routed MLP, 4 bits, groups of 64, one call: gate_up with 2
+// pairs per wave 6.1 us (4 pairs: 7.6, 8 pairs: 8.7, 1 pair: 6.6); down with 16 lanes per
+// row 5.9 us (8 lanes: 6.45, 8 lanes and two rows per lane: 8.8). Without the decode
+// arithmetic gate_up takes 5.2 us: the rest is the loads' latency.
 #include "common.hpp"
 #include "host.hpp"
 
@@ -42,13 +47,17 @@ namespace omnia {
 namespace {
 
 constexpr int kChunk = 32;                // values per lane per step (`bits` words)
-constexpr int kPairsPerWave = 4;          // gate_up: gate/up pairs per wave
+constexpr int kPairsPerWave = 2;          // gate_up: gate/up pairs per wave
 constexpr int kGateWaves = 4;             // gate_up: waves per workgroup
-constexpr int kDownRows = 8;              // down: output rows per workgroup
-constexpr int kLanesPerRow = kWave / kDownRows;
-constexpr int kMaxDownSteps = 6;          // down: chunks per lane, inner <= 8 * 6 * 32
+constexpr int kLanesPerRow = 16;          // down: lanes sharing an output row
+constexpr int kOctets = kWave / kLanesPerRow;
+constexpr int kRowsPerLane = 1;           // down: rows per lane (one activation load for all)
+constexpr int kDownRows = kOctets * kRowsPerLane;  // down: output rows per workgroup
+constexpr int kMaxInner = 1536;
+constexpr int kMaxDownSteps = kMaxInner / (32 * kLanesPerRow);  // down: chunks per lane
 constexpr int kMaxDownSlots = 16;         // down: one wave per slot
 constexpr uint32_t kMagic = 0x43004300u;  // the bf16 pair (128, 128)
+constexpr uint32_t kOnes = 0x3F803F80u;   // the bf16 pair (1, 1)
 
 struct Leaf {
   const uint32_t* weight;  // [experts, rows, in * bits / 32], or [rows, ...] when shared
@@ -114,7 +123,7 @@ __device__ __forceinline__ float pair_x(const u32x4 (&raw)[4], uint32_t (&xq)[16
     xp[4 * i + 3] = raw[i].w;
   }
 #pragma unroll
-  for (int m = 0; m < 16; ++m) sum += bf16_lo(xp[m]) + bf16_hi(xp[m]);
+  for (int m = 0; m < 16; ++m) sum = dot2(xp[m], kOnes, sum);
   constexpr int kSpan = B == 4 ? 8 : B == 2 ? 16 : 0;  // values per word
   if constexpr (kSpan != 0) {
     // Word d's pair i is values (kSpan d + i, kSpan d + i + kSpan / 2).
@@ -193,11 +202,13 @@ __device__ __forceinline__ float wave_fsum(float v) {
   return __uint_as_float(a) + __uint_as_float(b);
 }
 
-// Sum over each group of 8 lanes (8k .. 8k + 7), the same in each of them.
+// Sum over each group of kLanesPerRow (8 or 16) aligned lanes, the same in each of them.
 __device__ __forceinline__ float octet_sum(float v) {
   v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
   v += __uint_as_float(dpp<kQuadSwap2>(__float_as_uint(v)));
-  return v + __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
+  if constexpr (kLanesPerRow == 16) v += __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
+  return v;
 }
 
 __device__ __forceinline__ bool uses_shared(const Leaf& shared, int slot, int slots) {
@@ -279,19 +290,25 @@ __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(
     case 6: gate_up_rows<6>(a, leaf, row0, 2 * pairs, lane, r); break;
     default: gate_up_rows<8>(a, leaf, row0, 2 * pairs, lane, r); break;
   }
+  // Lane p takes pair p's sums and runs its activation.
+  float gate_sum = 0.0f, up_sum = 0.0f;
 #pragma unroll
   for (int p = 0; p < kPairsPerWave; ++p) {
-    float g = round_bf16(wave_fsum(r[2 * p]));
-    float u = round_bf16(wave_fsum(r[2 * p + 1]));
-    if (a.limit < __builtin_inff()) {
-      g = fminf(g, a.limit);
-      u = fminf(fmaxf(u, -a.limit), a.limit);
-    }
-    const float den = 1.0f + expf(-g);
-    const float sig = round_bf16(1.0f / den);
-    const float act = round_bf16(g * sig);
-    if (lane == p && p < pairs) out[p] = f32_to_bf16(act * u);
+    const float gp = wave_fsum(r[2 * p]);
+    const float up = wave_fsum(r[2 * p + 1]);
+    gate_sum = lane == p ? gp : gate_sum;
+    up_sum = lane == p ? up : up_sum;
   }
+  float g = round_bf16(gate_sum);
+  float u = round_bf16(up_sum);
+  if (a.limit < __builtin_inff()) {
+    g = fminf(g, a.limit);
+    u = fminf(fmaxf(u, -a.limit), a.limit);
+  }
+  const float den = 1.0f + expf(-g);
+  const float sig = round_bf16(1.0f / den);
+  const float act = round_bf16(g * sig);
+  if (lane < pairs) out[lane] = f32_to_bf16(act * u);
 }
 
 // ---- down_combine -------------------------------------------------------------------
@@ -310,28 +327,36 @@ struct DownArgs {
   int slots;
 };
 
-// The dot product of the lane's row (lane / 8) over the chunks part, part + 8, ... of
-// the slot's activation row, all weight words in flight before the first multiply.
+// The dot products of the lane's rows (row0 + 8 q for q < kRowsPerLane, those with
+// live[q]) over the chunks part, part + 8, ... of the slot's activation row: every
+// weight word in flight before the first multiply, each activation chunk loaded once for
+// all the rows.
 template <int B>
-__device__ __forceinline__ float down_row(const DownArgs& a, const Leaf& leaf, int64_t row, int slot,
-                                          int part) {
+__device__ __forceinline__ void down_rows(const DownArgs& a, const Leaf& leaf, int64_t row0,
+                                          const bool (&live)[kRowsPerLane], int slot, int part,
+                                          float (&t)[kRowsPerLane]) {
   const int chunks = a.inner / kChunk;
   const int64_t words = static_cast<int64_t>(a.inner) * B / 32;
   const int groups = a.inner / leaf.group;
-  uint32_t w[kMaxDownSteps][B];
-  uint16_t sb[kMaxDownSteps], bb[kMaxDownSteps];
+  uint32_t w[kRowsPerLane][kMaxDownSteps][B];
+  uint16_t sb[kRowsPerLane][kMaxDownSteps], bb[kRowsPerLane][kMaxDownSteps];
 #pragma unroll
-  for (int i = 0; i < kMaxDownSteps; ++i) {
-    const int c = part + kLanesPerRow * i;
-    if (c < chunks) {
-      load_words<B>(leaf.weight + row * words + static_cast<int64_t>(c) * B, w[i]);
-      const int64_t g = row * groups + (c * kChunk) / leaf.group;
-      sb[i] = leaf.scales[g];
-      bb[i] = leaf.biases[g];
+  for (int q = 0; q < kRowsPerLane; ++q) {
+    const int64_t row = row0 + kOctets * q;
+#pragma unroll
+    for (int i = 0; i < kMaxDownSteps; ++i) {
+      const int c = part + kLanesPerRow * i;
+      if (live[q] && c < chunks) {
+        load_words<B>(leaf.weight + row * words + static_cast<int64_t>(c) * B, w[q][i]);
+        const int64_t g = row * groups + (c * kChunk) / leaf.group;
+        sb[q][i] = leaf.scales[g];
+        bb[q][i] = leaf.biases[g];
+      }
     }
   }
   const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
-  float acc = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kRowsPerLane; ++q) t[q] = 0.0f;
 #pragma unroll
   for (int i = 0; i < kMaxDownSteps; ++i) {
     const int c = part + kLanesPerRow * i;
@@ -341,10 +366,12 @@ __device__ __forceinline__ float down_row(const DownArgs& a, const Leaf& leaf, i
       for (int j = 0; j < 4; ++j) raw[j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
       uint32_t xq[16];
       const float xsum = pair_x<B>(raw, xq);
-      acc += chunk_term<B>(chunk_dot<B>(w[i], xq), xsum, sb[i], bb[i]);
+#pragma unroll
+      for (int q = 0; q < kRowsPerLane; ++q) {
+        if (live[q]) t[q] += chunk_term<B>(chunk_dot<B>(w[q][i], xq), xsum, sb[q][i], bb[q][i]);
+      }
     }
   }
-  return acc;
 }
 
 __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(DownArgs a) {
@@ -352,32 +379,39 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(
   const int lane = threadIdx.x % kWave;
   const int slot = threadIdx.x / kWave;   // one wave per slot
   const int row_base = blockIdx.x * kDownRows;
-  const int r = lane / kLanesPerRow;
+  const int octet = lane / kLanesPerRow;
   const int part = lane % kLanesPerRow;
-  const bool row_valid = row_base + r < a.hidden;
   const bool shared = uses_shared(a.shared, slot, a.slots);
   const Leaf& leaf = shared ? a.shared : a.routed;
   bool valid = true;
-  int64_t row = row_base + r;
+  int64_t row0 = row_base + octet;
   if (!shared) {
     const int expert = a.chosen[slot];
     valid = expert >= 0 && expert < a.experts;
-    row += static_cast<int64_t>(valid ? expert : 0) * a.hidden;
+    row0 += static_cast<int64_t>(valid ? expert : 0) * a.hidden;
   }
-  float t = 0.0f;
-  if (valid && row_valid) {  // row_valid is uniform over the lane's octet
+  bool live[kRowsPerLane];  // uniform over the lane's octet
+#pragma unroll
+  for (int q = 0; q < kRowsPerLane; ++q) live[q] = valid && row_base + octet + kOctets * q < a.hidden;
+  float t[kRowsPerLane];
+#pragma unroll
+  for (int q = 0; q < kRowsPerLane; ++q) t[q] = 0.0f;
+  if (live[0]) {
     switch (leaf.bits) {  // wave-uniform
-      case 2: t = down_row<2>(a, leaf, row, slot, part); break;
-      case 3: t = down_row<3>(a, leaf, row, slot, part); break;
-      case 4: t = down_row<4>(a, leaf, row, slot, part); break;
-      case 5: t = down_row<5>(a, leaf, row, slot, part); break;
-      case 6: t = down_row<6>(a, leaf, row, slot, part); break;
-      default: t = down_row<8>(a, leaf, row, slot, part); break;
+      case 2: down_rows<2>(a, leaf, row0, live, slot, part, t); break;
+      case 3: down_rows<3>(a, leaf, row0, live, slot, part, t); break;
+      case 4: down_rows<4>(a, leaf, row0, live, slot, part, t); break;
+      case 5: down_rows<5>(a, leaf, row0, live, slot, part, t); break;
+      case 6: down_rows<6>(a, leaf, row0, live, slot, part, t); break;
+      default: down_rows<8>(a, leaf, row0, live, slot, part, t); break;
     }
   }
-  t = octet_sum(t);
-  if (part == 0) {
-    partial[slot][r] = valid ? round_bf16(round_bf16(t) * a.weights[slot]) : 0.0f;
+#pragma unroll
+  for (int q = 0; q < kRowsPerLane; ++q) {
+    const float sum = octet_sum(t[q]);
+    if (part == 0) {
+      partial[slot][octet + kOctets * q] = valid ? round_bf16(round_bf16(sum) * a.weights[slot]) : 0.0f;
+    }
   }
   __syncthreads();
   if (threadIdx.x < kDownRows && row_base + static_cast<int>(threadIdx.x) < a.hidden) {
@@ -445,7 +479,7 @@ extern "C" int32_t omnia_moe_down_combine_affine(
   using namespace omnia;
   OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), "moe_down_combine_affine: bad expert count");
   OMNIA_REQUIRE(hidden > 0 && hidden < (int64_t{1} << 24), "moe_down_combine_affine: bad hidden size");
-  OMNIA_REQUIRE(inner > 0 && inner % kChunk == 0 && inner <= kLanesPerRow * kMaxDownSteps * kChunk,
+  OMNIA_REQUIRE(inner > 0 && inner % kChunk == 0 && inner <= kMaxInner,
                 "moe_down_combine_affine: inner must be a multiple of 32 in [32, 1536]");
   OMNIA_REQUIRE(valid_format(bits, group_size) && inner % group_size == 0,
                 "moe_down_combine_affine: bits must be 2, 3, 4, 5, 6 or 8 and the group 32, 64 or 128, dividing inner");
