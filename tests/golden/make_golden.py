@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent.parent))
 
-from oracle import activations, add_norm, attention, embed, mlp, moe, rope, route  # noqa: E402
+from oracle import activations, add_norm, affine, attention, embed, mlp, moe, rope, route  # noqa: E402
 from oracle.bf16 import from_float  # noqa: E402
 
 
@@ -99,6 +99,28 @@ def make_moe() -> dict[str, np.ndarray]:
                 weights=weights, residual=residual, act=act, out=out)
 
 
+def make_moe_affine() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(9)
+    experts, hidden, inner = 4, 128, 64
+    gate_up = affine.quantize(rng.standard_normal((experts, 2 * inner, hidden)) / np.sqrt(hidden), 32, 4)
+    down = affine.quantize(rng.standard_normal((experts, hidden, inner)) / np.sqrt(inner), 64, 4)
+    shared_gate_up = affine.quantize(rng.standard_normal((2 * inner, hidden)) / np.sqrt(hidden), 64, 3)
+    shared_down = affine.quantize(rng.standard_normal((hidden, inner)) / np.sqrt(inner), 32, 3)
+    x = from_float(rng.standard_normal(hidden))
+    chosen = np.array([3, 0, 2, 0], dtype=np.int32)           # the last slot is the shared expert's
+    weights = np.array([0.4, 0.3, 0.2, 0.1], dtype=np.float32)
+    residual = from_float(rng.standard_normal(hidden))
+    act = affine.gate_up(x, gate_up, chosen, shared=shared_gate_up)
+    out = affine.down_combine(act, down, chosen, weights, residual, shared=shared_down)
+    arrays = dict(x=x, chosen=chosen, weights=weights, residual=residual, act=act, out=out)
+    for name, stack in (("gate_up", gate_up), ("down", down), ("shared_gate_up", shared_gate_up),
+                        ("shared_down", shared_down)):
+        arrays.update({f"{name}_weight": stack.weight, f"{name}_scales": stack.scales,
+                       f"{name}_biases": stack.biases,
+                       f"{name}_format": np.array([stack.bits, stack.group], dtype=np.int32)})
+    return arrays
+
+
 def make_mlp() -> dict[str, np.ndarray]:
     rng = np.random.default_rng(7)
     hidden, inner = 128, 192
@@ -134,7 +156,8 @@ def make_attention() -> dict[str, np.ndarray]:
 
 
 MAKERS = {"attention": make_attention, "add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed,
-          "activations": make_activations, "route": make_route, "moe": make_moe, "mlp": make_mlp}
+          "activations": make_activations, "route": make_route, "moe": make_moe, "mlp": make_mlp,
+          "moe_affine": make_moe_affine}
 
 
 def main(names: list[str]) -> None:

@@ -250,3 +250,21 @@ def test_down_facade_hands_more_than_16_slots_to_the_core_chain():
                f32_to_device(weights), None)
     want = affine.down_combine(act, dstack, chosen, weights, None)
     assert_bf16_close(bits_of(out.to(torch.bfloat16)), want, min_exact=0.5)
+
+
+def test_golden_fixture():
+    golden = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "moe_affine.npz")
+
+    def leaf(name):
+        bits, group = (int(v) for v in golden[f"{name}_format"])
+        return ops.AffineLeaf(torch.from_numpy(golden[f"{name}_weight"].view(np.int32)).cuda(),
+                              to_device(golden[f"{name}_scales"]), to_device(golden[f"{name}_biases"]),
+                              bits, group)
+
+    chosen = torch.from_numpy(golden["chosen"]).cuda()
+    act = ops.moe_gate_up_affine(to_device(golden["x"]), leaf("gate_up"), chosen, shared=leaf("shared_gate_up"))
+    assert_bf16_close(bits_of(act), golden["act"], min_exact=0.99)
+    out = ops.moe_down_combine_affine(to_device(golden["act"]), leaf("down"), chosen,
+                                      f32_to_device(golden["weights"]), to_device(golden["residual"]),
+                                      shared=leaf("shared_down"))
+    assert_bf16_close(bits_of(out), golden["out"], min_exact=0.99)
