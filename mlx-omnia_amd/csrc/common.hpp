@@ -169,6 +169,25 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
          __builtin_bit_cast(double, (static_cast<uint64_t>(hi_b) << 32) | lo_b);
 }
 
+// fp32 sum over the wave, the same in every lane: row rotations (each lane of a pair adds
+// the same two operands), then the two cross-row swaps.
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v += __uint_as_float(dpp<kRowRor8>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowRor4>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowRor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowRor1>(__float_as_uint(v)));
+  uint32_t a, b;
+  row_pair(__float_as_uint(v), a, b);
+  v = __uint_as_float(a) + __uint_as_float(b);
+  half_pair(__float_as_uint(v), a, b);
+  return __uint_as_float(a) + __uint_as_float(b);
+}
+
+// c + a.lo * b.lo + a.hi * b.hi over two packed bf16 pairs (v_dot2_f32_bf16), fp32.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                         false);
+}
 
 template <typename T>
 __device__ __forceinline__ T load_nt(const T* ptr) {

@@ -67,10 +67,7 @@ struct Leaf {
   int group;
 };
 
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
-                                         false);
-}
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) { return dot2_bf16(a, b, c); }
 
 // Value j of a 32-value chunk held in B words (j is a constant once unrolled).
 template <int B>
@@ -189,19 +186,6 @@ __device__ __forceinline__ float chunk_term(float dot, float xsum, uint16_t scal
   return __builtin_fmaf(s, dot, shifted * xsum);
 }
 
-// Sum over the wave, the same in every lane.
-__device__ __forceinline__ float wave_fsum(float v) {
-  v += __uint_as_float(dpp<kRowRor8>(__float_as_uint(v)));
-  v += __uint_as_float(dpp<kRowRor4>(__float_as_uint(v)));
-  v += __uint_as_float(dpp<kRowRor2>(__float_as_uint(v)));
-  v += __uint_as_float(dpp<kRowRor1>(__float_as_uint(v)));
-  uint32_t a, b;
-  row_pair(__float_as_uint(v), a, b);
-  v = __uint_as_float(a) + __uint_as_float(b);
-  half_pair(__float_as_uint(v), a, b);
-  return __uint_as_float(a) + __uint_as_float(b);
-}
-
 // Sum over each group of kLanesPerRow (8 or 16) aligned lanes, the same in each of them.
 __device__ __forceinline__ float octet_sum(float v) {
   v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
@@ -294,8 +278,8 @@ __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(
   float gate_sum = 0.0f, up_sum = 0.0f;
 #pragma unroll
   for (int p = 0; p < kPairsPerWave; ++p) {
-    const float gp = wave_fsum(r[2 * p]);
-    const float up = wave_fsum(r[2 * p + 1]);
+    const float gp = wave_sum_f32(r[2 * p]);
+    const float up = wave_sum_f32(r[2 * p + 1]);
     gate_sum = lane == p ? gp : gate_sum;
     up_sum = lane == p ? up : up_sum;
   }
