@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 6
+#define OMNIA_ABI_VERSION 7
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -253,6 +253,39 @@ int32_t omnia_moe_down_combine_affine(const uint16_t* act, const uint32_t* weigh
                                       const uint32_t* shared_weight, const uint16_t* shared_scales,
                                       const uint16_t* shared_biases, int64_t shared_bits,
                                       int64_t shared_group_size, uint16_t* out, hipStream_t stream);
+
+/* Routed expert gate/up of one token over an MXFP4 stack (MLX's QuantizedSwitchLinear,
+ * mode "mxfp4", the gpt-oss format), the interleaved layout, the clamped swiglu_oai fused:
+ *   r = sum over groups of 32 of s * sum_j x[j] v[j]       v e2m1, s = fp32(scale << 23)
+ *   g = bf16(r[2n] + bias[2n]), u = bf16(r[2n + 1] + bias[2n + 1]); with limit < +inf,
+ *   g = bf16(min(g, limit)), u = bf16(clamp(u, -limit, limit));
+ *   out[s, n] = bf16(bf16(g * bf16(1 / (1 + exp(-1.702 g)))) * bf16(u + 1))
+ * x [hidden] bf16; weight [experts, 2 * inner, hidden / 8] uint32 (two e2m1 codes per byte,
+ * low nibble first); scales [experts, 2 * inner, hidden / 32] uint8 (e8m0); bias
+ * [experts, 2 * inner] bf16 or NULL (zero); chosen [slots] int32; out [slots, inner] bf16.
+ * An index outside [0, experts) gives zeros. hidden a multiple of 32, at most 16384.
+ * Replaces: core/kernels/gate_up/mxfp4.py:24-138 (`Mxfp4GateUp`, `mxfp4_gateup_act`); Core
+ * chain core/kernels/gate_up/default.py:60-78. */
+int32_t omnia_moe_gate_up_mxfp4(const uint16_t* x, const uint32_t* weight, const uint8_t* scales,
+                                const uint16_t* bias, int64_t experts, int64_t hidden, int64_t inner,
+                                const int32_t* chosen, int64_t slots, float limit, uint16_t* out,
+                                hipStream_t stream);
+
+/* Routed expert down/combine of one token over an MXFP4 stack:
+ *   t[s, n] = sum over groups of 32 of s * sum_i act[s, i] v[i]                   fp32
+ *   acc[n] = sum over s in order of bf16(bf16(t[s, n] + bias[n]) * weights[s])    fp32
+ *   out[n] = bf16(bf16(acc[n]) + residual[n])   (no add when residual is null)
+ * act [slots, inner] bf16; weight [experts, hidden, inner / 8] uint32; scales [experts,
+ * hidden, inner / 32] uint8; bias [experts, hidden] bf16 or NULL; chosen [slots] int32;
+ * weights [slots] fp32; residual, out [hidden] bf16.
+ * inner a multiple of 32, at most 3072; 1 <= slots <= 16.
+ * Replaces: core/kernels/down_combine/mxfp4.py:16-120 (`Mxfp4DownCombine`,
+ * `mxfp4_down_combine`); Core chain core/kernels/down_combine/default.py:43-58. */
+int32_t omnia_moe_down_combine_mxfp4(const uint16_t* act, const uint32_t* weight, const uint8_t* scales,
+                                     const uint16_t* bias, int64_t experts, int64_t hidden,
+                                     int64_t inner, const int32_t* chosen, const float* weights,
+                                     int64_t slots, const uint16_t* residual, uint16_t* out,
+                                     hipStream_t stream);
 
 /* Dense SwiGLU MLP of one token, first half: the fused gate||up projection with the
  * SwiGLU applied in bf16 steps,

@@ -1,0 +1,282 @@
+// Routed expert MLP of a one-token step over MXFP4 expert stacks (MLX's
+// `QuantizedSwitchLinear`, mode "mxfp4", the gpt-oss format): gate/up with the clamped
+// swiglu_oai activation, then down/combine, the interleaved layout of the reference's
+// mxfp4 kernels.
+//
+// Format (core/layers.py:164-197; decoded as core/kernels/shared/mxfp4.py:8-32 reads it):
+// weight [E, rows, in / 8] uint32, two e2m1 codes per byte, the low nibble first (value j
+// is nibble j of the row); scales [E, rows, in / 32] uint8, an e8m0 exponent per 32
+// values applied as the fp32 whose bit pattern is `byte << 23` (2^(byte - 127) for
+// 1..254); the projection's own bias [E, rows] bf16.
+//
+// Arithmetic:
+//   gate_up (core/kernels/gate_up/mxfp4.py:24-65): r = sum over groups of
+//     s * sum_j x_j v_j (fp32, any order); rows 2n and 2n + 1 are output n's gate and up;
+//     g = T(r_gate + b_gate), u = T(r_up + b_up); g = T(min(g, limit)),
+//     u = T(clamp(u, -limit, limit)); sig = T(1 / (1 + exp(-1.702 g)));
+//     y = T(T(g * sig) * T(u + 1)), each operation in fp32.
+//   down_combine (core/kernels/down_combine/mxfp4.py:16-58): t the same dot product over
+//     the activation row of the slot; acc = sum over slots in order of
+//     T(fp32(T(t + b) * w)) in fp32; y = T(fp32(T(acc) + residual)).
+// An expert id outside [0, experts) gives zero rows.
+//
+// Decoding is gfx950's own: v_cvt_scalef32_pk_bf16_fp4 turns the two e2m1 codes of a
+// byte into a bf16 pair (low nibble first; checked on the box for every byte value), so
+// one conversion and one v_dot2_f32_bf16 take two weights against the activations in
+// memory order. A lane takes 32 values at a time, 16 bytes and exactly one scale group;
+// the group's dot product is scaled once in fp32.
+//
+// gate_up: a wave owns kPairsPerWave gate/up pairs of one slot and streams them together;
+// lane p runs pair p's activation. down_combine: a workgroup owns kDownRows output rows
+// with one wave per slot; 16 lanes share a row, each taking every 16th chunk of it, all of
+// its weight bytes loaded before any arithmetic; the slots' terms meet in LDS and are
+// summed in slot order.
+#include "common.hpp"
+#include "host.hpp"
+
+namespace omnia {
+namespace {
+
+constexpr int kChunk = 32;                // values per lane per step: 16 bytes, one group
+constexpr int kPairsPerWave = 2;          // gate_up: gate/up pairs per wave
+constexpr int kGateWaves = 4;             // gate_up: waves per workgroup
+constexpr int kLanesPerRow = 16;          // down: lanes sharing an output row
+constexpr int kDownRows = kWave / kLanesPerRow;
+constexpr int kMaxInner = 3072;           // down: inner / (32 * 16) steps per lane
+constexpr int kMaxDownSteps = kMaxInner / (kChunk * kLanesPerRow);
+constexpr int kMaxDownSlots = 16;
+
+// The e8m0 group scale as the reference applies it: the fp32 with exponent field `byte`.
+__device__ __forceinline__ float e8m0(uint8_t byte) { return __uint_as_float(static_cast<uint32_t>(byte) << 23); }
+
+// The e2m1 codes of byte B of a word as a bf16 pair, low nibble first.
+template <int B>
+__device__ __forceinline__ uint32_t fp4_pair(uint32_t word) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, 1.0f, B));
+}
+
+// sum_j x_j v_j over one chunk: 16 bytes of codes against 16 bf16 activation pairs.
+__device__ __forceinline__ float chunk_dot(const u32x4& w, const u32x4 (&x)[4]) {
+  float acc = 0.0f;
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    acc = dot2_bf16(fp4_pair<0>(words[d]), x[d].x, acc);
+    acc = dot2_bf16(fp4_pair<1>(words[d]), x[d].y, acc);
+    acc = dot2_bf16(fp4_pair<2>(words[d]), x[d].z, acc);
+    acc = dot2_bf16(fp4_pair<3>(words[d]), x[d].w, acc);
+  }
+  return acc;
+}
+
+// Sum over each group of 16 aligned lanes (one DPP row), the same in each of them.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kQuadSwap2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
+  return v + __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
+}
+
+struct Stack {
+  const u32x4* weight;     // [experts, rows, in / 32] chunks of 16 bytes
+  const uint8_t* scales;   // [experts, rows, in / 32]
+  const uint16_t* bias;    // [experts, rows] bf16, or null
+};
+
+// ---- gate_up ------------------------------------------------------------------------
+
+struct GateUpArgs {
+  const uint16_t* x;       // [hidden]
+  Stack stack;             // [experts, 2 * inner, ...]
+  const int32_t* chosen;   // [slots]
+  uint16_t* out;           // [slots, inner]
+  int64_t experts;
+  int hidden;
+  int inner;
+  float limit;             // +inf: no clamp
+};
+
+__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_mxfp4_kernel(GateUpArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int slot = blockIdx.y;
+  const int pair0 = (blockIdx.x * kGateWaves + threadIdx.x / kWave) * kPairsPerWave;
+  if (pair0 >= a.inner) return;  // whole wave; no barrier follows
+  const int pairs = min(kPairsPerWave, a.inner - pair0);
+  uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + pair0;
+  const int expert = a.chosen[slot];
+  if (expert < 0 || expert >= a.experts) {
+    if (lane < pairs) out[lane] = 0;
+    return;
+  }
+  constexpr int kRows = 2 * kPairsPerWave;
+  const int rows = 2 * pairs;
+  const int64_t row0 = static_cast<int64_t>(expert) * 2 * a.inner + 2 * static_cast<int64_t>(pair0);
+  const int chunks = a.hidden / kChunk;
+  float r[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) r[i] = 0.0f;
+  for (int c = lane; c < chunks; c += kWave) {
+    u32x4 w[kRows];
+    uint8_t s[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      if (i < rows) {
+        const int64_t at = (row0 + i) * chunks + c;
+        w[i] = load_nt(a.stack.weight + at);
+        s[i] = a.stack.scales[at];
+      }
+    }
+    u32x4 x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[i];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      if (i < rows) r[i] = __builtin_fmaf(e8m0(s[i]), chunk_dot(w[i], x), r[i]);
+    }
+  }
+  // Lane p takes pair p's sums and runs its activation.
+  float gate_sum = 0.0f, up_sum = 0.0f;
+#pragma unroll
+  for (int p = 0; p < kPairsPerWave; ++p) {
+    const float gp = wave_sum_f32(r[2 * p]);
+    const float up = wave_sum_f32(r[2 * p + 1]);
+    gate_sum = lane == p ? gp : gate_sum;
+    up_sum = lane == p ? up : up_sum;
+  }
+  if (lane >= pairs) return;
+  float gate_bias = 0.0f, up_bias = 0.0f;
+  if (a.stack.bias != nullptr) {
+    gate_bias = bf16_to_f32(a.stack.bias[row0 + 2 * lane]);
+    up_bias = bf16_to_f32(a.stack.bias[row0 + 2 * lane + 1]);
+  }
+  float g = round_bf16(gate_sum + gate_bias);
+  float u = round_bf16(up_sum + up_bias);
+  if (a.limit < __builtin_inff()) {
+    g = round_bf16(fminf(g, a.limit));
+    u = round_bf16(fminf(fmaxf(u, -a.limit), a.limit));
+  }
+  const float sig = round_bf16(1.0f / (1.0f + expf(-1.702f * g)));
+  const float act = round_bf16(g * sig);
+  out[lane] = f32_to_bf16(act * round_bf16(u + 1.0f));
+}
+
+// ---- down_combine -------------------------------------------------------------------
+
+struct DownArgs {
+  const uint16_t* act;      // [slots, inner]
+  Stack stack;              // [experts, hidden, ...]
+  const int32_t* chosen;    // [slots]
+  const float* weights;     // [slots]
+  const uint16_t* residual; // [hidden] or null
+  uint16_t* out;            // [hidden]
+  int64_t experts;
+  int hidden;
+  int inner;
+  int slots;
+};
+
+__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_mxfp4_kernel(DownArgs a) {
+  __shared__ float partial[kMaxDownSlots][kDownRows];
+  const int lane = threadIdx.x % kWave;
+  const int slot = threadIdx.x / kWave;   // one wave per slot
+  const int row_base = blockIdx.x * kDownRows;
+  const int r = lane / kLanesPerRow;
+  const int part = lane % kLanesPerRow;
+  const int expert = a.chosen[slot];
+  const bool valid = expert >= 0 && expert < a.experts;
+  const bool live = valid && row_base + r < a.hidden;   // uniform over the lane's row
+  const int64_t row = static_cast<int64_t>(valid ? expert : 0) * a.hidden + row_base + r;
+  const int chunks = a.inner / kChunk;
+  float t = 0.0f;
+  if (live) {
+    u32x4 w[kMaxDownSteps];
+    uint8_t s[kMaxDownSteps];
+#pragma unroll
+    for (int i = 0; i < kMaxDownSteps; ++i) {
+      const int c = part + kLanesPerRow * i;
+      if (c < chunks) {
+        w[i] = load_nt(a.stack.weight + row * chunks + c);
+        s[i] = a.stack.scales[row * chunks + c];
+      }
+    }
+    const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
+#pragma unroll
+    for (int i = 0; i < kMaxDownSteps; ++i) {
+      const int c = part + kLanesPerRow * i;
+      if (c < chunks) {
+        u32x4 xv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
+        t = __builtin_fmaf(e8m0(s[i]), chunk_dot(w[i], xv), t);
+      }
+    }
+  }
+  t = row_sum16(t);
+  if (part == 0) {
+    float term = 0.0f;
+    if (valid) {
+      const float bias = a.stack.bias != nullptr && live ? bf16_to_f32(a.stack.bias[row]) : 0.0f;
+      term = round_bf16(round_bf16(t + bias) * a.weights[slot]);
+    }
+    partial[slot][r] = term;
+  }
+  __syncthreads();
+  if (threadIdx.x < kDownRows && row_base + static_cast<int>(threadIdx.x) < a.hidden) {
+    const int n = row_base + threadIdx.x;
+    float sum = 0.0f;
+    for (int j = 0; j < a.slots; ++j) sum += partial[j][threadIdx.x];
+    float out = round_bf16(sum);
+    if (a.residual != nullptr) out = out + bf16_to_f32(a.residual[n]);
+    a.out[n] = f32_to_bf16(out);
+  }
+}
+
+}  // namespace
+}  // namespace omnia
+
+extern "C" int32_t omnia_moe_gate_up_mxfp4(const uint16_t* x, const uint32_t* weight, const uint8_t* scales,
+                                           const uint16_t* bias, int64_t experts, int64_t hidden,
+                                           int64_t inner, const int32_t* chosen, int64_t slots,
+                                           float limit, uint16_t* out, hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), "moe_gate_up_mxfp4: bad expert count");
+  OMNIA_REQUIRE(hidden > 0 && hidden % kChunk == 0 && hidden <= 16384,
+                "moe_gate_up_mxfp4: hidden must be a multiple of 32 in [32, 16384]");
+  OMNIA_REQUIRE(inner > 0 && inner < (int64_t{1} << 24), "moe_gate_up_mxfp4: bad inner size");
+  OMNIA_REQUIRE(slots >= 0 && slots <= 1024, "moe_gate_up_mxfp4: slots must be in [0, 1024]");
+  OMNIA_REQUIRE(!(limit < 0.0f), "moe_gate_up_mxfp4: the limit must be non-negative (+inf: none)");
+  if (slots == 0) return 0;
+  OMNIA_REQUIRE(x && weight && scales && chosen && out, "moe_gate_up_mxfp4: null pointer");
+  OMNIA_REQUIRE(aligned16(x) && aligned16(weight), "moe_gate_up_mxfp4: x and weight must be 16-byte aligned");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  GateUpArgs a{x, Stack{reinterpret_cast<const u32x4*>(weight), scales, bias}, chosen, out, experts,
+               static_cast<int>(hidden), static_cast<int>(inner), limit};
+  const int64_t waves = (inner + kPairsPerWave - 1) / kPairsPerWave;
+  const dim3 grid(static_cast<unsigned>((waves + kGateWaves - 1) / kGateWaves), static_cast<unsigned>(slots));
+  moe_gate_up_mxfp4_kernel<<<grid, kGateWaves * kWave, 0, stream>>>(a);
+  return launched("moe_gate_up_mxfp4");
+}
+
+extern "C" int32_t omnia_moe_down_combine_mxfp4(const uint16_t* act, const uint32_t* weight,
+                                                const uint8_t* scales, const uint16_t* bias,
+                                                int64_t experts, int64_t hidden, int64_t inner,
+                                                const int32_t* chosen, const float* weights,
+                                                int64_t slots, const uint16_t* residual, uint16_t* out,
+                                                hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), "moe_down_combine_mxfp4: bad expert count");
+  OMNIA_REQUIRE(hidden > 0 && hidden < (int64_t{1} << 24), "moe_down_combine_mxfp4: bad hidden size");
+  OMNIA_REQUIRE(inner > 0 && inner % kChunk == 0 && inner <= kMaxInner,
+                "moe_down_combine_mxfp4: inner must be a multiple of 32 in [32, 3072]");
+  OMNIA_REQUIRE(slots > 0 && slots <= kMaxDownSlots, "moe_down_combine_mxfp4: slots must be in [1, 16]");
+  OMNIA_REQUIRE(act && weight && scales && chosen && weights && out, "moe_down_combine_mxfp4: null pointer");
+  OMNIA_REQUIRE(aligned16(act) && aligned16(weight), "moe_down_combine_mxfp4: act and weight must be 16-byte aligned");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  DownArgs a{act, Stack{reinterpret_cast<const u32x4*>(weight), scales, bias}, chosen, weights, residual, out,
+             experts, static_cast<int>(hidden), static_cast<int>(inner), static_cast<int>(slots)};
+  const dim3 grid(static_cast<unsigned>((hidden + kDownRows - 1) / kDownRows));
+  moe_down_mxfp4_kernel<<<grid, static_cast<unsigned>(slots * kWave), 0, stream>>>(a);
+  return launched("moe_down_combine_mxfp4");
+}

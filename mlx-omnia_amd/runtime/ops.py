@@ -665,3 +665,104 @@ def attention_decode(
          workspace.numel() * workspace.element_size() if workspace is not None else 0,
          out.data_ptr(), _stream(raw_queries))
     return out
+
+
+@dataclass(frozen=True)
+class Mxfp4Leaf:
+    """An MXFP4 matrix set as the kernels read it: weight [..., rows, features / 8]
+    (int32 or uint32 words, two e2m1 codes per byte, the low nibble first), scales
+    [..., rows, features / 32] uint8 (e8m0), and the projection's bias [..., rows] bf16 or
+    None."""
+
+    weight: torch.Tensor
+    scales: torch.Tensor
+    bias: torch.Tensor | None
+
+    @property
+    def features(self) -> int:
+        return self.weight.shape[-1] * 8
+
+    def check(self, rows: int, features: int, name: str) -> None:
+        _require(features % 32 == 0, f"{name}: the contraction must be a multiple of 32")
+        _require(self.weight.dim() == 3 and self.scales.dim() == 3, f"{name}: expected [experts, rows, ...]")
+        _require(self.weight.dtype in (torch.int32, torch.uint32), f"{name}: weight must hold 32-bit words")
+        _require(self.weight.is_contiguous() and self.weight.data_ptr() % 16 == 0,
+                 f"{name}: weight must be contiguous and 16-byte aligned")
+        experts = self.weight.shape[0]
+        _require(tuple(self.weight.shape) == (experts, rows, features // 8), f"{name}: weight shape")
+        _require(self.scales.dtype == torch.uint8 and self.scales.is_contiguous()
+                 and tuple(self.scales.shape) == (experts, rows, features // 32), f"{name}: scales")
+        if self.bias is not None:
+            _require(self.bias.dtype == BF16 and self.bias.is_contiguous()
+                     and tuple(self.bias.shape) == (experts, rows), f"{name}: bias must be bf16 [experts, rows]")
+
+    def tensors(self) -> list[torch.Tensor]:
+        return [self.weight, self.scales] + ([self.bias] if self.bias is not None else [])
+
+
+def moe_gate_up_mxfp4(
+    x: torch.Tensor,
+    leaf: Mxfp4Leaf,
+    chosen: torch.Tensor,
+    *,
+    limit: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One token's routed gate/up over an MXFP4 stack, the interleaved layout, the clamped
+    swiglu_oai fused; see `omnia_moe_gate_up_mxfp4`. x [hidden] bf16, leaf [experts,
+    2 * inner, ...], chosen [slots] int32 -> [slots, inner] bf16."""
+    _require(x.dim() == 1 or x.numel() == x.shape[-1], "moe_gate_up_mxfp4: x must be one row")
+    hidden = x.shape[-1]
+    _dense(x, BF16, "x")
+    _require(leaf.weight.dim() == 3 and leaf.weight.shape[1] % 2 == 0,
+             "moe_gate_up_mxfp4: weight must be [experts, 2 * inner, words]")
+    experts, rows = leaf.weight.shape[0], leaf.weight.shape[1]
+    leaf.check(rows, hidden, "moe_gate_up_mxfp4")
+    _require(chosen.dtype == torch.int32 and chosen.is_contiguous() and chosen.dim() == 1,
+             "moe_gate_up_mxfp4: chosen must be contiguous int32 [slots]")
+    _require(limit is None or limit >= 0, "moe_gate_up_mxfp4: the limit must be non-negative")
+    _require(on_rocm(x, chosen, *leaf.tensors()), "moe_gate_up_mxfp4: tensors must share one ROCm device")
+    slots = chosen.numel()
+    out = _out(out, x, (slots, rows // 2), BF16, "out")
+    call("omnia_moe_gate_up_mxfp4", x.data_ptr(), leaf.weight.data_ptr(), leaf.scales.data_ptr(),
+         leaf.bias.data_ptr() if leaf.bias is not None else None, experts, hidden, rows // 2,
+         chosen.data_ptr(), slots, float("inf") if limit is None else float(limit), out.data_ptr(),
+         _stream(x))
+    return out
+
+
+def moe_down_combine_mxfp4(
+    act: torch.Tensor,
+    leaf: Mxfp4Leaf,
+    chosen: torch.Tensor,
+    weights: torch.Tensor,
+    residual: torch.Tensor | None = None,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One token's routed down projection over an MXFP4 stack with the projection bias, the
+    routing weights, the slot sum and the residual; see `omnia_moe_down_combine_mxfp4`.
+    act [slots, inner] bf16, leaf [experts, hidden, ...], chosen [slots] int32, weights
+    [slots] fp32, residual [hidden] bf16 or None -> [hidden] bf16."""
+    _require(leaf.weight.dim() == 3, "moe_down_combine_mxfp4: weight must be [experts, hidden, words]")
+    experts, hidden = leaf.weight.shape[0], leaf.weight.shape[1]
+    slots = chosen.numel()
+    _require(act.dim() == 2 and act.shape[0] == slots, "moe_down_combine_mxfp4: act must be [slots, inner]")
+    inner = act.shape[1]
+    _dense(act, BF16, "act")
+    leaf.check(hidden, inner, "moe_down_combine_mxfp4")
+    _require(chosen.dtype == torch.int32 and chosen.is_contiguous(), "moe_down_combine_mxfp4: chosen int32")
+    _require(weights.dtype == F32 and weights.is_contiguous() and weights.numel() == slots,
+             "moe_down_combine_mxfp4: weights must be contiguous fp32 [slots]")
+    tensors = [act, chosen, weights, *leaf.tensors()]
+    if residual is not None:
+        _require(residual.numel() == hidden and residual.dtype == BF16 and residual.is_contiguous(),
+                 "moe_down_combine_mxfp4: residual must be contiguous bf16 [hidden]")
+        tensors.append(residual)
+    _require(on_rocm(*tensors), "moe_down_combine_mxfp4: tensors must share one ROCm device")
+    out = _out(out, act, (hidden,), BF16, "out")
+    call("omnia_moe_down_combine_mxfp4", act.data_ptr(), leaf.weight.data_ptr(), leaf.scales.data_ptr(),
+         leaf.bias.data_ptr() if leaf.bias is not None else None, experts, hidden, inner,
+         chosen.data_ptr(), weights.data_ptr(), slots,
+         residual.data_ptr() if residual is not None else None, out.data_ptr(), _stream(act))
+    return out
