@@ -399,6 +399,62 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.moe_down_combine_affine(a["act"], a["dn"], a["ids"], a["w"], a["r"], out=a["o"]),
     ))
 
+    # The routed MLP of gpt-oss-120b (hidden 2880, inner 2880, 128 experts, top-4) over its
+    # MXFP4 stacks: random e2m1 words, e8m0 scales near 2^-6, a bf16 projection bias,
+    # gate/up rows interleaved, the clamp at 7. One layer's stacks (1.13 GB + 0.56 GB)
+    # dwarf the Infinity Cache; each argument set routes to its own random experts.
+    mx_e, mx_h, mx_i, mx_k, mx_limit = 128, 2880, 2880, 4, 7.0
+    mxfp4_stacks: dict = {}
+
+    def mxfp4_weights(device):
+        if not mxfp4_stacks:
+            gen = torch.Generator(device=device).manual_seed(12)
+            for name, rows, features in (("gate_up", 2 * mx_i, mx_h), ("down", mx_h, mx_i)):
+                words = torch.randint(-2**31, 2**31, (mx_e, rows, features // 8), generator=gen,
+                                      device=device, dtype=torch.int32)
+                scales = torch.randint(119, 123, (mx_e, rows, features // 32), generator=gen,
+                                       device=device, dtype=torch.int32).to(torch.uint8)
+                bias = (0.25 * torch.randn((mx_e, rows), generator=gen, device=device)).to(torch.bfloat16)
+                mxfp4_stacks[name] = ops.Mxfp4Leaf(words, scales, bias)
+        return mxfp4_stacks
+
+    def setup_moe_mxfp4(device, copies):
+        rng = np.random.default_rng(13)
+        stacks = mxfp4_weights(device)
+        sets = []
+        for _ in range(copies):
+            chosen = torch.from_numpy(rng.choice(mx_e, size=mx_k, replace=False).astype(np.int32)).to(device)
+            sets.append(dict(gu=stacks["gate_up"], dn=stacks["down"], ids=chosen,
+                             x=_to_bf16_device(_normal(rng, (mx_h,)), device),
+                             act=_to_bf16_device(_normal(rng, (mx_k, mx_i)), device),
+                             w=torch.from_numpy(rng.dirichlet(np.ones(mx_k)).astype(np.float32)).to(device),
+                             r=_to_bf16_device(_normal(rng, (mx_h,)), device),
+                             y=torch.empty((mx_k, mx_i), dtype=torch.bfloat16, device=device),
+                             o=torch.empty((mx_h,), dtype=torch.bfloat16, device=device)))
+        return sets
+
+    def mxfp4_row_bytes(features):
+        return features // 2 + features // 32 + 2       # codes, e8m0 scales, the row's bias
+
+    out.append(Workload(
+        name="moe_mxfp4_gate_up_decode",
+        kernel="moe_gate_up_mxfp4_kernel",
+        description="x [2880] bf16 x 4 of 128 experts' MXFP4 interleaved gate||up stacks "
+                    "[5760, 2880] + bias -> clamped swiglu_oai [4, 2880] bf16 (gpt-oss-120b, T=1)",
+        bytes_per_launch=mx_k * 2 * mx_i * mxfp4_row_bytes(mx_h) + mx_h * 2 + mx_k * 4 + mx_k * mx_i * 2,
+        setup=setup_moe_mxfp4,
+        launch=lambda a: ops.moe_gate_up_mxfp4(a["x"], a["gu"], a["ids"], limit=mx_limit, out=a["y"]),
+    ))
+    out.append(Workload(
+        name="moe_mxfp4_down_combine_decode",
+        kernel="moe_down_mxfp4_kernel",
+        description="activation [4, 2880] x 4 of 128 experts' MXFP4 down stacks [2880, 2880] + "
+                    "bias, routing weights, slot sum, residual (gpt-oss-120b, T=1)",
+        bytes_per_launch=mx_k * mx_h * mxfp4_row_bytes(mx_i) + mx_k * mx_i * 2 + mx_k * 8 + 2 * mx_h * 2,
+        setup=setup_moe_mxfp4,
+        launch=lambda a: ops.moe_down_combine_mxfp4(a["act"], a["dn"], a["ids"], a["w"], a["r"], out=a["o"]),
+    ))
+
     # Next after the routed MLP: the dense SwiGLU MLP of a one-token step at Qwen3-4B's
     # shape (hidden 2560, inner 9728: config 4's inner dimension), bf16 weights, gate rows
     # first. Each argument set holds its own weights, as each layer of a model does.

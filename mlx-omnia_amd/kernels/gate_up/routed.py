@@ -6,6 +6,11 @@ Mirrors core/kernels/gate_up/__init__.py and kernel.py (`GateUp`, `GateUpStrateg
 (activation, clamp, projection bias, layout, ordinal routing, a shared expert), and the
 first strategy whose `build` accepts the declaration serves it.
 
+- `HipMxfp4GateUp` (`omnia_moe_gate_up_mxfp4`, csrc/moe_mxfp4.hip) serves what the
+  reference's `Mxfp4GateUp` serves (core/kernels/gate_up/mxfp4.py:82-111): an MXFP4 stack
+  (`QuantizedSwitchLinearLeaf` mode "mxfp4") under the `interleaved` layout, swiglu_oai
+  with its clamp and the per-row projection bias, no ordinal routing or shared expert,
+  hidden and inner multiples of 32 (hidden up to 16384).
 - `HipAffineGateUp` (`omnia_moe_gate_up_affine`, csrc/moe_affine.hip) serves what the
   reference's `AffineGateUp` serves (core/kernels/gate_up/affine.py:105-191): an
   affine-quantized stack (`QuantizedSwitchLinearLeaf`, 2, 3, 4, 5, 6 or 8 bits, groups of
@@ -77,6 +82,30 @@ def affine_leaf(leaf, rows: int, features: int, stacked: bool) -> "ops.AffineLea
     view = ops.AffineLeaf(leaf.weight, leaf.scales, leaf.biases, leaf.bits, leaf.group_size)
     try:
         view.check(rows, features, stacked, "affine leaf")
+    except ValueError:
+        return None
+    if not all(hip_device(t) for t in view.tensors()):
+        return None
+    return view
+
+
+def mxfp4_applies(hidden: int, inner: int) -> bool:
+    """Both contractions cover whole 32-value e8m0 groups (core/kernels/shared/mxfp4.py:
+    35-38)."""
+    return hidden > 0 and inner > 0 and hidden % 32 == 0 and inner % 32 == 0
+
+
+def mxfp4_leaf(leaf, bias, rows: int, features: int) -> "ops.Mxfp4Leaf | None":
+    """The kernels' view of an MXFP4 stack and its projection bias [experts, rows], or None."""
+    if not isinstance(leaf, QuantizedSwitchLinearLeaf) or leaf.mode != "mxfp4":
+        return None
+    if leaf.biases is not None or leaf.bits != 4 or leaf.group_size != 32:
+        return None
+    if bias is None or bias.dtype != torch.bfloat16:
+        return None
+    view = ops.Mxfp4Leaf(leaf.weight, leaf.scales, bias.contiguous())
+    try:
+        view.check(rows, features, "mxfp4 leaf")
     except ValueError:
         return None
     if not all(hip_device(t) for t in view.tensors()):
@@ -185,7 +214,31 @@ class HipAffineGateUp(GateUpStrategy):
                                       limit=self.limit, shared=self.shared)
 
 
-_STRATEGIES = (HipAffineGateUp, HipDenseGateUp, DefaultGateUp)
+@dataclass(frozen=True)
+class HipMxfp4GateUp(GateUpStrategy):
+    leaf: "ops.Mxfp4Leaf"
+    limit: float
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, activation, limit, bias, layout, routing,
+              shared) -> "HipMxfp4GateUp | None":
+        # The spare slot is the affine kernel's: a shared expert beside this stack has no
+        # kernel here, as in the reference.
+        if shared is not None or layout != "interleaved" or routing is not None:
+            return None
+        if activation != "swiglu_oai" or limit is None or not limit >= 0 or bias is None:
+            return None
+        if not mxfp4_applies(hidden, inner) or hidden > 16384:
+            return None
+        view = mxfp4_leaf(leaf, bias, 2 * inner, hidden)
+        return None if view is None else cls(view, float(limit))
+
+    def __call__(self, row: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor:
+        ids = chosen.to(device=self.leaf.weight.device, dtype=torch.int32).contiguous().reshape(-1)
+        return ops.moe_gate_up_mxfp4(row.reshape(-1).contiguous(), self.leaf, ids, limit=self.limit)
+
+
+_STRATEGIES = (HipMxfp4GateUp, HipAffineGateUp, HipDenseGateUp, DefaultGateUp)
 
 
 class GateUp(GateUpStrategy):

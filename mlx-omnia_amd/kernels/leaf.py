@@ -53,12 +53,38 @@ def affine_dequantize(words: torch.Tensor, scales: torch.Tensor, biases: torch.T
     return s * q + b
 
 
+E2M1 = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0)
+
+
+def mxfp4_dequantize(words: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """e2m1 codes (4-bit, the low nibble of each byte first) times their 32-value group's
+    e8m0 factor, the fp32 whose exponent field is the scale byte (2^(byte - 127), 0 for
+    byte 0): float32 [..., out, in] (core/kernels/shared/mxfp4.py:8-32 decodes the same
+    bytes)."""
+    table = torch.tensor(E2M1, dtype=torch.float32, device=words.device)
+    values = table[unpack_words(words, 4)]
+    factors = (scales.to(torch.int32) << 23).contiguous().view(torch.float32)
+    return values * factors.repeat_interleave(32, dim=-1)
+
+
+def dequantize(leaf, index: torch.Tensor | None = None) -> torch.Tensor:
+    """A quantized leaf's matrices (the indexed experts' for a stack) as float32."""
+    pick = (lambda t: t) if index is None else (lambda t: t[index.long()])
+    if leaf.mode == "affine" and leaf.biases is not None:
+        return affine_dequantize(pick(leaf.weight), pick(leaf.scales), pick(leaf.biases),
+                                 leaf.group_size, leaf.bits)
+    if leaf.mode == "mxfp4" and leaf.biases is None and leaf.bits == 4 and leaf.group_size == 32:
+        return mxfp4_dequantize(pick(leaf.weight), pick(leaf.scales))
+    raise NotImplementedError(f"no decoder for quantization mode {leaf.mode!r}")
+
+
 @dataclass
 class QuantizedSwitchLinearLeaf:
-    """An affine-quantized expert stack, the reference's `QuantizedSwitchLinear` leaf
+    """A quantized expert stack, the reference's `QuantizedSwitchLinear` leaf
     (core/layers.py:164-197): weight [experts, out, in * bits / 32] 32-bit words (int32 or
-    uint32), scales and biases [experts, out, in / group_size] bf16. Only mode "affine"
-    carries biases; other modes are declared but decoded by nothing here."""
+    uint32) and scales [experts, out, in / group_size]. Mode "affine": bf16 scales and
+    biases, 2-8 bits. Mode "mxfp4": 4 bits, groups of 32, uint8 e8m0 scales, no biases.
+    Other modes are declared but decoded by nothing here."""
 
     weight: torch.Tensor
     scales: torch.Tensor
@@ -69,16 +95,13 @@ class QuantizedSwitchLinearLeaf:
 
     def matrices(self, index: torch.Tensor) -> torch.Tensor:
         """The indexed experts' dequantized matrices as float32 [k, out, in]."""
-        if self.mode != "affine" or self.biases is None:
-            raise NotImplementedError(f"no decoder for quantization mode {self.mode!r}")
-        i = index.long()
-        return affine_dequantize(self.weight[i], self.scales[i], self.biases[i], self.group_size, self.bits)
+        return dequantize(self, index)
 
 
 @dataclass
 class QuantizedLinearLeaf:
-    """One affine-quantized matrix, `nn.QuantizedLinear` (weight [out, in * bits / 32],
-    scales and biases [out, in / group_size]); called as the layer, x [..., in] ->
+    """One quantized matrix, `nn.QuantizedLinear` (weight [out, in * bits / 32], scales
+    [out, in / group_size], biases in mode "affine"); called as the layer, x [..., in] ->
     [..., out] with an fp32 sum rounded to x's dtype, as mx.quantized_matmul does."""
 
     weight: torch.Tensor
@@ -89,10 +112,7 @@ class QuantizedLinearLeaf:
     mode: str = "affine"
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
-        if self.mode != "affine" or self.biases is None:
-            raise NotImplementedError(f"no decoder for quantization mode {self.mode!r}")
-        w = affine_dequantize(self.weight, self.scales, self.biases, self.group_size, self.bits)
-        return (x.float() @ w.T).to(x.dtype)
+        return (x.float() @ dequantize(self).T).to(x.dtype)
 
 
 def swish(x: torch.Tensor) -> torch.Tensor:

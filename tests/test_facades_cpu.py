@@ -503,3 +503,67 @@ def test_attention_core_chain_matches_oracle_on_cpu():
             assert_bf16_close(got, want, min_exact=0.9)
             keys, values = bits(cache.keys[0]), bits(cache.values[0])
         assert cache.offset == 12
+
+
+def test_torch_mxfp4_decoder_matches_the_oracle():
+    from mlx_omnia_amd.kernels.leaf import mxfp4_dequantize
+    from oracle import mxfp4
+
+    rng = np.random.default_rng(31)
+    words = rng.integers(0, 1 << 32, size=(3, 5, 16), dtype=np.uint64).astype(np.uint32)
+    scales = rng.integers(0, 200, size=(3, 5, 4)).astype(np.uint8)
+    scales[0, 0, :2] = (0, 1)                 # a zero factor and the smallest normal one
+    got = mxfp4_dequantize(torch.from_numpy(words.view(np.int32)), torch.from_numpy(scales))
+    want = mxfp4.dequantize(mxfp4.Stack(words, scales, None))
+    assert np.array_equal(got.numpy().astype(np.float64), want)
+
+
+def _mxfp4_leaf(rng, experts, rows, features):
+    from mlx_omnia_amd.kernels.leaf import QuantizedSwitchLinearLeaf
+    from oracle import mxfp4
+
+    words = rng.integers(0, 1 << 32, size=(experts, rows, features // 8), dtype=np.uint64).astype(np.uint32)
+    scales = rng.integers(119, 123, size=(experts, rows, features // 32)).astype(np.uint8)
+    b = from_float(0.25 * rng.standard_normal((experts, rows)))
+    leaf = QuantizedSwitchLinearLeaf(torch.from_numpy(words.view(np.int32)), torch.from_numpy(scales),
+                                     None, 32, 4, mode="mxfp4")
+    return mxfp4.Stack(words, scales, b), leaf, cpu(b)
+
+
+def test_mxfp4_moe_cpu_resolves_to_core_and_matches_oracle():
+    from mlx_omnia_amd.kernels.down_combine import DefaultDownCombine, DownCombine, HipMxfp4DownCombine
+    from mlx_omnia_amd.kernels.gate_up import DefaultGateUp, GateUp, HipMxfp4GateUp
+    from oracle import mxfp4
+
+    experts, hidden, inner = 6, 128, 64
+    rng = np.random.default_rng(32)
+    gstack, gleaf, gbias = _mxfp4_leaf(rng, experts, 2 * inner, hidden)
+    dstack, dleaf, dbias = _mxfp4_leaf(rng, experts, hidden, inner)
+    declared = dict(hidden=hidden, inner=inner, activation="swiglu_oai", limit=7.0, bias=gbias)
+    gate_up = GateUp(gleaf, **declared)
+    down = DownCombine(dleaf, hidden=hidden, inner=inner, bias=dbias)
+    assert isinstance(gate_up.strategy, DefaultGateUp) and isinstance(down.strategy, DefaultDownCombine)
+    assert HipMxfp4GateUp.build(gleaf, layout="interleaved", routing=None, shared=None, **declared) is None
+    assert HipMxfp4DownCombine.build(dleaf, hidden=hidden, inner=inner, bias=dbias, shared=None,
+                                     layout="interleaved") is None
+    x = from_float(2 * rng.standard_normal(hidden))
+    chosen = np.array([5, 0, 3, 1], dtype=np.int32)
+    act_core = gate_up(cpu(x), torch.from_numpy(chosen))
+    # The Core chain rounds 1.702 g to bf16 before the sigmoid: the same function, looser.
+    np.testing.assert_allclose(to_f32(bits(act_core)), to_f32(mxfp4.gate_up(x, gstack, chosen, 7.0)),
+                               rtol=0.06, atol=0.02)
+    weights = to_f32(from_float(rng.dirichlet(np.ones(4))))
+    residual = from_float(rng.standard_normal(hidden))
+    out = down(act_core, torch.from_numpy(chosen), torch.from_numpy(weights).to(torch.bfloat16),
+               cpu(residual))
+    # The Core chain rounds the row before the bias add and sums in bf16.
+    assert_bf16_close(bits(out), mxfp4.down_combine(bits(act_core), dstack, chosen, weights, residual),
+                      min_exact=0.8)
+
+
+def test_mxfp4_predicate():
+    from mlx_omnia_amd.kernels.gate_up import mxfp4_applies
+
+    assert mxfp4_applies(2880, 2880) and mxfp4_applies(32, 32)
+    for args in ((2880, 2888), (2888, 2880), (0, 32), (32, 0)):
+        assert not mxfp4_applies(*args), args

@@ -137,3 +137,81 @@ def test_shape_checks_raise_before_launch():
     act = to_device(from_float(rng.standard_normal((2, 4096))))
     with pytest.raises(ValueError):                           # inner past the kernel's 3072
         ops.moe_down_combine_mxfp4(act, dleaf, _ids([0, 1]), f32_to_device(np.ones(2, np.float32)))
+
+
+def _switch_leaf(leaf):
+    from mlx_omnia_amd.kernels.leaf import QuantizedSwitchLinearLeaf
+
+    return QuantizedSwitchLinearLeaf(leaf.weight, leaf.scales, None, 32, 4, mode="mxfp4")
+
+
+def test_facades_resolve_to_the_mxfp4_bindings_and_agree_with_the_core_chain():
+    from mlx_omnia_amd.kernels.down_combine import DefaultDownCombine, DownCombine, HipMxfp4DownCombine
+    from mlx_omnia_amd.kernels.gate_up import DefaultGateUp, GateUp, HipMxfp4GateUp
+
+    rng = np.random.default_rng(10)
+    _, g = _leaf(rng, EXPERTS, 2 * INNER, HIDDEN)
+    _, d = _leaf(rng, EXPERTS, HIDDEN, INNER)
+    gleaf, dleaf = _switch_leaf(g), _switch_leaf(d)
+    declared = dict(hidden=HIDDEN, inner=INNER, activation="swiglu_oai", limit=7.0, bias=g.bias)
+    gate_up = GateUp(gleaf, **declared)
+    down = DownCombine(dleaf, hidden=HIDDEN, inner=INNER, bias=d.bias)
+    assert isinstance(gate_up.strategy, HipMxfp4GateUp)
+    assert isinstance(down.strategy, HipMxfp4DownCombine)
+    core_gate_up = GateUp(gleaf, reference=True, **declared)
+    core_down = DownCombine(dleaf, hidden=HIDDEN, inner=INNER, bias=d.bias, reference=True)
+    assert isinstance(core_gate_up.strategy, DefaultGateUp)
+    assert isinstance(core_down.strategy, DefaultDownCombine)
+    # What the kernels do not bake goes to the Core chain: no bias, no clamp, silu, the
+    # blocked layout, a shared expert.
+    for change in (dict(bias=None), dict(limit=None), dict(activation="silu"), dict(layout="blocked"),
+                   dict(shared=lambda row: row)):
+        assert isinstance(GateUp(gleaf, **dict(declared, **change)).strategy, DefaultGateUp), change
+    assert isinstance(DownCombine(dleaf, hidden=HIDDEN, inner=INNER).strategy, DefaultDownCombine)
+
+    x = from_float(2 * rng.standard_normal(HIDDEN))
+    chosen = torch.tensor([2, 7, 0, 5], dtype=torch.int32, device="cuda")
+    act = gate_up(to_device(x), chosen)
+    assert torch.equal(act, ops.moe_gate_up_mxfp4(to_device(x), g, chosen, limit=7.0))
+    # The Core chain rounds 1.702 g to bf16 before the sigmoid: the same function, looser.
+    core_act = core_gate_up(to_device(x), chosen)
+    np.testing.assert_allclose(act.float().cpu().numpy(), core_act.float().cpu().numpy(), rtol=0.06, atol=0.02)
+    weights = torch.tensor([0.4, 0.3, 0.2, 0.1], dtype=torch.float32, device="cuda")
+    residual = to_device(from_float(rng.standard_normal(HIDDEN)))
+    got = down(act, chosen, weights, residual)
+    assert torch.equal(got, ops.moe_down_combine_mxfp4(act, d, chosen, weights, residual))
+    core = core_down(act, chosen, weights.to(torch.bfloat16), residual).float().cpu().numpy()
+    # The Core chain rounds each row before the bias add and each weighted row to bf16: a
+    # few ulps of the largest term, so the bound is relative to the output's scale.
+    assert np.abs(got.float().cpu().numpy() - core).max() <= 4 * 2.0 ** -8 * np.abs(core).max()
+
+
+def test_down_facade_hands_more_than_16_slots_to_the_core_chain():
+    from mlx_omnia_amd.kernels.down_combine import DownCombine, HipMxfp4DownCombine
+
+    rng = np.random.default_rng(11)
+    stack, d = _leaf(rng, EXPERTS, HIDDEN, INNER)
+    down = DownCombine(_switch_leaf(d), hidden=HIDDEN, inner=INNER, bias=d.bias)
+    assert isinstance(down.strategy, HipMxfp4DownCombine)
+    ids = list(rng.integers(0, EXPERTS, size=20))
+    act = from_float(rng.standard_normal((20, INNER)))
+    weights = np.full(20, 0.05, dtype=np.float32)
+    got = down(to_device(act), _ids(ids), f32_to_device(weights), None).to(torch.bfloat16)
+    # The Core chain rounds each row before the bias add and sums in torch's order: within
+    # the bf16 bar (2 ulps of the output's scale), about 40% bit-identical at this shape.
+    assert_bf16_close(bits_of(got), mxfp4.down_combine(act, stack, ids, weights, None), min_exact=0.3)
+
+
+def test_golden_fixture():
+    golden = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "moe_mxfp4.npz")
+
+    def leaf(name):
+        return ops.Mxfp4Leaf(torch.from_numpy(golden[f"{name}_weight"].view(np.int32)).cuda(),
+                             torch.from_numpy(golden[f"{name}_scales"]).cuda(), to_device(golden[f"{name}_bias"]))
+
+    chosen = torch.from_numpy(golden["chosen"]).cuda()
+    act = ops.moe_gate_up_mxfp4(to_device(golden["x"]), leaf("gate_up"), chosen, limit=float(golden["limit"]))
+    assert_bf16_close(bits_of(act), golden["act"], min_exact=0.99)
+    out = ops.moe_down_combine_mxfp4(to_device(golden["act"]), leaf("down"), chosen,
+                                     f32_to_device(golden["weights"]), to_device(golden["residual"]))
+    assert_bf16_close(bits_of(out), golden["out"], min_exact=0.99)
