@@ -26,10 +26,15 @@
 // memory order. A lane takes 32 values at a time, 16 bytes and exactly one scale group;
 // the group's dot product is scaled once in fp32.
 //
-// gate_up: a wave owns kPairsPerWave gate/up pairs of one slot and streams them together;
-// lane p runs pair p's activation. down_combine: a workgroup owns kDownRows output rows
-// with one wave per slot; 16 lanes share a row, each taking every 16th chunk of it, all of
-// its weight bytes loaded before any arithmetic; the slots' terms meet in LDS and are
+// Both kernels issue every load of a lane (codes, the scale byte into a register of its
+// own, the activations) before any arithmetic and with no branch among the loads: a load
+// inside a divergent branch, or a scale byte packed beside another, makes the compiler
+// wait on it, one memory round trip per chunk.
+//
+// gate_up: a wave owns kPairsPerWave gate/up pairs of one slot and streams them together,
+// 64 lanes across each row; lane p runs pair p's activation. down_combine: a workgroup
+// owns kDownRows output rows with one wave per slot, 64 lanes across each row and the
+// slot's activations held once for all of them; the slots' terms meet in LDS and are
 // summed in slot order.
 #include "common.hpp"
 #include "host.hpp"
@@ -40,14 +45,14 @@ namespace {
 constexpr int kChunk = 32;                // values per lane per step: 16 bytes, one group
 constexpr int kPairsPerWave = 2;          // gate_up: gate/up pairs per wave
 constexpr int kGateWaves = 4;             // gate_up: waves per workgroup
-constexpr int kLanesPerRow = 16;          // down: lanes sharing an output row
-constexpr int kDownRows = kWave / kLanesPerRow;
-constexpr int kMaxInner = 3072;           // down: inner / (32 * 16) steps per lane
-constexpr int kMaxDownSteps = kMaxInner / (kChunk * kLanesPerRow);
+constexpr int kGateBatch = 2;             // gate_up: 64-chunk trips whose loads go out together
+constexpr int kDownRows = 4;              // down: output rows per workgroup, each wave's share
+constexpr int kMaxInner = 4096;           // down: at most two 64-chunk steps per lane
+constexpr int kMaxDownSteps = kMaxInner / (kChunk * kWave);
 constexpr int kMaxDownSlots = 16;
 
 // The e8m0 group scale as the reference applies it: the fp32 with exponent field `byte`.
-__device__ __forceinline__ float e8m0(uint8_t byte) { return __uint_as_float(static_cast<uint32_t>(byte) << 23); }
+__device__ __forceinline__ float e8m0(uint32_t byte) { return __uint_as_float(byte << 23); }
 
 // The e2m1 codes of byte B of a word as a bf16 pair, low nibble first.
 template <int B>
@@ -69,14 +74,6 @@ __device__ __forceinline__ float chunk_dot(const u32x4& w, const u32x4 (&x)[4]) 
   return acc;
 }
 
-// Sum over each group of 16 aligned lanes (one DPP row), the same in each of them.
-__device__ __forceinline__ float row_sum16(float v) {
-  v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
-  v += __uint_as_float(dpp<kQuadSwap2>(__float_as_uint(v)));
-  v += __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
-  return v + __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
-}
-
 struct Stack {
   const u32x4* weight;     // [experts, rows, in / 32] chunks of 16 bytes
   const uint8_t* scales;   // [experts, rows, in / 32]
@@ -96,6 +93,8 @@ struct GateUpArgs {
   float limit;             // +inf: no clamp
 };
 
+// kTrips > 0: hidden / 32 chunks span exactly kTrips 64-lane trips; 0: any number of trips.
+template <int kTrips>
 __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_mxfp4_kernel(GateUpArgs a) {
   const int lane = threadIdx.x % kWave;
   const int slot = blockIdx.y;
@@ -112,26 +111,40 @@ __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_mxfp4_kernel(G
   const int rows = 2 * pairs;
   const int64_t row0 = static_cast<int64_t>(expert) * 2 * a.inner + 2 * static_cast<int64_t>(pair0);
   const int chunks = a.hidden / kChunk;
+  constexpr int kBatch = kTrips > 0 ? kTrips : kGateBatch;
+  const int trips = kTrips > 0 ? kTrips : (chunks + kWave - 1) / kWave;
   float r[kRows];
 #pragma unroll
   for (int i = 0; i < kRows; ++i) r[i] = 0.0f;
-  for (int c = lane; c < chunks; c += kWave) {
-    u32x4 w[kRows];
-    uint8_t s[kRows];
+  // kBatch trips' loads are issued before their arithmetic, with no branch among them (a
+  // branch there makes the compiler wait on each load): a lane past the row's end re-reads
+  // the last chunk and drops the term, and a row past the wave's last pair re-reads the
+  // pair's last row (that sum is never stored).
+  for (int t0 = 0; t0 < trips; t0 += kBatch) {
+    u32x4 w[kBatch][kRows];
+    uint32_t s[kBatch][kRows];
+    u32x4 x[kBatch][4];
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-      if (i < rows) {
-        const int64_t at = (row0 + i) * chunks + c;
-        w[i] = load_nt(a.stack.weight + at);
-        s[i] = a.stack.scales[at];
+    for (int h = 0; h < kBatch; ++h) {
+      const int c = min(lane + (t0 + h) * kWave, chunks - 1);
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) {
+        const int64_t at = (row0 + min(i, rows - 1)) * chunks + c;
+        w[h][i] = load_nt(a.stack.weight + at);
+        s[h][i] = a.stack.scales[at];
       }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[h][j] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[j];
     }
-    u32x4 x[4];
+    __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[i];
+    for (int h = 0; h < kBatch; ++h) {
+      const bool in_row = lane + (t0 + h) * kWave < chunks;
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-      if (i < rows) r[i] = __builtin_fmaf(e8m0(s[i]), chunk_dot(w[i], x), r[i]);
+      for (int i = 0; i < kRows; ++i) {
+        const float term = __builtin_fmaf(e8m0(s[h][i]), chunk_dot(w[h][i], x[h]), r[i]);
+        r[i] = in_row ? term : r[i];
+      }
     }
   }
   // Lane p takes pair p's sums and runs its activation.
@@ -175,53 +188,70 @@ struct DownArgs {
   int slots;
 };
 
+// kSteps = ceil(inner / (32 * 64)) chunks per lane: 1 or 2.
+template <int kSteps>
 __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_mxfp4_kernel(DownArgs a) {
   __shared__ float partial[kMaxDownSlots][kDownRows];
   const int lane = threadIdx.x % kWave;
   const int slot = threadIdx.x / kWave;   // one wave per slot
   const int row_base = blockIdx.x * kDownRows;
-  const int r = lane / kLanesPerRow;
-  const int part = lane % kLanesPerRow;
+  const int rows = min(kDownRows, a.hidden - row_base);
   const int expert = a.chosen[slot];
-  const bool valid = expert >= 0 && expert < a.experts;
-  const bool live = valid && row_base + r < a.hidden;   // uniform over the lane's row
-  const int64_t row = static_cast<int64_t>(valid ? expert : 0) * a.hidden + row_base + r;
+  const bool valid = expert >= 0 && expert < a.experts;   // uniform over the wave
+  const int64_t row0 = static_cast<int64_t>(valid ? expert : 0) * a.hidden + row_base;
   const int chunks = a.inner / kChunk;
-  float t = 0.0f;
-  if (live) {
-    u32x4 w[kMaxDownSteps];
-    uint8_t s[kMaxDownSteps];
+  float t[kDownRows];
 #pragma unroll
-    for (int i = 0; i < kMaxDownSteps; ++i) {
-      const int c = part + kLanesPerRow * i;
-      if (c < chunks) {
-        w[i] = load_nt(a.stack.weight + row * chunks + c);
-        s[i] = a.stack.scales[row * chunks + c];
-      }
-    }
+  for (int i = 0; i < kDownRows; ++i) t[i] = 0.0f;
+  if (valid) {
+    // Every load (codes, scale bytes, the slot's activations, shared by the wave's rows)
+    // is issued before any arithmetic, with no branch among them: a lane past the row's
+    // last chunk re-reads that chunk and drops the term, and a row past the last one
+    // re-reads the last (its sum is never used).
     const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
+    u32x4 w[kSteps][kDownRows];
+    uint32_t s[kSteps][kDownRows];
+    u32x4 xv[kSteps][4];
 #pragma unroll
-    for (int i = 0; i < kMaxDownSteps; ++i) {
-      const int c = part + kLanesPerRow * i;
-      if (c < chunks) {
-        u32x4 xv[4];
+    for (int h = 0; h < kSteps; ++h) {
+      const int c = min(lane + kWave * h, chunks - 1);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xv[j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
-        t = __builtin_fmaf(e8m0(s[i]), chunk_dot(w[i], xv), t);
+      for (int i = 0; i < kDownRows; ++i) {
+        const int64_t at = (row0 + min(i, rows - 1)) * chunks + c;
+        w[h][i] = load_nt(a.stack.weight + at);
+        s[h][i] = a.stack.scales[at];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xv[h][j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
+#pragma unroll
+    for (int h = 0; h < kSteps; ++h) {
+      const bool in_row = lane + kWave * h < chunks;
+#pragma unroll
+      for (int i = 0; i < kDownRows; ++i) {
+        const float term = __builtin_fmaf(e8m0(s[h][i]), chunk_dot(w[h][i], xv[h]), t[i]);
+        t[i] = in_row ? term : t[i];
       }
     }
   }
-  t = row_sum16(t);
-  if (part == 0) {
+  // Lane i takes row i's sum.
+  float mine = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kDownRows; ++i) {
+    const float total = wave_sum_f32(t[i]);
+    mine = lane == i ? total : mine;
+  }
+  if (lane < rows) {
     float term = 0.0f;
     if (valid) {
-      const float bias = a.stack.bias != nullptr && live ? bf16_to_f32(a.stack.bias[row]) : 0.0f;
-      term = round_bf16(round_bf16(t + bias) * a.weights[slot]);
+      const float bias = a.stack.bias != nullptr ? bf16_to_f32(a.stack.bias[row0 + lane]) : 0.0f;
+      term = round_bf16(round_bf16(mine + bias) * a.weights[slot]);
     }
-    partial[slot][r] = term;
+    partial[slot][lane] = term;
   }
   __syncthreads();
-  if (threadIdx.x < kDownRows && row_base + static_cast<int>(threadIdx.x) < a.hidden) {
+  if (static_cast<int>(threadIdx.x) < rows) {
     const int n = row_base + threadIdx.x;
     float sum = 0.0f;
     for (int j = 0; j < a.slots; ++j) sum += partial[j][threadIdx.x];
@@ -254,7 +284,11 @@ extern "C" int32_t omnia_moe_gate_up_mxfp4(const uint16_t* x, const uint32_t* we
                static_cast<int>(hidden), static_cast<int>(inner), limit};
   const int64_t waves = (inner + kPairsPerWave - 1) / kPairsPerWave;
   const dim3 grid(static_cast<unsigned>((waves + kGateWaves - 1) / kGateWaves), static_cast<unsigned>(slots));
-  moe_gate_up_mxfp4_kernel<<<grid, kGateWaves * kWave, 0, stream>>>(a);
+  switch ((hidden / kChunk + kWave - 1) / kWave) {
+    case 1: moe_gate_up_mxfp4_kernel<1><<<grid, kGateWaves * kWave, 0, stream>>>(a); break;
+    case 2: moe_gate_up_mxfp4_kernel<2><<<grid, kGateWaves * kWave, 0, stream>>>(a); break;
+    default: moe_gate_up_mxfp4_kernel<0><<<grid, kGateWaves * kWave, 0, stream>>>(a); break;
+  }
   return launched("moe_gate_up_mxfp4");
 }
 
@@ -268,7 +302,7 @@ extern "C" int32_t omnia_moe_down_combine_mxfp4(const uint16_t* act, const uint3
   OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), "moe_down_combine_mxfp4: bad expert count");
   OMNIA_REQUIRE(hidden > 0 && hidden < (int64_t{1} << 24), "moe_down_combine_mxfp4: bad hidden size");
   OMNIA_REQUIRE(inner > 0 && inner % kChunk == 0 && inner <= kMaxInner,
-                "moe_down_combine_mxfp4: inner must be a multiple of 32 in [32, 3072]");
+                "moe_down_combine_mxfp4: inner must be a multiple of 32 in [32, 4096]");
   OMNIA_REQUIRE(slots > 0 && slots <= kMaxDownSlots, "moe_down_combine_mxfp4: slots must be in [1, 16]");
   OMNIA_REQUIRE(act && weight && scales && chosen && weights && out, "moe_down_combine_mxfp4: null pointer");
   OMNIA_REQUIRE(aligned16(act) && aligned16(weight), "moe_down_combine_mxfp4: act and weight must be 16-byte aligned");
@@ -277,6 +311,12 @@ extern "C" int32_t omnia_moe_down_combine_mxfp4(const uint16_t* act, const uint3
   DownArgs a{act, Stack{reinterpret_cast<const u32x4*>(weight), scales, bias}, chosen, weights, residual, out,
              experts, static_cast<int>(hidden), static_cast<int>(inner), static_cast<int>(slots)};
   const dim3 grid(static_cast<unsigned>((hidden + kDownRows - 1) / kDownRows));
-  moe_down_mxfp4_kernel<<<grid, static_cast<unsigned>(slots * kWave), 0, stream>>>(a);
+  const dim3 block(static_cast<unsigned>(slots * kWave));
+  static_assert(kMaxDownSteps == 2, "one instantiation per step count");
+  if (inner <= kChunk * kWave) {
+    moe_down_mxfp4_kernel<1><<<grid, block, 0, stream>>>(a);
+  } else {
+    moe_down_mxfp4_kernel<2><<<grid, block, 0, stream>>>(a);
+  }
   return launched("moe_down_combine_mxfp4");
 }

@@ -8,7 +8,7 @@ Mirrors core/kernels/down_combine/__init__.py and kernel.py (`DownCombine`,
 - `HipMxfp4DownCombine` (`omnia_moe_down_combine_mxfp4`, csrc/moe_mxfp4.hip) serves what
   the reference's `Mxfp4DownCombine` serves (core/kernels/down_combine/mxfp4.py:80-101):
   an MXFP4 stack under the `interleaved` layout with the per-row projection bias, no
-  shared expert, hidden and inner multiples of 32 (inner up to 3072), at most 16 slots
+  shared expert, hidden and inner multiples of 32 (inner up to 4096), at most 16 slots
   (more go to the Core chain). Per slot bf16(bf16(dot + bias) * weight), the slot sum in
   fp32 in slot order, then the residual add, in one dispatch.
 - `HipAffineDownCombine` (`omnia_moe_down_combine_affine`, csrc/moe_affine.hip) serves
@@ -179,7 +179,7 @@ class HipMxfp4DownCombine(DownCombineStrategy):
     def build(cls, leaf, *, hidden, inner, bias, shared, layout) -> "HipMxfp4DownCombine | None":
         if layout != "interleaved" or bias is None or shared is not None:
             return None
-        if not mxfp4_applies(hidden, inner) or inner > 3072:  # six 32-value steps per lane
+        if not mxfp4_applies(hidden, inner) or inner > 4096:  # two 64-chunk steps per lane
             return None
         view = mxfp4_leaf(leaf, bias, hidden, inner)
         if view is None:

@@ -41,6 +41,17 @@ def _ids(values):
     return torch.tensor(values, dtype=torch.int32, device="cuda")
 
 
+@pytest.mark.parametrize("hidden", [32, 2048, 4096 + 32, 16384])
+def test_gate_up_trip_counts(hidden):
+    """One, two and more 64-chunk trips per lane (the runtime loop, odd trip counts)."""
+    print(f"moe_gate_up_mxfp4 hidden={hidden}", flush=True)
+    rng = np.random.default_rng(hidden)
+    stack, leaf = _leaf(rng, 3, 2 * 96, hidden)
+    x = from_float(rng.standard_normal(hidden))
+    got = ops.moe_gate_up_mxfp4(to_device(x), leaf, _ids([2, 0]), limit=7.0)
+    assert_bf16_close(bits_of(got), mxfp4.gate_up(x, stack, [2, 0], 7.0), min_exact=0.99)
+
+
 @pytest.mark.parametrize("limit", [7.0, 0.5, None])
 def test_gate_up_matches_oracle(limit):
     print(f"moe_gate_up_mxfp4 limit={limit}", flush=True)
@@ -105,11 +116,12 @@ def test_down_combine_gpt_oss_shape():
                       min_exact=0.99)
 
 
-@pytest.mark.parametrize("slots", [1, 16])
-def test_down_combine_slots_no_bias_no_residual(slots):
-    print(f"moe_down_combine_mxfp4 slots={slots}", flush=True)
+@pytest.mark.parametrize("slots,hidden,inner", [(1, 520, 3072), (16, 522, 4096), (3, 64, 2048), (2, 7, 96)])
+def test_down_combine_slots_no_bias_no_residual(slots, hidden, inner):
+    """Row counts that leave the last workgroup short, one and two 64-chunk steps."""
+    print(f"moe_down_combine_mxfp4 slots={slots} hidden={hidden} inner={inner}", flush=True)
     rng = np.random.default_rng(6 + slots)
-    stack, leaf, act, weights, _ = _down(rng, slots, hidden=520, inner=3072, experts=20, bias=False)
+    stack, leaf, act, weights, _ = _down(rng, slots, hidden=hidden, inner=inner, experts=20, bias=False)
     chosen = list(rng.integers(0, 20, size=slots))
     got = ops.moe_down_combine_mxfp4(to_device(act), leaf, _ids(chosen), f32_to_device(weights))
     assert_bf16_close(bits_of(got), mxfp4.down_combine(act, stack, chosen, weights, None), min_exact=0.99)
@@ -133,9 +145,9 @@ def test_shape_checks_raise_before_launch():
     _, leaf = _leaf(rng, EXPERTS, 2 * INNER, HIDDEN)
     with pytest.raises(ValueError):
         ops.moe_gate_up_mxfp4(to_device(from_float(rng.standard_normal(HIDDEN + 32))), leaf, _ids([0]))
-    _, dleaf = _leaf(rng, EXPERTS, HIDDEN, 4096)
-    act = to_device(from_float(rng.standard_normal((2, 4096))))
-    with pytest.raises(ValueError):                           # inner past the kernel's 3072
+    _, dleaf = _leaf(rng, EXPERTS, HIDDEN, 4128)
+    act = to_device(from_float(rng.standard_normal((2, 4128))))
+    with pytest.raises(ValueError):                           # inner past the kernel's 4096
         ops.moe_down_combine_mxfp4(act, dleaf, _ids([0, 1]), f32_to_device(np.ones(2, np.float32)))
 
 
