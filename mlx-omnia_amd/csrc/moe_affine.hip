@@ -34,12 +34,16 @@
 // interleaved matrix) and streams them together; x is read per 32-value chunk from L2, and
 // lane p runs pair p's activation. down_combine: a workgroup owns kDownRows output rows
 // with one wave per slot; kLanesPerRow lanes share a row, each taking every kLanesPerRow-th
-// chunk of it, all of its weight words loaded before any arithmetic; the slots' terms meet
-// in LDS and are summed in slot order.
+// chunk of it; the slots' terms meet in LDS and are summed in slot order.
+// Both issue a lane's loads (words, scale and bias bits each in a register of its own, the
+// activations) before the arithmetic, with no branch among them: a scale packed beside
+// another or a load inside a divergent branch makes the compiler wait on each load, one
+// round trip per chunk. The down kernel is compiled per step count, so a lane issues no
+// load past the row's end.
 // Measured at Qwen3-30B-A3B's routed MLP, 4 bits, groups of 64, one call: gate_up with 2
-// pairs per wave 6.1 us (4 pairs: 7.6, 8 pairs: 8.7, 1 pair: 6.6); down with 16 lanes per
-// row 5.9 us (8 lanes: 6.45, 8 lanes and two rows per lane: 8.8). Without the decode
-// arithmetic gate_up takes 5.2 us: the rest is the loads' latency.
+// pairs per wave 6.0 us (before the load issue was fixed: 4 pairs 7.6, 8 pairs 8.7, 1 pair
+// 6.6 against 6.1 for 2); down with 16 lanes per row 5.4 us (before: 8 lanes 6.45, 8 lanes
+// and two rows per lane 8.8 against 5.9 for 16).
 #include "common.hpp"
 #include "host.hpp"
 
@@ -179,9 +183,9 @@ __device__ __forceinline__ float chunk_dot(const uint32_t (&w)[B], const uint32_
 
 // The chunk's contribution scale * sum(x q) + bias * sum(x), from chunk_dot's value.
 template <int B>
-__device__ __forceinline__ float chunk_term(float dot, float xsum, uint16_t scale_bits, uint16_t bias_bits) {
-  const float s = bf16_to_f32(scale_bits);
-  const float b = bf16_to_f32(bias_bits);
+__device__ __forceinline__ float chunk_term(float dot, float xsum, uint32_t scale_bits, uint32_t bias_bits) {
+  const float s = __uint_as_float(scale_bits << 16);   // bf16 bits, zero-extended
+  const float b = __uint_as_float(bias_bits << 16);
   const float shifted = B == 8 ? b : b - 128.0f * s;
   return __builtin_fmaf(s, dot, shifted * xsum);
 }
@@ -220,27 +224,33 @@ __device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const Leaf& le
   const int chunks = a.hidden / kChunk;
   const int64_t words = static_cast<int64_t>(a.hidden) * B / 32;
   const int groups = a.hidden / leaf.group;
-  for (int c = lane; c < chunks; c += kWave) {
+  const int trips = (chunks + kWave - 1) / kWave;   // uniform over the wave
+  for (int trip = 0; trip < trips; ++trip) {
+    // Every load of the trip goes out before its arithmetic, with no branch among them:
+    // a lane past the row's end re-reads the last chunk and drops the term, and a row
+    // past the wave's last pair re-reads the pair's last row (that sum is never stored).
+    const int c = min(lane + kWave * trip, chunks - 1);
     uint32_t w[2 * kPairsPerWave][B];
-    uint16_t sb[2 * kPairsPerWave], bb[2 * kPairsPerWave];
+    uint32_t sb[2 * kPairsPerWave], bb[2 * kPairsPerWave];
 #pragma unroll
     for (int i = 0; i < 2 * kPairsPerWave; ++i) {
-      if (i < rows) {
-        const int64_t row = row0 + i;
-        load_words<B>(leaf.weight + row * words + static_cast<int64_t>(c) * B, w[i]);
-        const int64_t g = row * groups + (c * kChunk) / leaf.group;
-        sb[i] = leaf.scales[g];
-        bb[i] = leaf.biases[g];
-      }
+      const int64_t row = row0 + min(i, rows - 1);
+      load_words<B>(leaf.weight + row * words + static_cast<int64_t>(c) * B, w[i]);
+      const int64_t g = row * groups + (c * kChunk) / leaf.group;
+      sb[i] = leaf.scales[g];
+      bb[i] = leaf.biases[g];
     }
     u32x4 raw[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) raw[i] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[i];
+    __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
     uint32_t xq[16];
     const float xsum = pair_x<B>(raw, xq);
+    const bool in_row = lane + kWave * trip < chunks;
 #pragma unroll
     for (int i = 0; i < 2 * kPairsPerWave; ++i) {
-      if (i < rows) r[i] += chunk_term<B>(chunk_dot<B>(w[i], xq), xsum, sb[i], bb[i]);
+      const float term = r[i] + chunk_term<B>(chunk_dot<B>(w[i], xq), xsum, sb[i], bb[i]);
+      r[i] = in_row ? term : r[i];
     }
   }
 }
@@ -315,49 +325,44 @@ struct DownArgs {
 // live[q]) over the chunks part, part + 8, ... of the slot's activation row: every
 // weight word in flight before the first multiply, each activation chunk loaded once for
 // all the rows.
-template <int B>
+template <int B, int kSteps>
 __device__ __forceinline__ void down_rows(const DownArgs& a, const Leaf& leaf, int64_t row0,
                                           const bool (&live)[kRowsPerLane], int slot, int part,
                                           float (&t)[kRowsPerLane]) {
   const int chunks = a.inner / kChunk;
   const int64_t words = static_cast<int64_t>(a.inner) * B / 32;
   const int groups = a.inner / leaf.group;
-  uint32_t w[kRowsPerLane][kMaxDownSteps][B];
-  uint16_t sb[kRowsPerLane][kMaxDownSteps], bb[kRowsPerLane][kMaxDownSteps];
-#pragma unroll
-  for (int q = 0; q < kRowsPerLane; ++q) {
-    const int64_t row = row0 + kOctets * q;
-#pragma unroll
-    for (int i = 0; i < kMaxDownSteps; ++i) {
-      const int c = part + kLanesPerRow * i;
-      if (live[q] && c < chunks) {
-        load_words<B>(leaf.weight + row * words + static_cast<int64_t>(c) * B, w[q][i]);
-        const int64_t g = row * groups + (c * kChunk) / leaf.group;
-        sb[q][i] = leaf.scales[g];
-        bb[q][i] = leaf.biases[g];
-      }
-    }
-  }
+  static_assert(kRowsPerLane == 1, "the caller checks the lane's one row for liveness");
+  // Every load (words, scale and bias bits in registers of their own, the activations)
+  // goes out before any arithmetic, with no branch among them: a lane past the row's
+  // last chunk re-reads that chunk and drops the term.
+  uint32_t w[kSteps][B];
+  uint32_t sb[kSteps], bb[kSteps];
+  u32x4 raw[kSteps][4];
   const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
 #pragma unroll
-  for (int q = 0; q < kRowsPerLane; ++q) t[q] = 0.0f;
+  for (int i = 0; i < kSteps; ++i) {
+    const int c = min(part + kLanesPerRow * i, chunks - 1);
+    load_words<B>(leaf.weight + row0 * words + static_cast<int64_t>(c) * B, w[i]);
+    const int64_t g = row0 * groups + (c * kChunk) / leaf.group;
+    sb[i] = leaf.scales[g];
+    bb[i] = leaf.biases[g];
 #pragma unroll
-  for (int i = 0; i < kMaxDownSteps; ++i) {
-    const int c = part + kLanesPerRow * i;
-    if (c < chunks) {
-      u32x4 raw[4];
+    for (int j = 0; j < 4; ++j) raw[i][j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
+  }
+  __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
+  t[0] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) raw[j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
-      uint32_t xq[16];
-      const float xsum = pair_x<B>(raw, xq);
-#pragma unroll
-      for (int q = 0; q < kRowsPerLane; ++q) {
-        if (live[q]) t[q] += chunk_term<B>(chunk_dot<B>(w[q][i], xq), xsum, sb[q][i], bb[q][i]);
-      }
-    }
+  for (int i = 0; i < kSteps; ++i) {
+    uint32_t xq[16];
+    const float xsum = pair_x<B>(raw[i], xq);
+    const float term = t[0] + chunk_term<B>(chunk_dot<B>(w[i], xq), xsum, sb[i], bb[i]);
+    t[0] = part + kLanesPerRow * i < chunks ? term : t[0];
   }
 }
 
+// kSteps = ceil(inner / (32 * kLanesPerRow)) chunks per lane.
+template <int kSteps>
 __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(DownArgs a) {
   __shared__ float partial[kMaxDownSlots][kDownRows];
   const int lane = threadIdx.x % kWave;
@@ -382,12 +387,12 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(
   for (int q = 0; q < kRowsPerLane; ++q) t[q] = 0.0f;
   if (live[0]) {
     switch (leaf.bits) {  // wave-uniform
-      case 2: down_rows<2>(a, leaf, row0, live, slot, part, t); break;
-      case 3: down_rows<3>(a, leaf, row0, live, slot, part, t); break;
-      case 4: down_rows<4>(a, leaf, row0, live, slot, part, t); break;
-      case 5: down_rows<5>(a, leaf, row0, live, slot, part, t); break;
-      case 6: down_rows<6>(a, leaf, row0, live, slot, part, t); break;
-      default: down_rows<8>(a, leaf, row0, live, slot, part, t); break;
+      case 2: down_rows<2, kSteps>(a, leaf, row0, live, slot, part, t); break;
+      case 3: down_rows<3, kSteps>(a, leaf, row0, live, slot, part, t); break;
+      case 4: down_rows<4, kSteps>(a, leaf, row0, live, slot, part, t); break;
+      case 5: down_rows<5, kSteps>(a, leaf, row0, live, slot, part, t); break;
+      case 6: down_rows<6, kSteps>(a, leaf, row0, live, slot, part, t); break;
+      default: down_rows<8, kSteps>(a, leaf, row0, live, slot, part, t); break;
     }
   }
 #pragma unroll
@@ -486,6 +491,12 @@ extern "C" int32_t omnia_moe_down_combine_affine(
              chosen, weights, residual, out, experts, static_cast<int>(hidden),
              static_cast<int>(inner), static_cast<int>(slots)};
   const dim3 grid(static_cast<unsigned>((hidden + kDownRows - 1) / kDownRows));
-  moe_down_affine_kernel<<<grid, static_cast<unsigned>(slots * kWave), 0, stream>>>(a);
+  const dim3 block(static_cast<unsigned>(slots * kWave));
+  static_assert(kMaxDownSteps == 3, "one instantiation per step count");
+  switch ((inner / kChunk + kLanesPerRow - 1) / kLanesPerRow) {
+    case 1: moe_down_affine_kernel<1><<<grid, block, 0, stream>>>(a); break;
+    case 2: moe_down_affine_kernel<2><<<grid, block, 0, stream>>>(a); break;
+    default: moe_down_affine_kernel<3><<<grid, block, 0, stream>>>(a); break;
+  }
   return launched("moe_down_combine_affine");
 }
