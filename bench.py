@@ -455,6 +455,65 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.moe_down_combine_mxfp4(a["act"], a["dn"], a["ids"], a["w"], a["r"], out=a["o"]),
     ))
 
+    # Qwen3-30B-A3B's routed MLP over NVFP4 stacks (e2m1 codes, an e4m3 scale per 16
+    # values, the interleaved layout, the plain SwiGLU): random words and scales near
+    # 2^-4. A layer's stacks (226 MB + 113 MB) fit the Infinity Cache, so the copies cycle
+    # over four layers' stacks, as for the affine stacks.
+    nv_layers = 4
+    nvfp4_stacks: list = []
+
+    def nvfp4_weights(device):
+        if not nvfp4_stacks:
+            gen = torch.Generator(device=device).manual_seed(14)
+            for _ in range(nv_layers):
+                layer = {}
+                for name, rows, features in (("gate_up", 2 * moe_i, moe_h), ("down", moe_h, moe_i)):
+                    words = torch.randint(-2**31, 2**31, (moe_e, rows, features // 8), generator=gen,
+                                          device=device, dtype=torch.int32)
+                    scales = torch.randint(0x18, 0x28, (moe_e, rows, features // 16), generator=gen,
+                                           device=device, dtype=torch.int32).to(torch.uint8)
+                    layer[name] = ops.Nvfp4Leaf(words, scales, None)
+                nvfp4_stacks.append(layer)
+        return nvfp4_stacks
+
+    def setup_moe_nvfp4(device, copies):
+        rng = np.random.default_rng(15)
+        layers = nvfp4_weights(device)
+        sets = []
+        for i in range(copies):
+            stacks = layers[i % nv_layers]
+            chosen = torch.from_numpy(rng.choice(moe_e, size=moe_k, replace=False).astype(np.int32)).to(device)
+            sets.append(dict(gu=stacks["gate_up"], dn=stacks["down"], ids=chosen,
+                             x=_to_bf16_device(_normal(rng, (moe_h,)), device),
+                             act=_to_bf16_device(_normal(rng, (moe_k, moe_i)), device),
+                             w=torch.from_numpy(rng.dirichlet(np.ones(moe_k)).astype(np.float32)).to(device),
+                             r=_to_bf16_device(_normal(rng, (moe_h,)), device),
+                             y=torch.empty((moe_k, moe_i), dtype=torch.bfloat16, device=device),
+                             o=torch.empty((moe_h,), dtype=torch.bfloat16, device=device)))
+        return sets
+
+    def nvfp4_row_bytes(features):
+        return features // 2 + features // 16          # codes and e4m3 scales
+
+    out.append(Workload(
+        name="moe_nvfp4_gate_up_decode",
+        kernel="moe_gate_up_nvfp4_kernel",
+        description="x [2048] bf16 x 8 of 128 experts' NVFP4 interleaved gate||up stacks [1536, 2048] "
+                    "-> silu(gate)*up [8, 768] bf16 (Qwen3-30B-A3B, T=1)",
+        bytes_per_launch=moe_k * 2 * moe_i * nvfp4_row_bytes(moe_h) + moe_h * 2 + moe_k * 4 + moe_k * moe_i * 2,
+        setup=setup_moe_nvfp4,
+        launch=lambda a: ops.moe_gate_up_nvfp4(a["x"], a["gu"], a["ids"], out=a["y"]),
+    ))
+    out.append(Workload(
+        name="moe_nvfp4_down_combine_decode",
+        kernel="moe_down_nvfp4_kernel",
+        description="activation [8, 768] x 8 of 128 experts' NVFP4 down stacks [2048, 768], routing "
+                    "weights, slot sum, residual (Qwen3-30B-A3B, T=1)",
+        bytes_per_launch=moe_k * moe_h * nvfp4_row_bytes(moe_i) + moe_k * moe_i * 2 + moe_k * 8 + 2 * moe_h * 2,
+        setup=setup_moe_nvfp4,
+        launch=lambda a: ops.moe_down_combine_nvfp4(a["act"], a["dn"], a["ids"], a["w"], a["r"], out=a["o"]),
+    ))
+
     # Next after the routed MLP: the dense SwiGLU MLP of a one-token step at Qwen3-4B's
     # shape (hidden 2560, inner 9728: config 4's inner dimension), bf16 weights, gate rows
     # first. Each argument set holds its own weights, as each layer of a model does.

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 7
+#define OMNIA_ABI_VERSION 8
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -278,7 +278,7 @@ int32_t omnia_moe_gate_up_mxfp4(const uint16_t* x, const uint32_t* weight, const
  * act [slots, inner] bf16; weight [experts, hidden, inner / 8] uint32; scales [experts,
  * hidden, inner / 32] uint8; bias [experts, hidden] bf16 or NULL; chosen [slots] int32;
  * weights [slots] fp32; residual, out [hidden] bf16.
- * inner a multiple of 32, at most 3072; 1 <= slots <= 16.
+ * inner a multiple of 32, at most 4096; 1 <= slots <= 16.
  * Replaces: core/kernels/down_combine/mxfp4.py:16-120 (`Mxfp4DownCombine`,
  * `mxfp4_down_combine`); Core chain core/kernels/down_combine/default.py:43-58. */
 int32_t omnia_moe_down_combine_mxfp4(const uint16_t* act, const uint32_t* weight, const uint8_t* scales,
@@ -286,6 +286,35 @@ int32_t omnia_moe_down_combine_mxfp4(const uint16_t* act, const uint32_t* weight
                                      int64_t inner, const int32_t* chosen, const float* weights,
                                      int64_t slots, const uint16_t* residual, uint16_t* out,
                                      hipStream_t stream);
+
+/* Routed expert gate/up of one token over an NVFP4 stack (MLX's QuantizedSwitchLinear,
+ * mode "nvfp4"), the interleaved layout, the plain SwiGLU chain fused:
+ *   r = sum over groups of 16 of s * sum_j x[j] v[j]      v e2m1, s the group's e4m3 byte
+ *   decoded as mlx does (0x7F and 0xFF are +-480)
+ *   g = bf16(r[2n]), u = bf16(r[2n + 1]); out[s, n] = bf16(bf16(g * bf16(1 / (1 + exp(-g)))) * u)
+ * x [hidden] bf16; weight [experts, 2 * inner, hidden / 8] uint32 (two e2m1 codes per byte,
+ * low nibble first); scales [experts, 2 * inner, hidden / 16] uint8, 2-byte aligned;
+ * chosen [slots] int32; out [slots, inner] bf16. An index outside [0, experts) gives
+ * zeros. hidden a multiple of 32 (the reference's 16), at most 16384.
+ * Replaces: core/kernels/gate_up/nvfp4.py:24-128 (`Nvfp4GateUp`, `nvfp4_gateup_act`); Core
+ * chain core/kernels/gate_up/default.py:60-81. */
+int32_t omnia_moe_gate_up_nvfp4(const uint16_t* x, const uint32_t* weight, const uint8_t* scales,
+                                int64_t experts, int64_t hidden, int64_t inner, const int32_t* chosen,
+                                int64_t slots, uint16_t* out, hipStream_t stream);
+
+/* Routed expert down/combine of one token over an NVFP4 stack:
+ *   t[s, n] = sum over groups of 16 of s * sum_i act[s, i] v[i]       fp32
+ *   acc[n] = sum over s in order of bf16(bf16(t[s, n]) * weights[s])  fp32
+ *   out[n] = bf16(bf16(acc[n]) + residual[n])   (no add when residual is null)
+ * act [slots, inner] bf16; weight [experts, hidden, inner / 8] uint32; scales [experts,
+ * hidden, inner / 16] uint8, 2-byte aligned; chosen [slots] int32; weights [slots] fp32;
+ * residual, out [hidden] bf16. inner a multiple of 32, at most 4096; 1 <= slots <= 16.
+ * Replaces: core/kernels/down_combine/nvfp4.py:16-117 (`Nvfp4DownCombine`,
+ * `nvfp4_down_combine`); Core chain core/kernels/down_combine/default.py:43-58. */
+int32_t omnia_moe_down_combine_nvfp4(const uint16_t* act, const uint32_t* weight, const uint8_t* scales,
+                                     int64_t experts, int64_t hidden, int64_t inner, const int32_t* chosen,
+                                     const float* weights, int64_t slots, const uint16_t* residual,
+                                     uint16_t* out, hipStream_t stream);
 
 /* Dense SwiGLU MLP of one token, first half: the fused gate||up projection with the
  * SwiGLU applied in bf16 steps,

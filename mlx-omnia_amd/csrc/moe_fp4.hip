@@ -1,0 +1,434 @@
+// Routed expert MLP of a one-token step over FP4 expert stacks (MLX's
+// `QuantizedSwitchLinear`, modes "mxfp4" and "nvfp4"): gate/up with its activation, then
+// down/combine, the interleaved layout of the reference's mxfp4 and nvfp4 kernels.
+//
+// Formats (core/layers.py:164-197): weight [E, rows, in / 8] uint32, two e2m1 codes per
+// byte, the low nibble first (value j is nibble j of the row), and
+// - mxfp4 (core/kernels/shared/mxfp4.py:8-32): scales [E, rows, in / 32] uint8, an e8m0
+//   exponent per 32 values, applied as the fp32 whose bit pattern is `byte << 23`; the
+//   projection's own bias [E, rows] bf16;
+// - nvfp4 (core/kernels/shared/nvfp4/qmoe.py:8-50): scales [E, rows, in / 16] uint8, a
+//   signed e4m3 per 16 values decoded as mlx decodes it (0x7F and 0xFF are +-480, not
+//   NaN); no bias.
+//
+// Arithmetic:
+//   gate_up: r = sum over groups of s * sum_j x_j v_j (fp32, any order); rows 2n and
+//     2n + 1 are output n's gate and up.
+//     mxfp4 (core/kernels/gate_up/mxfp4.py:24-65): g = T(r_gate + b_gate),
+//       u = T(r_up + b_up); g = T(min(g, limit)), u = T(clamp(u, -limit, limit));
+//       sig = T(1 / (1 + exp(-1.702 g))); y = T(T(g * sig) * T(u + 1)).
+//     nvfp4 (core/kernels/gate_up/nvfp4.py:24-68): g = T(r_gate), u = T(r_up);
+//       sig = T(1 / (1 + exp(-g))); y = T(T(g * sig) * u).
+//     Each operation in fp32.
+//   down_combine (core/kernels/down_combine/mxfp4.py:16-58, nvfp4.py:16-61): t the same
+//     dot product over the activation row of the slot; acc = sum over slots in order of
+//     T(fp32(T(t + b) * w)) in fp32 (b = 0 for nvfp4); y = T(fp32(T(acc) + residual)).
+// An expert id outside [0, experts) gives zero rows.
+//
+// Decoding is gfx950's own: v_cvt_scalef32_pk_bf16_fp4 turns the two e2m1 codes of a
+// byte into a bf16 pair (low nibble first; checked on the box for every byte value), so
+// one conversion and one v_dot2_f32_bf16 take two weights against the activations in
+// memory order. A lane takes 32 values at a time: 16 bytes of codes and one e8m0 byte, or
+// two e4m3 bytes read as one 16-bit load; each group's dot product is scaled once in fp32.
+//
+// Both kernels issue every load of a lane (codes, the scale bits into a register of their
+// own, the activations) before any arithmetic and with no branch among the loads: a load
+// inside a divergent branch, or a scale byte packed beside another, makes the compiler
+// wait on it, one memory round trip per chunk.
+//
+// gate_up: a wave owns kPairsPerWave gate/up pairs of one slot and streams them together,
+// 64 lanes across each row; lane p runs pair p's activation. down_combine: a workgroup
+// owns kDownRows output rows with one wave per slot, 64 lanes across each row and the
+// slot's activations held once for all of them; the slots' terms meet in LDS and are
+// summed in slot order.
+#include "common.hpp"
+#include "host.hpp"
+
+namespace omnia {
+namespace {
+
+constexpr int kChunk = 32;                // values per lane per step: 16 bytes of codes
+constexpr int kPairsPerWave = 2;          // gate_up: gate/up pairs per wave
+constexpr int kGateWaves = 4;             // gate_up: waves per workgroup
+constexpr int kGateBatch = 2;             // gate_up: 64-chunk trips whose loads go out together
+constexpr int kDownRows = 4;              // down: output rows per workgroup, each wave's share
+constexpr int kMaxInner = 4096;           // down: at most two 64-chunk steps per lane
+constexpr int kMaxDownSteps = kMaxInner / (kChunk * kWave);
+constexpr int kMaxDownSlots = 16;
+
+enum class Fp4 { kMx, kNv };
+
+// The e8m0 group scale as the reference applies it: the fp32 with exponent field `byte`.
+__device__ __forceinline__ float e8m0(uint32_t byte) { return __uint_as_float(byte << 23); }
+
+// The e4m3 group scale as mlx decodes it: sign, 4 exponent bits (bias 7), 3 mantissa bits;
+// exponent 0 is subnormal (m / 8 * 2^-6) and the all-ones codes are +-480. A normal code's
+// 7 magnitude bits shifted to the top of an fp32's exponent and mantissa, with the
+// exponent rebased by 127 - 7, give 2^(e - 7) (1 + m / 8) exactly.
+__device__ __forceinline__ float e4m3(uint32_t byte) {
+  const uint32_t mag = byte & 0x7Fu;
+  const float normal = __uint_as_float((mag << 20) + (120u << 23));
+  const float subnormal = static_cast<float>(mag) * 0x1p-9f;
+  const float v = mag < 8u ? subnormal : normal;
+  return __uint_as_float(__float_as_uint(v) | ((byte & 0x80u) << 24));
+}
+
+// The e2m1 codes of byte B of a word as a bf16 pair, low nibble first.
+template <int B>
+__device__ __forceinline__ uint32_t fp4_pair(uint32_t word) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, 1.0f, B));
+}
+
+// sum_j x_j v_j over 8 values: one word of codes against 4 bf16 activation pairs.
+__device__ __forceinline__ float word_dot(uint32_t word, const u32x4& x, float acc) {
+  acc = dot2_bf16(fp4_pair<0>(word), x.x, acc);
+  acc = dot2_bf16(fp4_pair<1>(word), x.y, acc);
+  acc = dot2_bf16(fp4_pair<2>(word), x.z, acc);
+  return dot2_bf16(fp4_pair<3>(word), x.w, acc);
+}
+
+// acc plus one 32-value chunk's scaled dot product: one e8m0 group, or two e4m3 groups of
+// 16 (the low scale byte is the first group's).
+template <Fp4 F>
+__device__ __forceinline__ float chunk_value(uint32_t s, const u32x4& w, const u32x4 (&x)[4], float acc) {
+  if constexpr (F == Fp4::kMx) {
+    float d = word_dot(w.x, x[0], 0.0f);
+    d = word_dot(w.y, x[1], d);
+    d = word_dot(w.z, x[2], d);
+    d = word_dot(w.w, x[3], d);
+    return __builtin_fmaf(e8m0(s), d, acc);
+  } else {
+    const float lo = word_dot(w.y, x[1], word_dot(w.x, x[0], 0.0f));
+    const float hi = word_dot(w.w, x[3], word_dot(w.z, x[2], 0.0f));
+    return __builtin_fmaf(e4m3(s >> 8), hi, __builtin_fmaf(e4m3(s & 0xFFu), lo, acc));
+  }
+}
+
+// The scale bits of one chunk: [rows, in / 32] bytes (mxfp4) or [rows, in / 32] 16-bit
+// pairs of bytes (nvfp4), at the chunk's index.
+template <Fp4 F>
+__device__ __forceinline__ uint32_t load_scales(const void* scales, int64_t at) {
+  if constexpr (F == Fp4::kMx) return static_cast<const uint8_t*>(scales)[at];
+  else return static_cast<const uint16_t*>(scales)[at];
+}
+
+struct Stack {
+  const u32x4* weight;     // [experts, rows, in / 32] chunks of 16 bytes
+  const void* scales;      // per chunk: one e8m0 byte or two e4m3 bytes
+  const uint16_t* bias;    // [experts, rows] bf16, or null
+};
+
+// ---- gate_up ------------------------------------------------------------------------
+
+struct GateUpArgs {
+  const uint16_t* x;       // [hidden]
+  Stack stack;             // [experts, 2 * inner, ...]
+  const int32_t* chosen;   // [slots]
+  uint16_t* out;           // [slots, inner]
+  int64_t experts;
+  int hidden;
+  int inner;
+  float limit;             // mxfp4: +inf for no clamp
+};
+
+// kTrips > 0: hidden / 32 chunks span exactly kTrips 64-lane trips; 0: any number of trips.
+template <Fp4 F, int kTrips>
+__device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
+  const int lane = threadIdx.x % kWave;
+  const int slot = blockIdx.y;
+  const int pair0 = (blockIdx.x * kGateWaves + threadIdx.x / kWave) * kPairsPerWave;
+  if (pair0 >= a.inner) return;  // whole wave; no barrier follows
+  const int pairs = min(kPairsPerWave, a.inner - pair0);
+  uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + pair0;
+  const int expert = a.chosen[slot];
+  if (expert < 0 || expert >= a.experts) {
+    if (lane < pairs) out[lane] = 0;
+    return;
+  }
+  constexpr int kRows = 2 * kPairsPerWave;
+  const int rows = 2 * pairs;
+  const int64_t row0 = static_cast<int64_t>(expert) * 2 * a.inner + 2 * static_cast<int64_t>(pair0);
+  const int chunks = a.hidden / kChunk;
+  constexpr int kBatch = kTrips > 0 ? kTrips : kGateBatch;
+  const int trips = kTrips > 0 ? kTrips : (chunks + kWave - 1) / kWave;
+  float r[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) r[i] = 0.0f;
+  // kBatch trips' loads are issued before their arithmetic, with no branch among them: a
+  // lane past the row's end re-reads the last chunk and drops the term, and a row past
+  // the wave's last pair re-reads the pair's last row (that sum is never stored).
+  for (int t0 = 0; t0 < trips; t0 += kBatch) {
+    u32x4 w[kBatch][kRows];
+    uint32_t s[kBatch][kRows];
+    u32x4 x[kBatch][4];
+#pragma unroll
+    for (int h = 0; h < kBatch; ++h) {
+      const int c = min(lane + (t0 + h) * kWave, chunks - 1);
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) {
+        const int64_t at = (row0 + min(i, rows - 1)) * chunks + c;
+        w[h][i] = load_nt(a.stack.weight + at);
+        s[h][i] = load_scales<F>(a.stack.scales, at);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[h][j] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[j];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
+#pragma unroll
+    for (int h = 0; h < kBatch; ++h) {
+      const bool in_row = lane + (t0 + h) * kWave < chunks;
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) {
+        const float term = chunk_value<F>(s[h][i], w[h][i], x[h], r[i]);
+        r[i] = in_row ? term : r[i];
+      }
+    }
+  }
+  // Lane p takes pair p's sums and runs its activation.
+  float gate_sum = 0.0f, up_sum = 0.0f;
+#pragma unroll
+  for (int p = 0; p < kPairsPerWave; ++p) {
+    const float gp = wave_sum_f32(r[2 * p]);
+    const float up = wave_sum_f32(r[2 * p + 1]);
+    gate_sum = lane == p ? gp : gate_sum;
+    up_sum = lane == p ? up : up_sum;
+  }
+  if (lane >= pairs) return;
+  if constexpr (F == Fp4::kMx) {
+    float gate_bias = 0.0f, up_bias = 0.0f;
+    if (a.stack.bias != nullptr) {
+      gate_bias = bf16_to_f32(a.stack.bias[row0 + 2 * lane]);
+      up_bias = bf16_to_f32(a.stack.bias[row0 + 2 * lane + 1]);
+    }
+    float g = round_bf16(gate_sum + gate_bias);
+    float u = round_bf16(up_sum + up_bias);
+    if (a.limit < __builtin_inff()) {
+      g = round_bf16(fminf(g, a.limit));
+      u = round_bf16(fminf(fmaxf(u, -a.limit), a.limit));
+    }
+    const float sig = round_bf16(1.0f / (1.0f + expf(-1.702f * g)));
+    const float act = round_bf16(g * sig);
+    out[lane] = f32_to_bf16(act * round_bf16(u + 1.0f));
+  } else {
+    const float g = round_bf16(gate_sum);
+    const float u = round_bf16(up_sum);
+    const float sig = round_bf16(1.0f / (1.0f + expf(-g)));
+    const float act = round_bf16(g * sig);
+    out[lane] = f32_to_bf16(act * u);
+  }
+}
+
+template <int kTrips>
+__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_mxfp4_kernel(GateUpArgs a) {
+  gate_up_body<Fp4::kMx, kTrips>(a);
+}
+
+template <int kTrips>
+__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_nvfp4_kernel(GateUpArgs a) {
+  gate_up_body<Fp4::kNv, kTrips>(a);
+}
+
+// ---- down_combine -------------------------------------------------------------------
+
+struct DownArgs {
+  const uint16_t* act;      // [slots, inner]
+  Stack stack;              // [experts, hidden, ...]
+  const int32_t* chosen;    // [slots]
+  const float* weights;     // [slots]
+  const uint16_t* residual; // [hidden] or null
+  uint16_t* out;            // [hidden]
+  int64_t experts;
+  int hidden;
+  int inner;
+  int slots;
+};
+
+// kSteps = ceil(inner / (32 * 64)) chunks per lane: 1 or 2.
+template <Fp4 F, int kSteps>
+__device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kMaxDownSlots][kDownRows]) {
+  const int lane = threadIdx.x % kWave;
+  const int slot = threadIdx.x / kWave;   // one wave per slot
+  const int row_base = blockIdx.x * kDownRows;
+  const int rows = min(kDownRows, a.hidden - row_base);
+  const int expert = a.chosen[slot];
+  const bool valid = expert >= 0 && expert < a.experts;   // uniform over the wave
+  const int64_t row0 = static_cast<int64_t>(valid ? expert : 0) * a.hidden + row_base;
+  const int chunks = a.inner / kChunk;
+  float t[kDownRows];
+#pragma unroll
+  for (int i = 0; i < kDownRows; ++i) t[i] = 0.0f;
+  if (valid) {
+    // Every load (codes, scale bits, the slot's activations, shared by the wave's rows)
+    // is issued before any arithmetic, with no branch among them: a lane past the row's
+    // last chunk re-reads that chunk and drops the term, and a row past the last one
+    // re-reads the last (its sum is never used).
+    const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
+    u32x4 w[kSteps][kDownRows];
+    uint32_t s[kSteps][kDownRows];
+    u32x4 xv[kSteps][4];
+#pragma unroll
+    for (int h = 0; h < kSteps; ++h) {
+      const int c = min(lane + kWave * h, chunks - 1);
+#pragma unroll
+      for (int i = 0; i < kDownRows; ++i) {
+        const int64_t at = (row0 + min(i, rows - 1)) * chunks + c;
+        w[h][i] = load_nt(a.stack.weight + at);
+        s[h][i] = load_scales<F>(a.stack.scales, at);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xv[h][j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
+#pragma unroll
+    for (int h = 0; h < kSteps; ++h) {
+      const bool in_row = lane + kWave * h < chunks;
+#pragma unroll
+      for (int i = 0; i < kDownRows; ++i) {
+        const float term = chunk_value<F>(s[h][i], w[h][i], xv[h], t[i]);
+        t[i] = in_row ? term : t[i];
+      }
+    }
+  }
+  // Lane i takes row i's sum.
+  float mine = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kDownRows; ++i) {
+    const float total = wave_sum_f32(t[i]);
+    mine = lane == i ? total : mine;
+  }
+  if (lane < rows) {
+    float term = 0.0f;
+    if (valid) {
+      const float bias = a.stack.bias != nullptr ? bf16_to_f32(a.stack.bias[row0 + lane]) : 0.0f;
+      term = round_bf16(round_bf16(mine + bias) * a.weights[slot]);
+    }
+    partial[slot][lane] = term;
+  }
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) < rows) {
+    const int n = row_base + threadIdx.x;
+    float sum = 0.0f;
+    for (int j = 0; j < a.slots; ++j) sum += partial[j][threadIdx.x];
+    float out = round_bf16(sum);
+    if (a.residual != nullptr) out = out + bf16_to_f32(a.residual[n]);
+    a.out[n] = f32_to_bf16(out);
+  }
+}
+
+template <int kSteps>
+__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_mxfp4_kernel(DownArgs a) {
+  __shared__ float partial[kMaxDownSlots][kDownRows];
+  down_body<Fp4::kMx, kSteps>(a, partial);
+}
+
+template <int kSteps>
+__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_nvfp4_kernel(DownArgs a) {
+  __shared__ float partial[kMaxDownSlots][kDownRows];
+  down_body<Fp4::kNv, kSteps>(a, partial);
+}
+
+// Host side: shape checks and launches shared by both formats.
+
+int32_t launch_gate_up(Fp4 format, const char* name, const uint16_t* x, const uint32_t* weight,
+                       const void* scales, const uint16_t* bias, int64_t experts, int64_t hidden,
+                       int64_t inner, const int32_t* chosen, int64_t slots, float limit, uint16_t* out,
+                       hipStream_t stream) {
+  OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), std::string(name) + ": bad expert count");
+  OMNIA_REQUIRE(hidden > 0 && hidden % kChunk == 0 && hidden <= 16384,
+                std::string(name) + ": hidden must be a multiple of 32 in [32, 16384]");
+  OMNIA_REQUIRE(inner > 0 && inner < (int64_t{1} << 24), std::string(name) + ": bad inner size");
+  OMNIA_REQUIRE(slots >= 0 && slots <= 1024, std::string(name) + ": slots must be in [0, 1024]");
+  OMNIA_REQUIRE(!(limit < 0.0f), std::string(name) + ": the limit must be non-negative (+inf: none)");
+  if (slots == 0) return 0;
+  OMNIA_REQUIRE(x && weight && scales && chosen && out, std::string(name) + ": null pointer");
+  OMNIA_REQUIRE(aligned16(x) && aligned16(weight), std::string(name) + ": x and weight must be 16-byte aligned");
+  OMNIA_REQUIRE(format == Fp4::kMx || reinterpret_cast<uintptr_t>(scales) % 2 == 0,
+                std::string(name) + ": the scales must be 2-byte aligned");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  GateUpArgs a{x, Stack{reinterpret_cast<const u32x4*>(weight), scales, bias}, chosen, out, experts,
+               static_cast<int>(hidden), static_cast<int>(inner), limit};
+  const int64_t waves = (inner + kPairsPerWave - 1) / kPairsPerWave;
+  const dim3 grid(static_cast<unsigned>((waves + kGateWaves - 1) / kGateWaves), static_cast<unsigned>(slots));
+  const dim3 block(kGateWaves * kWave);
+  const int64_t trips = (hidden / kChunk + kWave - 1) / kWave;
+  if (format == Fp4::kMx) {
+    if (trips == 1) moe_gate_up_mxfp4_kernel<1><<<grid, block, 0, stream>>>(a);
+    else if (trips == 2) moe_gate_up_mxfp4_kernel<2><<<grid, block, 0, stream>>>(a);
+    else moe_gate_up_mxfp4_kernel<0><<<grid, block, 0, stream>>>(a);
+  } else {
+    if (trips == 1) moe_gate_up_nvfp4_kernel<1><<<grid, block, 0, stream>>>(a);
+    else if (trips == 2) moe_gate_up_nvfp4_kernel<2><<<grid, block, 0, stream>>>(a);
+    else moe_gate_up_nvfp4_kernel<0><<<grid, block, 0, stream>>>(a);
+  }
+  return launched(name);
+}
+
+int32_t launch_down(Fp4 format, const char* name, const uint16_t* act, const uint32_t* weight,
+                    const void* scales, const uint16_t* bias, int64_t experts, int64_t hidden,
+                    int64_t inner, const int32_t* chosen, const float* weights, int64_t slots,
+                    const uint16_t* residual, uint16_t* out, hipStream_t stream) {
+  OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), std::string(name) + ": bad expert count");
+  OMNIA_REQUIRE(hidden > 0 && hidden < (int64_t{1} << 24), std::string(name) + ": bad hidden size");
+  OMNIA_REQUIRE(inner > 0 && inner % kChunk == 0 && inner <= kMaxInner,
+                std::string(name) + ": inner must be a multiple of 32 in [32, 4096]");
+  OMNIA_REQUIRE(slots > 0 && slots <= kMaxDownSlots, std::string(name) + ": slots must be in [1, 16]");
+  OMNIA_REQUIRE(act && weight && scales && chosen && weights && out, std::string(name) + ": null pointer");
+  OMNIA_REQUIRE(aligned16(act) && aligned16(weight), std::string(name) + ": act and weight must be 16-byte aligned");
+  OMNIA_REQUIRE(format == Fp4::kMx || reinterpret_cast<uintptr_t>(scales) % 2 == 0,
+                std::string(name) + ": the scales must be 2-byte aligned");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  DownArgs a{act, Stack{reinterpret_cast<const u32x4*>(weight), scales, bias}, chosen, weights, residual, out,
+             experts, static_cast<int>(hidden), static_cast<int>(inner), static_cast<int>(slots)};
+  const dim3 grid(static_cast<unsigned>((hidden + kDownRows - 1) / kDownRows));
+  const dim3 block(static_cast<unsigned>(slots * kWave));
+  static_assert(kMaxDownSteps == 2, "one instantiation per step count");
+  const bool one = inner <= kChunk * kWave;
+  if (format == Fp4::kMx) {
+    if (one) moe_down_mxfp4_kernel<1><<<grid, block, 0, stream>>>(a);
+    else moe_down_mxfp4_kernel<2><<<grid, block, 0, stream>>>(a);
+  } else {
+    if (one) moe_down_nvfp4_kernel<1><<<grid, block, 0, stream>>>(a);
+    else moe_down_nvfp4_kernel<2><<<grid, block, 0, stream>>>(a);
+  }
+  return launched(name);
+}
+
+}  // namespace
+}  // namespace omnia
+
+extern "C" int32_t omnia_moe_gate_up_mxfp4(const uint16_t* x, const uint32_t* weight, const uint8_t* scales,
+                                           const uint16_t* bias, int64_t experts, int64_t hidden,
+                                           int64_t inner, const int32_t* chosen, int64_t slots,
+                                           float limit, uint16_t* out, hipStream_t stream) {
+  return omnia::launch_gate_up(omnia::Fp4::kMx, "moe_gate_up_mxfp4", x, weight, scales, bias, experts, hidden,
+                               inner, chosen, slots, limit, out, stream);
+}
+
+extern "C" int32_t omnia_moe_down_combine_mxfp4(const uint16_t* act, const uint32_t* weight,
+                                                const uint8_t* scales, const uint16_t* bias,
+                                                int64_t experts, int64_t hidden, int64_t inner,
+                                                const int32_t* chosen, const float* weights,
+                                                int64_t slots, const uint16_t* residual, uint16_t* out,
+                                                hipStream_t stream) {
+  return omnia::launch_down(omnia::Fp4::kMx, "moe_down_combine_mxfp4", act, weight, scales, bias, experts,
+                            hidden, inner, chosen, weights, slots, residual, out, stream);
+}
+
+extern "C" int32_t omnia_moe_gate_up_nvfp4(const uint16_t* x, const uint32_t* weight, const uint8_t* scales,
+                                           int64_t experts, int64_t hidden, int64_t inner,
+                                           const int32_t* chosen, int64_t slots, uint16_t* out,
+                                           hipStream_t stream) {
+  return omnia::launch_gate_up(omnia::Fp4::kNv, "moe_gate_up_nvfp4", x, weight, scales, nullptr, experts, hidden,
+                               inner, chosen, slots, __builtin_inff(), out, stream);
+}
+
+extern "C" int32_t omnia_moe_down_combine_nvfp4(const uint16_t* act, const uint32_t* weight,
+                                                const uint8_t* scales, int64_t experts, int64_t hidden,
+                                                int64_t inner, const int32_t* chosen, const float* weights,
+                                                int64_t slots, const uint16_t* residual, uint16_t* out,
+                                                hipStream_t stream) {
+  return omnia::launch_down(omnia::Fp4::kNv, "moe_down_combine_nvfp4", act, weight, scales, nullptr, experts,
+                            hidden, inner, chosen, weights, slots, residual, out, stream);
+}

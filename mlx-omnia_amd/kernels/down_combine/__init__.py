@@ -5,7 +5,12 @@ down-projected by its expert, routing-weighted, summed and residual-added.
 Mirrors core/kernels/down_combine/__init__.py and kernel.py (`DownCombine`,
 `DownCombineStrategy`, `Layout`).
 
-- `HipMxfp4DownCombine` (`omnia_moe_down_combine_mxfp4`, csrc/moe_mxfp4.hip) serves what
+- `HipNvfp4DownCombine` (`omnia_moe_down_combine_nvfp4`, csrc/moe_fp4.hip) serves what
+  the reference's `Nvfp4DownCombine` serves (core/kernels/down_combine/nvfp4.py:76-98): an
+  NVFP4 stack under the `interleaved` layout, no bias or shared expert, hidden and inner
+  multiples of 32 (inner up to 4096), at most 16 slots (more go to the Core chain). Per
+  slot bf16(bf16(dot) * weight), the slot sum in fp32 in slot order, then the residual.
+- `HipMxfp4DownCombine` (`omnia_moe_down_combine_mxfp4`, csrc/moe_fp4.hip) serves what
   the reference's `Mxfp4DownCombine` serves (core/kernels/down_combine/mxfp4.py:80-101):
   an MXFP4 stack under the `interleaved` layout with the per-row projection bias, no
   shared expert, hidden and inner multiples of 32 (inner up to 4096), at most 16 slots
@@ -40,7 +45,7 @@ import torch
 
 from ...runtime import ops
 from .._device import hip_device
-from ..gate_up.routed import affine_leaf, mxfp4_applies, mxfp4_leaf
+from ..gate_up.routed import affine_leaf, mxfp4_applies, mxfp4_leaf, nvfp4_leaf
 from ..leaf import QuantizedLinearLeaf, QuantizedSwitchLinearLeaf
 from ..resolve import resolve
 
@@ -48,7 +53,7 @@ Layout = Literal["interleaved", "blocked"]
 MAX_SLOTS = 16
 
 __all__ = ["DefaultDownCombine", "DownCombine", "DownCombineStrategy", "HipAffineDownCombine",
-           "HipDenseDownCombine", "HipMxfp4DownCombine", "Layout", "affine_down_applies",
+           "HipDenseDownCombine", "HipMxfp4DownCombine", "HipNvfp4DownCombine", "Layout", "affine_down_applies",
            "dense_down_applies"]
 
 
@@ -199,7 +204,37 @@ class HipMxfp4DownCombine(DownCombineStrategy):
         )
 
 
-_STRATEGIES = (HipMxfp4DownCombine, HipAffineDownCombine, HipDenseDownCombine, DefaultDownCombine)
+@dataclass(frozen=True)
+class HipNvfp4DownCombine(DownCombineStrategy):
+    leaf: "ops.Nvfp4Leaf"
+    fallback: DefaultDownCombine
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, bias, shared, layout) -> "HipNvfp4DownCombine | None":
+        if layout != "interleaved" or bias is not None or shared is not None:
+            return None
+        if not mxfp4_applies(hidden, inner) or inner > 4096:  # two 64-chunk steps per lane
+            return None
+        view = nvfp4_leaf(leaf, hidden, inner)
+        if view is None:
+            return None
+        return cls(view, DefaultDownCombine(leaf, bias, shared, layout))
+
+    def __call__(self, act, chosen, weights, residual):
+        slots = chosen.numel()
+        if slots == 0 or slots > MAX_SLOTS:  # one wave per slot in a workgroup
+            return self.fallback(act, chosen, weights, residual)
+        device = self.leaf.weight.device
+        return ops.moe_down_combine_nvfp4(
+            act.reshape(slots, -1).to(torch.bfloat16).contiguous(), self.leaf,
+            chosen.to(device=device, dtype=torch.int32).contiguous().reshape(-1),
+            weights.to(device=device, dtype=torch.float32).contiguous().reshape(-1),
+            None if residual is None else residual.reshape(-1).to(torch.bfloat16).contiguous(),
+        )
+
+
+_STRATEGIES = (HipNvfp4DownCombine, HipMxfp4DownCombine, HipAffineDownCombine, HipDenseDownCombine,
+               DefaultDownCombine)
 
 
 class DownCombine(DownCombineStrategy):

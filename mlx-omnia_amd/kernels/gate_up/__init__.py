@@ -1,7 +1,7 @@
 """Gate/up: the activation facade (`GateUpActivation`: `HipSwiGLU` ahead of the Core
 chain `DefaultGateUpActivation`) and the routed projection of a one-token step
-(`GateUp` in routed.py: `HipMxfp4GateUp`, `HipAffineGateUp` and `HipDenseGateUp`
-ahead of `DefaultGateUp`), each resolved by its declaration with the reference's
+(`GateUp` in routed.py: `HipNvfp4GateUp`, `HipMxfp4GateUp`, `HipAffineGateUp` and
+`HipDenseGateUp` ahead of `DefaultGateUp`), each resolved by its declaration with the reference's
 first-build-wins rule."""
 
 from __future__ import annotations
@@ -13,7 +13,7 @@ from .default import DefaultGateUpActivation, swiglu_core
 from .hip import HipSwiGLU, applies
 from .kernel import Activation, GateUpActivationStrategy, Layout, split
 from .routed import (DefaultGateUp, GateUp, GateUpStrategy, HipAffineGateUp, HipDenseGateUp,
-                     HipMxfp4GateUp, OrdinalRouting, affine_gate_up_applies,
+                     HipMxfp4GateUp, HipNvfp4GateUp, OrdinalRouting, affine_gate_up_applies,
                      dense_gate_up_applies, mxfp4_applies)
 
 __all__ = [
@@ -24,6 +24,7 @@ __all__ = [
     "HipAffineGateUp",
     "HipDenseGateUp",
     "HipMxfp4GateUp",
+    "HipNvfp4GateUp",
     "OrdinalRouting",
     "affine_gate_up_applies",
     "dense_gate_up_applies",

@@ -6,11 +6,16 @@ Mirrors core/kernels/gate_up/__init__.py and kernel.py (`GateUp`, `GateUpStrateg
 (activation, clamp, projection bias, layout, ordinal routing, a shared expert), and the
 first strategy whose `build` accepts the declaration serves it.
 
-- `HipMxfp4GateUp` (`omnia_moe_gate_up_mxfp4`, csrc/moe_mxfp4.hip) serves what the
+- `HipMxfp4GateUp` (`omnia_moe_gate_up_mxfp4`, csrc/moe_fp4.hip) serves what the
   reference's `Mxfp4GateUp` serves (core/kernels/gate_up/mxfp4.py:82-111): an MXFP4 stack
   (`QuantizedSwitchLinearLeaf` mode "mxfp4") under the `interleaved` layout, swiglu_oai
   with its clamp and the per-row projection bias, no ordinal routing or shared expert,
   hidden and inner multiples of 32 (hidden up to 16384).
+- `HipNvfp4GateUp` (`omnia_moe_gate_up_nvfp4`, csrc/moe_fp4.hip) serves what the
+  reference's `Nvfp4GateUp` serves (core/kernels/gate_up/nvfp4.py:79-110): an NVFP4 stack
+  (mode "nvfp4", e4m3 scales per 16) under the `interleaved` layout, silu without clamp,
+  bias, ordinal routing or shared expert; hidden and inner multiples of 32 (the
+  reference's 16: the others go to the Core chain), hidden up to 16384.
 - `HipAffineGateUp` (`omnia_moe_gate_up_affine`, csrc/moe_affine.hip) serves what the
   reference's `AffineGateUp` serves (core/kernels/gate_up/affine.py:105-191): an
   affine-quantized stack (`QuantizedSwitchLinearLeaf`, 2, 3, 4, 5, 6 or 8 bits, groups of
@@ -106,6 +111,22 @@ def mxfp4_leaf(leaf, bias, rows: int, features: int) -> "ops.Mxfp4Leaf | None":
     view = ops.Mxfp4Leaf(leaf.weight, leaf.scales, bias.contiguous())
     try:
         view.check(rows, features, "mxfp4 leaf")
+    except ValueError:
+        return None
+    if not all(hip_device(t) for t in view.tensors()):
+        return None
+    return view
+
+
+def nvfp4_leaf(leaf, rows: int, features: int) -> "ops.Nvfp4Leaf | None":
+    """The kernels' view of an NVFP4 stack [experts, rows, ...], or None."""
+    if not isinstance(leaf, QuantizedSwitchLinearLeaf) or leaf.mode != "nvfp4":
+        return None
+    if leaf.biases is not None or leaf.bits != 4 or leaf.group_size != 16:
+        return None
+    view = ops.Nvfp4Leaf(leaf.weight, leaf.scales, None)
+    try:
+        view.check(rows, features, "nvfp4 leaf")
     except ValueError:
         return None
     if not all(hip_device(t) for t in view.tensors()):
@@ -238,7 +259,29 @@ class HipMxfp4GateUp(GateUpStrategy):
         return ops.moe_gate_up_mxfp4(row.reshape(-1).contiguous(), self.leaf, ids, limit=self.limit)
 
 
-_STRATEGIES = (HipMxfp4GateUp, HipAffineGateUp, HipDenseGateUp, DefaultGateUp)
+@dataclass(frozen=True)
+class HipNvfp4GateUp(GateUpStrategy):
+    leaf: "ops.Nvfp4Leaf"
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, activation, limit, bias, layout, routing,
+              shared) -> "HipNvfp4GateUp | None":
+        if shared is not None or layout != "interleaved" or routing is not None:
+            return None
+        # The kernel carries neither clamp nor projection bias, as the reference's.
+        if activation != "silu" or limit is not None or bias is not None:
+            return None
+        if not mxfp4_applies(hidden, inner) or hidden > 16384:
+            return None
+        view = nvfp4_leaf(leaf, 2 * inner, hidden)
+        return None if view is None else cls(view)
+
+    def __call__(self, row: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor:
+        ids = chosen.to(device=self.leaf.weight.device, dtype=torch.int32).contiguous().reshape(-1)
+        return ops.moe_gate_up_nvfp4(row.reshape(-1).contiguous(), self.leaf, ids)
+
+
+_STRATEGIES = (HipNvfp4GateUp, HipMxfp4GateUp, HipAffineGateUp, HipDenseGateUp, DefaultGateUp)
 
 
 class GateUp(GateUpStrategy):

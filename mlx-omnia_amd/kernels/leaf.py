@@ -67,6 +67,22 @@ def mxfp4_dequantize(words: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     return values * factors.repeat_interleave(32, dim=-1)
 
 
+def e4m3_values(scales: torch.Tensor) -> torch.Tensor:
+    """e4m3 bytes -> float32 as mlx decodes them: the magnitude bits placed in a half's
+    exponent and top mantissa bits and scaled by 2^8, the sign from bit 7, so 0x7F is 480
+    (core/kernels/shared/nvfp4/qmoe.py:22-37)."""
+    b = scales.to(torch.int32)
+    half = ((b & 0x7F) << 7).to(torch.int16).view(torch.float16).float() * 256.0
+    return torch.where((b & 0x80) != 0, -half, half)
+
+
+def nvfp4_dequantize(words: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """e2m1 codes times their 16-value group's e4m3 factor: float32 [..., out, in]."""
+    table = torch.tensor(E2M1, dtype=torch.float32, device=words.device)
+    values = table[unpack_words(words, 4)]
+    return values * e4m3_values(scales.contiguous()).repeat_interleave(16, dim=-1)
+
+
 def dequantize(leaf, index: torch.Tensor | None = None) -> torch.Tensor:
     """A quantized leaf's matrices (the indexed experts' for a stack) as float32."""
     pick = (lambda t: t) if index is None else (lambda t: t[index.long()])
@@ -75,6 +91,8 @@ def dequantize(leaf, index: torch.Tensor | None = None) -> torch.Tensor:
                                  leaf.group_size, leaf.bits)
     if leaf.mode == "mxfp4" and leaf.biases is None and leaf.bits == 4 and leaf.group_size == 32:
         return mxfp4_dequantize(pick(leaf.weight), pick(leaf.scales))
+    if leaf.mode == "nvfp4" and leaf.biases is None and leaf.bits == 4 and leaf.group_size == 16:
+        return nvfp4_dequantize(pick(leaf.weight), pick(leaf.scales))
     raise NotImplementedError(f"no decoder for quantization mode {leaf.mode!r}")
 
 
@@ -84,7 +102,8 @@ class QuantizedSwitchLinearLeaf:
     (core/layers.py:164-197): weight [experts, out, in * bits / 32] 32-bit words (int32 or
     uint32) and scales [experts, out, in / group_size]. Mode "affine": bf16 scales and
     biases, 2-8 bits. Mode "mxfp4": 4 bits, groups of 32, uint8 e8m0 scales, no biases.
-    Other modes are declared but decoded by nothing here."""
+    Mode "nvfp4": 4 bits, groups of 16, uint8 e4m3 scales, no biases. Other modes are
+    declared but decoded by nothing here."""
 
     weight: torch.Tensor
     scales: torch.Tensor

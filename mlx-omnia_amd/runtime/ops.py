@@ -682,6 +682,8 @@ class Mxfp4Leaf:
     def features(self) -> int:
         return self.weight.shape[-1] * 8
 
+    group = 32   # values per scale byte
+
     def check(self, rows: int, features: int, name: str) -> None:
         _require(features % 32 == 0, f"{name}: the contraction must be a multiple of 32")
         _require(self.weight.dim() == 3 and self.scales.dim() == 3, f"{name}: expected [experts, rows, ...]")
@@ -691,7 +693,9 @@ class Mxfp4Leaf:
         experts = self.weight.shape[0]
         _require(tuple(self.weight.shape) == (experts, rows, features // 8), f"{name}: weight shape")
         _require(self.scales.dtype == torch.uint8 and self.scales.is_contiguous()
-                 and tuple(self.scales.shape) == (experts, rows, features // 32), f"{name}: scales")
+                 and tuple(self.scales.shape) == (experts, rows, features // self.group), f"{name}: scales")
+        _require(self.group == 32 or self.scales.data_ptr() % 2 == 0,
+                 f"{name}: the scales must be 2-byte aligned")   # read two groups at a time
         if self.bias is not None:
             _require(self.bias.dtype == BF16 and self.bias.is_contiguous()
                      and tuple(self.bias.shape) == (experts, rows), f"{name}: bias must be bf16 [experts, rows]")
@@ -764,5 +768,79 @@ def moe_down_combine_mxfp4(
     call("omnia_moe_down_combine_mxfp4", act.data_ptr(), leaf.weight.data_ptr(), leaf.scales.data_ptr(),
          leaf.bias.data_ptr() if leaf.bias is not None else None, experts, hidden, inner,
          chosen.data_ptr(), weights.data_ptr(), slots,
+         residual.data_ptr() if residual is not None else None, out.data_ptr(), _stream(act))
+    return out
+
+
+@dataclass(frozen=True)
+class Nvfp4Leaf(Mxfp4Leaf):
+    """An NVFP4 matrix set as the kernels read it: weight [..., rows, features / 8] (two e2m1
+    codes per byte, the low nibble first), scales [..., rows, features / 16] uint8 (e4m3),
+    no bias."""
+
+    group = 16
+
+
+def moe_gate_up_nvfp4(
+    x: torch.Tensor,
+    leaf: Nvfp4Leaf,
+    chosen: torch.Tensor,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One token's routed gate/up over an NVFP4 stack, the interleaved layout, the plain
+    SwiGLU chain fused; see `omnia_moe_gate_up_nvfp4`. x [hidden] bf16, leaf [experts,
+    2 * inner, ...], chosen [slots] int32 -> [slots, inner] bf16."""
+    _require(x.dim() == 1 or x.numel() == x.shape[-1], "moe_gate_up_nvfp4: x must be one row")
+    hidden = x.shape[-1]
+    _dense(x, BF16, "x")
+    _require(leaf.bias is None, "moe_gate_up_nvfp4: NVFP4 stacks carry no bias")
+    _require(leaf.weight.dim() == 3 and leaf.weight.shape[1] % 2 == 0,
+             "moe_gate_up_nvfp4: weight must be [experts, 2 * inner, words]")
+    experts, rows = leaf.weight.shape[0], leaf.weight.shape[1]
+    leaf.check(rows, hidden, "moe_gate_up_nvfp4")
+    _require(chosen.dtype == torch.int32 and chosen.is_contiguous() and chosen.dim() == 1,
+             "moe_gate_up_nvfp4: chosen must be contiguous int32 [slots]")
+    _require(on_rocm(x, chosen, *leaf.tensors()), "moe_gate_up_nvfp4: tensors must share one ROCm device")
+    slots = chosen.numel()
+    out = _out(out, x, (slots, rows // 2), BF16, "out")
+    call("omnia_moe_gate_up_nvfp4", x.data_ptr(), leaf.weight.data_ptr(), leaf.scales.data_ptr(), experts,
+         hidden, rows // 2, chosen.data_ptr(), slots, out.data_ptr(), _stream(x))
+    return out
+
+
+def moe_down_combine_nvfp4(
+    act: torch.Tensor,
+    leaf: Nvfp4Leaf,
+    chosen: torch.Tensor,
+    weights: torch.Tensor,
+    residual: torch.Tensor | None = None,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One token's routed down projection over an NVFP4 stack with the routing weights, the
+    slot sum and the residual; see `omnia_moe_down_combine_nvfp4`. act [slots, inner] bf16,
+    leaf [experts, hidden, ...], chosen [slots] int32, weights [slots] fp32, residual
+    [hidden] bf16 or None -> [hidden] bf16."""
+    _require(leaf.bias is None, "moe_down_combine_nvfp4: NVFP4 stacks carry no bias")
+    _require(leaf.weight.dim() == 3, "moe_down_combine_nvfp4: weight must be [experts, hidden, words]")
+    experts, hidden = leaf.weight.shape[0], leaf.weight.shape[1]
+    slots = chosen.numel()
+    _require(act.dim() == 2 and act.shape[0] == slots, "moe_down_combine_nvfp4: act must be [slots, inner]")
+    inner = act.shape[1]
+    _dense(act, BF16, "act")
+    leaf.check(hidden, inner, "moe_down_combine_nvfp4")
+    _require(chosen.dtype == torch.int32 and chosen.is_contiguous(), "moe_down_combine_nvfp4: chosen int32")
+    _require(weights.dtype == F32 and weights.is_contiguous() and weights.numel() == slots,
+             "moe_down_combine_nvfp4: weights must be contiguous fp32 [slots]")
+    tensors = [act, chosen, weights, *leaf.tensors()]
+    if residual is not None:
+        _require(residual.numel() == hidden and residual.dtype == BF16 and residual.is_contiguous(),
+                 "moe_down_combine_nvfp4: residual must be contiguous bf16 [hidden]")
+        tensors.append(residual)
+    _require(on_rocm(*tensors), "moe_down_combine_nvfp4: tensors must share one ROCm device")
+    out = _out(out, act, (hidden,), BF16, "out")
+    call("omnia_moe_down_combine_nvfp4", act.data_ptr(), leaf.weight.data_ptr(), leaf.scales.data_ptr(), experts,
+         hidden, inner, chosen.data_ptr(), weights.data_ptr(), slots,
          residual.data_ptr() if residual is not None else None, out.data_ptr(), _stream(act))
     return out

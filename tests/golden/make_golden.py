@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent.parent))
 
-from oracle import activations, add_norm, affine, attention, embed, mlp, moe, mxfp4, rope, route  # noqa: E402
+from oracle import activations, add_norm, affine, attention, embed, mlp, moe, mxfp4, nvfp4, rope, route  # noqa: E402
 from oracle.bf16 import from_float  # noqa: E402
 
 
@@ -144,6 +144,28 @@ def make_moe_mxfp4() -> dict[str, np.ndarray]:
     return arrays
 
 
+def make_moe_nvfp4() -> dict[str, np.ndarray]:
+    rng = np.random.default_rng(11)
+    experts, hidden, inner = 4, 128, 64
+
+    def stack(rows, features):
+        codes = rng.integers(0, 16, size=(experts, rows, features))
+        scales = rng.integers(0x18, 0x28, size=(experts, rows, features // 16)).astype(np.uint8)
+        return nvfp4.Stack(nvfp4.pack(codes), scales)
+
+    gate_up, down = stack(2 * inner, hidden), stack(hidden, inner)
+    x = from_float(2 * rng.standard_normal(hidden))
+    chosen = np.array([3, 0, 2], dtype=np.int32)
+    weights = np.array([0.5, 0.3, 0.2], dtype=np.float32)
+    residual = from_float(rng.standard_normal(hidden))
+    act = nvfp4.gate_up(x, gate_up, chosen)
+    out = nvfp4.down_combine(act, down, chosen, weights, residual)
+    arrays = dict(x=x, chosen=chosen, weights=weights, residual=residual, act=act, out=out)
+    for name, s in (("gate_up", gate_up), ("down", down)):
+        arrays.update({f"{name}_weight": s.weight, f"{name}_scales": s.scales})
+    return arrays
+
+
 def make_mlp() -> dict[str, np.ndarray]:
     rng = np.random.default_rng(7)
     hidden, inner = 128, 192
@@ -180,7 +202,8 @@ def make_attention() -> dict[str, np.ndarray]:
 
 MAKERS = {"attention": make_attention, "add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed,
           "activations": make_activations, "route": make_route, "moe": make_moe, "mlp": make_mlp,
-          "moe_affine": make_moe_affine, "moe_mxfp4": make_moe_mxfp4}
+          "moe_affine": make_moe_affine, "moe_mxfp4": make_moe_mxfp4,
+          "moe_nvfp4": make_moe_nvfp4}
 
 
 def main(names: list[str]) -> None:

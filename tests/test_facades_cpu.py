@@ -567,3 +567,51 @@ def test_mxfp4_predicate():
     assert mxfp4_applies(2880, 2880) and mxfp4_applies(32, 32)
     for args in ((2880, 2888), (2888, 2880), (0, 32), (32, 0)):
         assert not mxfp4_applies(*args), args
+
+
+def test_torch_nvfp4_decoder_matches_the_oracle():
+    from mlx_omnia_amd.kernels.leaf import nvfp4_dequantize
+    from oracle import nvfp4
+
+    rng = np.random.default_rng(33)
+    words = rng.integers(0, 1 << 32, size=(3, 5, 16), dtype=np.uint64).astype(np.uint32)
+    scales = rng.integers(0, 256, size=(3, 5, 8)).astype(np.uint8)
+    scales[0, 0, :4] = (0x7F, 0xFF, 0x01, 0x80)
+    got = nvfp4_dequantize(torch.from_numpy(words.view(np.int32)), torch.from_numpy(scales))
+    assert np.array_equal(got.numpy().astype(np.float64), nvfp4.dequantize(nvfp4.Stack(words, scales)))
+
+
+def test_nvfp4_moe_cpu_resolves_to_core_and_matches_oracle():
+    from mlx_omnia_amd.kernels.down_combine import DefaultDownCombine, DownCombine, HipNvfp4DownCombine
+    from mlx_omnia_amd.kernels.gate_up import DefaultGateUp, GateUp, HipNvfp4GateUp
+    from mlx_omnia_amd.kernels.leaf import QuantizedSwitchLinearLeaf
+    from oracle import nvfp4
+
+    experts, hidden, inner = 5, 128, 64
+    rng = np.random.default_rng(34)
+
+    def leaf(rows, features):
+        words = rng.integers(0, 1 << 32, size=(experts, rows, features // 8), dtype=np.uint64).astype(np.uint32)
+        scales = rng.integers(0x18, 0x28, size=(experts, rows, features // 16)).astype(np.uint8)
+        return nvfp4.Stack(words, scales), QuantizedSwitchLinearLeaf(
+            torch.from_numpy(words.view(np.int32)), torch.from_numpy(scales), None, 16, 4, mode="nvfp4")
+
+    gstack, gleaf = leaf(2 * inner, hidden)
+    dstack, dleaf = leaf(hidden, inner)
+    gate_up = GateUp(gleaf, hidden=hidden, inner=inner)
+    down = DownCombine(dleaf, hidden=hidden, inner=inner)
+    assert isinstance(gate_up.strategy, DefaultGateUp) and isinstance(down.strategy, DefaultDownCombine)
+    assert HipNvfp4GateUp.build(gleaf, hidden=hidden, inner=inner, activation="silu", limit=None, bias=None,
+                                layout="interleaved", routing=None, shared=None) is None
+    assert HipNvfp4DownCombine.build(dleaf, hidden=hidden, inner=inner, bias=None, shared=None,
+                                     layout="interleaved") is None
+    x = from_float(2 * rng.standard_normal(hidden))
+    chosen = np.array([4, 0, 2], dtype=np.int32)
+    act_core = gate_up(cpu(x), torch.from_numpy(chosen))
+    # The Core chain's sigmoid and product are bf16 tensor ops: one ulp from the oracle.
+    assert ulp_distance(bits(act_core), nvfp4.gate_up(x, gstack, chosen)).max() <= 1
+    weights = to_f32(from_float(np.array([0.5, 0.3, 0.2])))
+    residual = from_float(rng.standard_normal(hidden))
+    out = down(act_core, torch.from_numpy(chosen), torch.from_numpy(weights).to(torch.bfloat16), cpu(residual))
+    assert_bf16_close(bits(out), nvfp4.down_combine(bits(act_core), dstack, chosen, weights, residual),
+                      min_exact=0.8)

@@ -1,4 +1,4 @@
-"""HIP MXFP4 routed-expert kernels (csrc/moe_mxfp4.hip) against the oracle
+"""HIP MXFP4 routed-expert kernels (csrc/moe_fp4.hip) against the oracle
 (oracle/mxfp4.py).
 
 Mirrors the reference's mxfp4 strategies (core/kernels/gate_up/mxfp4.py,
