@@ -34,30 +34,33 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(
   if (row >= rows) return;  // whole wave leaves together; no barrier follows
   const int64_t base = row * vecs;
 
-  u32x4 xv[VPL], bv[VPL];
+  // Every load goes out before any arithmetic, with no branch among them (a load in a
+  // divergent branch makes the compiler wait on it): a lane past the row's end re-reads
+  // the row's last vector and adds nothing to the sum. The weight vectors come with them
+  // up to 8 per lane; wider rows read them in the output loop rather than spill.
+  constexpr bool kWeightFirst = VPL <= 8;
+  u32x4 xv[VPL], bv[VPL], wv[kWeightFirst ? VPL : 1];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const int v = lane + i * kWave;
-    if (v < vecs) {
-      xv[i] = load_nt(x + base + v);
-      bv[i] = load_nt(branch + base + v);
-    }
+    const int v = min(lane + i * kWave, vecs - 1);
+    xv[i] = load_nt(x + base + v);
+    bv[i] = load_nt(branch + base + v);
+    if constexpr (kWeightFirst) wv[i] = weight[v];
   }
+  __builtin_amdgcn_sched_barrier(0);
 
   float s[VPL][8];
   double acc = 0.0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const int v = lane + i * kWave;
-    if (v < vecs) {
-      float a[8], b[8];
-      unpack8(xv[i], a);
-      unpack8(bv[i], b);
+    const bool in_row = lane + i * kWave < vecs;
+    float a[8], b[8];
+    unpack8(xv[i], a);
+    unpack8(bv[i], b);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        s[i][j] = round_bf16(a[j] + b[j]);
-        acc += static_cast<double>(s[i][j] * s[i][j]);
-      }
+    for (int j = 0; j < 8; ++j) {
+      s[i][j] = round_bf16(a[j] + b[j]);
+      acc += in_row ? static_cast<double>(s[i][j] * s[i][j]) : 0.0;
     }
   }
   acc = wave_sum_f64(acc);
@@ -68,7 +71,8 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(
     const int v = lane + i * kWave;
     if (v < vecs) {
       float w[8], n[8];
-      unpack8(weight[v], w);
+      if constexpr (kWeightFirst) unpack8(wv[i], w);
+      else unpack8(weight[v], w);
 #pragma unroll
       for (int j = 0; j < 8; ++j) n[j] = w[j] * round_bf16(s[i][j] * inv);
       store_nt(summed + base + v, pack8(s[i]));
