@@ -51,17 +51,18 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void embed_atlas_kernel(Emb
     const bool valid = id >= 0 && id < a.vocab;  // wave-uniform
     const u32x4* src = a.embedding + (valid ? id : 0) * a.vecs;
     u32x4* dst = a.hidden_out + row * a.vecs;
+    // Every load goes out before the first store, with no branch among them (a load in a
+    // branch makes the compiler wait on it): a lane past the row's end re-reads the row's
+    // last vector, and an invalid id reads row 0 and writes zeros.
     u32x4 v[VPL];
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int k = lane + i * kWave;
-      v[i] = u32x4{0u, 0u, 0u, 0u};
-      if (valid && k < a.vecs) v[i] = src[k];
-    }
+    for (int i = 0; i < VPL; ++i) v[i] = src[min(lane + i * kWave, a.vecs - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    const u32x4 zero{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int k = lane + i * kWave;
-      if (k < a.vecs) store_nt(dst + k, v[i]);
+      if (k < a.vecs) store_nt(dst + k, valid ? v[i] : zero);
     }
     return;
   }
