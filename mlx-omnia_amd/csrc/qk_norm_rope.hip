@@ -342,14 +342,33 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
   const int64_t position = a.offset + t;
   const int base = g * 8;                    // first pair of this lane
 
-  float c[8], s[8];
+  // Every load goes out before any arithmetic, in the order the arithmetic needs them
+  // (vector-memory results are counted in issue order): the weights and the head's two
+  // halves, then the table row, with no branch among them (a load in a branch makes the
+  // compiler wait on it). A lane of a head past the last reads the last head and is
+  // zeroed afterwards.
+  const uint16_t* weight = is_query ? a.query_weight : a.key_weight;
+  const u32x4 wraw1 = *reinterpret_cast<const u32x4*>(weight + base);
+  const u32x4 wraw2 = *reinterpret_cast<const u32x4*>(weight + P + base);
+  const int head_read = live ? head : heads - 1;
+  const uint16_t* in = (is_query ? a.queries_in + t * a.query_stride
+                                 : a.keys_in + t * a.key_stride) + head_read * D + base;
+  u32x4 first = load_nt(reinterpret_cast<const u32x4*>(in));
+  u32x4 second = load_nt(reinterpret_cast<const u32x4*>(in + P));
+  f32x4 c0, c1, s0, s1;
   if constexpr (TABLE) {
     const float* crow = a.cos_table + position * a.table_stride + base;
     const float* srow = a.sin_table + position * a.table_stride + base;
-    const f32x4 c0 = *reinterpret_cast<const f32x4*>(crow);
-    const f32x4 c1 = *reinterpret_cast<const f32x4*>(crow + 4);
-    const f32x4 s0 = *reinterpret_cast<const f32x4*>(srow);
-    const f32x4 s1 = *reinterpret_cast<const f32x4*>(srow + 4);
+    c0 = *reinterpret_cast<const f32x4*>(crow);
+    c1 = *reinterpret_cast<const f32x4*>(crow + 4);
+    s0 = *reinterpret_cast<const f32x4*>(srow);
+    s1 = *reinterpret_cast<const f32x4*>(srow + 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (!live) first = second = u32x4{0u, 0u, 0u, 0u};
+
+  float c[8], s[8];
+  if constexpr (TABLE) {
     c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w;
     c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
     s[0] = s0.x; s[1] = s0.y; s[2] = s0.z; s[3] = s0.w;
@@ -375,20 +394,9 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
       }
     }
   }
-  const uint16_t* weight = is_query ? a.query_weight : a.key_weight;
   float w1[8], w2[8];
-  unpack8(*reinterpret_cast<const u32x4*>(weight + base), w1);
-  unpack8(*reinterpret_cast<const u32x4*>(weight + P + base), w2);
-
-  // The head loads go out after the table row and weight loads (vector-memory results
-  // are counted in issue order).
-  const uint16_t* in = (is_query ? a.queries_in + t * a.query_stride
-                                 : a.keys_in + t * a.key_stride) + head * D + base;
-  u32x4 first = u32x4{0u, 0u, 0u, 0u}, second = u32x4{0u, 0u, 0u, 0u};
-  if (live) {
-    first = load_nt(reinterpret_cast<const u32x4*>(in));
-    second = load_nt(reinterpret_cast<const u32x4*>(in + P));
-  }
+  unpack8(wraw1, w1);
+  unpack8(wraw2, w2);
   float x1[8], x2[8];
   unpack8(first, x1);
   unpack8(second, x2);
