@@ -504,6 +504,22 @@ def workloads() -> list[Workload]:
         setup=setup_moe_nvfp4,
         launch=lambda a: ops.moe_gate_up_nvfp4(a["x"], a["gu"], a["ids"], out=a["y"]),
     ))
+    def setup_moe_nvfp4_ordinal(device, copies):
+        sets = setup_moe_nvfp4(device, copies)
+        rng = np.random.default_rng(16)
+        for entry in sets:   # the router's ordinal keys over all experts
+            entry["keys"] = torch.from_numpy(rng.permutation(moe_e).astype(np.uint32)).to(device)
+        return sets
+
+    out.append(Workload(
+        name="moe_nvfp4_gate_up_ordinal_decode",
+        kernel="moe_gate_up_nvfp4_kernel",
+        description="the same NVFP4 gate/up with the top-8 of 128 ordinal keys ranked in the kernel "
+                    "(Qwen3-30B-A3B, T=1)",
+        bytes_per_launch=moe_k * 2 * moe_i * nvfp4_row_bytes(moe_h) + moe_h * 2 + moe_e * 4 + moe_k * moe_i * 2,
+        setup=setup_moe_nvfp4_ordinal,
+        launch=lambda a: ops.moe_gate_up_nvfp4_ordinal(a["x"], a["gu"], a["keys"], moe_k, out=a["y"]),
+    ))
     out.append(Workload(
         name="moe_nvfp4_down_combine_decode",
         kernel="moe_down_nvfp4_kernel",

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 8
+#define OMNIA_ABI_VERSION 9
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -301,6 +301,18 @@ int32_t omnia_moe_down_combine_mxfp4(const uint16_t* act, const uint32_t* weight
 int32_t omnia_moe_gate_up_nvfp4(const uint16_t* x, const uint32_t* weight, const uint8_t* scales,
                                 int64_t experts, int64_t hidden, int64_t inner, const int32_t* chosen,
                                 int64_t slots, uint16_t* out, hipStream_t stream);
+
+/* The same NVFP4 gate/up with the routing decided in the kernel: slot s (s < top_k) runs
+ * the expert of rank s in the ordinal keys (ascending = better, equal keys to the lower
+ * index), as the reference's OrdinalRouting declaration defines it. keys [experts] uint32;
+ * experts <= 1024, top_k <= experts; out [top_k, inner] bf16. Other arguments as
+ * omnia_moe_gate_up_nvfp4.
+ * Replaces: core/kernels/gate_up/nvfp4_packed.py:1-346 (`Nvfp4PackedGateUp`, routing
+ * inside the kernel; its repacked weight layout is not used); ordinal routing
+ * core/kernels/gate_up/kernel.py:23-36. */
+int32_t omnia_moe_gate_up_nvfp4_ordinal(const uint16_t* x, const uint32_t* weight, const uint8_t* scales,
+                                        int64_t experts, int64_t hidden, int64_t inner, const uint32_t* keys,
+                                        int64_t top_k, uint16_t* out, hipStream_t stream);
 
 /* Routed expert down/combine of one token over an NVFP4 stack:
  *   t[s, n] = sum over groups of 16 of s * sum_i act[s, i] v[i]       fp32

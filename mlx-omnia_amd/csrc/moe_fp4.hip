@@ -123,7 +123,8 @@ struct Stack {
 struct GateUpArgs {
   const uint16_t* x;       // [hidden]
   Stack stack;             // [experts, 2 * inner, ...]
-  const int32_t* chosen;   // [slots]
+  const int32_t* chosen;   // [slots]; null when `keys` routes
+  const uint32_t* keys;    // [experts] ordinal keys (ascending = better), or null
   uint16_t* out;           // [slots, inner]
   int64_t experts;
   int hidden;
@@ -131,8 +132,74 @@ struct GateUpArgs {
   float limit;             // mxfp4: +inf for no clamp
 };
 
+constexpr int kMaxOrdinalExperts = 1024;   // keys per lane: at most 16
+
+// (hi, lo) = the smaller of itself and (ohi, olo), as one 64-bit unsigned value.
+__device__ __forceinline__ void min_u64(uint32_t& hi, uint32_t& lo, uint32_t ohi, uint32_t olo) {
+  const bool take = ohi < hi || (ohi == hi && olo < lo);
+  hi = take ? ohi : hi;
+  lo = take ? olo : lo;
+}
+
+template <int kCtrl>
+__device__ __forceinline__ void min_dpp_step(uint32_t& hi, uint32_t& lo) {
+  min_u64(hi, lo, dpp<kCtrl>(hi), dpp<kCtrl>(lo));
+}
+
+// Minimum over the wave of a 64-bit value, the same in every lane: DPP steps inside each
+// 16-lane row (quad swaps, half-row and row mirrors), then the two cross-row swaps, all in
+// vector registers.
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+  uint32_t hi = static_cast<uint32_t>(v >> 32), lo = static_cast<uint32_t>(v);
+  min_dpp_step<kQuadSwap1>(hi, lo);
+  min_dpp_step<kQuadSwap2>(hi, lo);
+  min_dpp_step<kRowHalfMirror>(hi, lo);
+  min_dpp_step<kRowMirror>(hi, lo);
+  uint32_t ha, hb, la, lb;
+  row_pair(hi, ha, hb);
+  row_pair(lo, la, lb);
+  hi = ha;
+  lo = la;
+  min_u64(hi, lo, hb, lb);
+  half_pair(hi, ha, hb);
+  half_pair(lo, la, lb);
+  hi = ha;
+  lo = la;
+  min_u64(hi, lo, hb, lb);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// The expert in rank `slot` of the ordinal keys (ascending, equal keys to the lower index,
+// the sort's rule of core/kernels/gate_up/kernel.py:23-36): slot + 1 rounds of a wave
+// argmin over (key, index), each removing its winner. Every wave of the slot computes it.
+// kKeys keys per lane (expert lane + 64 j), loaded at a clamped index with no branch (a
+// load in a branch makes the compiler wait on it); an index past the last is never chosen.
+template <int kKeys>
+__device__ __forceinline__ int ordinal_expert(const uint32_t* keys, int experts, int slot, int lane) {
+  uint32_t raw[kKeys];
+#pragma unroll
+  for (int j = 0; j < kKeys; ++j) raw[j] = keys[min(lane + kWave * j, experts - 1)];
+  uint64_t mine[kKeys];
+#pragma unroll
+  for (int j = 0; j < kKeys; ++j) {
+    const int e = lane + kWave * j;
+    mine[j] = e < experts ? (static_cast<uint64_t>(raw[j]) << 32) | static_cast<uint32_t>(e) : ~uint64_t{0};
+  }
+  uint64_t best = ~uint64_t{0};
+  for (int round = 0; round <= slot; ++round) {   // slot < experts: bounded
+    uint64_t local = mine[0];
+#pragma unroll
+    for (int j = 1; j < kKeys; ++j) local = mine[j] < local ? mine[j] : local;
+    best = wave_min_u64(local);
+#pragma unroll
+    for (int j = 0; j < kKeys; ++j) mine[j] = mine[j] == best ? ~uint64_t{0} : mine[j];
+  }
+  return static_cast<int>(static_cast<uint32_t>(best));
+}
+
 // kTrips > 0: hidden / 32 chunks span exactly kTrips 64-lane trips; 0: any number of trips.
-template <Fp4 F, int kTrips>
+// kKeys > 0: the slot's expert comes from the ordinal keys (kKeys per lane), not `chosen`.
+template <Fp4 F, int kTrips, int kKeys = 0>
 __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   const int lane = threadIdx.x % kWave;
   const int slot = blockIdx.y;
@@ -140,7 +207,9 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   if (pair0 >= a.inner) return;  // whole wave; no barrier follows
   const int pairs = min(kPairsPerWave, a.inner - pair0);
   uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + pair0;
-  const int expert = a.chosen[slot];
+  int expert;
+  if constexpr (kKeys > 0) expert = ordinal_expert<kKeys>(a.keys, static_cast<int>(a.experts), slot, lane);
+  else expert = a.chosen[slot];
   if (expert < 0 || expert >= a.experts) {
     if (lane < pairs) out[lane] = 0;
     return;
@@ -223,9 +292,16 @@ __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_mxfp4_kernel(G
   gate_up_body<Fp4::kMx, kTrips>(a);
 }
 
-template <int kTrips>
+template <int kTrips, int kKeys>
 __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_nvfp4_kernel(GateUpArgs a) {
-  gate_up_body<Fp4::kNv, kTrips>(a);
+  gate_up_body<Fp4::kNv, kTrips, kKeys>(a);
+}
+
+template <int kKeys>
+void launch_nvfp4_gate_up(int64_t trips, dim3 grid, dim3 block, hipStream_t stream, const GateUpArgs& a) {
+  if (trips == 1) moe_gate_up_nvfp4_kernel<1, kKeys><<<grid, block, 0, stream>>>(a);
+  else if (trips == 2) moe_gate_up_nvfp4_kernel<2, kKeys><<<grid, block, 0, stream>>>(a);
+  else moe_gate_up_nvfp4_kernel<0, kKeys><<<grid, block, 0, stream>>>(a);
 }
 
 // ---- down_combine -------------------------------------------------------------------
@@ -331,8 +407,8 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_nvfp4_kernel(D
 
 int32_t launch_gate_up(Fp4 format, const char* name, const uint16_t* x, const uint32_t* weight,
                        const void* scales, const uint16_t* bias, int64_t experts, int64_t hidden,
-                       int64_t inner, const int32_t* chosen, int64_t slots, float limit, uint16_t* out,
-                       hipStream_t stream) {
+                       int64_t inner, const int32_t* chosen, const uint32_t* keys, int64_t slots, float limit,
+                       uint16_t* out, hipStream_t stream) {
   OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), std::string(name) + ": bad expert count");
   OMNIA_REQUIRE(hidden > 0 && hidden % kChunk == 0 && hidden <= 16384,
                 std::string(name) + ": hidden must be a multiple of 32 in [32, 16384]");
@@ -340,13 +416,15 @@ int32_t launch_gate_up(Fp4 format, const char* name, const uint16_t* x, const ui
   OMNIA_REQUIRE(slots >= 0 && slots <= 1024, std::string(name) + ": slots must be in [0, 1024]");
   OMNIA_REQUIRE(!(limit < 0.0f), std::string(name) + ": the limit must be non-negative (+inf: none)");
   if (slots == 0) return 0;
-  OMNIA_REQUIRE(x && weight && scales && chosen && out, std::string(name) + ": null pointer");
+  OMNIA_REQUIRE(x && weight && scales && (chosen || keys) && out, std::string(name) + ": null pointer");
+  OMNIA_REQUIRE(keys == nullptr || (format == Fp4::kNv && experts <= kMaxOrdinalExperts && slots <= experts),
+                std::string(name) + ": ordinal routing takes at most 1024 experts and top_k <= experts");
   OMNIA_REQUIRE(aligned16(x) && aligned16(weight), std::string(name) + ": x and weight must be 16-byte aligned");
   OMNIA_REQUIRE(format == Fp4::kMx || reinterpret_cast<uintptr_t>(scales) % 2 == 0,
                 std::string(name) + ": the scales must be 2-byte aligned");
   int32_t rc = check_device();
   if (rc != 0) return rc;
-  GateUpArgs a{x, Stack{reinterpret_cast<const u32x4*>(weight), scales, bias}, chosen, out, experts,
+  GateUpArgs a{x, Stack{reinterpret_cast<const u32x4*>(weight), scales, bias}, chosen, keys, out, experts,
                static_cast<int>(hidden), static_cast<int>(inner), limit};
   const int64_t waves = (inner + kPairsPerWave - 1) / kPairsPerWave;
   const dim3 grid(static_cast<unsigned>((waves + kGateWaves - 1) / kGateWaves), static_cast<unsigned>(slots));
@@ -356,10 +434,14 @@ int32_t launch_gate_up(Fp4 format, const char* name, const uint16_t* x, const ui
     if (trips == 1) moe_gate_up_mxfp4_kernel<1><<<grid, block, 0, stream>>>(a);
     else if (trips == 2) moe_gate_up_mxfp4_kernel<2><<<grid, block, 0, stream>>>(a);
     else moe_gate_up_mxfp4_kernel<0><<<grid, block, 0, stream>>>(a);
+  } else if (keys == nullptr) {
+    launch_nvfp4_gate_up<0>(trips, grid, block, stream, a);
+  } else if (experts <= 2 * kWave) {
+    launch_nvfp4_gate_up<2>(trips, grid, block, stream, a);
+  } else if (experts <= 4 * kWave) {
+    launch_nvfp4_gate_up<4>(trips, grid, block, stream, a);
   } else {
-    if (trips == 1) moe_gate_up_nvfp4_kernel<1><<<grid, block, 0, stream>>>(a);
-    else if (trips == 2) moe_gate_up_nvfp4_kernel<2><<<grid, block, 0, stream>>>(a);
-    else moe_gate_up_nvfp4_kernel<0><<<grid, block, 0, stream>>>(a);
+    launch_nvfp4_gate_up<kMaxOrdinalExperts / kWave>(trips, grid, block, stream, a);
   }
   return launched(name);
 }
@@ -403,7 +485,7 @@ extern "C" int32_t omnia_moe_gate_up_mxfp4(const uint16_t* x, const uint32_t* we
                                            int64_t inner, const int32_t* chosen, int64_t slots,
                                            float limit, uint16_t* out, hipStream_t stream) {
   return omnia::launch_gate_up(omnia::Fp4::kMx, "moe_gate_up_mxfp4", x, weight, scales, bias, experts, hidden,
-                               inner, chosen, slots, limit, out, stream);
+                               inner, chosen, nullptr, slots, limit, out, stream);
 }
 
 extern "C" int32_t omnia_moe_down_combine_mxfp4(const uint16_t* act, const uint32_t* weight,
@@ -421,7 +503,15 @@ extern "C" int32_t omnia_moe_gate_up_nvfp4(const uint16_t* x, const uint32_t* we
                                            const int32_t* chosen, int64_t slots, uint16_t* out,
                                            hipStream_t stream) {
   return omnia::launch_gate_up(omnia::Fp4::kNv, "moe_gate_up_nvfp4", x, weight, scales, nullptr, experts, hidden,
-                               inner, chosen, slots, __builtin_inff(), out, stream);
+                               inner, chosen, nullptr, slots, __builtin_inff(), out, stream);
+}
+
+extern "C" int32_t omnia_moe_gate_up_nvfp4_ordinal(const uint16_t* x, const uint32_t* weight,
+                                                   const uint8_t* scales, int64_t experts, int64_t hidden,
+                                                   int64_t inner, const uint32_t* keys, int64_t top_k,
+                                                   uint16_t* out, hipStream_t stream) {
+  return omnia::launch_gate_up(omnia::Fp4::kNv, "moe_gate_up_nvfp4_ordinal", x, weight, scales, nullptr, experts,
+                               hidden, inner, nullptr, keys, top_k, __builtin_inff(), out, stream);
 }
 
 extern "C" int32_t omnia_moe_down_combine_nvfp4(const uint16_t* act, const uint32_t* weight,

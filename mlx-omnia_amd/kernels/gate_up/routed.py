@@ -14,8 +14,11 @@ first strategy whose `build` accepts the declaration serves it.
 - `HipNvfp4GateUp` (`omnia_moe_gate_up_nvfp4`, csrc/moe_fp4.hip) serves what the
   reference's `Nvfp4GateUp` serves (core/kernels/gate_up/nvfp4.py:79-110): an NVFP4 stack
   (mode "nvfp4", e4m3 scales per 16) under the `interleaved` layout, silu without clamp,
-  bias, ordinal routing or shared expert; hidden and inner multiples of 32 (the
-  reference's 16: the others go to the Core chain), hidden up to 16384.
+  bias or shared expert; hidden and inner multiples of 32 (the reference's 16: the others
+  go to the Core chain), hidden up to 16384. With an `OrdinalRouting` declaration it
+  serves what `Nvfp4PackedGateUp` serves (core/kernels/gate_up/nvfp4_packed.py:286-321)
+  through `omnia_moe_gate_up_nvfp4_ordinal`, which ranks uint32 ordinal keys in the
+  kernel (up to 1024 experts; other key types go to the Core chain).
 - `HipAffineGateUp` (`omnia_moe_gate_up_affine`, csrc/moe_affine.hip) serves what the
   reference's `AffineGateUp` serves (core/kernels/gate_up/affine.py:105-191): an
   affine-quantized stack (`QuantizedSwitchLinearLeaf`, 2, 3, 4, 5, 6 or 8 bits, groups of
@@ -262,11 +265,13 @@ class HipMxfp4GateUp(GateUpStrategy):
 @dataclass(frozen=True)
 class HipNvfp4GateUp(GateUpStrategy):
     leaf: "ops.Nvfp4Leaf"
+    routing: OrdinalRouting | None
+    fallback: "DefaultGateUp"
 
     @classmethod
     def build(cls, leaf, *, hidden, inner, activation, limit, bias, layout, routing,
               shared) -> "HipNvfp4GateUp | None":
-        if shared is not None or layout != "interleaved" or routing is not None:
+        if shared is not None or layout != "interleaved":
             return None
         # The kernel carries neither clamp nor projection bias, as the reference's.
         if activation != "silu" or limit is not None or bias is not None:
@@ -274,11 +279,26 @@ class HipNvfp4GateUp(GateUpStrategy):
         if not mxfp4_applies(hidden, inner) or hidden > 16384:
             return None
         view = nvfp4_leaf(leaf, 2 * inner, hidden)
-        return None if view is None else cls(view)
+        if view is None:
+            return None
+        if routing is not None and not 0 < routing.top_k <= view.weight.shape[0] <= 1024:
+            return None
+        fallback = DefaultGateUp.build(leaf, hidden=hidden, inner=inner, activation=activation,
+                                       limit=limit, bias=bias, layout=layout, routing=routing,
+                                       shared=shared)
+        return cls(view, routing, fallback)
 
     def __call__(self, row: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor:
+        x = row.reshape(-1).contiguous()
+        if self.routing is not None:
+            # Ordinal keys are uint32 (the router's ordinals); the kernel ranks them in place
+            # of the sort (core/kernels/gate_up/nvfp4_packed.py:1-13).
+            if chosen.dtype != torch.uint32:
+                return self.fallback(row, chosen)
+            keys = chosen.to(device=self.leaf.weight.device).contiguous().reshape(-1)
+            return ops.moe_gate_up_nvfp4_ordinal(x, self.leaf, keys, self.routing.top_k)
         ids = chosen.to(device=self.leaf.weight.device, dtype=torch.int32).contiguous().reshape(-1)
-        return ops.moe_gate_up_nvfp4(row.reshape(-1).contiguous(), self.leaf, ids)
+        return ops.moe_gate_up_nvfp4(x, self.leaf, ids)
 
 
 _STRATEGIES = (HipNvfp4GateUp, HipMxfp4GateUp, HipAffineGateUp, HipDenseGateUp, DefaultGateUp)

@@ -809,6 +809,35 @@ def moe_gate_up_nvfp4(
     return out
 
 
+def moe_gate_up_nvfp4_ordinal(
+    x: torch.Tensor,
+    leaf: Nvfp4Leaf,
+    keys: torch.Tensor,
+    top_k: int,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """`moe_gate_up_nvfp4` with the routing decided in the kernel: slot s runs the expert of
+    rank s in the ordinal keys [experts] (ascending, equal keys to the lower index); see
+    `omnia_moe_gate_up_nvfp4_ordinal`. -> [top_k, inner] bf16."""
+    _require(x.dim() == 1 or x.numel() == x.shape[-1], "moe_gate_up_nvfp4_ordinal: x must be one row")
+    hidden = x.shape[-1]
+    _dense(x, BF16, "x")
+    _require(leaf.bias is None, "moe_gate_up_nvfp4_ordinal: NVFP4 stacks carry no bias")
+    _require(leaf.weight.dim() == 3 and leaf.weight.shape[1] % 2 == 0,
+             "moe_gate_up_nvfp4_ordinal: weight must be [experts, 2 * inner, words]")
+    experts, rows = leaf.weight.shape[0], leaf.weight.shape[1]
+    leaf.check(rows, hidden, "moe_gate_up_nvfp4_ordinal")
+    _require(keys.dtype in (torch.int32, torch.uint32) and keys.is_contiguous() and keys.numel() == experts,
+             "moe_gate_up_nvfp4_ordinal: keys must be contiguous 32-bit [experts]")
+    _require(0 < top_k <= experts <= 1024, "moe_gate_up_nvfp4_ordinal: 0 < top_k <= experts <= 1024")
+    _require(on_rocm(x, keys, *leaf.tensors()), "moe_gate_up_nvfp4_ordinal: tensors must share one ROCm device")
+    out = _out(out, x, (top_k, rows // 2), BF16, "out")
+    call("omnia_moe_gate_up_nvfp4_ordinal", x.data_ptr(), leaf.weight.data_ptr(), leaf.scales.data_ptr(), experts,
+         hidden, rows // 2, keys.data_ptr(), top_k, out.data_ptr(), _stream(x))
+    return out
+
+
 def moe_down_combine_nvfp4(
     act: torch.Tensor,
     leaf: Nvfp4Leaf,

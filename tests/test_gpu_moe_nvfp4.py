@@ -134,3 +134,44 @@ def test_shape_checks_raise_before_launch():
         ops.moe_gate_up_nvfp4(to_device(from_float(rng.standard_normal(256))),
                               ops.Nvfp4Leaf(leaf.weight, leaf.scales, torch.zeros(4, 128, dtype=torch.bfloat16,
                                                                                    device="cuda")), _ids([0]))
+
+
+def _ranked(keys, top_k):
+    """Ascending ordinal keys, equal keys to the lower index (a stable sort)."""
+    return list(np.argsort(keys.astype(np.uint64), kind="stable")[:top_k])
+
+
+@pytest.mark.parametrize("experts,top_k,hidden", [(128, 8, 2048), (200, 8, 256), (1024, 4, 512), (64, 64, 96), (32, 1, 32)])
+def test_ordinal_routing_in_the_kernel(experts, top_k, hidden):
+    print(f"moe_gate_up_nvfp4_ordinal experts={experts} top_k={top_k}", flush=True)
+    rng = np.random.default_rng(experts + top_k)
+    stack, leaf = _leaf(rng, experts, 2 * 64, hidden)
+    keys = rng.integers(0, 1 << 32, size=experts, dtype=np.uint64).astype(np.uint32)
+    keys[5::7] = keys[3]                                  # ties, resolved to the lower index
+    keys[1] = np.uint32(0xFFFFFFF0)                       # above 2^31: compared unsigned
+    x = from_float(rng.standard_normal(hidden))
+    got = ops.moe_gate_up_nvfp4_ordinal(to_device(x), leaf, torch.from_numpy(keys).cuda(), top_k)
+    chosen = _ranked(keys, top_k)
+    assert_bf16_close(bits_of(got), nvfp4.gate_up(x, stack, chosen), min_exact=0.99)
+    by_index = ops.moe_gate_up_nvfp4(to_device(x), leaf, _ids(chosen))
+    assert torch.equal(got, by_index)
+
+
+def test_ordinal_facade():
+    from mlx_omnia_amd.kernels.gate_up import GateUp, HipNvfp4GateUp, OrdinalRouting
+    from mlx_omnia_amd.kernels.leaf import QuantizedSwitchLinearLeaf
+
+    rng = np.random.default_rng(12)
+    _, g = _leaf(rng, 64, 2 * 128, 256)
+    gleaf = QuantizedSwitchLinearLeaf(g.weight, g.scales, None, 16, 4, mode="nvfp4")
+    gate_up = GateUp(gleaf, hidden=256, inner=128, routing=OrdinalRouting(top_k=6))
+    assert isinstance(gate_up.strategy, HipNvfp4GateUp)
+    keys = rng.permutation(64).astype(np.uint32)
+    x = to_device(from_float(rng.standard_normal(256)))
+    got = gate_up(x, torch.from_numpy(keys).cuda())
+    core = GateUp(gleaf, hidden=256, inner=128, routing=OrdinalRouting(top_k=6), reference=True)(
+        x, torch.from_numpy(keys.astype(np.int64)).cuda())
+    assert_bf16_close(bits_of(got), bits_of(core), min_exact=0.95)
+    # int32 keys take the Core chain, which sorts them as signed integers.
+    signed = gate_up(x, torch.from_numpy(keys.astype(np.int32)).cuda())
+    assert torch.equal(signed, core)
