@@ -615,3 +615,26 @@ def test_nvfp4_moe_cpu_resolves_to_core_and_matches_oracle():
     out = down(act_core, torch.from_numpy(chosen), torch.from_numpy(weights).to(torch.bfloat16), cpu(residual))
     assert_bf16_close(bits(out), nvfp4.down_combine(bits(act_core), dstack, chosen, weights, residual),
                       min_exact=0.8)
+
+
+def test_nvfp4_ordinal_routing_core_chain_matches_a_stable_argsort():
+    from mlx_omnia_amd.kernels.gate_up import DefaultGateUp, GateUp, HipNvfp4GateUp, OrdinalRouting
+    from mlx_omnia_amd.kernels.leaf import QuantizedSwitchLinearLeaf
+    from oracle import nvfp4
+
+    experts, hidden, inner = 40, 64, 32
+    rng = np.random.default_rng(35)
+    words = rng.integers(0, 1 << 32, size=(experts, 2 * inner, hidden // 8), dtype=np.uint64).astype(np.uint32)
+    scales = rng.integers(0x18, 0x28, size=(experts, 2 * inner, hidden // 16)).astype(np.uint8)
+    leaf = QuantizedSwitchLinearLeaf(torch.from_numpy(words.view(np.int32)), torch.from_numpy(scales), None, 16, 4,
+                                     mode="nvfp4")
+    gate_up = GateUp(leaf, hidden=hidden, inner=inner, routing=OrdinalRouting(top_k=5))
+    assert isinstance(gate_up.strategy, DefaultGateUp)      # CPU tensors: the Core chain
+    assert HipNvfp4GateUp.build(leaf, hidden=hidden, inner=inner, activation="silu", limit=None, bias=None,
+                                layout="interleaved", routing=OrdinalRouting(top_k=5), shared=None) is None
+    keys = rng.integers(0, 1 << 32, size=experts, dtype=np.uint64).astype(np.uint32)
+    keys[[7, 11, 30]] = keys[2]                              # ties resolve to the lower index
+    x = from_float(rng.standard_normal(hidden))
+    got = gate_up(cpu(x), torch.from_numpy(keys))
+    chosen = list(np.argsort(keys.astype(np.uint64), kind="stable")[:5])
+    assert ulp_distance(bits(got), nvfp4.gate_up(x, nvfp4.Stack(words, scales), chosen)).max() <= 1
