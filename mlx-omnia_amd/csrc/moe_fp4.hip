@@ -319,10 +319,15 @@ struct DownArgs {
   int slots;
 };
 
-// kSteps = ceil(inner / (32 * 64)) chunks per lane: 1 or 2.
-template <Fp4 F, int kSteps>
+// kLanes lanes run across each row (64, or 32 for short rows: the wave's two halves then
+// take rows h and h + 2); kSteps = ceil(inner / (32 * kLanes)) chunks per lane.
+template <Fp4 F, int kSteps, int kLanes = kWave>
 __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kMaxDownSlots][kDownRows]) {
+  constexpr int kHalves = kWave / kLanes;            // row groups per wave
+  constexpr int kRowsPerGroup = kDownRows / kHalves;
   const int lane = threadIdx.x % kWave;
+  const int part = lane % kLanes;
+  const int group = lane / kLanes;
   const int slot = threadIdx.x / kWave;   // one wave per slot
   const int row_base = blockIdx.x * kDownRows;
   const int rows = min(kDownRows, a.hidden - row_base);
@@ -330,26 +335,26 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
   const bool valid = expert >= 0 && expert < a.experts;   // uniform over the wave
   const int64_t row0 = static_cast<int64_t>(valid ? expert : 0) * a.hidden + row_base;
   const int chunks = a.inner / kChunk;
-  float t[kDownRows];
+  float t[kRowsPerGroup];
 #pragma unroll
-  for (int i = 0; i < kDownRows; ++i) t[i] = 0.0f;
+  for (int q = 0; q < kRowsPerGroup; ++q) t[q] = 0.0f;
   if (valid) {
-    // Every load (codes, scale bits, the slot's activations, shared by the wave's rows)
+    // Every load (codes, scale bits, the slot's activations, shared by the group's rows)
     // is issued before any arithmetic, with no branch among them: a lane past the row's
     // last chunk re-reads that chunk and drops the term, and a row past the last one
     // re-reads the last (its sum is never used).
     const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
-    u32x4 w[kSteps][kDownRows];
-    uint32_t s[kSteps][kDownRows];
+    u32x4 w[kSteps][kRowsPerGroup];
+    uint32_t s[kSteps][kRowsPerGroup];
     u32x4 xv[kSteps][4];
 #pragma unroll
     for (int h = 0; h < kSteps; ++h) {
-      const int c = min(lane + kWave * h, chunks - 1);
+      const int c = min(part + kLanes * h, chunks - 1);
 #pragma unroll
-      for (int i = 0; i < kDownRows; ++i) {
-        const int64_t at = (row0 + min(i, rows - 1)) * chunks + c;
-        w[h][i] = load_nt(a.stack.weight + at);
-        s[h][i] = load_scales<F>(a.stack.scales, at);
+      for (int q = 0; q < kRowsPerGroup; ++q) {
+        const int64_t at = (row0 + min(group + kHalves * q, rows - 1)) * chunks + c;
+        w[h][q] = load_nt(a.stack.weight + at);
+        s[h][q] = load_scales<F>(a.stack.scales, at);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) xv[h][j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
@@ -357,20 +362,36 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
     __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
 #pragma unroll
     for (int h = 0; h < kSteps; ++h) {
-      const bool in_row = lane + kWave * h < chunks;
+      const bool in_row = part + kLanes * h < chunks;
 #pragma unroll
-      for (int i = 0; i < kDownRows; ++i) {
-        const float term = chunk_value<F>(s[h][i], w[h][i], xv[h], t[i]);
-        t[i] = in_row ? term : t[i];
+      for (int q = 0; q < kRowsPerGroup; ++q) {
+        const float term = chunk_value<F>(s[h][q], w[h][q], xv[h], t[q]);
+        t[q] = in_row ? term : t[q];
       }
     }
   }
-  // Lane i takes row i's sum.
+  // Lane i takes row i's sum (row g + kHalves q is group g's q-th). With two groups, one
+  // permlane32 swap hands every lane both groups' sums.
   float mine = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kDownRows; ++i) {
-    const float total = wave_sum_f32(t[i]);
-    mine = lane == i ? total : mine;
+  for (int q = 0; q < kRowsPerGroup; ++q) {
+    if constexpr (kLanes == kWave) {
+      const float total = wave_sum_f32(t[q]);
+      mine = lane == q ? total : mine;
+    } else {
+      float v = t[q];
+      v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
+      v += __uint_as_float(dpp<kQuadSwap2>(__float_as_uint(v)));
+      v += __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
+      v += __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
+      uint32_t lo, hi;
+      row_pair(__float_as_uint(v), lo, hi);
+      const float group_total = __uint_as_float(lo) + __uint_as_float(hi);
+      uint32_t g0, g1;
+      half_pair(__float_as_uint(group_total), g0, g1);
+      mine = lane == kHalves * q ? __uint_as_float(g0) : mine;
+      mine = lane == kHalves * q + 1 ? __uint_as_float(g1) : mine;
+    }
   }
   if (lane < rows) {
     float term = 0.0f;
@@ -397,10 +418,10 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_mxfp4_kernel(D
   down_body<Fp4::kMx, kSteps>(a, partial);
 }
 
-template <int kSteps>
+template <int kSteps, int kLanes>
 __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_nvfp4_kernel(DownArgs a) {
   __shared__ float partial[kMaxDownSlots][kDownRows];
-  down_body<Fp4::kNv, kSteps>(a, partial);
+  down_body<Fp4::kNv, kSteps, kLanes>(a, partial);
 }
 
 // Host side: shape checks and launches shared by both formats.
@@ -465,14 +486,17 @@ int32_t launch_down(Fp4 format, const char* name, const uint16_t* act, const uin
              experts, static_cast<int>(hidden), static_cast<int>(inner), static_cast<int>(slots)};
   const dim3 grid(static_cast<unsigned>((hidden + kDownRows - 1) / kDownRows));
   const dim3 block(static_cast<unsigned>(slots * kWave));
-  static_assert(kMaxDownSteps == 2, "one instantiation per step count");
+  static_assert(kMaxDownSteps == 2 && kDownRows == 4, "one instantiation per step count");
   const bool one = inner <= kChunk * kWave;
   if (format == Fp4::kMx) {
     if (one) moe_down_mxfp4_kernel<1><<<grid, block, 0, stream>>>(a);
     else moe_down_mxfp4_kernel<2><<<grid, block, 0, stream>>>(a);
+  } else if (inner <= kChunk * kWave / 2) {   // at most 32 chunks: 32 lanes per row
+    moe_down_nvfp4_kernel<1, kWave / 2><<<grid, block, 0, stream>>>(a);
+  } else if (one) {
+    moe_down_nvfp4_kernel<1, kWave><<<grid, block, 0, stream>>>(a);
   } else {
-    if (one) moe_down_nvfp4_kernel<1><<<grid, block, 0, stream>>>(a);
-    else moe_down_nvfp4_kernel<2><<<grid, block, 0, stream>>>(a);
+    moe_down_nvfp4_kernel<2, kWave><<<grid, block, 0, stream>>>(a);
   }
   return launched(name);
 }
