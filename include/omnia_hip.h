@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 9
+#define OMNIA_ABI_VERSION 10
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -390,6 +390,34 @@ int32_t omnia_attention_decode(const uint16_t* raw_queries, const uint16_t* raw_
                                int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
                                float eps, void* workspace, int64_t workspace_bytes,
                                uint16_t* out, hipStream_t stream);
+
+/* Bytes of the static device array omnia_attention_decode_noalloc keeps its per-chunk
+ * softmax states in (one array per GPU, held until the process ends). */
+#define OMNIA_ATTENTION_SCRATCH_BYTES (4 * 1024 * 1024)
+
+/* omnia_attention_decode without a workspace argument: the same step, the same kernels
+ * and the same results, with the per-chunk states in a static device array of
+ * OMNIA_ATTENTION_SCRATCH_BYTES per GPU instead of caller memory. It calls no
+ * hipMalloc, hipFree or allocating library routine.
+ * No counterpart in the reference. It is for callers that cannot allocate device
+ * memory: code under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc. The array's device address is looked up once per device, on the first
+ * call there.
+ * Limits: -EINVAL when the step needs more than OMNIA_ATTENTION_SCRATCH_BYTES of
+ * states: 520 bytes per query head and chunk, at most
+ * (511 + kv_heads) * (heads / kv_heads) * 520 bytes at any cache length (1.1 MB for 32
+ * query heads over 8 kv heads; none when max_rows <= 128). Every call on one GPU shares
+ * that GPU's array and it keeps the last call's contents: calls that overlap on one
+ * GPU (other streams, or other threads without ordering) race. */
+int32_t omnia_attention_decode_noalloc(const uint16_t* raw_queries, const uint16_t* raw_keys,
+                                       const uint16_t* raw_values, const uint16_t* query_weight,
+                                       const uint16_t* key_weight, const float* angles,
+                                       int64_t angle_rows, int64_t rotary_pairs, float mscale,
+                                       uint16_t* key_cache, uint16_t* value_cache,
+                                       int64_t capacity, int64_t window, const int32_t* position,
+                                       int64_t max_rows, int64_t heads, int64_t kv_heads,
+                                       int64_t head_dim, float scale, float eps, uint16_t* out,
+                                       hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,9 @@
 //
 // The chunk holding the write row computes the new key row itself and reads that row
 // from LDS, never from the cache line it has just written.
+#include <mutex>
+#include <string>
+
 #include "common.hpp"
 #include "host.hpp"
 
@@ -610,34 +613,19 @@ extern "C" int64_t omnia_attention_workspace_bytes(int64_t heads, int64_t kv_hea
   return kv_heads * splits * (heads / kv_heads) * kPartial * static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int32_t omnia_attention_decode(
+namespace omnia {
+namespace {
+
+// Checks the arguments, sizes the split and launches both kernels; `workspace` holds
+// the per-chunk states when the cache is split over several workgroups per kv head.
+int32_t attention_decode_checked(
     const uint16_t* raw_queries, const uint16_t* raw_keys, const uint16_t* raw_values,
     const uint16_t* query_weight, const uint16_t* key_weight, const float* angles,
     int64_t angle_rows, int64_t rotary_pairs, float mscale, uint16_t* key_cache,
     uint16_t* value_cache, int64_t capacity, int64_t window, const int32_t* position,
     int64_t max_rows, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale, float eps,
     void* workspace, int64_t workspace_bytes, uint16_t* out, hipStream_t stream) {
-  using namespace omnia;
-  OMNIA_REQUIRE(head_dim == kD, "attention_decode: head_dim must be 128");
-  OMNIA_REQUIRE(kv_heads > 0 && heads > 0 && heads % kv_heads == 0,
-                "attention_decode: heads must be a positive multiple of kv_heads");
   const int64_t gqa = heads / kv_heads;
-  OMNIA_REQUIRE(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8,
-                "attention_decode: heads / kv_heads must be 1, 2, 4 or 8");
-  OMNIA_REQUIRE(kv_heads <= 65535, "attention_decode: too many kv heads");
-  OMNIA_REQUIRE(rotary_pairs == 8 || rotary_pairs == 16 || rotary_pairs == 32 || rotary_pairs == 64,
-                "attention_decode: rotary_pairs must be 8, 16, 32 or 64");
-  OMNIA_REQUIRE(capacity > 0 && capacity < (int64_t{1} << 30), "attention_decode: bad capacity");
-  OMNIA_REQUIRE(window == 0 || window == capacity,
-                "attention_decode: a ring's window must be its capacity (0: fixed cache)");
-  OMNIA_REQUIRE(max_rows > 0 && max_rows <= capacity, "attention_decode: max_rows must be in [1, capacity]");
-  OMNIA_REQUIRE(angle_rows > 0 && angle_rows < (int64_t{1} << 30), "attention_decode: bad angle_rows");
-  OMNIA_REQUIRE(raw_queries && raw_keys && raw_values && query_weight && key_weight && angles &&
-                key_cache && value_cache && position && out, "attention_decode: null pointer");
-  OMNIA_REQUIRE(aligned16(raw_queries) && aligned16(raw_keys) && aligned16(raw_values) &&
-                aligned16(query_weight) && aligned16(key_weight) && aligned16(key_cache) &&
-                aligned16(value_cache) && aligned16(out) && aligned16(angles),
-                "attention_decode: bf16 rows and the angle table must be 16-byte aligned");
   const int chunk = chunk_rows(static_cast<int>(max_rows), static_cast<int>(kv_heads));
   const int splits = static_cast<int>((max_rows + chunk - 1) / chunk);
   if (splits > 1) {
@@ -660,4 +648,139 @@ extern "C" int32_t omnia_attention_decode(
     default: launch<8>(a, stream); break;
   }
   return launched("attention_decode");
+}
+
+// The geometry checks both entry points share; 0 when the step can be served.
+int32_t check_geometry(const uint16_t* raw_queries, const uint16_t* raw_keys,
+                       const uint16_t* raw_values, const uint16_t* query_weight,
+                       const uint16_t* key_weight, const float* angles, int64_t angle_rows,
+                       int64_t rotary_pairs, const uint16_t* key_cache,
+                       const uint16_t* value_cache, int64_t capacity, int64_t window,
+                       const int32_t* position, int64_t max_rows, int64_t heads,
+                       int64_t kv_heads, int64_t head_dim, const uint16_t* out) {
+  OMNIA_REQUIRE(head_dim == kD, "attention_decode: head_dim must be 128");
+  OMNIA_REQUIRE(kv_heads > 0 && heads > 0 && heads % kv_heads == 0,
+                "attention_decode: heads must be a positive multiple of kv_heads");
+  const int64_t gqa = heads / kv_heads;
+  OMNIA_REQUIRE(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8,
+                "attention_decode: heads / kv_heads must be 1, 2, 4 or 8");
+  OMNIA_REQUIRE(kv_heads <= 65535, "attention_decode: too many kv heads");
+  OMNIA_REQUIRE(rotary_pairs == 8 || rotary_pairs == 16 || rotary_pairs == 32 || rotary_pairs == 64,
+                "attention_decode: rotary_pairs must be 8, 16, 32 or 64");
+  OMNIA_REQUIRE(capacity > 0 && capacity < (int64_t{1} << 30), "attention_decode: bad capacity");
+  OMNIA_REQUIRE(window == 0 || window == capacity,
+                "attention_decode: a ring's window must be its capacity (0: fixed cache)");
+  OMNIA_REQUIRE(max_rows > 0 && max_rows <= capacity, "attention_decode: max_rows must be in [1, capacity]");
+  OMNIA_REQUIRE(angle_rows > 0 && angle_rows < (int64_t{1} << 30), "attention_decode: bad angle_rows");
+  OMNIA_REQUIRE(raw_queries && raw_keys && raw_values && query_weight && key_weight && angles &&
+                key_cache && value_cache && position && out, "attention_decode: null pointer");
+  OMNIA_REQUIRE(aligned16(raw_queries) && aligned16(raw_keys) && aligned16(raw_values) &&
+                aligned16(query_weight) && aligned16(key_weight) && aligned16(key_cache) &&
+                aligned16(value_cache) && aligned16(out) && aligned16(angles),
+                "attention_decode: bf16 rows and the angle table must be 16-byte aligned");
+  return 0;
+}
+
+}  // namespace
+}  // namespace omnia
+
+extern "C" int32_t omnia_attention_decode(
+    const uint16_t* raw_queries, const uint16_t* raw_keys, const uint16_t* raw_values,
+    const uint16_t* query_weight, const uint16_t* key_weight, const float* angles,
+    int64_t angle_rows, int64_t rotary_pairs, float mscale, uint16_t* key_cache,
+    uint16_t* value_cache, int64_t capacity, int64_t window, const int32_t* position,
+    int64_t max_rows, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale, float eps,
+    void* workspace, int64_t workspace_bytes, uint16_t* out, hipStream_t stream) {
+  using namespace omnia;
+  int32_t rc = check_geometry(raw_queries, raw_keys, raw_values, query_weight, key_weight, angles,
+                              angle_rows, rotary_pairs, key_cache, value_cache, capacity, window,
+                              position, max_rows, heads, kv_heads, head_dim, out);
+  if (rc != 0) return rc;
+  return attention_decode_checked(raw_queries, raw_keys, raw_values, query_weight, key_weight,
+                                  angles, angle_rows, rotary_pairs, mscale, key_cache, value_cache,
+                                  capacity, window, position, max_rows, heads, kv_heads, head_dim,
+                                  scale, eps, workspace, workspace_bytes, out, stream);
+}
+
+// ---- the same step with the per-chunk states in a static device array ------------
+//
+// For callers that cannot allocate device memory (code under graph capture, serving
+// loops that forbid hipMalloc). The states live in `scratch`, one array per GPU that
+// the library runs on, held until the process ends. Its device address comes from
+// hipGetSymbolAddress once per device, at the entry point's first call on that device;
+// the host-side name `scratch` is never passed to a kernel. Every call on one GPU
+// shares that GPU's array: calls that overlap on one GPU (different streams, or
+// different host threads without ordering) race. Nothing in it has to start at zero:
+// each chunk that the combine kernel reads is written by the split kernel first.
+
+constexpr int64_t kAttentionScratchBytes = OMNIA_ATTENTION_SCRATCH_BYTES;
+
+static __device__ __align__(256) float scratch[kAttentionScratchBytes / sizeof(float)];
+
+namespace omnia {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex scratch_lock;
+void* scratch_address[kMaxScratchDevices] = {};
+
+// The current device's copy of `scratch`, looked up on the first call there.
+int32_t device_scratch(void** address) {
+  int device = 0;
+  hipError_t status = hipGetDevice(&device);
+  if (status != hipSuccess) {
+    return fail(-ENODEV, std::string("hipGetDevice: ") + hipGetErrorString(status));
+  }
+  if (device < 0 || device >= kMaxScratchDevices) {
+    return fail(-ENODEV, "attention_decode_noalloc: device ordinal out of range");
+  }
+  std::lock_guard<std::mutex> hold(scratch_lock);
+  if (scratch_address[device] == nullptr) {
+    void* found = nullptr;
+    status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+    if (status != hipSuccess || found == nullptr) {
+      return fail(-1, std::string("attention_decode_noalloc: hipGetSymbolAddress(scratch): ") +
+                          hipGetErrorString(status));
+    }
+    scratch_address[device] = found;
+  }
+  *address = scratch_address[device];
+  return 0;
+}
+
+}  // namespace
+}  // namespace omnia
+
+extern "C" int32_t omnia_attention_decode_noalloc(
+    const uint16_t* raw_queries, const uint16_t* raw_keys, const uint16_t* raw_values,
+    const uint16_t* query_weight, const uint16_t* key_weight, const float* angles,
+    int64_t angle_rows, int64_t rotary_pairs, float mscale, uint16_t* key_cache,
+    uint16_t* value_cache, int64_t capacity, int64_t window, const int32_t* position,
+    int64_t max_rows, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale, float eps,
+    uint16_t* out, hipStream_t stream) {
+  using namespace omnia;
+  int32_t rc = check_geometry(raw_queries, raw_keys, raw_values, query_weight, key_weight, angles,
+                              angle_rows, rotary_pairs, key_cache, value_cache, capacity, window,
+                              position, max_rows, heads, kv_heads, head_dim, out);
+  if (rc != 0) return rc;
+  const int chunk = chunk_rows(static_cast<int>(max_rows), static_cast<int>(kv_heads));
+  const int64_t splits = (max_rows + chunk - 1) / chunk;
+  const int64_t need = splits > 1 ? kv_heads * splits * (heads / kv_heads) * kPartial *
+                                        static_cast<int64_t>(sizeof(float))
+                                  : 0;
+  if (need > kAttentionScratchBytes) {
+    return fail(-EINVAL, "attention_decode_noalloc: this step needs " + std::to_string(need) +
+                             " bytes of chunk states, above the static scratch of " +
+                             std::to_string(kAttentionScratchBytes) +
+                             " bytes; use omnia_attention_decode with a workspace");
+  }
+  rc = check_device();
+  if (rc != 0) return rc;
+  void* address = nullptr;
+  rc = device_scratch(&address);
+  if (rc != 0) return rc;
+  return attention_decode_checked(raw_queries, raw_keys, raw_values, query_weight, key_weight,
+                                  angles, angle_rows, rotary_pairs, mscale, key_cache, value_cache,
+                                  capacity, window, position, max_rows, heads, kv_heads, head_dim,
+                                  scale, eps, address, kAttentionScratchBytes, out, stream);
 }

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libomnia_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -68,6 +68,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "omnia_attention_decode": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _P, _P, _I64,
                                       _I64, _P, _I64, _I64, _I64, _I64, _F32, _F32, _P, _I64,
                                       _P, _P]),
+    "omnia_attention_decode_noalloc": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _P, _P,
+                                              _I64, _I64, _P, _I64, _I64, _I64, _I64, _F32, _F32,
+                                              _P, _P]),
     "omnia_embed_atlas": (
         _I32,
         [_P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P],

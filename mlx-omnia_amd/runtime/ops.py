@@ -603,6 +603,34 @@ def attention_workspace_bytes(heads: int, kv_heads: int, head_dim: int, capacity
     return nbytes
 
 
+ATTENTION_SCRATCH_BYTES = 4 * 1024 * 1024  # OMNIA_ATTENTION_SCRATCH_BYTES
+
+
+def _attention_checks(raw_queries, raw_keys, raw_values, query_weight, key_weight, atlas,
+                      key_cache, value_cache, position, heads, kv_heads, extra=()):
+    head_dim = 128
+    for t, name, count in ((raw_queries, "raw_queries", heads * head_dim),
+                           (raw_keys, "raw_keys", kv_heads * head_dim),
+                           (raw_values, "raw_values", kv_heads * head_dim)):
+        _dense(t, BF16, name)
+        _require(t.numel() == count, f"attention_decode: {name} must hold {count} values")
+    _dense(query_weight, BF16, "query_weight")
+    _dense(key_weight, BF16, "key_weight")
+    _require(query_weight.numel() == head_dim and key_weight.numel() == head_dim,
+             "attention_decode: norm weights must be [128]")
+    _dense(atlas, F32, "atlas")
+    _require(atlas.dim() == 2 and atlas.shape[1] % 2 == 0, "attention_decode: atlas must be [rows, 2P]")
+    _dense(key_cache, BF16, "key_cache")
+    _dense(value_cache, BF16, "value_cache")
+    _require(key_cache.shape == value_cache.shape and key_cache.shape[-1] == head_dim
+             and key_cache.shape[-3] == kv_heads and key_cache.numel() == kv_heads * key_cache.shape[-2] * head_dim,
+             "attention_decode: caches must be [(1,) kv_heads, capacity, 128]")
+    _require(position.dtype == torch.int32 and position.numel() == 1, "attention_decode: position int32 [1]")
+    _require(on_rocm(raw_queries, raw_keys, raw_values, query_weight, key_weight, atlas, key_cache,
+                     value_cache, position, *extra),
+             "attention_decode: tensors must share one ROCm device")
+
+
 def attention_decode(
     raw_queries: torch.Tensor,
     raw_keys: torch.Tensor,
@@ -631,30 +659,13 @@ def attention_decode(
     key_cache / value_cache [(1,) kv_heads, capacity, 128] bf16 (written in place),
     position: device int32 [1] (read, not advanced) -> [heads, 128] bf16."""
     head_dim = 128
-    for t, name, count in ((raw_queries, "raw_queries", heads * head_dim),
-                           (raw_keys, "raw_keys", kv_heads * head_dim),
-                           (raw_values, "raw_values", kv_heads * head_dim)):
-        _dense(t, BF16, name)
-        _require(t.numel() == count, f"attention_decode: {name} must hold {count} values")
-    _dense(query_weight, BF16, "query_weight")
-    _dense(key_weight, BF16, "key_weight")
-    _require(query_weight.numel() == head_dim and key_weight.numel() == head_dim,
-             "attention_decode: norm weights must be [128]")
-    _dense(atlas, F32, "atlas")
-    _require(atlas.dim() == 2 and atlas.shape[1] % 2 == 0, "attention_decode: atlas must be [rows, 2P]")
-    _dense(key_cache, BF16, "key_cache")
-    _dense(value_cache, BF16, "value_cache")
-    _require(key_cache.shape == value_cache.shape and key_cache.shape[-1] == head_dim
-             and key_cache.shape[-3] == kv_heads and key_cache.numel() == kv_heads * key_cache.shape[-2] * head_dim,
-             "attention_decode: caches must be [(1,) kv_heads, capacity, 128]")
-    _require(position.dtype == torch.int32 and position.numel() == 1, "attention_decode: position int32 [1]")
-    capacity = key_cache.shape[-2]
-    tensors = [raw_queries, raw_keys, raw_values, query_weight, key_weight, atlas, key_cache,
-               value_cache, position]
+    extra = ()
     if workspace is not None:
         _require(workspace.is_contiguous(), "attention_decode: workspace must be contiguous")
-        tensors.append(workspace)
-    _require(on_rocm(*tensors), "attention_decode: tensors must share one ROCm device")
+        extra = (workspace,)
+    _attention_checks(raw_queries, raw_keys, raw_values, query_weight, key_weight, atlas,
+                      key_cache, value_cache, position, heads, kv_heads, extra)
+    capacity = key_cache.shape[-2]
     out = _out(out, raw_queries, (heads, head_dim), BF16, "out")
     call("omnia_attention_decode", raw_queries.data_ptr(), raw_keys.data_ptr(),
          raw_values.data_ptr(), query_weight.data_ptr(), key_weight.data_ptr(), atlas.data_ptr(),
@@ -664,6 +675,43 @@ def attention_decode(
          workspace.data_ptr() if workspace is not None else None,
          workspace.numel() * workspace.element_size() if workspace is not None else 0,
          out.data_ptr(), _stream(raw_queries))
+    return out
+
+
+def attention_decode_noalloc(
+    raw_queries: torch.Tensor,
+    raw_keys: torch.Tensor,
+    raw_values: torch.Tensor,
+    query_weight: torch.Tensor,
+    key_weight: torch.Tensor,
+    atlas: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    position: torch.Tensor,
+    *,
+    heads: int,
+    kv_heads: int,
+    max_rows: int,
+    scale: float,
+    eps: float,
+    mscale: float = 1.0,
+    window: int = 0,
+    out: torch.Tensor,
+) -> torch.Tensor:
+    """`attention_decode` with the chunk states in the library's static device array
+    (`omnia_attention_decode_noalloc`): the caller brings every buffer, `out` included, so
+    the call allocates nothing. Calls that overlap on one GPU race on that array."""
+    head_dim = 128
+    _attention_checks(raw_queries, raw_keys, raw_values, query_weight, key_weight, atlas,
+                      key_cache, value_cache, position, heads, kv_heads, (out,))
+    _dense(out, BF16, "out")
+    _require(out.numel() == heads * head_dim, "attention_decode_noalloc: out must hold heads * 128 values")
+    capacity = key_cache.shape[-2]
+    call("omnia_attention_decode_noalloc", raw_queries.data_ptr(), raw_keys.data_ptr(),
+         raw_values.data_ptr(), query_weight.data_ptr(), key_weight.data_ptr(), atlas.data_ptr(),
+         atlas.shape[0], atlas.shape[1] // 2, mscale, key_cache.data_ptr(),
+         value_cache.data_ptr(), capacity, window, position.data_ptr(), max_rows, heads,
+         kv_heads, head_dim, scale, eps, out.data_ptr(), _stream(raw_queries))
     return out
 
 
