@@ -248,7 +248,7 @@ def workloads() -> list[Workload]:
 
     out.append(Workload(
         name="residual_rms_router",
-        kernel="residual_rms_router_kernel",
+        kernel="residual_rms_router_split_kernel",
         description="x, residual bf16 [4096, 2048] ~N(0,1), norm weight 1+N(0,0.1), router "
                     "[128, 2048] ~N(0,0.02) (packed once) -> summed, normed, top-8 indices + "
                     "fp32 weights",

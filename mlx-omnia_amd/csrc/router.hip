@@ -98,20 +98,31 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __uint_as_float(a) + __uint_as_float(b);
 }
 
-// Extracts the top k of the wave's keys (V per lane; a taken key becomes 0, below
-// every real key). Lane j < k ends with the j-th winner; returns the k-th (uniform).
+// Extracts the top k of the wave's keys (V per lane; keys are distinct, 0 is below every
+// real key). Each lane first sorts its keys (descending); a round then takes the wave
+// maximum of the lanes' first keys, and the lane holding it shifts its keys up. Lane
+// j < k ends with the j-th winner; returns the k-th (uniform). `keys` is consumed.
 template <int V>
 __device__ __forceinline__ uint32_t select_topk(uint32_t (&keys)[V], int k, int lane,
                                                 uint32_t& chosen) {
+#pragma unroll
+  for (int i = 0; i < V; ++i) {  // insertion sort of V <= 4 keys
+#pragma unroll
+    for (int j = V - 1; j > i; --j) {
+      const uint32_t hi = umax(keys[j - 1], keys[j]);
+      const uint32_t lo = keys[j - 1] ^ keys[j] ^ hi;
+      keys[j - 1] = hi;
+      keys[j] = lo;
+    }
+  }
   chosen = 0;
   uint32_t best = 0;
   for (int j = 0; j < k; ++j) {
-    uint32_t local = 0;
+    best = wave_max(keys[0]);
+    const bool take = keys[0] == best;
 #pragma unroll
-    for (int v = 0; v < V; ++v) local = umax(local, keys[v]);
-    best = wave_max(local);
-#pragma unroll
-    for (int v = 0; v < V; ++v) keys[v] = keys[v] == best ? 0u : keys[v];
+    for (int v = 0; v + 1 < V; ++v) keys[v] = take ? keys[v + 1] : keys[v];
+    keys[V - 1] = take ? 0u : keys[V - 1];
     chosen = lane == j ? best : chosen;
   }
   return best;
@@ -567,6 +578,352 @@ int32_t launch_fused(const RouterArgs& a, hipStream_t stream) {
   return launched("residual_rms_router");
 }
 
+// ---- H = 2048: the same arithmetic with the phases overlapped by wave roles --------
+//
+// Every CU holds one 16-token workgroup at the config (4096 tokens, 256 CUs), so the
+// phases cannot overlap across workgroups; here they overlap inside one. Waves
+// [0, kRowWaves) are row waves: phase 1 for two token rows each, whose summed and
+// normalized rows they store as soon as they are formed. Waves [kRowWaves, 16) are
+// walkers: at launch they load the first kRing blocks of their share of W (from L2)
+// into registers, while the rows stream from HBM, then run the MFMA walk while the row
+// waves' stores drain. A store counts in the issuing wave's vmcnt until it completes,
+// so only walkers, which store nothing before the end, load anything after phase 1:
+// the walk and the exact recomputations.
+// A workgroup barrier ordering LDS traffic only. __syncthreads() also drains each
+// wave's outstanding global loads and stores (its fence waits for vmcnt(0)), which would
+// make every wave wait for the row waves' stores; nothing here reads global memory
+// another wave of the workgroup wrote.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int E>
+struct SplitShape {
+  static constexpr int VPL = 4;
+  static constexpr int H = 512 * VPL;
+  static constexpr int kRowWaves = 8;                        // two rows each in phase 1
+  static constexpr int kWalkers = kWaves - kRowWaves;
+  static constexpr int kTiles = E / 16;                      // 16-expert MFMA tiles
+  static constexpr int kSlices = 2;                          // halves of H
+  static constexpr int kSlice = H / kSlices;
+  static constexpr int kSteps = kSlice / 32;                 // MFMA steps per (tile, slice)
+  static constexpr int kTilesPerWalker = kTiles * kSlices / kWalkers;
+  static constexpr int kBlocks = kTilesPerWalker * kSteps;   // B blocks one walker streams
+  static constexpr int kRing = E <= 128 ? 18 : 8;           // blocks in flight per walker
+  static constexpr int kRowPitch = H + 8;
+  // LDS: the normalized tile, one fp32 logit tile per slice [16][E] (the first reused
+  // for the recomputed bits), the row norms, the task count (padded to 16 bytes) and
+  // the task list [16 * E] of uint16.
+  static constexpr size_t kTileBytes = static_cast<size_t>(kTileTokens) * kRowPitch * 2;
+  static constexpr size_t kLogitBytes = static_cast<size_t>(kTileTokens) * E * 4;
+  static constexpr size_t kLds = kTileBytes + kSlices * kLogitBytes + kTileTokens * 4 + 16 +
+                                 static_cast<size_t>(kTileTokens) * E * 2;
+  // Each 32-wide step is two v_mfma_f32_16x16x16_bf16 with a zero accumulator (the low
+  // and high 8 bytes of each lane's operands: any split of k works, A and B split
+  // alike), each summing 16 exact products with at most 15 roundings, counted at a full
+  // ulp (30 half-ulps). With two tiles per walker the 2 kSteps half-step results of a
+  // (tile, slice) are summed in groups of kGroup, each in order (kGroup - 1 roundings:
+  // the first is a copy), and the group sums in a tree of depth 3 (at four tiles per
+  // walker the tree's registers would spill, and the half-steps are summed in order:
+  // 2 kSteps - 1 roundings); then the two slices. Each fp32 add on an element's path
+  // carries one half-ulp rounding of a partial sum bounded by A; 1% covers the rounding
+  // of A, delta and L +- delta.
+  static constexpr int kGroup = 8;
+  static constexpr bool kTree = kTilesPerWalker <= 2;
+  static constexpr int kChain = kTree ? (kGroup - 1) + 3 : 2 * kSteps - 1;
+  static constexpr float kDelta = (30.0f + kChain + (kSlices - 1)) * 1.01f / 16777216.0f;
+  static_assert(2 * kSteps == 8 * kGroup, "eight groups of half-steps per (tile, slice)");
+  static_assert(kTiles * kSlices % kWalkers == 0 && kWalkers % kSlices == 0, "shape");
+  static_assert(kTileTokens == 2 * kRowWaves, "two rows per row wave");
+};
+
+// Phase 1 of one token row, for a row wave: residual add + RMSNorm (the arithmetic of
+// add_rms_norm.hip), the outputs stored, the bf16 normalized row and an upper bound of
+// its norm kept. The sum of squares is fp64 (four independent chains; the squares of
+// bf16 values are exact, and the fp64 sum rounds to the fp32 of the exact sum, which
+// is what the arithmetic defines). The norm of the normalized row only bounds the
+// logits' error, so it is summed in fp32 from the products w * bf16(s * inv) before
+// their bf16 rounding and inflated: a rounding to bf16 moves a value by at most 2^-9 of
+// itself, and the 8 FMAs of a chain, the 2 adds joining the chains and the 6 of the wave
+// sum round at most 16 times, so the sum times (1 + 2^-7) bounds the squared norm.
+template <int VPL>
+__device__ __forceinline__ void router_row(const u32x4 (&xv)[VPL], const u32x4 (&bv)[VPL],
+                                           const u32x4 (&wv)[VPL], bool live, int64_t t,
+                                           float eps, int lane, const RouterArgs& a,
+                                           uint16_t* tile_row, float* norm_slot) {
+  constexpr int H = 512 * VPL;
+  u32x4 sv[VPL];  // s = bf16(x + b), packed as stored
+  double part[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    float xf[8], bf[8];
+    unpack8(xv[i], xf);
+    unpack8(bv[i], bf);
+    uint32_t words[4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      words[j / 2] = pack_bf16(xf[j] + bf[j], xf[j + 1] + bf[j + 1]);
+      const double lo = bf16_lo(words[j / 2]), hi = bf16_hi(words[j / 2]);
+      part[j / 2] = __builtin_fma(lo, lo, part[j / 2]);
+      part[j / 2] = __builtin_fma(hi, hi, part[j / 2]);
+    }
+    sv[i] = u32x4{words[0], words[1], words[2], words[3]};
+  }
+  const double sumsq = wave_sum_f64((part[0] + part[1]) + (part[2] + part[3]));
+  const float inv = 1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(H) + eps);
+  float nparts[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    float s[8], w[8], n[8];
+    unpack8(sv[i], s);
+    unpack8(wv[i], w);
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      float lo = s[j] * inv, hi = s[j + 1] * inv;
+      round_pair(lo, hi);
+      n[j] = w[j] * lo;
+      n[j + 1] = w[j + 1] * hi;
+      nparts[j / 2] = __builtin_fmaf(n[j], n[j], nparts[j / 2]);
+      nparts[j / 2] = __builtin_fmaf(n[j + 1], n[j + 1], nparts[j / 2]);
+    }
+    const u32x4 packed = pack8(n);
+    const int v = lane + i * kWave;
+    *reinterpret_cast<u32x4*>(tile_row + v * 8) = live ? packed : u32x4{0u, 0u, 0u, 0u};
+    if (live) {
+      store_nt(a.summed + t * (H / 8) + v, sv[i]);
+      store_nt(a.normalized + t * (H / 8) + v, packed);
+    }
+  }
+  const float nsq = wave_sum((nparts[0] + nparts[1]) + (nparts[2] + nparts[3]));
+  if (lane == 0) *norm_slot = live ? norm_upper(static_cast<double>(nsq) * (1.0 + 0x1p-7)) : 0.0f;
+}
+
+template <int E>
+__global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(RouterArgs a) {
+  using S = SplitShape<E>;
+  constexpr int VPL = S::VPL, H = S::H, kRowPitch = S::kRowPitch;
+  constexpr int kTPW = S::kTilesPerWalker, kSteps = S::kSteps, kBlocks = S::kBlocks;
+  constexpr int kRing = S::kRing;
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* tile = reinterpret_cast<uint16_t*>(smem);
+  float* logit_tile = reinterpret_cast<float*>(smem + S::kTileBytes);            // slice 0
+  float* logit_tile1 = reinterpret_cast<float*>(smem + S::kTileBytes + S::kLogitBytes);
+  float* row_norm = reinterpret_cast<float*>(smem + S::kTileBytes + S::kSlices * S::kLogitBytes);
+  int* task_count = reinterpret_cast<int*>(row_norm + kTileTokens);
+  uint16_t* tasks = reinterpret_cast<uint16_t*>(task_count + 4);
+  if (threadIdx.x == 0) *task_count = 0;  // ordered before phase 3 by the barriers below
+
+  // The wave index through readfirstlane: the compiler then knows the role branches are
+  // uniform and keeps the walkers' ring and the row waves' rows in the same registers.
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+  const int lane = threadIdx.x % kWave;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kTileTokens;
+  const bool walker = wave >= S::kRowWaves;
+
+  // Walker geometry: slice of H, first tile, and the block stream (step-major, the
+  // walker's tiles inside a step). Each workgroup starts its steps at a different
+  // offset, so the workgroups of an XCD do not read the same W lines at once (the order
+  // of the step adds changes per workgroup; the error bound does not).
+  const int wk = wave - S::kRowWaves;
+  const int slice = wk / (S::kWalkers / S::kSlices);
+  const int tile0 = (wk % (S::kWalkers / S::kSlices)) * kTPW;
+  const int start = static_cast<int>(blockIdx.x % kSteps);
+  const uint16_t* wbase =
+      a.packed + (static_cast<int64_t>(tile0) * (H / 32) + slice * kSteps) * 512 + lane * 8;
+  auto block_at = [&](int i) {
+    const int step = (start + i / kTPW) % kSteps;
+    return wbase + (static_cast<int64_t>(i % kTPW) * (H / 32) + step) * 512;
+  };
+
+  u32x4 ring[kRing];
+  if (walker) {
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) ring[i] = *reinterpret_cast<const u32x4*>(block_at(i));
+  } else {
+    // Phase 1: rows 2 * wave and 2 * wave + 1.
+    const int r0 = 2 * wave;
+    const int64_t t0 = first + r0, t1 = t0 + 1;
+    const bool live0 = t0 < a.rows, live1 = t1 < a.rows;
+    u32x4 x0[VPL], b0[VPL], x1[VPL], b1[VPL], wv[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int v = lane + i * kWave;
+      x0[i] = live0 ? load_nt(a.x + t0 * (H / 8) + v) : u32x4{0u, 0u, 0u, 0u};
+      b0[i] = live0 ? load_nt(a.branch + t0 * (H / 8) + v) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int v = lane + i * kWave;
+      x1[i] = live1 ? load_nt(a.x + t1 * (H / 8) + v) : u32x4{0u, 0u, 0u, 0u};
+      b1[i] = live1 ? load_nt(a.branch + t1 * (H / 8) + v) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) wv[i] = a.norm_weight[lane + i * kWave];  // L2-resident
+    router_row<VPL>(x0, b0, wv, live0, t0, a.eps, lane, a, tile + r0 * kRowPitch, row_norm + r0);
+    router_row<VPL>(x1, b1, wv, live1, t1, a.eps, lane, a, tile + (r0 + 1) * kRowPitch,
+                    row_norm + r0 + 1);
+  }
+  lds_barrier();
+
+  // Phase 2 (walkers): logits = tile x W^T over the walker's slice for its tiles. Lane l
+  // feeds row (token) l % 16 of A and column (expert) l % 16 of B, both over
+  // k = (l / 16) * 8 .. + 8 of each 32-wide step.
+  if (walker) {
+    const f32x4 zero = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[kTPW], l1[kTPW], l2[kTPW], l3[kTPW];  // group sum, tree levels
+    const uint16_t* arow = tile + (lane % 16) * kRowPitch + slice * S::kSlice + (lane / 16) * 8;
+    u32x4 av;
+    // Adds one half-step result at position h of this walker's order into tile tt's sum.
+    auto add_half = [&](int tt, int h, const f32x4& part) {
+      if (h % (S::kTree ? S::kGroup : 2 * kSteps) == 0) {
+        acc[tt] = part;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[tt][j] = acc[tt][j] + part[j];
+      }
+      if (S::kTree && h % S::kGroup == S::kGroup - 1) {  // group g done: binary-counter fold
+        const int g = h / S::kGroup;
+        if (g % 2 == 0) {
+          l1[tt] = acc[tt];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) l1[tt][j] = l1[tt][j] + acc[tt][j];
+          if (g % 4 == 1) {
+            l2[tt] = l1[tt];
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) l2[tt][j] = l2[tt][j] + l1[tt][j];
+            if (g == 3) {
+              l3[tt] = l2[tt];
+            } else {  // g == 7: the tile's total
+#pragma unroll
+              for (int j = 0; j < 4; ++j) acc[tt][j] = l3[tt][j] + l2[tt][j];
+            }
+          }
+        }
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < kBlocks; ++i) {
+      const int tt = i % kTPW;
+      const int n = i / kTPW;  // position of the step in this walker's order
+      if (tt == 0) {
+        const int step = (start + n) % kSteps;
+        av = *reinterpret_cast<const u32x4*>(arow + step * 32);
+      }
+      const u32x4 b = ring[i % kRing];
+      if (i + kRing < kBlocks) ring[i % kRing] = *reinterpret_cast<const u32x4*>(block_at(i + kRing));
+      // Halves taken from a cast of the whole vector: this hipcc compiles a bit cast of
+      // an ext-vector swizzle (av.zw) as one of its first elements.
+      const s16x8 a8 = __builtin_bit_cast(s16x8, av), b8 = __builtin_bit_cast(s16x8, b);
+      const f32x4 lo = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a8.s0123, b8.s0123, zero, 0, 0, 0);
+      const f32x4 hi = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a8.s4567, b8.s4567, zero, 0, 0, 0);
+      add_half(tt, 2 * n, lo);
+      add_half(tt, 2 * n + 1, hi);
+    }
+    // D layout: lane l holds column (expert) l % 16, rows (tokens) (l / 16) * 4 + i.
+    float* out = slice == 0 ? logit_tile : logit_tile1;
+#pragma unroll
+    for (int tt = 0; tt < kTPW; ++tt) {
+      const int e = (tile0 + tt) * 16 + lane % 16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[((lane / 16) * 4 + i) * E + e] = acc[tt][i];
+    }
+  }
+  lds_barrier();
+
+  // Phase 3: as in residual_rms_router_kernel, one token per wave; the recomputations
+  // go to the walkers only.
+  constexpr int V = E / kWave;
+  const int r = wave;
+  const int64_t t = first + r;
+  const bool active = t < a.rows;  // wave-uniform; inactive waves still meet the barriers
+  const bool emit = a.logits != nullptr;
+  const float n_norm = row_norm[r];
+  uint32_t bits[V], upper[V], keys[V];
+  bool unsure[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int e = lane + v * kWave;
+    const float logit = logit_tile[r * E + e] + logit_tile1[r * E + e];
+    const float w_norm = a.weight_norms[e];
+    const float delta = S::kDelta * (n_norm * w_norm) + kDeltaFloor * (n_norm + w_norm + 1.0f);
+    const uint32_t lo = f32_to_bf16(logit - delta);
+    const uint32_t hi = f32_to_bf16(logit + delta);
+    bits[v] = lo;
+    unsure[v] = lo != hi;
+    keys[v] = route_key(lo, e);
+    upper[v] = route_key(hi, e);
+  }
+  uint32_t chosen = 0;
+  uint32_t threshold = 0xFFFFFFFFu;
+  if (active) threshold = select_topk<V>(keys, a.k, lane, chosen);
+  bool need[V];
+  bool refined = false;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    need[v] = active && unsure[v] && (emit || upper[v] >= threshold);
+    const uint64_t mask = __ballot(need[v]);
+    if (mask != 0) {  // wave-uniform
+      refined = true;
+      int base = 0;
+      if (lane == 0) base = atomicAdd(task_count, __popcll(mask));
+      base = __builtin_amdgcn_readfirstlane(base);
+      const int below = __builtin_amdgcn_mbcnt_hi(
+          static_cast<uint32_t>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+      if (need[v]) tasks[base + below] = static_cast<uint16_t>(r * E + lane + v * kWave);
+    }
+  }
+  lds_barrier();
+  uint32_t* exact_bits = reinterpret_cast<uint32_t*>(logit_tile);
+  const int count = *task_count;
+  if (walker) {
+    for (int i = 2 * wk; i < count; i += 2 * S::kWalkers) {  // wave-uniform
+      const int task0 = tasks[i];
+      const int task1 = i + 1 < count ? tasks[i + 1] : task0;
+      uint32_t exact0, exact1;
+      exact_logits<VPL>(tile + (task0 / E) * kRowPitch, tile + (task1 / E) * kRowPitch,
+                        a.weight_rows + static_cast<int64_t>(task0 % E) * H,
+                        a.weight_rows + static_cast<int64_t>(task1 % E) * H, lane, exact0, exact1);
+      if (lane == 0) {
+        exact_bits[task0] = exact0;
+        exact_bits[task1] = exact1;
+      }
+    }
+  }
+  lds_barrier();
+  if (!active) return;  // no barrier follows
+  if (refined) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      if (need[v]) bits[v] = exact_bits[r * E + lane + v * kWave];
+      keys[v] = route_key(bits[v], lane + v * kWave);
+    }
+    select_topk<V>(keys, a.k, lane, chosen);
+  }
+  if (emit) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
+  }
+  write_winners(chosen, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
+}
+
+template <int E>
+int32_t launch_split(const RouterArgs& a, hipStream_t stream) {
+  constexpr size_t lds = SplitShape<E>::kLds;
+  const hipError_t status = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&residual_rms_router_split_kernel<E>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  if (status != hipSuccess) {
+    return fail(-1, std::string("residual_rms_router: LDS attribute: ") + hipGetErrorString(status));
+  }
+  const dim3 grid(static_cast<unsigned>((a.rows + kTileTokens - 1) / kTileTokens));
+  residual_rms_router_split_kernel<E><<<grid, kThreads, lds, stream>>>(a);
+  return launched("residual_rms_router");
+}
+
 bool fused_shape(int64_t hidden, int64_t experts) {
   return (hidden == 2048 && (experts == 128 || experts == 256)) ||
          (hidden == 4096 && (experts == 128 || experts == 256));
@@ -658,7 +1015,11 @@ extern "C" int32_t omnia_residual_rms_router(
                reinterpret_cast<u32x4*>(summed), reinterpret_cast<u32x4*>(normalized),
                logits, indices, weights, rows, static_cast<int>(k), eps};
   if (hidden == 2048) {
+#ifdef ROUTER_OLD
     return experts == 128 ? launch_fused<4, 128>(a, stream) : launch_fused<4, 256>(a, stream);
+#else
+    return experts == 128 ? launch_split<128>(a, stream) : launch_split<256>(a, stream);
+#endif
   }
   return experts == 128 ? launch_fused<8, 128>(a, stream) : launch_fused<8, 256>(a, stream);
 }
