@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 10
+#define OMNIA_ABI_VERSION 11
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -182,6 +182,42 @@ int32_t omnia_residual_rms_router(const uint16_t* x, const uint16_t* branch,
                                   float eps, uint16_t* summed, uint16_t* normalized,
                                   uint16_t* logits, int32_t* indices, float* weights,
                                   hipStream_t stream);
+
+/* Sigmoid routing with a correction bias over given router logits, one row per wave:
+ *   score_e = sigmoid(x_e), correctly rounded to fp32 (x_e the fp32 logit, or the bf16
+ *             logit widened)
+ *   key_e   = ordinal(-(score_e + bias_e)), the sum in fp32; ordinal maps fp32 bits to a
+ *             uint32 whose ascending order is the float order (+-0 one value, NaN above all)
+ *   indices = the k smallest keys, the lower expert first on equal keys (NaN last)
+ *   weights_j = score_{i_j} / (sum of the k winners' scores, in fp32, in winner order)
+ * logits [rows, stride] bf16 (logits_fp32 = 0) or fp32 (logits_fp32 = 1); bias [experts]
+ * fp32; keys [rows, experts] uint32 or null; indices [rows, k] int32 and weights [rows, k]
+ * fp32, both or neither (then k is ignored); keys or indices must be given.
+ * Replaces: core/kernels/route/ordinal.py:200-286 (`router_tournament`,
+ * OrdinalRoute.__call__) and `ordinal_keys` at :253-262, which the Core chain restates.
+ * experts <= 1024; k in [1, min(experts, 64)]. */
+int32_t omnia_sigmoid_topk(const void* logits, int64_t stride, int32_t logits_fp32,
+                           const float* bias, int64_t rows, int64_t experts, int64_t k,
+                           uint32_t* keys, int32_t* indices, float* weights,
+                           hipStream_t stream);
+
+/* The fused residual router's sigmoid form: the join, the norm and the exact logits of
+ * omnia_residual_rms_router, then the keys and optional selection of
+ * omnia_sigmoid_topk from those bf16 logits and bias [experts] fp32.
+ *   logits [rows, experts] bf16 or null; keys [rows, experts] uint32 or null;
+ *   indices [rows, k] int32 and weights [rows, k] fp32, both or neither.
+ * Every logit is the correctly rounded bf16 of the exact dot product, so the keys and
+ * the selection equal those computed from the exact logits.
+ * Replaces: core/kernels/route/residual.py:117-299 (`residual_rms_router` with its
+ * `correction_bias`, emitting logits and ordinal keys; its T = 1 only).
+ * hidden 2048 or 4096, experts 128 or 256. */
+int32_t omnia_residual_rms_router_sigmoid(const uint16_t* x, const uint16_t* branch,
+                                          const uint16_t* norm_weight, const void* packed_router,
+                                          const float* bias, int64_t rows, int64_t hidden,
+                                          int64_t experts, int64_t k, float eps,
+                                          uint16_t* summed, uint16_t* normalized,
+                                          uint16_t* logits, uint32_t* keys, int32_t* indices,
+                                          float* weights, hipStream_t stream);
 
 /* Routed expert gate/up projection of one token, dense bf16 weights, "blocked" layout
  * (gate and up block-concatenated on the output axis and left un-activated):

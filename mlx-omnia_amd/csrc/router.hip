@@ -10,10 +10,21 @@
 // logits (l_1 the largest), the same quantity to within fp32 rounding.
 //
 // Keys: each logit becomes a 32-bit key, an order-preserving map of its bf16 bits
-// (sign flip for positives, all bits for negatives, -0 folded onto +0, NaN above
-// everything) in the high half and 0xFFFF - expert in the low half. Unsigned key order
+// (sign flip for positives, all bits for negatives, -0 folded onto +0, NaN below
+// everything, so a NaN logit ranks last as core/kernels/route/ordinal.py:37-47 ranks a
+// NaN score) in the high half and 0xFFFF - expert in the low half. Unsigned key order
 // is then descending logit with the lower index first on ties; k rounds of a wave-wide
 // max extract the winners.
+//
+// Sigmoid routing with a correction bias (core/kernels/route/ordinal.py:200-286,
+// `router_tournament`): score = sigmoid(x) of the float32 logit, correctly rounded (the
+// stable form y = 1 / (1 + exp|x|), x < 0 ? y : 1 - y, in fp64, rounded once); key =
+// ordinal(-(score + bias)) with the sum in fp32 and `ordinal` the map of ordinal.py:
+// 37-47 (ascending unsigned order = ascending float order, +-0 one value, NaN above
+// everything). The k smallest keys win, lower expert first on equal keys; the weights
+// are the winners' unbiased scores over their fp32 sum taken in winner order. The fused
+// router's sigmoid form (core/kernels/route/residual.py:109-115) emits the exact bf16
+// logits and these keys, and optionally the selection.
 //
 // Fused kernel (core/kernels/route/residual.py:117-299 is the one-token precedent;
 // config: x, residual [4096, 2048], router [128, 2048], k = 8): a workgroup of 16
@@ -54,7 +65,7 @@ constexpr int kThreads = kWaves * kWave;
 constexpr int kMaxTopK = 64;
 
 __device__ __forceinline__ uint32_t order16(uint32_t bits) {
-  if ((bits & 0x7FFFu) > 0x7F80u) return 0xFFFFu;  // NaN above everything
+  if ((bits & 0x7FFFu) > 0x7F80u) return 0u;       // NaN below everything (-inf is 0x7F)
   if (bits == 0x8000u) bits = 0u;                  // -0 == +0
   return (bits & 0x8000u) ? (~bits & 0xFFFFu) : (bits | 0x8000u);
 }
@@ -143,6 +154,108 @@ __device__ __forceinline__ void write_winners(uint32_t chosen, int k, int lane,
     indices[lane] = static_cast<int32_t>(0xFFFFu - (chosen & 0xFFFFu));
     weights[lane] = e / total;
   }
+}
+
+// ---- sigmoid scores, ordinal keys and their selection ---------------------------------
+
+// Correctly rounded fp32 sigmoid of an fp32 value.
+__device__ __forceinline__ float sigmoid_rounded(float x) {
+  const double y = 1.0 / (1.0 + exp(fabs(static_cast<double>(x))));
+  return static_cast<float>(x < 0.0f ? y : 1.0 - y);
+}
+
+// ordinal.py:37-47 `router_key_ordinal`.
+__device__ __forceinline__ uint32_t ordinal_of(float key) {
+  const uint32_t bits = __float_as_uint(key);
+  const uint32_t magnitude = bits & 0x7FFFFFFFu;
+  if (magnitude > 0x7F800000u) return 0xFFFFFFFFu;
+  if (magnitude == 0u) return 0x80000000u;
+  return (bits & 0x80000000u) ? ~bits : (bits ^ 0x80000000u);
+}
+
+// The k smallest ordinal keys of one wave's row (V per lane: expert lane + 64 v; lanes
+// past `experts` hold nothing), lower expert first on equal keys; writes the experts and
+// the winners' scores over their fp32 sum in winner order. Each round takes the lanes'
+// best (largest ~key, then largest 0xFFFF - expert) in two wave maxima and reads the
+// winner's score from the lane that holds it.
+template <int V>
+__device__ __forceinline__ void ordinal_topk_write(const uint32_t (&keys)[V], const float (&scores)[V],
+                                                   int experts, int k, int lane,
+                                                   int32_t* indices, float* weights) {
+  uint32_t hi[V], lo[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int e = lane + v * kWave;
+    hi[v] = e < experts ? ~keys[v] : 0u;   // a NaN key (0xFFFFFFFF) still beats a
+    lo[v] = e < experts ? 0xFFFFu - static_cast<uint32_t>(e) : 0u;  // padded slot
+  }
+  float total = 0.0f, mine = 0.0f;
+  int my_expert = 0;
+  for (int j = 0; j < k; ++j) {
+    uint32_t bh = 0u, bl = 0u;
+    float bs = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const bool better = hi[v] > bh || (hi[v] == bh && lo[v] > bl);
+      bh = better ? hi[v] : bh;
+      bl = better ? lo[v] : bl;
+      bs = better ? scores[v] : bs;
+    }
+    const uint32_t top_hi = wave_max(bh);
+    const uint32_t top_lo = wave_max(bh == top_hi ? bl : 0u);
+    const int expert = __builtin_amdgcn_readfirstlane(static_cast<int>(0xFFFFu - top_lo));
+    const int owner = expert % kWave;
+    const float score = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs), owner));
+    total = score + total;
+    if (lane == owner) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if (lane + v * kWave == expert) {
+          hi[v] = 0u;
+          lo[v] = 0u;
+        }
+      }
+    }
+    if (lane == j) {
+      my_expert = expert;
+      mine = score;
+    }
+  }
+  if (lane < k) {
+    indices[lane] = my_expert;
+    weights[lane] = mine / total;
+  }
+}
+
+// ---- sigmoid + bias -> ordinal keys -> top-k over given logits: one wave per row ----
+
+template <int V, bool kF32>
+__global__ __launch_bounds__(256) void sigmoid_topk_kernel(const void* __restrict__ logits,
+                                                           int64_t stride,
+                                                           const float* __restrict__ bias,
+                                                           int64_t rows, int experts, int k,
+                                                           uint32_t* __restrict__ keys_out,
+                                                           int32_t* __restrict__ indices,
+                                                           float* __restrict__ weights) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  if (row >= rows) return;
+  uint32_t keys[V];
+  float scores[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int e = lane + v * kWave;
+    keys[v] = 0xFFFFFFFFu;
+    scores[v] = 0.0f;
+    if (e < experts) {
+      const float x = kF32 ? static_cast<const float*>(logits)[row * stride + e]
+                           : bf16_to_f32(static_cast<const uint16_t*>(logits)[row * stride + e]);
+      scores[v] = sigmoid_rounded(x);
+      keys[v] = ordinal_of(-(scores[v] + bias[e]));
+      if (keys_out) keys_out[row * experts + e] = keys[v];
+    }
+  }
+  if (indices) ordinal_topk_write<V>(keys, scores, experts, k, lane, indices + row * k, weights + row * k);
 }
 
 // ---- softmax -> top-k over given bf16 logits: one wave per row --------------------
@@ -284,8 +397,10 @@ struct RouterArgs {
   u32x4* summed;
   u32x4* normalized;
   uint16_t* logits;               // [T, E] bf16, optional
-  int32_t* indices;               // [T, k]
+  int32_t* indices;               // [T, k]; optional in the sigmoid form
   float* weights;                 // [T, k]
+  const float* bias;              // [E] fp32: the sigmoid form; null: softmax
+  uint32_t* keys;                 // [T, E] ordinal keys (sigmoid form), optional
   int64_t rows;
   int k;
   float eps;
@@ -316,6 +431,22 @@ struct FusedShape {
 // subnormal bf16 inputs or fp32 products would lose at most H * 2^-126 times those.
 constexpr float kDeltaFloor = 0x1p-113f;
 
+// The sigmoid form's tail for one token, from its exact bf16 logits (V per lane):
+// scores, ordinal keys (written when asked) and the selection (when asked).
+template <int V, int E>
+__device__ __forceinline__ void sigmoid_finish(const uint32_t (&bits)[V], const float (&bias)[V],
+                                               const RouterArgs& a, int64_t t, int lane) {
+  uint32_t keys[V];
+  float scores[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    scores[v] = sigmoid_rounded(bf16_to_f32(static_cast<uint16_t>(bits[v])));
+    keys[v] = ordinal_of(-(scores[v] + bias[v]));
+    if (a.keys) a.keys[t * E + lane + v * kWave] = keys[v];
+  }
+  if (a.indices) ordinal_topk_write<V>(keys, scores, E, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
+}
+
 template <int VPL, int E>
 __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArgs a) {
   using S = FusedShape<VPL, E>;
@@ -336,6 +467,9 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   float weight_norm[V];         // loaded now, used in phase 3
 #pragma unroll
   for (int v = 0; v < V; ++v) weight_norm[v] = a.weight_norms[lane + v * kWave];
+  float bias[V];                // the sigmoid form's correction bias, loaded with them
+#pragma unroll
+  for (int v = 0; v < V; ++v) bias[v] = a.bias ? a.bias[lane + v * kWave] : 0.0f;
 
   // The walk of phase 2 over W: wave w owns expert tile w % kTiles over slice w / kTiles
   // of H, in kOuter blocks of kUnroll steps. Each workgroup starts at a different block,
@@ -489,6 +623,8 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   const int64_t t = first + r;
   const bool active = t < a.rows;  // wave-uniform; inactive waves still meet the barriers
   const bool emit = a.logits != nullptr;
+  const bool sigmoid = a.bias != nullptr;
+  const bool exact_all = emit || sigmoid;  // every logit exact: no selection on the bounds
   const float n_norm = row_norm[r];
   uint32_t bits[V], upper[V], keys[V];
   bool unsure[V];
@@ -511,12 +647,12 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   // selection is final.
   uint32_t chosen = 0;
   uint32_t threshold = 0xFFFFFFFFu;
-  if (active) threshold = select_topk<V>(keys, a.k, lane, chosen);
+  if (active && !exact_all) threshold = select_topk<V>(keys, a.k, lane, chosen);
   bool need[V];
   bool refined = false;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
-    need[v] = active && unsure[v] && (emit || upper[v] >= threshold);
+    need[v] = active && unsure[v] && (exact_all || upper[v] >= threshold);
     const uint64_t mask = __ballot(need[v]);
     if (mask != 0) {  // wave-uniform
       refined = true;
@@ -551,13 +687,20 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       if (need[v]) bits[v] = exact_bits[r * E + lane + v * kWave];
-      keys[v] = route_key(bits[v], lane + v * kWave);
     }
-    select_topk<V>(keys, a.k, lane, chosen);
   }
   if (emit) {
 #pragma unroll
     for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
+  }
+  if (sigmoid) {
+    sigmoid_finish<V, E>(bits, bias, a, t, lane);
+    return;
+  }
+  if (refined || exact_all) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) keys[v] = route_key(bits[v], lane + v * kWave);
+    select_topk<V>(keys, a.k, lane, chosen);
   }
   write_winners(chosen, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
 }
@@ -737,6 +880,14 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     return wbase + (static_cast<int64_t>(i % kTPW) * (H / 32) + step) * 512;
   };
 
+  constexpr int V = E / kWave;  // experts per lane in phase 3
+  float weight_norm[V];         // loaded first: a row wave's later loads would wait for its stores
+#pragma unroll
+  for (int v = 0; v < V; ++v) weight_norm[v] = a.weight_norms[lane + v * kWave];
+  float bias[V];                // the sigmoid form's correction bias, loaded with them
+#pragma unroll
+  for (int v = 0; v < V; ++v) bias[v] = a.bias ? a.bias[lane + v * kWave] : 0.0f;
+
   u32x4 ring[kRing];
   if (walker) {
 #pragma unroll
@@ -836,11 +987,12 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
 
   // Phase 3: as in residual_rms_router_kernel, one token per wave; the recomputations
   // go to the walkers only.
-  constexpr int V = E / kWave;
   const int r = wave;
   const int64_t t = first + r;
   const bool active = t < a.rows;  // wave-uniform; inactive waves still meet the barriers
   const bool emit = a.logits != nullptr;
+  const bool sigmoid = a.bias != nullptr;
+  const bool exact_all = emit || sigmoid;  // every logit exact: no selection on the bounds
   const float n_norm = row_norm[r];
   uint32_t bits[V], upper[V], keys[V];
   bool unsure[V];
@@ -848,7 +1000,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   for (int v = 0; v < V; ++v) {
     const int e = lane + v * kWave;
     const float logit = logit_tile[r * E + e] + logit_tile1[r * E + e];
-    const float w_norm = a.weight_norms[e];
+    const float w_norm = weight_norm[v];
     const float delta = S::kDelta * (n_norm * w_norm) + kDeltaFloor * (n_norm + w_norm + 1.0f);
     const uint32_t lo = f32_to_bf16(logit - delta);
     const uint32_t hi = f32_to_bf16(logit + delta);
@@ -859,12 +1011,12 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   }
   uint32_t chosen = 0;
   uint32_t threshold = 0xFFFFFFFFu;
-  if (active) threshold = select_topk<V>(keys, a.k, lane, chosen);
+  if (active && !exact_all) threshold = select_topk<V>(keys, a.k, lane, chosen);
   bool need[V];
   bool refined = false;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
-    need[v] = active && unsure[v] && (emit || upper[v] >= threshold);
+    need[v] = active && unsure[v] && (exact_all || upper[v] >= threshold);
     const uint64_t mask = __ballot(need[v]);
     if (mask != 0) {  // wave-uniform
       refined = true;
@@ -899,13 +1051,20 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       if (need[v]) bits[v] = exact_bits[r * E + lane + v * kWave];
-      keys[v] = route_key(bits[v], lane + v * kWave);
     }
-    select_topk<V>(keys, a.k, lane, chosen);
   }
   if (emit) {
 #pragma unroll
     for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
+  }
+  if (sigmoid) {
+    sigmoid_finish<V, E>(bits, bias, a, t, lane);
+    return;
+  }
+  if (refined || exact_all) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) keys[v] = route_key(bits[v], lane + v * kWave);
+    select_topk<V>(keys, a.k, lane, chosen);
   }
   write_winners(chosen, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
 }
@@ -987,6 +1146,23 @@ extern "C" int32_t omnia_pack_router_weight(const uint16_t* router_weight, int64
   return launched("pack_router_weight");
 }
 
+namespace omnia {
+namespace {
+
+int32_t launch_router(const RouterArgs& a, int64_t hidden, int64_t experts, hipStream_t stream) {
+  if (hidden == 2048) {
+#ifdef ROUTER_OLD
+    return experts == 128 ? launch_fused<4, 128>(a, stream) : launch_fused<4, 256>(a, stream);
+#else
+    return experts == 128 ? launch_split<128>(a, stream) : launch_split<256>(a, stream);
+#endif
+  }
+  return experts == 128 ? launch_fused<8, 128>(a, stream) : launch_fused<8, 256>(a, stream);
+}
+
+}  // namespace
+}  // namespace omnia
+
 extern "C" int32_t omnia_residual_rms_router(
     const uint16_t* x, const uint16_t* branch, const uint16_t* norm_weight,
     const void* packed_router, int64_t rows, int64_t hidden, int64_t experts, int64_t k,
@@ -1013,13 +1189,71 @@ extern "C" int32_t omnia_residual_rms_router(
                reinterpret_cast<const float*>(packed + packed_weight_elements(experts, hidden)),
                packed + packed_rows_offset(experts, hidden),
                reinterpret_cast<u32x4*>(summed), reinterpret_cast<u32x4*>(normalized),
-               logits, indices, weights, rows, static_cast<int>(k), eps};
-  if (hidden == 2048) {
-#ifdef ROUTER_OLD
-    return experts == 128 ? launch_fused<4, 128>(a, stream) : launch_fused<4, 256>(a, stream);
-#else
-    return experts == 128 ? launch_split<128>(a, stream) : launch_split<256>(a, stream);
-#endif
-  }
-  return experts == 128 ? launch_fused<8, 128>(a, stream) : launch_fused<8, 256>(a, stream);
+               logits, indices, weights, nullptr, nullptr, rows, static_cast<int>(k), eps};
+  return launch_router(a, hidden, experts, stream);
+}
+
+extern "C" int32_t omnia_residual_rms_router_sigmoid(
+    const uint16_t* x, const uint16_t* branch, const uint16_t* norm_weight,
+    const void* packed_router, const float* bias, int64_t rows, int64_t hidden, int64_t experts,
+    int64_t k, float eps, uint16_t* summed, uint16_t* normalized, uint16_t* logits,
+    uint32_t* keys, int32_t* indices, float* weights, hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), "residual_rms_router_sigmoid: bad row count");
+  OMNIA_REQUIRE(fused_shape(hidden, experts),
+                "residual_rms_router_sigmoid: hidden must be 2048 or 4096 and experts 128 or 256");
+  OMNIA_REQUIRE((indices == nullptr) == (weights == nullptr),
+                "residual_rms_router_sigmoid: indices and weights come together");
+  OMNIA_REQUIRE(indices == nullptr || (k > 0 && k <= experts && k <= kMaxTopK),
+                "residual_rms_router_sigmoid: k must be in [1, min(experts, 64)]");
+  if (rows == 0) return 0;
+  OMNIA_REQUIRE(x && branch && norm_weight && packed_router && bias && summed && normalized,
+                "residual_rms_router_sigmoid: null pointer");
+  OMNIA_REQUIRE(aligned16(x) && aligned16(branch) && aligned16(norm_weight) &&
+                    aligned16(packed_router) && aligned16(summed) && aligned16(normalized),
+                "residual_rms_router_sigmoid: pointers must be 16-byte aligned");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  const uint16_t* packed = static_cast<const uint16_t*>(packed_router);
+  RouterArgs a{reinterpret_cast<const u32x4*>(x), reinterpret_cast<const u32x4*>(branch),
+               reinterpret_cast<const u32x4*>(norm_weight), packed,
+               reinterpret_cast<const float*>(packed + packed_weight_elements(experts, hidden)),
+               packed + packed_rows_offset(experts, hidden),
+               reinterpret_cast<u32x4*>(summed), reinterpret_cast<u32x4*>(normalized),
+               logits, indices, weights, bias, keys, rows,
+               indices ? static_cast<int>(k) : 0, eps};
+  return launch_router(a, hidden, experts, stream);
+}
+
+extern "C" int32_t omnia_sigmoid_topk(const void* logits, int64_t stride, int32_t logits_fp32,
+                                      const float* bias, int64_t rows, int64_t experts, int64_t k,
+                                      uint32_t* keys, int32_t* indices, float* weights,
+                                      hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), "sigmoid_topk: bad row count");
+  OMNIA_REQUIRE(experts > 0 && experts <= 16 * kWave, "sigmoid_topk: experts must be in [1, 1024]");
+  OMNIA_REQUIRE(stride >= experts, "sigmoid_topk: row stride smaller than experts");
+  OMNIA_REQUIRE(logits_fp32 == 0 || logits_fp32 == 1, "sigmoid_topk: logits_fp32 must be 0 or 1");
+  OMNIA_REQUIRE((indices == nullptr) == (weights == nullptr),
+                "sigmoid_topk: indices and weights come together");
+  OMNIA_REQUIRE(indices == nullptr || (k > 0 && k <= experts && k <= kMaxTopK),
+                "sigmoid_topk: k must be in [1, min(experts, 64)]");
+  if (rows == 0) return 0;
+  OMNIA_REQUIRE(logits && bias && (keys || indices), "sigmoid_topk: null pointer");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  const int kk = indices ? static_cast<int>(k) : 0;
+  const int e = static_cast<int>(experts);
+  const int v = (e + kWave - 1) / kWave;
+#define OMNIA_SIGMOID_TOPK(V)                                                                  \
+  (logits_fp32 ? sigmoid_topk_kernel<V, true><<<grid, 256, 0, stream>>>(logits, stride, bias, rows, e, kk, keys, indices, weights) \
+               : sigmoid_topk_kernel<V, false><<<grid, 256, 0, stream>>>(logits, stride, bias, rows, e, kk, keys, indices, weights))
+  if (v <= 1) OMNIA_SIGMOID_TOPK(1);
+  else if (v <= 2) OMNIA_SIGMOID_TOPK(2);
+  else if (v <= 4) OMNIA_SIGMOID_TOPK(4);
+  else if (v <= 8) OMNIA_SIGMOID_TOPK(8);
+  else OMNIA_SIGMOID_TOPK(16);
+#undef OMNIA_SIGMOID_TOPK
+  return launched("sigmoid_topk");
 }

@@ -2,8 +2,9 @@
 
 Mirrors core/kernels/route/__init__.py:48-100: a block declares its routing and `Route`
 binds the first strategy whose `build` accepts it. `HipSoftmaxTopkRoute` serves plain
-softmax routing (lowest-index ties) on a gfx950 device; `DefaultRoute` (the Core chain)
-serves every declaration.
+softmax routing (lowest-index ties) on a gfx950 device, `HipOrdinalRoute` sigmoid
+routing with a correction bias where the reference's `OrdinalRoute` binds;
+`DefaultRoute` (the Core chain) serves every declaration.
 """
 
 from __future__ import annotations
@@ -11,8 +12,9 @@ from __future__ import annotations
 import torch
 
 from ..resolve import resolve
-from .default import DefaultRoute, top_k
-from .hip import HipSoftmaxTopkRoute, softmax_topk_applies
+from .default import DefaultRoute, ordinal_keys, top_k
+from .hip import (HipOrdinalRoute, HipSoftmaxTopkRoute, ordinal_route_applies,
+                  sigmoid_bias_routing, softmax_topk_applies)
 from .kernel import RouteStrategy, Routing, Scoring, Ties, gate_logits
 from .residual import (
     DefaultResidualRouter,
@@ -24,6 +26,7 @@ from .residual import (
 __all__ = [
     "DefaultResidualRouter",
     "DefaultRoute",
+    "HipOrdinalRoute",
     "HipResidualRouter",
     "HipSoftmaxTopkRoute",
     "ResidualRouter",
@@ -33,12 +36,15 @@ __all__ = [
     "Scoring",
     "Ties",
     "gate_logits",
+    "ordinal_keys",
+    "ordinal_route_applies",
     "residual_router_applies",
+    "sigmoid_bias_routing",
     "softmax_topk_applies",
     "top_k",
 ]
 
-_STRATEGIES = (HipSoftmaxTopkRoute, DefaultRoute)
+_STRATEGIES = (HipSoftmaxTopkRoute, HipOrdinalRoute, DefaultRoute)
 
 
 class Route(RouteStrategy):

@@ -21,6 +21,14 @@ def top_k(scores: torch.Tensor, k: int, ties: str) -> torch.Tensor:
     return experts - 1 - flipped
 
 
+def ordinal_keys(biased: torch.Tensor) -> torch.Tensor:
+    """core/kernels/route/ordinal.py:253-262 in torch ops: the keys whose ascending
+    unsigned order is the descending order of the biased scores (uint32)."""
+    bits = (-biased.float()).view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    negative = (bits & 0x80000000) != 0
+    return torch.where(negative, (~bits) & 0xFFFFFFFF, bits ^ 0x80000000).to(torch.uint32)
+
+
 @dataclass(frozen=True)
 class DefaultRoute(RouteStrategy):
     gate: torch.Tensor | None

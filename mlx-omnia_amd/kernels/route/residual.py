@@ -4,12 +4,15 @@ core/kernels/route/residual.py:117-299 fuses the one-token residual join with th
 gemv (sigmoid scoring, ordinal keys) as machinery beside the routing strategies. Here the
 same fusion is a facade of its own, declared by the norm leaf (`.weight`, `.eps`), the
 router gate [experts, hidden] and a `Routing`, and called as
-`(x, projected) -> (summed, normalized, indices, weights)`. `HipResidualRouter` serves
-softmax routing at hidden 2048 or 4096 and 128 or 256 experts in one dispatch
-(`omnia_residual_rms_router`, csrc/router.hip); it repacks the gate once when it is
-built (`omnia_pack_router_weight`), as the reference's strategies take their weights at
-build. `DefaultResidualRouter` is the Core chain (the residual join, the gate matmul,
-the routing chain).
+`(x, projected) -> (summed, normalized, indices, weights)`, or as `with_keys(x, projected)
+-> (summed, normalized, logits, keys)`, the reference's own return (residual.py:268-299)
+for a sigmoid declaration with a correction bias. `HipResidualRouter` serves softmax
+routing (`omnia_residual_rms_router`) and sigmoid routing with a correction bias
+(`omnia_residual_rms_router_sigmoid`) at hidden 2048 or 4096 and 128 or 256 experts in
+one dispatch (csrc/router.hip); it repacks the gate once when it is built
+(`omnia_pack_router_weight`), as the reference's strategies take their weights at build.
+`DefaultResidualRouter` is the Core chain (the residual join, the gate matmul, the
+routing chain, and the ordinal keys of ordinal.py:253-262 in torch ops).
 """
 
 from __future__ import annotations
@@ -23,7 +26,8 @@ from ...runtime import ops
 from .._device import hip_device
 from ..add_norm import AddRmsNorm
 from ..resolve import resolve
-from .default import DefaultRoute
+from .default import DefaultRoute, ordinal_keys
+from .hip import sigmoid_bias_routing
 from .kernel import Routing
 
 
@@ -51,6 +55,14 @@ class DefaultResidualRouter(ResidualRouterStrategy):
         indices, weights = self.route(normalized, logits=logits)
         return summed, normalized, indices, weights
 
+    def with_keys(self, x, projected):
+        routing = self.route.routing
+        assert routing.scoring == "sigmoid" and routing.bias is not None
+        summed, normalized = self.join(x, projected)
+        logits = normalized @ self.route.gate.T
+        keys = ordinal_keys(torch.sigmoid(logits.float()) + routing.bias)
+        return summed, normalized, logits, keys
+
 
 @dataclass(frozen=True)
 class HipResidualRouter(ResidualRouterStrategy):
@@ -62,7 +74,11 @@ class HipResidualRouter(ResidualRouterStrategy):
     @classmethod
     def build(cls, leaf, gate, *, routing: Routing) -> "HipResidualRouter | None":
         weight = leaf.weight
-        if not routing.plain_softmax() or gate.shape[0] != routing.experts:
+        sigmoid = sigmoid_bias_routing(routing)
+        if not (routing.plain_softmax() or sigmoid) or gate.shape[0] != routing.experts:
+            return None
+        if sigmoid and (routing.bias.dtype != torch.float32 or routing.bias.numel() != routing.experts
+                        or not hip_device(routing.bias)):
             return None
         if not residual_router_applies(weight.numel(), routing.experts, routing.k):
             return None
@@ -74,11 +90,26 @@ class HipResidualRouter(ResidualRouterStrategy):
                    routing)
 
     def __call__(self, x, projected):
+        if self.routing.bias is not None:
+            summed, normalized, _, _, indices, weights = ops.residual_rms_router_sigmoid(
+                x.contiguous(), projected.contiguous(), self.norm_weight, self.gate,
+                self.routing.bias.contiguous(), k=self.routing.k, eps=self.eps,
+                emit_logits=False, emit_keys=False, select=True,
+            )
+            return summed, normalized, indices, weights
         summed, normalized, _, indices, weights = ops.residual_rms_router(
             x.contiguous(), projected.contiguous(), self.norm_weight, self.gate,
             k=self.routing.k, eps=self.eps,
         )
         return summed, normalized, indices, weights
+
+    def with_keys(self, x, projected):
+        assert self.routing.bias is not None, "with_keys: a sigmoid declaration with a bias"
+        summed, normalized, logits, keys, _, _ = ops.residual_rms_router_sigmoid(
+            x.contiguous(), projected.contiguous(), self.norm_weight, self.gate,
+            self.routing.bias.contiguous(), k=self.routing.k, eps=self.eps,
+        )
+        return summed, normalized, logits, keys
 
 
 _STRATEGIES = (HipResidualRouter, DefaultResidualRouter)
@@ -92,3 +123,7 @@ class ResidualRouter(ResidualRouterStrategy):
 
     def __call__(self, x, projected):
         return self.strategy(x, projected)
+
+    def with_keys(self, x, projected):
+        """(summed, normalized, logits, keys) of a sigmoid declaration with a bias."""
+        return self.strategy.with_keys(x, projected)

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libomnia_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -42,6 +42,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "omnia_residual_rms_router": (
         _I32,
         [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _P, _P, _P, _P],
+    ),
+    "omnia_sigmoid_topk": (_I32, [_P, _I64, _I32, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "omnia_residual_rms_router_sigmoid": (
+        _I32,
+        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _P, _P, _P, _P, _P, _P],
     ),
     "omnia_moe_gate_up": (_I32, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "omnia_moe_down_combine": (

@@ -363,6 +363,83 @@ def residual_rms_router(
     return summed, normalized, logits, indices, weights
 
 
+def sigmoid_topk(logits: torch.Tensor, bias: torch.Tensor, k: int, *, emit_keys: bool = False,
+                 select: bool = True, keys: torch.Tensor | None = None,
+                 indices: torch.Tensor | None = None, weights: torch.Tensor | None = None):
+    """Sigmoid routing with a correction bias over [..., E] bf16 or fp32 logits (rows may
+    be strided); see `omnia_sigmoid_topk`. Returns (indices or None, weights or None,
+    keys or None): indices int32 and weights fp32 [..., k], keys uint32 [..., E]."""
+    _require(logits.dtype in (BF16, F32), "sigmoid_topk: logits must be bf16 or fp32")
+    experts = logits.shape[-1]
+    _require(logits.stride(-1) == 1, "sigmoid_topk: logits rows must be contiguous")
+    stride = logits.stride(-2) if logits.dim() > 1 else experts
+    _require(logits.dim() <= 2 or logits.is_contiguous(), "sigmoid_topk: logits must be 2-D or contiguous")
+    _dense(bias, F32, "bias")
+    _require(bias.numel() == experts, "sigmoid_topk: bias must be [experts]")
+    _require(on_rocm(logits, bias), "sigmoid_topk: tensors must share one ROCm device")
+    rows = logits.numel() // experts if logits.is_contiguous() else logits.shape[0]
+    lead = logits.shape[:-1]
+    if emit_keys or keys is not None:
+        keys = _out(keys, logits, (*lead, experts), torch.uint32, "keys")
+    if select:
+        indices = _out(indices, logits, (*lead, k), torch.int32, "indices")
+        weights = _out(weights, logits, (*lead, k), F32, "weights")
+    else:
+        indices = weights = None
+    call("omnia_sigmoid_topk", logits.data_ptr(), stride, 1 if logits.dtype == F32 else 0,
+         bias.data_ptr(), rows, experts, int(k), keys.data_ptr() if keys is not None else None,
+         indices.data_ptr() if indices is not None else None,
+         weights.data_ptr() if weights is not None else None, _stream(logits))
+    return indices, weights, keys
+
+
+def residual_rms_router_sigmoid(
+    x: torch.Tensor,
+    branch: torch.Tensor,
+    norm_weight: torch.Tensor,
+    router: torch.Tensor | PackedRouterWeight,
+    bias: torch.Tensor,
+    *,
+    k: int,
+    eps: float,
+    emit_logits: bool = True,
+    emit_keys: bool = True,
+    select: bool = False,
+):
+    """The fused router's sigmoid form; see `omnia_residual_rms_router_sigmoid`.
+    Returns (summed, normalized, logits or None, keys or None, indices or None,
+    weights or None)."""
+    hidden = norm_weight.numel()
+    if not isinstance(router, PackedRouterWeight):
+        _require(router.dim() == 2 and router.shape[-1] == hidden,
+                 "residual_rms_router_sigmoid: router weight shape")
+        router = pack_router_weight(router)
+    experts = router.experts
+    _require(router.hidden == hidden, "residual_rms_router_sigmoid: router weight shape")
+    _require(x.shape == branch.shape and x.shape[-1] == hidden,
+             "residual_rms_router_sigmoid: shape mismatch")
+    for t, name in ((x, "x"), (branch, "branch"), (norm_weight, "norm_weight")):
+        _dense(t, BF16, name)
+    _dense(bias, F32, "bias")
+    _require(bias.numel() == experts, "residual_rms_router_sigmoid: bias must be [experts]")
+    _require(on_rocm(x, branch, norm_weight, router.buffer, bias),
+             "residual_rms_router_sigmoid: tensors must share one ROCm device")
+    rows = x.numel() // hidden
+    lead = x.shape[:-1]
+    summed = torch.empty_like(x)
+    normalized = torch.empty_like(x)
+    logits = torch.empty((*lead, experts), dtype=BF16, device=x.device) if emit_logits else None
+    keys = torch.empty((*lead, experts), dtype=torch.uint32, device=x.device) if emit_keys else None
+    indices = torch.empty((*lead, k), dtype=torch.int32, device=x.device) if select else None
+    weights = torch.empty((*lead, k), dtype=F32, device=x.device) if select else None
+    ptr = lambda t: t.data_ptr() if t is not None else None
+    call("omnia_residual_rms_router_sigmoid", x.data_ptr(), branch.data_ptr(),
+         norm_weight.data_ptr(), router.buffer.data_ptr(), bias.data_ptr(), rows, hidden,
+         experts, int(k), float(eps), summed.data_ptr(), normalized.data_ptr(), ptr(logits),
+         ptr(keys), ptr(indices), ptr(weights), _stream(x))
+    return summed, normalized, logits, keys, indices, weights
+
+
 def moe_gate_up(
     x: torch.Tensor,
     weight: torch.Tensor,

@@ -13,6 +13,22 @@ models/qwen3/layers/moe.py:34-42) with the definitions the build adopts:
 
 The fused residual router (core/kernels/route/residual.py:117-299) is the residual
 join of oracle/add_norm.py followed by the above.
+
+Sigmoid routing with a correction bias (core/kernels/route/ordinal.py:200-286,
+`router_tournament` / `OrdinalRoute`; the keys of route/residual.py:109-115):
+
+- score = sigmoid(x) of the float32 logit, the stable form of ordinal.py:74-76
+  (y = 1 / (1 + exp|x|), x < 0 ? y : 1 - y) evaluated in float64 and rounded once to
+  float32 (the correctly rounded value; the reference's Metal `exp` is not);
+- key = ordinal(-(score + bias)), the sum in float32, `ordinal` the map of
+  ordinal.py:37-47 (ascending unsigned order = ascending float order, +-0 one value,
+  NaN above everything);
+- selection: the first k of the stable ascending order of the keys (descending
+  score + bias, lower index first on ties, NaN last);
+- weights: the winners' unbiased scores over their float32 sum, taken in winner order
+  (ordinal.py:183-193), divided in float32.
+
+NaN in the softmax chain ranks last as well, the place ordinal.py gives a NaN score.
 """
 
 from __future__ import annotations
@@ -30,11 +46,12 @@ def router_logits(n_bits: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
 
 
 def order_keys(logit_bits: np.ndarray) -> np.ndarray:
-    """Order-preserving integer map of bf16 bits: -0 folded onto +0, NaN above all."""
+    """Order-preserving integer map of bf16 bits: -0 folded onto +0, NaN below all (so a
+    NaN logit ranks last, as ordinal.py:37-47 ranks a NaN score)."""
     b = np.asarray(logit_bits, dtype=np.uint16).astype(np.int64)
     b = np.where(b == 0x8000, 0, b)
     key = np.where(b & 0x8000, (~b) & 0xFFFF, b | 0x8000)
-    return np.where((b & 0x7FFF) > 0x7F80, 0xFFFF, key)
+    return np.where((b & 0x7FFF) > 0x7F80, 0, key)
 
 
 def select(logit_bits: np.ndarray, k: int) -> np.ndarray:
@@ -64,3 +81,68 @@ def residual_rms_router(x_bits, branch_bits, norm_bits, router_bits, eps: float,
     logits = router_logits(normalized, router_bits)
     indices, weights = softmax_topk(logits, k)
     return summed, normalized, logits, indices, weights
+
+
+def sigmoid_f32(x: np.ndarray) -> np.ndarray:
+    """Correctly rounded float32 sigmoid of float32 values (ordinal.py:74-76's stable
+    form, in float64, rounded once)."""
+    x64 = np.asarray(x, dtype=np.float32).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        y = 1.0 / (1.0 + np.exp(np.abs(x64)))
+        score = np.where(x64 < 0.0, y, 1.0 - y)
+    return score.astype(np.float32)
+
+
+def ordinal(key: np.ndarray) -> np.ndarray:
+    """ordinal.py:37-47 `router_key_ordinal`: uint32 whose ascending order is the float
+    order of `key` (float32), +-0 -> 0x80000000, NaN -> 0xFFFFFFFF."""
+    bits = np.ascontiguousarray(key, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    magnitude = bits & 0x7FFFFFFF
+    out = np.where(bits & 0x80000000, (~bits) & 0xFFFFFFFF, bits ^ 0x80000000)
+    out = np.where(magnitude == 0, 0x80000000, out)
+    out = np.where(magnitude > 0x7F800000, 0xFFFFFFFF, out)
+    return out.astype(np.uint32)
+
+
+def sigmoid_keys(logits_f32: np.ndarray, bias: np.ndarray):
+    """(scores, keys) of a row of float32 logits: scores = sigmoid_f32(logits),
+    keys = ordinal(-(score + bias)) with the sum rounded to float32 (ordinal.py:74-78,
+    residual.py:109-115)."""
+    scores = sigmoid_f32(logits_f32)
+    with np.errstate(invalid="ignore"):
+        biased = (scores + np.asarray(bias, dtype=np.float32)).astype(np.float32)
+    return scores, ordinal(-biased)
+
+
+def ordinal_select(keys: np.ndarray, k: int) -> np.ndarray:
+    """The first k of the stable ascending order of the keys (ties: lower index)."""
+    return np.argsort(keys, axis=-1, kind="stable")[..., :k].astype(np.int32)
+
+
+def ordinal_weights(scores: np.ndarray, indices: np.ndarray) -> np.ndarray:
+    """ordinal.py:183-193: the winners' unbiased scores over their float32 sum, the sum
+    taken in winner order, the quotient rounded to float32."""
+    picked = np.take_along_axis(scores, indices.astype(np.int64), axis=-1).astype(np.float32)
+    total = np.zeros(picked.shape[:-1], dtype=np.float32)
+    for j in range(picked.shape[-1]):
+        total = (picked[..., j] + total).astype(np.float32)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        return (picked / total[..., None]).astype(np.float32)
+
+
+def sigmoid_topk(logits_f32: np.ndarray, bias: np.ndarray, k: int):
+    """(indices, weights, keys) of sigmoid routing with a correction bias
+    (ordinal.py:200-286, `router_tournament`)."""
+    scores, keys = sigmoid_keys(logits_f32, bias)
+    indices = ordinal_select(keys, k)
+    return indices, ordinal_weights(scores, indices), keys
+
+
+def residual_rms_router_sigmoid(x_bits, branch_bits, norm_bits, router_bits, bias,
+                                eps: float, k: int):
+    """The fused router's sigmoid form (residual.py:117-299): (summed, normalized,
+    logits, keys, indices, weights), the keys built from the bf16 logits."""
+    summed, normalized = add_rms_norm(x_bits, branch_bits, norm_bits, eps)
+    logits = router_logits(normalized, router_bits)
+    indices, weights, keys = sigmoid_topk(to_f32(logits), bias, k)
+    return summed, normalized, logits, keys, indices, weights

@@ -218,6 +218,71 @@ def test_residual_router_cpu_resolves_to_core_and_matches_oracle():
     np.testing.assert_allclose(wts.numpy().sum(axis=-1), 1.0, rtol=1e-5)
 
 
+def test_ordinal_route_predicate_and_core_sigmoid_chain():
+    from mlx_omnia_amd.kernels.route import ordinal_keys, ordinal_route_applies, sigmoid_bias_routing
+    # ordinal.py:158-174: (experts / 32) * k == 64
+    assert ordinal_route_applies(256, 8) and ordinal_route_applies(128, 16) and ordinal_route_applies(1024, 2)
+    assert not ordinal_route_applies(128, 8) and not ordinal_route_applies(250, 8)
+    bias = torch.zeros(256)
+    assert sigmoid_bias_routing(Routing(experts=256, k=8, scoring="sigmoid", bias=bias))
+    for knob in (dict(bias=None), dict(scoring="softmax"), dict(normalize=False), dict(scale=2.0),
+                 dict(ties="higher"), dict(softcap=10.0)):
+        decl = dict(experts=256, k=8, scoring="sigmoid", bias=bias) | knob
+        assert not sigmoid_bias_routing(Routing(**decl)), knob
+    # On CPU tensors the Core chain serves; it agrees with the oracle off near-ties.
+    values = np.random.default_rng(20).standard_normal((20, 256)).astype(np.float32) * 2
+    bias = (np.random.default_rng(21).standard_normal(256) * 0.1).astype(np.float32)
+    route = Route(None, experts=256, k=8, scoring="sigmoid", bias=torch.from_numpy(bias))
+    assert isinstance(route.strategy, DefaultRoute)
+    idx, w = route.rows(torch.from_numpy(values))
+    want_idx, want_w, want_keys = oracle_route.sigmoid_topk(values, bias, 8)
+    assert np.array_equal(idx.numpy(), want_idx)
+    np.testing.assert_allclose(w.numpy(), want_w, rtol=1e-6)
+    # The Core chain's ordinal keys (ordinal.py:253-262) order the experts as the oracle's.
+    scores = torch.sigmoid(torch.from_numpy(values).double()).float()
+    keys = ordinal_keys(scores + torch.from_numpy(bias)).numpy()
+    assert np.array_equal(keys, want_keys)
+
+
+def test_call_time_fallback_is_recorded():
+    """A built HIP strategy handed logits its kernel does not take passes the call to the
+    Core chain and says so (RESOLVED gets the Core module, FALLBACKS counts it)."""
+    import importlib
+
+    from mlx_omnia_amd.kernels.route import HipSoftmaxTopkRoute
+    resolve = importlib.import_module("mlx_omnia_amd.kernels.resolve")
+    routing = Routing(experts=128, k=8)
+    strategy = HipSoftmaxTopkRoute(None, routing, DefaultRoute(None, routing))  # built as on a GPU
+    resolve.RESOLVED.discard(DefaultRoute.__module__)
+    before = resolve.FALLBACKS.get("HipSoftmaxTopkRoute -> DefaultRoute", 0)
+    logits = torch.from_numpy(np.random.default_rng(22).standard_normal((4, 128)).astype(np.float32))
+    idx, w = strategy.rows(logits)                   # fp32 on the CPU: not the kernel's input
+    assert resolve.FALLBACKS["HipSoftmaxTopkRoute -> DefaultRoute"] == before + 1
+    assert DefaultRoute.__module__ in resolve.RESOLVED
+    want, _ = DefaultRoute(None, routing).rows(logits)
+    assert torch.equal(idx, want)
+
+
+def test_residual_router_core_keys_on_cpu():
+    rows, hidden, experts = 3, 2048, 256
+    rng = np.random.default_rng(23)
+    x = from_float(rng.standard_normal((rows, hidden)))
+    r = from_float(rng.standard_normal((rows, hidden)))
+    w = from_float(1 + 0.1 * rng.standard_normal(hidden))
+    gate = from_float(0.02 * rng.standard_normal((experts, hidden)))
+    bias = (rng.standard_normal(experts) * 0.1).astype(np.float32)
+    routing = Routing(experts=experts, k=8, scoring="sigmoid", bias=torch.from_numpy(bias))
+    router = ResidualRouter(RMSNormLeaf(cpu(w), EPS), cpu(gate), routing=routing)
+    assert isinstance(router.strategy, DefaultResidualRouter)
+    summed, normed, logits, keys = router.with_keys(cpu(x), cpu(r))
+    want = oracle_route.residual_rms_router_sigmoid(x, r, w, gate, bias, EPS, 8)
+    assert np.array_equal(bits(summed), want[0])
+    # The Core keys order the experts as the Core chain's own logits say.
+    core_scores = torch.sigmoid(logits.float()).double() + torch.from_numpy(bias).double()
+    order = np.argsort(-core_scores.numpy(), axis=-1, kind="stable")
+    assert np.array_equal(np.argsort(keys.numpy().astype(np.int64), axis=-1, kind="stable"), order)
+
+
 # ---- routed expert gate/up and down/combine ---------------------------------------
 
 
