@@ -26,7 +26,7 @@ import torch
 from ...runtime import ops
 from .._device import hip_device
 from ..qkv_rope.kernel import AngleTable
-from ..resolve import resolve
+from ..resolve import record_fallback, resolve
 from .cache import FixedKVCache, RingKVCache
 
 __all__ = ["AttentionStep", "AttentionStepStrategy", "DefaultAttentionStep", "FixedKVCache",
@@ -178,14 +178,23 @@ class HipAttentionStep(AttentionStepStrategy):
 
     def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
         if raw_queries.shape[1] != 1:
+            record_fallback(self, self.fallback)
             return self.fallback(raw_queries, raw_keys, raw_values, mask)
         cache = self.cache
         if cache.window == 0 and cache.offset >= cache.capacity:
             raise ValueError(f"cache of {cache.capacity} rows is full")
         if cache.offset >= self.atlas.shape[0]:
             raise ValueError(f"position {cache.offset} is past the angle table's {self.atlas.shape[0]} rows")
+        # A captured step is replayed at positions the host never sees (the device position
+        # advances; the host offset stays where the capture left it). The grid is then
+        # sized for the whole cache and the kernel takes the attended rows from the device
+        # position; a fixed cache's table must cover every row a replay can write.
+        capturing = torch.cuda.is_current_stream_capturing()
+        if capturing and cache.window == 0 and self.atlas.shape[0] < cache.capacity:
+            raise ValueError(f"a captured step needs an angle table covering the cache's "
+                             f"{cache.capacity} rows, not {self.atlas.shape[0]}")
         keys, values = cache.fetch()
-        max_rows = min(cache.offset + 1, cache.capacity)
+        max_rows = cache.capacity if capturing else min(cache.offset + 1, cache.capacity)
         out = ops.attention_decode(
             raw_queries.contiguous(), raw_keys.contiguous(), raw_values.contiguous(),
             self.query_weight, self.key_weight, self.atlas, keys, values, cache.position,

@@ -47,7 +47,7 @@ from ...runtime import ops
 from .._device import hip_device
 from ..gate_up.routed import affine_leaf, mxfp4_applies, mxfp4_leaf, nvfp4_leaf
 from ..leaf import QuantizedLinearLeaf, QuantizedSwitchLinearLeaf
-from ..resolve import resolve
+from ..resolve import record_fallback, resolve
 
 Layout = Literal["interleaved", "blocked"]
 MAX_SLOTS = 16
@@ -124,6 +124,7 @@ class HipDenseDownCombine(DownCombineStrategy):
     def __call__(self, act, chosen, weights, residual):
         k = chosen.numel()
         if k == 0 or k > MAX_SLOTS:  # one wave per expert in a workgroup
+            record_fallback(self, self.fallback)
             return self.fallback(act, chosen, weights, residual)
         device = self.weight.device
         return ops.moe_down_combine(
@@ -164,6 +165,7 @@ class HipAffineDownCombine(DownCombineStrategy):
     def __call__(self, act, chosen, weights, residual):
         slots = chosen.numel()
         if slots == 0 or slots > MAX_SLOTS:  # one wave per slot in a workgroup
+            record_fallback(self, self.fallback)
             return self.fallback(act, chosen, weights, residual)
         device = self.leaf.weight.device
         return ops.moe_down_combine_affine(
@@ -194,6 +196,7 @@ class HipMxfp4DownCombine(DownCombineStrategy):
     def __call__(self, act, chosen, weights, residual):
         slots = chosen.numel()
         if slots == 0 or slots > MAX_SLOTS:  # one wave per slot in a workgroup
+            record_fallback(self, self.fallback)
             return self.fallback(act, chosen, weights, residual)
         device = self.leaf.weight.device
         return ops.moe_down_combine_mxfp4(
@@ -223,6 +226,7 @@ class HipNvfp4DownCombine(DownCombineStrategy):
     def __call__(self, act, chosen, weights, residual):
         slots = chosen.numel()
         if slots == 0 or slots > MAX_SLOTS:  # one wave per slot in a workgroup
+            record_fallback(self, self.fallback)
             return self.fallback(act, chosen, weights, residual)
         device = self.leaf.weight.device
         return ops.moe_down_combine_nvfp4(

@@ -17,7 +17,7 @@ import torch
 
 from ...runtime import ops
 from .._device import hip_device
-from ..resolve import resolve
+from ..resolve import record_fallback, resolve
 
 __all__ = ["DefaultGateSoftplus", "GateSoftplus", "GateSoftplusStrategy", "HipGateSoftplus"]
 
@@ -66,6 +66,7 @@ class HipGateSoftplus(GateSoftplusStrategy):
 
     def __call__(self, a: torch.Tensor) -> torch.Tensor:
         if a.dtype != torch.bfloat16 or a.shape[-1] != self.a_log.numel() or a.stride(-1) != 1:
+            record_fallback(self, self.fallback)
             return self.fallback(a)
         return ops.gate_softplus(a, self.a_log, self.dt_bias)
 

@@ -15,6 +15,7 @@ from dataclasses import dataclass
 import torch
 
 from ...runtime import ops
+from ..resolve import record_fallback
 from .._device import hip_device
 from .default import DefaultGateUpActivation
 from .kernel import GateUpActivationStrategy, split
@@ -41,5 +42,6 @@ class HipSwiGLU(GateUpActivationStrategy):
             and gate.shape == up.shape and applies(gate.shape[-1])
         )
         if not served or not hip_device(gate, up):
+            record_fallback(self, self.fallback)
             return self.fallback(gate, up)
         return ops.swiglu(gate, up)

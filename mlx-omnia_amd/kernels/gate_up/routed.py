@@ -44,7 +44,7 @@ import torch
 from ...runtime import ops
 from .._device import hip_device
 from ..leaf import QuantizedLinearLeaf, QuantizedSwitchLinearLeaf
-from ..resolve import resolve
+from ..resolve import record_fallback, resolve
 
 Activation = Literal["silu", "swiglu_oai"]
 Layout = Literal["interleaved", "blocked"]
@@ -294,6 +294,7 @@ class HipNvfp4GateUp(GateUpStrategy):
             # Ordinal keys are uint32 (the router's ordinals); the kernel ranks them in place
             # of the sort (core/kernels/gate_up/nvfp4_packed.py:1-13).
             if chosen.dtype != torch.uint32:
+                record_fallback(self, self.fallback)
                 return self.fallback(row, chosen)
             keys = chosen.to(device=self.leaf.weight.device).contiguous().reshape(-1)
             return ops.moe_gate_up_nvfp4_ordinal(x, self.leaf, keys, self.routing.top_k)

@@ -7,7 +7,8 @@ core/kernels/qkv_rope/epilogue.py:157-195 (`RopeEpilogue.build`): a bare `base`,
 rotary, no mscale, now for any number of tokens rather than one. Both read q and k
 straight out of the fused projection rows (no split copy) and write head-major q, k;
 v stays a view of the projection. A segment the kernels do not serve (batch > 1, a
-tensor offset) goes to the Core fallback, as in the reference.
+tensor offset) goes to the Core fallback, as in the reference, and the hand-off is
+recorded (`resolve.record_fallback`).
 """
 
 from __future__ import annotations
@@ -18,6 +19,7 @@ from dataclasses import dataclass
 import torch
 
 from ...runtime import ops
+from ..resolve import record_fallback
 from .._device import hip_device
 from .default import DefaultQkvRope
 from .kernel import AngleTable, Angles, Projection, QkvRopeStrategy
@@ -87,6 +89,7 @@ class HipQkNormRope(QkvRopeStrategy):
     def __call__(self, x: torch.Tensor, offset):
         fused = self.projection(x)
         if fused.shape[0] != 1 or not isinstance(offset, int) or fused.dtype != torch.bfloat16:
+            record_fallback(self, self.fallback)
             return self.fallback.epilogue(fused, offset)
         rows = fused[0]
         if rows.stride(-1) != 1:
@@ -138,6 +141,7 @@ class HipRopeEpilogue(QkvRopeStrategy):
     def __call__(self, x: torch.Tensor, offset):
         fused = self.projection(x)
         if fused.shape[0] != 1 or not isinstance(offset, int) or fused.dtype != torch.bfloat16:
+            record_fallback(self, self.fallback)
             return self.fallback.epilogue(fused, offset)
         rows = fused[0]
         if rows.stride(-1) != 1 or (rows.shape[0] > 1 and rows.stride(0) % 8):

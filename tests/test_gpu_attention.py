@@ -238,6 +238,55 @@ def test_captured_graph_replays_with_the_device_position():
         assert int(pos.item()) == position + 1
 
 
+@pytest.mark.parametrize("ring", [False, True])
+def test_facade_step_captured_and_replayed(ring):
+    """The facade's step captured once and replayed over several positions: each replay
+    writes its row and attends the rows the device position gives (the grid sized for the
+    whole cache under capture), with eager work between replays."""
+    print(f"attention facade graph replay, ring={ring}", flush=True)
+    heads, kv_heads, capacity, pairs = 8, 2, 64 if ring else 256, 64
+    case = Case(heads, kv_heads, capacity, pairs, seed=13)
+    start = 60 if ring else 10                      # the ring wraps during the replays
+    keys = case.kc.clone().unsqueeze(0)
+    values = case.vc.clone().unsqueeze(0)
+    cache = (RingKVCache(keys, values, position=start) if ring
+             else FixedKVCache(keys, values, position=start))
+    table = AngleTable(torch.from_numpy(case.atlas[:, :pairs]).cuda(),
+                       torch.from_numpy(case.atlas[:, pairs:]).cuda())
+    step = AttentionStep(cache, heads=heads, kv_heads=kv_heads, head_dim=D, scale=SCALE,
+                         dtype=torch.bfloat16, query_weight=to_device(case.qw),
+                         key_weight=to_device(case.kw), eps=EPS, rotary_pairs=pairs, angles=table)
+    assert isinstance(step.strategy, HipAttentionStep)
+    q, k, v = (to_device(x).reshape(1, 1, -1) for x in (case.raw_q, case.raw_k, case.raw_v))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        step(q, k, v)                               # warm-up outside the capture
+    torch.cuda.synchronize()
+    cache.offset = start
+    cache.position.fill_(start)
+    keys.copy_(case.kc.unsqueeze(0))
+    values.copy_(case.vc.unsqueeze(0))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = step(q, k, v)
+    torch.cuda.synchronize()
+    cache.position.fill_(start)
+    keys.copy_(case.kc.unsqueeze(0))
+    values.copy_(case.vc.unsqueeze(0))
+    want_keys, want_values = bits_of(case.kc), bits_of(case.vc)
+    for position in range(start, start + 8):
+        graph.replay()
+        torch.cuda.synchronize()
+        _ = torch.ones(1000, device="cuda").sum().item()   # eager work between replays
+        want, want_keys, want_values = attn.decode_step(
+            case.raw_q, case.raw_k, case.raw_v, case.qw, case.kw, case.atlas[position], want_keys,
+            want_values, position, window=capacity if ring else 0, scale=SCALE, eps=EPS, pairs=pairs)
+        assert_bf16_close(bits_of(out.reshape(heads, D)), want, min_exact=0.99)
+        assert int(cache.position.item()) == position + 1
+    row = (start + 7) % capacity if ring else start + 7
+    assert np.array_equal(bits_of(values[0])[:, row], want_values[:, row])
+
+
 def test_golden_fixture():
     from pathlib import Path
 
