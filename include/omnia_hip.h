@@ -29,13 +29,24 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 11
+#define OMNIA_ABI_VERSION 12
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
 
 /* Text of the last error raised on the calling thread ("" if none). */
 const char* omnia_last_error(void);
+
+/* Builds rows of a rotary angle atlas on the device:
+ *   atlas[r][i]         = fp32(cos(theta)),  atlas[r][pairs + i] = fp32(sin(theta)),
+ *   theta = (first + r) * frequencies[i] in fp64, cos and sin in fp64, each rounded once,
+ * for r < rows, i < pairs. frequencies [pairs] fp64 (device): exp(-ln(base) * i / pairs)
+ * for the plain rotary, 1 / freqs for a YaRN table; atlas rows `stride` floats apart.
+ * Replaces: models/laguna/layers/attention.py:171-196,235-243 (`LagunaAttention.angles`,
+ * `_angle_atlas`, built once and regrown past its last row) with the fp64 build of
+ * tests/test_kernel_qk_norm_rope.py:51-66. */
+int32_t omnia_rope_angle_atlas(const double* frequencies, int64_t pairs, int64_t first,
+                               int64_t rows, float* atlas, int64_t stride, hipStream_t stream);
 
 /* Residual add + RMSNorm over `rows` rows of `hidden` bf16 values.
  *   summed[r]     = bf16(x[r] + branch[r])

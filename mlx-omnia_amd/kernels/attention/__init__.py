@@ -25,6 +25,7 @@ import torch
 
 from ...runtime import ops
 from .._device import hip_device
+from ..qkv_rope.atlas import AngleAtlas
 from ..qkv_rope.kernel import AngleTable
 from ..resolve import record_fallback, resolve
 from .cache import FixedKVCache, RingKVCache
@@ -142,7 +143,8 @@ class HipAttentionStep(AttentionStepStrategy):
     mscale: float
     query_weight: torch.Tensor
     key_weight: torch.Tensor
-    atlas: torch.Tensor
+    atlas: torch.Tensor              # a fixed table's cos || sin rows
+    growable: AngleAtlas | None      # or the atlas that grows past its last row
     workspace: torch.Tensor
     fallback: DefaultAttentionStep
 
@@ -151,7 +153,11 @@ class HipAttentionStep(AttentionStepStrategy):
               eps, rotary_pairs, mscale, angles, base, sinks) -> "HipAttentionStep | None":
         if not isinstance(cache, FixedKVCache) or sinks is not None:
             return None
-        if not isinstance(angles, AngleTable) or angles.pairs != rotary_pairs:
+        growable = angles if isinstance(angles, AngleAtlas) else None
+        if growable is not None:
+            if angles.pairs != rotary_pairs:
+                return None
+        elif not isinstance(angles, AngleTable) or angles.pairs != rotary_pairs:
             return None
         if query_weight is None or key_weight is None:
             return None
@@ -164,9 +170,11 @@ class HipAttentionStep(AttentionStepStrategy):
             return None
         if query_weight.dtype != torch.bfloat16 or key_weight.dtype != torch.bfloat16:
             return None
-        if not hip_device(keys, values, query_weight, key_weight, angles.cos, angles.sin):
+        table = growable.table() if growable is not None else angles
+        if not hip_device(keys, values, query_weight, key_weight, table.cos, table.sin):
             return None
-        atlas = torch.cat([angles.cos, angles.sin], dim=-1).to(torch.float32).contiguous()
+        atlas = (growable.atlas if growable is not None
+                 else torch.cat([angles.cos, angles.sin], dim=-1).to(torch.float32).contiguous())
         nbytes = ops.attention_workspace_bytes(heads, kv_heads, head_dim, keys.shape[2])
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=keys.device)
         fallback = DefaultAttentionStep.build(
@@ -174,7 +182,7 @@ class HipAttentionStep(AttentionStepStrategy):
             query_weight=query_weight, key_weight=key_weight, eps=eps, rotary_pairs=rotary_pairs,
             mscale=mscale, angles=angles, base=base, sinks=sinks)
         return cls(cache, heads, kv_heads, scale, eps, mscale, query_weight.contiguous(),
-                   key_weight.contiguous(), atlas, workspace, fallback)
+                   key_weight.contiguous(), atlas, growable, workspace, fallback)
 
     def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
         if raw_queries.shape[1] != 1:
@@ -183,21 +191,27 @@ class HipAttentionStep(AttentionStepStrategy):
         cache = self.cache
         if cache.window == 0 and cache.offset >= cache.capacity:
             raise ValueError(f"cache of {cache.capacity} rows is full")
-        if cache.offset >= self.atlas.shape[0]:
-            raise ValueError(f"position {cache.offset} is past the angle table's {self.atlas.shape[0]} rows")
         # A captured step is replayed at positions the host never sees (the device position
         # advances; the host offset stays where the capture left it). The grid is then
         # sized for the whole cache and the kernel takes the attended rows from the device
-        # position; a fixed cache's table must cover every row a replay can write.
+        # position; a fixed cache's table must cover every row a replay can write (an
+        # atlas is grown before the capture: it cannot allocate inside one).
         capturing = torch.cuda.is_current_stream_capturing()
-        if capturing and cache.window == 0 and self.atlas.shape[0] < cache.capacity:
+        atlas = self.atlas
+        if self.growable is not None:
+            if not capturing:
+                self.growable.ensure(cache.offset)  # grown past its last row, as the reference's
+            atlas = self.growable.atlas
+        if cache.offset >= atlas.shape[0]:
+            raise ValueError(f"position {cache.offset} is past the angle table's {atlas.shape[0]} rows")
+        if capturing and cache.window == 0 and atlas.shape[0] < cache.capacity:
             raise ValueError(f"a captured step needs an angle table covering the cache's "
-                             f"{cache.capacity} rows, not {self.atlas.shape[0]}")
+                             f"{cache.capacity} rows, not {atlas.shape[0]}")
         keys, values = cache.fetch()
         max_rows = cache.capacity if capturing else min(cache.offset + 1, cache.capacity)
         out = ops.attention_decode(
             raw_queries.contiguous(), raw_keys.contiguous(), raw_values.contiguous(),
-            self.query_weight, self.key_weight, self.atlas, keys, values, cache.position,
+            self.query_weight, self.key_weight, atlas, keys, values, cache.position,
             heads=self.heads, kv_heads=self.kv_heads, max_rows=max_rows, scale=self.scale,
             eps=self.eps, mscale=self.mscale, window=cache.window, workspace=self.workspace)
         cache.advance()

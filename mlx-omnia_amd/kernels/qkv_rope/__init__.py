@@ -11,11 +11,12 @@ from __future__ import annotations
 import torch
 
 from ..resolve import resolve
+from .atlas import AngleAtlas, rope_frequencies
 from .default import DefaultQkvRope, rope_core, split_heads
 from .hip import HipQkNormRope, HipRopeEpilogue, qk_norm_rope_applies, rope_epilogue_applies
 from .kernel import AngleTable, Angles, Projection, QkvRopeStrategy, Rotation
 
-__all__ = [
+__all__ = ["AngleAtlas", "rope_frequencies", 
     "AngleTable",
     "Angles",
     "DefaultQkvRope",

@@ -22,6 +22,7 @@ from ...runtime import ops
 from ..resolve import record_fallback
 from .._device import hip_device
 from .default import DefaultQkvRope
+from .atlas import AngleAtlas
 from .kernel import AngleTable, Angles, Projection, QkvRopeStrategy
 
 HEAD_DIMS = (64, 128, 256)
@@ -81,6 +82,10 @@ class HipQkNormRope(QkvRopeStrategy):
                    _fallback(projection, heads, kv_heads, head_dim, rope, eps, q_norm, k_norm))
 
     def _tables(self, offset: int, length: int):
+        if isinstance(self.angles, AngleAtlas):
+            self.angles.ensure(offset + length - 1)
+            table = self.angles.table()
+            return table.cos, table.sin, offset
         if isinstance(self.angles, AngleTable):
             return self.angles.cos, self.angles.sin, offset
         rows = self.angles(offset, length).to(torch.float32)

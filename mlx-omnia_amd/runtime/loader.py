@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libomnia_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -26,6 +26,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "omnia_abi_version": (_I32, []),
     "omnia_last_error": (ctypes.c_char_p, []),
     "omnia_add_rms_norm": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _F32, _P]),
+    "omnia_rope_angle_atlas": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _P]),
     "omnia_qk_norm_rope": (
         _I32,
         [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64,

@@ -51,6 +51,21 @@ def _out(out: torch.Tensor | None, like: torch.Tensor, shape, dtype, name: str) 
     return out
 
 
+def rope_angle_atlas(frequencies: torch.Tensor, first: int, rows: int, *,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Atlas rows [rows, 2 * pairs] fp32 (cos || sin) for positions first .. first+rows-1
+    from fp64 frequencies [pairs] on the device; see `omnia_rope_angle_atlas`."""
+    _dense(frequencies, torch.float64, "frequencies")
+    pairs = frequencies.numel()
+    out = _out(out, frequencies, (rows, 2 * pairs), F32, "atlas")
+    _require(out.dim() == 2 and out.stride(-1) == 1 and out.shape == (rows, 2 * pairs),
+             "rope_angle_atlas: out must be [rows, 2 * pairs] with unit column stride")
+    _require(on_rocm(frequencies, out), "rope_angle_atlas: tensors must share one ROCm device")
+    call("omnia_rope_angle_atlas", frequencies.data_ptr(), pairs, int(first), int(rows),
+         out.data_ptr(), out.stride(0), _stream(frequencies))
+    return out
+
+
 def add_rms_norm(
     x: torch.Tensor,
     branch: torch.Tensor,
@@ -953,8 +968,10 @@ def moe_gate_up_nvfp4_ordinal(
              "moe_gate_up_nvfp4_ordinal: weight must be [experts, 2 * inner, words]")
     experts, rows = leaf.weight.shape[0], leaf.weight.shape[1]
     leaf.check(rows, hidden, "moe_gate_up_nvfp4_ordinal")
-    _require(keys.dtype in (torch.int32, torch.uint32) and keys.is_contiguous() and keys.numel() == experts,
-             "moe_gate_up_nvfp4_ordinal: keys must be contiguous 32-bit [experts]")
+    # The kernel ranks the keys as unsigned 32-bit values: only uint32 keys are taken, so
+    # an int32 key never ranks by an order its caller did not mean.
+    _require(keys.dtype == torch.uint32 and keys.is_contiguous() and keys.numel() == experts,
+             "moe_gate_up_nvfp4_ordinal: keys must be contiguous uint32 [experts]")
     _require(0 < top_k <= experts <= 1024, "moe_gate_up_nvfp4_ordinal: 0 < top_k <= experts <= 1024")
     _require(on_rocm(x, keys, *leaf.tensors()), "moe_gate_up_nvfp4_ordinal: tensors must share one ROCm device")
     out = _out(out, x, (top_k, rows // 2), BF16, "out")

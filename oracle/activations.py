@@ -50,8 +50,9 @@ def swiglu(gate_bits: np.ndarray, up_bits: np.ndarray) -> np.ndarray:
     g = to_f32(gate_bits)
     u = to_f32(up_bits)
     s = to_f32(sigmoid_bf16(g))
-    t = to_f32(to_bf16(g * s))
-    return to_bf16(t * u)
+    with np.errstate(invalid="ignore"):  # -inf * sigmoid(-inf) = -inf * 0 is NaN, as on the device
+        t = to_f32(to_bf16(g * s))
+        return to_bf16(t * u)
 
 
 def softplus_f32(dt: np.ndarray) -> np.ndarray:

@@ -82,6 +82,24 @@ def test_qkv_rope_table_declaration_on_cpu_and_reference_flag():
     assert isinstance(QkvRope(lambda x: x, reference=True, **declaration).strategy, DefaultQkvRope)
 
 
+def test_angle_atlas_on_cpu_matches_oracle_and_grows():
+    from mlx_omnia_amd.kernels.qkv_rope import AngleAtlas, rope_frequencies
+    assert np.array_equal(rope_frequencies(64, 1e6), np.exp(-np.log(1e6) * np.arange(64) / 64))
+    atlas = AngleAtlas(64, base=1e6, rows=512)
+    cos, sin = oracle_rope.angle_table(2048, 64, 1e6)
+    got = atlas.atlas.numpy()
+    # torch's and numpy's fp64 cos/sin may differ in a last fp64 bit, which moves an fp32
+    # rounding only at a midpoint: one fp32 ulp at most, almost never.
+    assert np.abs(got[:, :64] - cos[:512]).max() <= np.spacing(np.float32(1.0))
+    assert np.mean(got[:, :64] == cos[:512]) > 0.9999
+    kept = atlas.atlas.clone()
+    atlas.ensure(1500)
+    assert atlas.rows == 1501 and torch.equal(atlas.atlas[:512], kept)
+    assert np.abs(atlas.atlas.numpy()[:, 64:] - sin[:1501]).max() <= np.spacing(np.float32(1.0))
+    with pytest.raises(ValueError):
+        AngleAtlas(64)
+
+
 def test_angle_table_contract_and_atlas_view():
     cos, sin = oracle_rope.angle_table(32, 8, 1e4)
     atlas = torch.from_numpy(np.concatenate([cos, sin], axis=-1))

@@ -15,7 +15,7 @@ from mlx_omnia_amd.kernels.gate_softplus import GateSoftplus, HipGateSoftplus
 from mlx_omnia_amd.kernels.gate_up import GateUpActivation, HipSwiGLU
 from mlx_omnia_amd.runtime import ops
 from oracle import activations as act
-from oracle.bf16 import from_float
+from oracle.bf16 import from_float, to_f32
 from util import bits_of, f32_to_device, to_device
 
 pytestmark = pytest.mark.gpu
@@ -39,17 +39,28 @@ def test_swiglu_fused_halves_and_specials_via_facade():
     fused = rng.standard_normal((33, 2 * 520)).astype(np.float32) * 6
     fused[0, :8] = [0.0, -0.0, 88.0, -88.0, 90.0, -90.0, 1e-30, -1e-30]
     fused[1, :3] = [np.inf, -np.inf, np.nan]
+    # inf gates against zero, negative, positive and infinite ups; a NaN up.
+    fused[2, :6] = [np.inf, np.inf, -np.inf, -np.inf, 100.0, 3.0]
+    fused[2, 520:526] = [0.0, -3.0, 2.0, np.inf, np.inf, np.nan]
     bits = from_float(fused)
     activation = GateUpActivation()
     assert isinstance(activation.strategy, HipSwiGLU)
     y = activation(to_device(bits))
     want = act.swiglu(bits[:, :520], bits[:, 520:])
-    got = bits_of(y)
-    nan = np.isnan(fused[:, :520]) | np.isnan(fused[:, 520:]) | np.isinf(fused[:, :520])
-    assert np.array_equal(got[~nan], want[~nan])
+
+    def same(got):
+        # NaN exactly where the oracle has NaN (its sign and payload are the platform's:
+        # x86 makes -inf * 0 a negative NaN, the GPU a positive one); every other element,
+        # infinities included, bit for bit.
+        nan = np.isnan(to_f32(want))
+        assert np.array_equal(np.isnan(to_f32(got)), nan)
+        assert np.array_equal(got[~nan], want[~nan])
+        assert nan.any() and np.isinf(to_f32(want)).any()
+
+    same(bits_of(y))
     # Separate tensors with row strides, one row, empty.
     y2 = ops.swiglu(to_device(bits)[:, :520], to_device(bits)[:, 520:])
-    assert np.array_equal(bits_of(y2)[~nan], want[~nan])
+    same(bits_of(y2))
     assert ops.swiglu(to_device(bits[:0, :8]), to_device(bits[:0, :8])).shape == (0, 8)
 
 

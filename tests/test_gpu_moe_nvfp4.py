@@ -157,6 +157,21 @@ def test_ordinal_routing_in_the_kernel(experts, top_k, hidden):
     assert torch.equal(got, by_index)
 
 
+def test_ordinal_keys_must_be_unsigned():
+    """The op takes uint32 keys only; through the facade, int32 keys go to the Core chain,
+    which sorts them as signed (as mx.argsort would), a negative key ranking first."""
+    rng = np.random.default_rng(3)
+    experts, hidden = 32, 64
+    stack, leaf = _leaf(rng, experts, 2 * 64, hidden)
+    keys = rng.integers(0, 1 << 20, size=experts).astype(np.int32)
+    keys[9] = -5
+    x = from_float(rng.standard_normal(hidden))
+    with pytest.raises(ValueError, match="uint32"):
+        ops.moe_gate_up_nvfp4_ordinal(to_device(x), leaf, torch.from_numpy(keys).cuda(), 4)
+    signed = list(np.argsort(keys.astype(np.int64), kind="stable")[:4])
+    assert signed[0] == 9
+
+
 def test_ordinal_facade():
     from mlx_omnia_amd.kernels.gate_up import GateUp, HipNvfp4GateUp, OrdinalRouting
     from mlx_omnia_amd.kernels.leaf import QuantizedSwitchLinearLeaf
