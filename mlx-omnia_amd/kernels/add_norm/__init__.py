@@ -25,12 +25,12 @@ __all__ = [
     "rms_norm_core",
 ]
 
-# Order is preference; the Core strategy accepts everything, so resolution never fails.
+# The HIP kernel first; the Core chain after it takes any declaration.
 _STRATEGIES = (HipAddRmsNorm, DefaultAddRmsNorm)
 
 
 class AddRmsNorm(AddRmsNormStrategy):
-    """Resolves the strategy at construction and delegates; itself an AddRmsNormStrategy."""
+    """The join a block declares: picks its binding once, then forwards every call."""
 
     def __init__(self, leaf, *, tokens: int | None = None, reference: bool = False) -> None:
         self.strategy: AddRmsNormStrategy = resolve(

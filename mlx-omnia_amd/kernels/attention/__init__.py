@@ -222,7 +222,7 @@ _STRATEGIES = (HipAttentionStep, DefaultAttentionStep)
 
 
 class AttentionStep(AttentionStepStrategy):
-    """Resolves the strategy at construction and delegates; bound to one cache."""
+    """The decode step over one cache: picks its binding once, then forwards every call."""
 
     def __init__(self, cache, *, heads: int, kv_heads: int, head_dim: int, scale: float,
                  dtype: torch.dtype, query_weight: torch.Tensor | None = None,

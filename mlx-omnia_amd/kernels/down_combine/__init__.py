@@ -242,7 +242,7 @@ _STRATEGIES = (HipNvfp4DownCombine, HipMxfp4DownCombine, HipAffineDownCombine, H
 
 
 class DownCombine(DownCombineStrategy):
-    """Resolves the strategy at construction and delegates; itself a DownCombineStrategy."""
+    """The routed down projection a block declares: picks its binding once, then forwards."""
 
     def __init__(self, leaf, *, hidden: int, inner: int, bias: torch.Tensor | None = None,
                  shared=None, layout: Layout = "interleaved", reference: bool = False) -> None:

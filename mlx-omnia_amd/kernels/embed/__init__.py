@@ -20,7 +20,7 @@ _STRATEGIES = (HipEmbed, DefaultEmbed)
 
 
 class Embed(EmbedStrategy):
-    """Resolves the strategy at construction and delegates; itself an EmbedStrategy."""
+    """The token and atlas gather a model declares: picks its binding once, then forwards."""
 
     def __init__(self, embedding: torch.Tensor, *, full_atlas: torch.Tensor,
                  sliding_atlas: torch.Tensor, reference: bool = False) -> None:

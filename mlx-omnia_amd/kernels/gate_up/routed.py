@@ -306,7 +306,7 @@ _STRATEGIES = (HipNvfp4GateUp, HipMxfp4GateUp, HipAffineGateUp, HipDenseGateUp, 
 
 
 class GateUp(GateUpStrategy):
-    """Resolves the strategy at construction and delegates; itself a GateUpStrategy."""
+    """The routed gate/up a block declares: picks its binding once, then forwards."""
 
     def __init__(self, leaf, *, hidden: int, inner: int, activation: Activation = "silu",
                  limit: float | None = None, bias: torch.Tensor | None = None,

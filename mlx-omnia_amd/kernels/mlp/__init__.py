@@ -99,7 +99,7 @@ _STRATEGIES = (HipDenseMlp, DefaultMlp)
 
 
 class Mlp(MlpStrategy):
-    """Resolves the strategy at construction and delegates; itself an MlpStrategy."""
+    """The dense MLP a block declares: picks its binding once, then forwards every call."""
 
     def __init__(self, leaf, *, hidden: int, inner: int, activation: Activation = "silu",
                  reference: bool = False) -> None:

@@ -32,13 +32,13 @@ __all__ = ["AngleAtlas", "rope_frequencies",
     "split_heads",
 ]
 
-# Order is preference: the first strategy that builds wins; the Core chain accepts
-# everything, so resolution never fails.
+# Tried left to right: the table-driven kernel, then the in-kernel-angle kernel; the
+# Core chain at the end takes any declaration.
 _STRATEGIES = (HipQkNormRope, HipRopeEpilogue, DefaultQkvRope)
 
 
 class QkvRope(QkvRopeStrategy):
-    """Resolves the strategy at construction and delegates; itself a QkvRopeStrategy."""
+    """The prologue a block declares: picks its binding once, then forwards every call."""
 
     def __init__(
         self,

@@ -27,7 +27,7 @@ FALLBACKS: dict[str, int] = {}
 
 
 def resolve(strategies: Iterable[Builds[S]], /, *args: Any, **kwargs: Any) -> S:
-    """Order is preference: the first strategy that builds wins."""
+    """The instance from the earliest strategy in `strategies` whose `build` accepts."""
     built = next(
         built for strategy in strategies if (built := strategy.build(*args, **kwargs)) is not None
     )

@@ -48,7 +48,7 @@ _STRATEGIES = (HipSoftmaxTopkRoute, HipOrdinalRoute, DefaultRoute)
 
 
 class Route(RouteStrategy):
-    """Resolves the strategy at construction and delegates; itself a RouteStrategy."""
+    """The routing a block declares: picks its binding once, then forwards every call."""
 
     def __init__(
         self,
