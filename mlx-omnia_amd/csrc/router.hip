@@ -763,21 +763,23 @@ struct SplitShape {
   static constexpr size_t kLogitBytes = static_cast<size_t>(kTileTokens) * E * 4;
   static constexpr size_t kLds = kTileBytes + kSlices * kLogitBytes + kTileTokens * 4 + 16 +
                                  static_cast<size_t>(kTileTokens) * E * 2;
-  // Each 32-wide step is two v_mfma_f32_16x16x16_bf16 with a zero accumulator (the low
-  // and high 8 bytes of each lane's operands: any split of k works, A and B split
-  // alike), each summing 16 exact products with at most 15 roundings, counted at a full
-  // ulp (30 half-ulps). With two tiles per walker the 2 kSteps half-step results of a
-  // (tile, slice) are summed in groups of kGroup, each in order (kGroup - 1 roundings:
-  // the first is a copy), and the group sums in a tree of depth 3 (at four tiles per
-  // walker the tree's registers would spill, and the half-steps are summed in order:
-  // 2 kSteps - 1 roundings); then the two slices. Each fp32 add on an element's path
-  // carries one half-ulp rounding of a partial sum bounded by A; 1% covers the rounding
-  // of A, delta and L +- delta.
+  // Each 32-wide step is one v_mfma_f32_16x16x32_bf16 with a zero accumulator, summing
+  // 32 exact products with at most 31 roundings, counted at a full ulp (62 half-ulps of
+  // a partial bounded by the step's Cauchy-Schwarz product; those sum to at most A).
+  // With two tiles per walker the kSteps step results of a (tile, slice) are summed in
+  // groups of kGroup, each in order (kGroup - 1 roundings: the first is a copy), and
+  // the four group sums in a tree of depth 2 (at four tiles per walker the tree's
+  // registers would spill, and the steps are summed in order: kSteps - 1 roundings);
+  // then the two slices. Each fp32 add on an element's path carries one half-ulp
+  // rounding of a partial sum bounded by A; 1% covers the rounding of A, delta and
+  // L +- delta. One MFMA per step rather than two 16x16x16 halves (30 half-ulps each
+  // at the half's own bound) doubles the internal term but halves the fp32 adds, which
+  // the walk's VALU time is made of.
   static constexpr int kGroup = 8;
   static constexpr bool kTree = kTilesPerWalker <= 2;
-  static constexpr int kChain = kTree ? (kGroup - 1) + 3 : 2 * kSteps - 1;
-  static constexpr float kDelta = (30.0f + kChain + (kSlices - 1)) * 1.01f / 16777216.0f;
-  static_assert(2 * kSteps == 8 * kGroup, "eight groups of half-steps per (tile, slice)");
+  static constexpr int kChain = kTree ? (kGroup - 1) + 2 : kSteps - 1;
+  static constexpr float kDelta = (62.0f + kChain + (kSlices - 1)) * 1.01f / 16777216.0f;
+  static_assert(kSteps == 4 * kGroup, "four groups of steps per (tile, slice)");
   static_assert(kTiles * kSlices % kWalkers == 0 && kWalkers % kSlices == 0, "shape");
   static_assert(kTileTokens == 2 * kRowWaves, "two rows per row wave");
 };
@@ -897,21 +899,28 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     const int r0 = 2 * wave;
     const int64_t t0 = first + r0, t1 = t0 + 1;
     const bool live0 = t0 < a.rows, live1 = t1 < a.rows;
+    // Every load issued before any arithmetic, none inside a branch (a row past the end
+    // loads the last row, in bounds, and is discarded): the waits then count loads
+    // exactly, so row 0's arithmetic starts as soon as its own data is in, while row 1
+    // is still arriving. The order is row 0, the norm weight, row 1.
+    const int64_t l0 = live0 ? t0 : a.rows - 1, l1 = live1 ? t1 : a.rows - 1;
     u32x4 x0[VPL], b0[VPL], x1[VPL], b1[VPL], wv[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int v = lane + i * kWave;
-      x0[i] = live0 ? load_nt(a.x + t0 * (H / 8) + v) : u32x4{0u, 0u, 0u, 0u};
-      b0[i] = live0 ? load_nt(a.branch + t0 * (H / 8) + v) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int v = lane + i * kWave;
-      x1[i] = live1 ? load_nt(a.x + t1 * (H / 8) + v) : u32x4{0u, 0u, 0u, 0u};
-      b1[i] = live1 ? load_nt(a.branch + t1 * (H / 8) + v) : u32x4{0u, 0u, 0u, 0u};
+      x0[i] = load_nt(a.x + l0 * (H / 8) + v);
+      b0[i] = load_nt(a.branch + l0 * (H / 8) + v);
     }
 #pragma unroll
     for (int i = 0; i < VPL; ++i) wv[i] = a.norm_weight[lane + i * kWave];  // L2-resident
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int v = lane + i * kWave;
+      x1[i] = load_nt(a.x + l1 * (H / 8) + v);
+      b1[i] = load_nt(a.branch + l1 * (H / 8) + v);
+    }
+    // Keeps the scheduler from sinking row 1's loads below row 0's arithmetic.
+    __builtin_amdgcn_sched_barrier(0);
     router_row<VPL>(x0, b0, wv, live0, t0, a.eps, lane, a, tile + r0 * kRowPitch, row_norm + r0);
     router_row<VPL>(x1, b1, wv, live1, t1, a.eps, lane, a, tile + (r0 + 1) * kRowPitch,
                     row_norm + r0 + 1);
@@ -923,40 +932,36 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   // k = (l / 16) * 8 .. + 8 of each 32-wide step.
   if (walker) {
     const f32x4 zero = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 acc[kTPW], l1[kTPW], l2[kTPW], l3[kTPW];  // group sum, tree levels
+    f32x4 acc[kTPW], l1[kTPW], l2[kTPW];  // group sum, tree levels
     const uint16_t* arow = tile + (lane % 16) * kRowPitch + slice * S::kSlice + (lane / 16) * 8;
     u32x4 av;
-    // Adds one half-step result at position h of this walker's order into tile tt's sum.
-    auto add_half = [&](int tt, int h, const f32x4& part) {
-      if (h % (S::kTree ? S::kGroup : 2 * kSteps) == 0) {
+    // Adds the step result at position n of this walker's order into tile tt's sum:
+    // in order inside a group of kGroup steps, then ((g0 + g1) + (g2 + g3)).
+    auto add_step = [&](int tt, int n, const f32x4& part) {
+      if (n % (S::kTree ? S::kGroup : kSteps) == 0) {
         acc[tt] = part;
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[tt][j] = acc[tt][j] + part[j];
       }
-      if (S::kTree && h % S::kGroup == S::kGroup - 1) {  // group g done: binary-counter fold
-        const int g = h / S::kGroup;
-        if (g % 2 == 0) {
+      if (S::kTree && n % S::kGroup == S::kGroup - 1) {
+        const int g = n / S::kGroup;
+        if (g == 0 || g == 2) {
           l1[tt] = acc[tt];
-        } else {
+        } else if (g == 1) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) l2[tt][j] = l1[tt][j] + acc[tt][j];
+        } else {  // g == 3: the tile's total
 #pragma unroll
           for (int j = 0; j < 4; ++j) l1[tt][j] = l1[tt][j] + acc[tt][j];
-          if (g % 4 == 1) {
-            l2[tt] = l1[tt];
-          } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) l2[tt][j] = l2[tt][j] + l1[tt][j];
-            if (g == 3) {
-              l3[tt] = l2[tt];
-            } else {  // g == 7: the tile's total
-#pragma unroll
-              for (int j = 0; j < 4; ++j) acc[tt][j] = l3[tt][j] + l2[tt][j];
-            }
-          }
+          for (int j = 0; j < 4; ++j) acc[tt][j] = l2[tt][j] + l1[tt][j];
         }
       }
     };
-#pragma unroll
+    // Fully unrolled: the ring is indexed by constants only (a partly unrolled loop
+    // would index it at run time and put it in scratch memory).
+#pragma clang loop unroll(full)
     for (int i = 0; i < kBlocks; ++i) {
       const int tt = i % kTPW;
       const int n = i / kTPW;  // position of the step in this walker's order
@@ -966,13 +971,9 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
       }
       const u32x4 b = ring[i % kRing];
       if (i + kRing < kBlocks) ring[i % kRing] = *reinterpret_cast<const u32x4*>(block_at(i + kRing));
-      // Halves taken from a cast of the whole vector: this hipcc compiles a bit cast of
-      // an ext-vector swizzle (av.zw) as one of its first elements.
-      const s16x8 a8 = __builtin_bit_cast(s16x8, av), b8 = __builtin_bit_cast(s16x8, b);
-      const f32x4 lo = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a8.s0123, b8.s0123, zero, 0, 0, 0);
-      const f32x4 hi = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a8.s4567, b8.s4567, zero, 0, 0, 0);
-      add_half(tt, 2 * n, lo);
-      add_half(tt, 2 * n + 1, hi);
+      const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, b), zero, 0, 0, 0);
+      add_step(tt, n, part);
     }
     // D layout: lane l holds column (expert) l % 16, rows (tokens) (l / 16) * 4 + i.
     float* out = slice == 0 ? logit_tile : logit_tile1;
@@ -1151,11 +1152,7 @@ namespace {
 
 int32_t launch_router(const RouterArgs& a, int64_t hidden, int64_t experts, hipStream_t stream) {
   if (hidden == 2048) {
-#ifdef ROUTER_OLD
-    return experts == 128 ? launch_fused<4, 128>(a, stream) : launch_fused<4, 256>(a, stream);
-#else
     return experts == 128 ? launch_split<128>(a, stream) : launch_split<256>(a, stream);
-#endif
   }
   return experts == 128 ? launch_fused<8, 128>(a, stream) : launch_fused<8, 256>(a, stream);
 }
