@@ -19,10 +19,14 @@ Method, per kernel:
 - achieved = algorithmic bytes per launch (each input read once, each output written
   once) / average launch duration.
 The CPU baseline is the repo's numpy oracle (a port of the reference's Core chains;
-MLX does not exist on these machines) timed on a bounded sample of the headline
-workload, single-threaded.
+MLX does not exist on these machines), timed on this host for every workload on a
+bounded sample of that workload's own shapes (about 0.8 s each, 3 s for the headline).
+Each `kernels[...]` entry carries its own `cpu_baseline` with the threads it used (one
+for elementwise numpy, the BLAS pool for legs that multiply matrices), the cores this
+process may use and the thread environment.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only NAME[,NAME]]
+       python bench.py --phase-clocks   (the fused router's per-phase wall clocks)
 """
 
 from __future__ import annotations
@@ -737,31 +741,336 @@ def time_workload(w: Workload, steps: int, warmup: int, device, graph_mode: bool
                 launch="hip graph" if graph_mode else "direct")
 
 
-def cpu_baseline(seconds: float = 12.0) -> dict:
-    """The numpy oracle (single-threaded port of the Core chain) on a bounded sample of
-    the headline workload: repeated 256-token slices of the T=4096 prefill shape."""
-    from oracle import rope
+def _bits(rng: np.random.Generator, shape, low: int = 0x3A00, high: int = 0x3D00,
+          signed: bool = True) -> np.ndarray:
+    """Random finite bf16 bit patterns (magnitudes 2^-11 .. 2^-5 by default), for large
+    CPU-leg operands whose values do not change the oracle's work."""
+    bits = rng.integers(low, high, size=shape, dtype=np.uint16)
+    if not signed:
+        return bits
+    return bits | (rng.integers(0, 2, size=shape, dtype=np.uint16) << np.uint16(15))
 
-    rng = np.random.default_rng(2)
-    tokens, hq, hkv, d, pairs = 256, 32, 8, 128, 64
+
+def _cpu_legs() -> dict:
+    """Per workload: a factory returning (run, algorithmic bytes one run stands for,
+    sample description, uses BLAS). Each run is the numpy oracle (a port of the
+    reference's Core chain) on a bounded sample of the workload's own shapes."""
+    from oracle import activations, add_norm, attention, embed, mlp, moe, route, rope
+    from oracle import affine, mxfp4, nvfp4
     from oracle.bf16 import from_float
 
-    raw_q = from_float(rng.standard_normal((tokens, hq, d)))
-    raw_k = from_float(rng.standard_normal((tokens, hkv, d)))
-    qw = from_float(1 + 0.1 * rng.standard_normal(d))
-    kw = from_float(1 + 0.1 * rng.standard_normal(d))
-    cos, sin = rope.angle_table(40960, pairs, 1e6)
-    bytes_per_token = 2 * (hq + hkv) * d * 2 + 2 * pairs * 4
+    rng = np.random.default_rng(42)
+
+    def bf(shape, scale=1.0, shift=0.0):
+        return from_float(shift + scale * rng.standard_normal(shape, dtype=np.float32))
+
+    def add_norm_leg(rows):
+        x, r, w = bf((rows, 2560)), bf((rows, 2560)), bf((2560,), 0.1, 1.0)
+        return (lambda: add_norm.add_rms_norm(x, r, w, 1e-6),
+                rows * 4 * 2 * 2560 + 2 * 2560, f"[{rows}, 2560], whole", False)
+
+    tables = {}
+
+    def angle_table():
+        if "t" not in tables:
+            tables["t"] = rope.angle_table(40960, 64, 1e6)
+        return tables["t"]
+
+    def qk_leg(tokens, total):
+        q, k = bf((tokens, 32, 128)), bf((tokens, 8, 128))
+        qw, kw = bf((128,), 0.1, 1.0), bf((128,), 0.1, 1.0)
+        cos, sin = angle_table()
+        return (lambda: rope.qk_norm_rope(q, k, qw, kw, cos, sin, int(rng.integers(0, 32768)),
+                                          1e-6, 64),
+                tokens * (2 * 40 * 128 * 2 + 2 * 64 * 4) + 2 * 128 * 2,
+                f"{tokens} of {total} tokens", False)
+
+    def epilogue_leg():
+        fused, qw, kw = bf((256, 48 * 128)), bf((128,), 0.1, 1.0), bf((128,), 0.1, 1.0)
+        return (lambda: rope.rope_epilogue(fused, 32, 8, 128, qw, kw, int(rng.integers(0, 32768)),
+                                           1e6, 1e-6),
+                256 * 2 * 40 * 128 * 2 + 2 * 128 * 2, "256 of 4096 tokens", False)
+
+    def swiglu_leg():
+        g, u = bf((64, 9728)), bf((64, 9728))
+        return (lambda: activations.swiglu(g, u), 3 * 64 * 9728 * 2, "64 of 8192 rows", False)
+
+    def softplus_leg():
+        a = bf((8192, 32))
+        a_log = rng.uniform(0, 2.7, 32).astype(np.float32)
+        dt_bias = (0.5 * rng.standard_normal(32)).astype(np.float32)
+        return (lambda: activations.gate_softplus(a, a_log, dt_bias),
+                8192 * 32 * 2 + 2 * 32 * 4 + 8192 * 32 * 4, "[8192, 32], whole", False)
+
+    def router_leg():
+        x, r, w = bf((256, 2048)), bf((256, 2048)), bf((2048,), 0.1, 1.0)
+        gate = bf((128, 2048), 0.02)
+        return (lambda: route.residual_rms_router(x, r, w, gate, 1e-6, 8),
+                256 * (4 * 2048 * 2 + 2 * 8 * 4) + 2048 * 2 + 128 * 2048 * 2,
+                "256 of 4096 tokens", True)
+
+    def embed_leg():
+        table = np.full((151936, 2560), 0x3C00, dtype=np.uint16)  # a gather: values do not matter
+        ids = rng.integers(0, 151936, 2048, dtype=np.int32)
+        cos, sin = angle_table()
+        return (lambda: embed.embed_atlas(ids, table, cos, sin, 0, 2048),
+                2048 * 4 + 2 * 2048 * 2560 * 2 + 2 * 2048 * 2 * 64 * 4,
+                "1 of 8 sequences (2048 tokens), full table", False)
+
+    # Routed experts: a stack of just the routed experts (the oracle only touches those).
+    def moe_leg(down):
+        chosen = np.arange(8, dtype=np.int32)
+        weights = rng.dirichlet(np.ones(8)).astype(np.float32)
+        if down:
+            stack, act, res = _bits(rng, (8, 2048, 768)), bf((8, 1536)), bf((2048,))
+            return (lambda: moe.down_combine(act, stack, chosen, weights, res),
+                    8 * 2048 * 768 * 2 + 8 * 1536 * 2 + 8 * 8 + 2 * 2048 * 2, "the 8 routed experts", True)
+        stack, x = _bits(rng, (8, 1536, 2048)), bf((2048,))
+        return (lambda: moe.gate_up(x, stack, chosen),
+                8 * 1536 * 2048 * 2 + 2048 * 2 + 8 * 4 + 8 * 1536 * 2, "the 8 routed experts", True)
+
+    def affine_stack(slots, rows, features):
+        words = rng.integers(0, 2**32, (slots, rows, features // 8), dtype=np.uint32)
+        scale = 4.0 / (16 * features ** 0.5)
+        scales = from_float(scale * (0.5 + rng.random((slots, rows, features // 64), dtype=np.float32)))
+        biases = from_float(-scale * 7.5 * np.ones((slots, rows, features // 64), dtype=np.float32))
+        return affine.Stack(words, scales, biases, 64, 4)
+
+    def affine_leg(down):
+        slots = 2  # of the workload's 8: the oracle's bit unpacking is slow
+        chosen = np.arange(slots)
+        weights = rng.dirichlet(np.ones(slots)).astype(np.float32)
+        if down:
+            stack, act, res = affine_stack(slots, 2048, 768), bf((slots, 768)), bf((2048,))
+            return (lambda: affine.down_combine(act, stack, chosen, weights, res),
+                    slots * 2048 * (768 // 2 + 4 * 12) + slots * (768 * 2 + 8) + 2 * 2048 * 2,
+                    f"{slots} of the 8 routed experts", True)
+        stack, x = affine_stack(slots, 1536, 2048), bf((2048,))
+        return (lambda: affine.gate_up(x, stack, chosen),
+                slots * 1536 * (2048 // 2 + 4 * 32) + 2048 * 2 + slots * (4 + 768 * 2),
+                f"{slots} of the 8 routed experts", True)
+
+    def mxfp4_leg(down):
+        slots = 1  # of the workload's 4
+        rows, features = (2880, 2880) if down else (5760, 2880)
+        stack = mxfp4.Stack(rng.integers(0, 2**32, (slots, rows, features // 8), dtype=np.uint32),
+                            rng.integers(119, 123, (slots, rows, features // 32), dtype=np.uint8),
+                            bf((slots, rows), 0.25))
+        row_bytes = features // 2 + features // 32 + 2
+        chosen = np.arange(slots)
+        if down:
+            act, weights, res = bf((slots, 2880)), np.ones(slots, dtype=np.float32), bf((2880,))
+            return (lambda: mxfp4.down_combine(act, stack, chosen, weights, res),
+                    slots * (2880 * row_bytes + 2880 * 2 + 8) + 2 * 2880 * 2,
+                    f"{slots} of the 4 routed experts", True)
+        x = bf((2880,))
+        return (lambda: mxfp4.gate_up(x, stack, chosen, 7.0),
+                slots * (5760 * row_bytes + 4 + 2880 * 2) + 2880 * 2,
+                f"{slots} of the 4 routed experts", True)
+
+    def nvfp4_leg(down, ordinal=False):
+        rows, features = (2048, 768) if down else (1536, 2048)
+        stack = nvfp4.Stack(rng.integers(0, 2**32, (8, rows, features // 8), dtype=np.uint32),
+                            rng.integers(0x18, 0x28, (8, rows, features // 16), dtype=np.uint8))
+        row_bytes = features // 2 + features // 16
+        if down:
+            act, weights, res = bf((8, 768)), rng.dirichlet(np.ones(8)).astype(np.float32), bf((2048,))
+            return (lambda: nvfp4.down_combine(act, stack, np.arange(8), weights, res),
+                    8 * 2048 * row_bytes + 8 * 768 * 2 + 8 * 8 + 2 * 2048 * 2, "the 8 routed experts", True)
+        x = bf((2048,))
+        if ordinal:  # the 8 lowest of 128 keys name experts 0..7, the stack's slots
+            keys = np.concatenate([rng.permutation(8), 8 + rng.permutation(120)]).astype(np.uint32)
+            return (lambda: nvfp4.gate_up(x, stack, np.argsort(keys, kind="stable")[:8]),
+                    8 * 1536 * row_bytes + 2048 * 2 + 128 * 4 + 8 * 768 * 2,
+                    "the 8 routed experts, ranked from 128 keys", True)
+        return (lambda: nvfp4.gate_up(x, stack, np.arange(8)),
+                8 * 1536 * row_bytes + 2048 * 2 + 8 * 4 + 8 * 768 * 2, "the 8 routed experts", True)
+
+    def mlp_leg(down):
+        if down:
+            w, act, res = _bits(rng, (2560, 9728)), bf((9728,)), bf((2560,))
+            return (lambda: mlp.down_residual(act, w, res),
+                    2560 * 9728 * 2 + 9728 * 2 + 2 * 2560 * 2, "[2560, 9728], whole", True)
+        inner = 9728 // 8  # an eighth of the gate rows with their up rows: a smaller GEMV
+        w, x = _bits(rng, (2 * inner, 2560)), bf((2560,))
+        return (lambda: mlp.gate_up_swiglu(x, w),
+                2 * inner * 2560 * 2 + 2560 * 2 + inner * 2, "1/8 of the gate and up rows", True)
+
+    def attention_leg(rows):
+        kc, vc = _bits(rng, (8, rows, 128)), _bits(rng, (8, rows, 128))
+        q, k, v = bf((32 * 128,)), bf((8 * 128,)), bf((8 * 128,))
+        qw, kw = bf((128,), 0.1, 1.0), bf((128,), 0.1, 1.0)
+        cos, sin = angle_table()
+        row = np.concatenate([cos[rows - 1], sin[rows - 1]]).astype(np.float32)
+        byte_count = (2 * 8 * rows * 128 * 2 + 48 * 128 * 2 + 32 * 128 * 2 + 2 * 8 * 128 * 2
+                      + 2 * 128 * 2 + 2 * 64 * 4)
+        return (lambda: attention.decode_step(q, k, v, qw, kw, row, kc, vc, rows - 1, window=0,
+                                              scale=128 ** -0.5, eps=1e-6, pairs=64),
+                byte_count, f"position {rows - 1} of a {rows}-row cache, whole", True)
+
+    return {
+        "add_rms_norm_prefill": lambda: add_norm_leg(512),
+        "add_rms_norm_decode": lambda: add_norm_leg(1),
+        "qk_norm_rope_prefill": lambda: qk_leg(256, 4096),
+        "qk_norm_rope_decode": lambda: qk_leg(64, 64),
+        "rope_epilogue_prefill": epilogue_leg,
+        "swiglu": swiglu_leg,
+        "gate_softplus": softplus_leg,
+        "residual_rms_router": router_leg,
+        "embed_atlas": embed_leg,
+        "moe_gate_up_decode": lambda: moe_leg(False),
+        "moe_down_combine_decode": lambda: moe_leg(True),
+        "moe_affine_gate_up_decode": lambda: affine_leg(False),
+        "moe_affine_down_combine_decode": lambda: affine_leg(True),
+        "moe_mxfp4_gate_up_decode": lambda: mxfp4_leg(False),
+        "moe_mxfp4_down_combine_decode": lambda: mxfp4_leg(True),
+        "moe_nvfp4_gate_up_decode": lambda: nvfp4_leg(False),
+        "moe_nvfp4_gate_up_ordinal_decode": lambda: nvfp4_leg(False, ordinal=True),
+        "moe_nvfp4_down_combine_decode": lambda: nvfp4_leg(True),
+        "dense_mlp_gate_up_decode": lambda: mlp_leg(False),
+        "dense_mlp_down_decode": lambda: mlp_leg(True),
+        "attention_decode_32k": lambda: attention_leg(32768),
+        "attention_decode_4k": lambda: attention_leg(4096),
+    }
+
+
+def _thread_settings() -> tuple[int, dict, int]:
+    """(BLAS threads in effect, the thread environment, cores this process may use)."""
+    env = {name: os.environ.get(name) for name in
+           ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")}
+    blas = 1
+    try:
+        from threadpoolctl import threadpool_info
+
+        pools = [p for p in threadpool_info() if p.get("user_api") == "blas"]
+        if pools:
+            blas = int(pools[0].get("num_threads") or 1)
+    except Exception:  # threadpoolctl absent or unable to inspect: report one thread
+        blas = 1
+    return blas, env, len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(name: str, full_bytes: int, seconds: float = 0.8) -> dict | None:
+    """The numpy oracle on a bounded sample of one workload, timed on this host: runs
+    for at least `seconds` (one run at least); value = algorithmic bytes per second.
+    `cores` is the threads the leg used: one for elementwise numpy, the BLAS pool's size
+    for legs whose oracle multiplies matrices (numpy's `@` runs in BLAS)."""
+    legs = _cpu_legs()
+    if name not in legs:
+        return None
+    run, sample_bytes, sample, uses_blas = legs[name]()
+    run()  # untimed: first touch of the sample's pages
     done, start = 0, time.perf_counter()
-    while time.perf_counter() - start < seconds:
-        offset = int(rng.integers(0, 32768))
-        rope.qk_norm_rope(raw_q, raw_k, qw, kw, cos, sin, offset, 1e-6, pairs)
-        done += tokens
+    while done == 0 or time.perf_counter() - start < seconds:
+        run()
+        done += 1
     elapsed = time.perf_counter() - start
-    return dict(value=round(done * bytes_per_token / elapsed / 1e9, 4), unit="GB/s",
-                cores=1, kind="port",
-                sample=f"numpy oracle (oracle/rope.py) on {done} tokens of the T=4096 "
-                       f"q/k shape in 256-token slices, {elapsed:.1f} s, one thread")
+    blas, env, affinity = _thread_settings()
+    rate = done * sample_bytes / elapsed
+    return dict(value=round(rate / 1e9, 4), unit="GB/s",
+                us_per_launch=round(full_bytes / rate * 1e6, 1),
+                cores=blas if uses_blas else 1, kind="port",
+                sample=f"numpy oracle, {sample}: {done} run(s) in {elapsed:.2f} s",
+                affinity_cores=affinity, threads_env=env)
+
+
+PHASES = ("entry", "row 0 done", "phase 1 done", "tile complete", "walk done",
+          "logits complete", "selection + tasks", "task list complete", "recomputed", "written")
+
+
+def router_phase_clocks(device, stamped: int = 8, timed: int = 200) -> dict:
+    """Per-phase wall clocks of the fused residual router at configs[4] ([4096, 2048],
+    128 experts, k = 8), from `libomnia_router_clocks.so` (the same source compiled with
+    its phase marks on): each of `stamped` launches, taken in the rotation's steady state,
+    records the 100 MHz wall clock of every wave at ten phase boundaries; the summary is
+    each boundary's spread over the 256 workgroups (median over launches of each
+    statistic), in µs from the launch's earliest entry. `launch_us` is the event-timed
+    mean of `timed` back-to-back launches of the diagnostic build."""
+    import ctypes
+
+    import torch
+
+    path = REPO / "mlx-omnia_amd" / "libomnia_router_clocks.so"
+    if not path.exists():
+        raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(path))
+    lib.omnia_router_pack_bytes.restype = ctypes.c_int64
+    lib.omnia_router_pack_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64]
+    lib.omnia_pack_router_weight.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                             ctypes.c_void_p, ctypes.c_void_p]
+    lib.omnia_residual_rms_router.argtypes = ([ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4
+                                              + [ctypes.c_float] + [ctypes.c_void_p] * 6)
+    lib.omnia_router_phase_clocks_set.argtypes = [ctypes.c_void_p]
+    lib.omnia_last_error.restype = ctypes.c_char_p
+    rows, hidden, experts, k = 4096, 2048, 128, 8
+    groups, slots = rows // 16, len(PHASES)
+    rng = np.random.default_rng(7)
+    copies = 8  # 8 x 68 MB: past the 256 MB Infinity Cache
+    xs = [_to_bf16_device(_normal(rng, (rows, hidden)), device) for _ in range(copies)]
+    rs = [_to_bf16_device(_normal(rng, (rows, hidden)), device) for _ in range(copies)]
+    w = _to_bf16_device(_normal(rng, (hidden,), 0.1, 1.0), device)
+    gate = _to_bf16_device(_normal(rng, (experts, hidden), 0.02), device)
+    outs = [dict(s=torch.empty_like(xs[0]), n=torch.empty_like(xs[0]),
+                 i=torch.empty((rows, k), dtype=torch.int32, device=device),
+                 w=torch.empty((rows, k), dtype=torch.float32, device=device)) for _ in range(copies)]
+    stream = torch.cuda.current_stream(device)
+    handle = ctypes.c_void_p(stream.cuda_stream)
+    packed = torch.empty(lib.omnia_router_pack_bytes(experts, hidden), dtype=torch.uint8,
+                         device=device)
+    if lib.omnia_pack_router_weight(gate.data_ptr(), experts, hidden, packed.data_ptr(), handle):
+        raise RuntimeError(lib.omnia_last_error().decode())
+
+    def launch(c: int) -> None:
+        o = outs[c]
+        if lib.omnia_residual_rms_router(xs[c].data_ptr(), rs[c].data_ptr(), w.data_ptr(),
+                                         packed.data_ptr(), rows, hidden, experts, k,
+                                         ctypes.c_float(1e-6), o["s"].data_ptr(), o["n"].data_ptr(),
+                                         None, o["i"].data_ptr(), o["w"].data_ptr(), handle):
+            raise RuntimeError(lib.omnia_last_error().decode())
+
+    for i in range(400):
+        launch(i % copies)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(timed):
+        launch(i % copies)
+    end.record(stream)
+    torch.cuda.synchronize(device)
+    launch_us = start.elapsed_time(end) * 1000.0 / timed
+    records = []
+    for rep in range(stamped):
+        buffer = torch.zeros(groups * 16 * slots, dtype=torch.int64, device=device)
+        lib.omnia_router_phase_clocks_set(ctypes.c_void_p(buffer.data_ptr()))
+        launch(rep % copies)
+        lib.omnia_router_phase_clocks_set(None)
+        for i in range(8):  # back to the steady state before the next stamped launch
+            launch((rep + 1 + i) % copies)
+        records.append(buffer)
+    torch.cuda.synchronize(device)
+    walkers = np.arange(16) >= 8
+    per_launch = []
+    for buffer in records:
+        ticks = buffer.view(groups, 16, slots).cpu().numpy().astype(np.int64)
+        rel = (ticks - ticks[:, :, 0].min()) * 0.01  # 100 MHz ticks -> µs
+        stats = {}
+        for j, name in enumerate(PHASES):
+            if j in (1, 2):
+                col = rel[:, ~walkers, j]  # row waves only
+            elif j == 4:
+                col = rel[:, walkers, j]   # walkers only
+            elif j == 9:
+                col = rel[:, :, j].max(axis=1)  # a workgroup's last wave
+            else:
+                col = rel[:, 0, j]         # barrier exits: every wave alike
+            stats[name] = [float(np.percentile(col, q)) for q in (10, 50, 90)] + [float(col.max())]
+        per_launch.append(stats)
+    summary = {name: [round(float(np.median([s[name][q] for s in per_launch])), 2) for q in range(4)]
+               for name in PHASES}
+    return dict(kernel="residual_rms_router_split_kernel<128>",
+                workload="x, residual bf16 [4096, 2048], router [128, 2048], k = 8",
+                launch_us=round(launch_us, 3), stamped_launches=stamped,
+                columns=["p10", "median", "p90", "max"], unit="us from the launch's first entry",
+                phases=summary)
 
 
 def _traffic(kernel_name: str) -> int | None:
@@ -786,6 +1095,9 @@ def main() -> int:
     parser.add_argument("--graph", action="store_true", help="also time a captured HIP graph")
     parser.add_argument("--ceiling", action="store_true",
                         help="also time a plain device copy moving each workload's bytes")
+    parser.add_argument("--phase-clocks", action="store_true",
+                        help="print the fused router's per-phase wall clocks (diagnostic "
+                             "build) as one JSON line instead of the bench line")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not run "
@@ -802,6 +1114,9 @@ def main() -> int:
         print("bench.py: no ROCm device visible", file=sys.stderr)
         return 1
     device = torch.device("cuda:0")
+    if args.phase_clocks:
+        print(json.dumps(router_phase_clocks(device)), flush=True)
+        return 0
     only = [n for n in args.only.split(",") if n]
     selected = [w for w in workloads() if ((w.name in only) if only else w.default)]
     results = {}
@@ -825,7 +1140,18 @@ def main() -> int:
 
     head = results.get(HEADLINE) or next(iter(results.values()))
     head_name = HEADLINE if HEADLINE in results else next(iter(results))
-    baseline = None if args.no_cpu else cpu_baseline()
+    baseline = None
+    if not args.no_cpu:
+        # The numpy oracle on each workload's own shapes (bounded samples), after the GPU
+        # timing; the headline's sample runs longest.
+        for name, r in results.items():
+            seconds = 3.0 if name == head_name else 0.8
+            r["cpu_baseline"] = cpu_baseline(name, r["bytes"], seconds)
+            if r["cpu_baseline"]:
+                print(f"[bench] {name}: CPU oracle {r['cpu_baseline']['value']} GB/s "
+                      f"({r['cpu_baseline']['us_per_launch']} us per launch, "
+                      f"{r['cpu_baseline']['cores']} core(s))", file=sys.stderr, flush=True)
+        baseline = results[head_name].get("cpu_baseline")
     line = {
         "metric": METRIC,
         "value": head["GBps"],
@@ -848,6 +1174,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": head["frac"],
             "traffic": _traffic(head_name),
+            "traffic_source": "profiles/hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, "
+                              "WRITE_SIZE of this workload, scaled by a copy of known size); "
+                              "not measured in this run",
         },
         "cpu_baseline": baseline,
         "kernels": results,

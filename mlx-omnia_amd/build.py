@@ -50,9 +50,15 @@ def _hipcc() -> str:
     return found
 
 
-def _compile(source: Path) -> Path:
-    obj = OBJDIR / (source.name + ".o")
-    cmd = [_hipcc(), *FLAGS, "-c", str(source), "-o", str(obj)]
+# Diagnostic library: the router and the ABI bookkeeping compiled with the phase-clock
+# marks on (`bench.py --phase-clocks` loads it). Not loaded by the package.
+CLOCKS_LIBRARY = PACKAGE / "libomnia_router_clocks.so"
+CLOCKS_SOURCES = ("router.hip", "abi.cpp")
+
+
+def _compile(source: Path, defines: tuple[str, ...] = (), tag: str = "") -> Path:
+    obj = OBJDIR / (source.name + tag + ".o")
+    cmd = [_hipcc(), *FLAGS, *defines, "-c", str(source), "-o", str(obj)]
     if source.suffix == ".hip":
         cmd[1:1] = ["-x", "hip"]
     done = subprocess.run(cmd, capture_output=True, text=True)
@@ -61,24 +67,36 @@ def _compile(source: Path) -> Path:
     return obj
 
 
-def build_library(verbose: bool = True) -> Path:
-    """Compile every source under `csrc/` and link `libomnia_hip.so`; returns its path."""
-    OBJDIR.mkdir(exist_ok=True)
-    sources = sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp")])
-    if not sources:
-        raise FileNotFoundError(f"no sources under {CSRC}")
-    workers = min(len(sources), max(1, (os.cpu_count() or 2) // 2), 8)
-    with ThreadPoolExecutor(max_workers=workers) as pool:
-        objects = list(pool.map(_compile, sources))
-    staged = LIBRARY.with_suffix(".so.tmp")
+def _link(objects: list[Path], target: Path) -> None:
+    staged = target.with_suffix(".so.tmp")
     cmd = [_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objects),
            "-o", str(staged)]
     done = subprocess.run(cmd, capture_output=True, text=True)
     if done.returncode != 0:
         raise RuntimeError(f"link failed:\n{done.stdout}\n{done.stderr}")
-    os.replace(staged, LIBRARY)
+    os.replace(staged, target)
+
+
+def build_library(verbose: bool = True) -> Path:
+    """Compile every source under `csrc/` and link `libomnia_hip.so` (and the router's
+    phase-clock diagnostic library); returns the product library's path."""
+    OBJDIR.mkdir(exist_ok=True)
+    sources = sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp")])
+    if not sources:
+        raise FileNotFoundError(f"no sources under {CSRC}")
+    clock_sources = [CSRC / name for name in CLOCKS_SOURCES]
+    workers = min(len(sources) + len(clock_sources), max(1, (os.cpu_count() or 2) // 2), 8)
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        product = [pool.submit(_compile, source) for source in sources]
+        clocks = [pool.submit(_compile, source, ("-DOMNIA_PHASE_CLOCKS",), ".clocks")
+                  for source in clock_sources]
+        objects = [job.result() for job in product]
+        clock_objects = [job.result() for job in clocks]
+    _link(objects, LIBRARY)
+    _link(clock_objects, CLOCKS_LIBRARY)
     if verbose:
-        print(f"built {LIBRARY.relative_to(REPO)} from {len(sources)} sources", flush=True)
+        print(f"built {LIBRARY.relative_to(REPO)} from {len(sources)} sources "
+              f"(and {CLOCKS_LIBRARY.name})", flush=True)
     return LIBRARY
 
 

@@ -404,7 +404,28 @@ struct RouterArgs {
   int64_t rows;
   int k;
   float eps;
+#ifdef OMNIA_PHASE_CLOCKS
+  uint64_t* clocks;               // [workgroups, 16 waves, kClockSlots] or null
+#endif
 };
+
+// Phase clocks: a diagnostic build (-DOMNIA_PHASE_CLOCKS, libomnia_router_clocks.so)
+// records the 100 MHz wall clock (s_memrealtime) at the phase boundaries of the H = 2048
+// kernel, one vector store per wave from lane 0, into a buffer set with
+// omnia_router_phase_clocks_set. The product library compiles the marks to nothing.
+constexpr int kClockSlots = 10;
+#ifdef OMNIA_PHASE_CLOCKS
+#define OMNIA_CLOCK(args, wave, lane, slot)                                                   \
+  do {                                                                                        \
+    if ((lane) == 0 && (args).clocks != nullptr)                                              \
+      (args).clocks[(static_cast<int64_t>(blockIdx.x) * kWaves + (wave)) * kClockSlots + (slot)] = \
+          static_cast<uint64_t>(wall_clock64());                                              \
+  } while (0)
+#else
+#define OMNIA_CLOCK(args, wave, lane, slot) \
+  do {                                      \
+  } while (0)
+#endif
 
 template <int VPL, int E>
 struct FusedShape {
@@ -890,6 +911,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
 #pragma unroll
   for (int v = 0; v < V; ++v) bias[v] = a.bias ? a.bias[lane + v * kWave] : 0.0f;
 
+  OMNIA_CLOCK(a, wave, lane, 0);  // entry
   u32x4 ring[kRing];
   if (walker) {
 #pragma unroll
@@ -922,10 +944,13 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     // Keeps the scheduler from sinking row 1's loads below row 0's arithmetic.
     __builtin_amdgcn_sched_barrier(0);
     router_row<VPL>(x0, b0, wv, live0, t0, a.eps, lane, a, tile + r0 * kRowPitch, row_norm + r0);
+    OMNIA_CLOCK(a, wave, lane, 1);  // row 0 normalized and stored
     router_row<VPL>(x1, b1, wv, live1, t1, a.eps, lane, a, tile + (r0 + 1) * kRowPitch,
                     row_norm + r0 + 1);
   }
+  OMNIA_CLOCK(a, wave, lane, 2);  // phase 1 done (walkers: ring issued)
   lds_barrier();
+  OMNIA_CLOCK(a, wave, lane, 3);  // tile complete
 
   // Phase 2 (walkers): logits = tile x W^T over the walker's slice for its tiles. Lane l
   // feeds row (token) l % 16 of A and column (expert) l % 16 of B, both over
@@ -983,8 +1008,10 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
 #pragma unroll
       for (int i = 0; i < 4; ++i) out[((lane / 16) * 4 + i) * E + e] = acc[tt][i];
     }
+    OMNIA_CLOCK(a, wave, lane, 4);  // walk done
   }
   lds_barrier();
+  OMNIA_CLOCK(a, wave, lane, 5);  // logits complete
 
   // Phase 3: as in residual_rms_router_kernel, one token per wave; the recomputations
   // go to the walkers only.
@@ -1029,7 +1056,9 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
       if (need[v]) tasks[base + below] = static_cast<uint16_t>(r * E + lane + v * kWave);
     }
   }
+  OMNIA_CLOCK(a, wave, lane, 6);  // bounds, selection on them, tasks posted
   lds_barrier();
+  OMNIA_CLOCK(a, wave, lane, 7);  // task list complete
   uint32_t* exact_bits = reinterpret_cast<uint32_t*>(logit_tile);
   const int count = *task_count;
   if (walker) {
@@ -1047,6 +1076,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     }
   }
   lds_barrier();
+  OMNIA_CLOCK(a, wave, lane, 8);  // recomputations done
   if (!active) return;  // no barrier follows
   if (refined) {
 #pragma unroll
@@ -1060,6 +1090,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   }
   if (sigmoid) {
     sigmoid_finish<V, E>(bits, bias, a, t, lane);
+    OMNIA_CLOCK(a, wave, lane, 9);  // token written
     return;
   }
   if (refined || exact_all) {
@@ -1068,6 +1099,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     select_topk<V>(keys, a.k, lane, chosen);
   }
   write_winners(chosen, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
+  OMNIA_CLOCK(a, wave, lane, 9);  // token written
 }
 
 template <int E>
@@ -1150,7 +1182,14 @@ extern "C" int32_t omnia_pack_router_weight(const uint16_t* router_weight, int64
 namespace omnia {
 namespace {
 
-int32_t launch_router(const RouterArgs& a, int64_t hidden, int64_t experts, hipStream_t stream) {
+#ifdef OMNIA_PHASE_CLOCKS
+uint64_t* phase_clocks = nullptr;  // set by omnia_router_phase_clocks_set
+#endif
+
+int32_t launch_router(RouterArgs a, int64_t hidden, int64_t experts, hipStream_t stream) {
+#ifdef OMNIA_PHASE_CLOCKS
+  a.clocks = hidden == 2048 ? phase_clocks : nullptr;
+#endif
   if (hidden == 2048) {
     return experts == 128 ? launch_split<128>(a, stream) : launch_split<256>(a, stream);
   }
@@ -1254,3 +1293,11 @@ extern "C" int32_t omnia_sigmoid_topk(const void* logits, int64_t stride, int32_
 #undef OMNIA_SIGMOID_TOPK
   return launched("sigmoid_topk");
 }
+
+#ifdef OMNIA_PHASE_CLOCKS
+// Diagnostic build only: the buffer the H = 2048 router kernels record their phase
+// clocks into ([workgroups, 16, 10] uint64, 100 MHz ticks), or null to stop recording.
+extern "C" void omnia_router_phase_clocks_set(void* buffer) {
+  omnia::phase_clocks = static_cast<uint64_t*>(buffer);
+}
+#endif
