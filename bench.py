@@ -230,6 +230,26 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.gate_softplus(a["a"], a["a_log"], a["dt_bias"], out=a["g"]),
     ))
 
+    # configs[3] as one dispatch: both gated activations in one grid.
+    def setup_gated(device, copies):
+        sets = setup_swiglu(device, copies)
+        softplus = setup_softplus(device, copies)
+        for entry, extra in zip(sets, softplus):
+            entry.update(a=extra["a"], a_log=extra["a_log"], dt_bias=extra["dt_bias"],
+                         g_out=extra["g"])
+        return sets
+
+    out.append(Workload(
+        name="gated_activations",
+        kernel="gated_activations_kernel",
+        description="SwiGLU gate, up bf16 [8192, 9728] and gate-softplus a bf16 [8192, 32] "
+                    "(A_log, dt_bias fp32 [32]) in one dispatch",
+        bytes_per_launch=3 * 8192 * 9728 * 2 + 8192 * 32 * 2 + 2 * 32 * 4 + 8192 * 32 * 4,
+        setup=setup_gated,
+        launch=lambda a: ops.gated_activations(a["g"], a["u"], a["a"], a["a_log"], a["dt_bias"],
+                                               y=a["y"], g=a["g_out"]),
+    ))
+
     # residual add + RMSNorm + router projection + softmax top-8 (Qwen3-30B-A3B).
     def setup_router(device, copies, rows=4096, hidden=2048, experts=128, k=8):
         rng = np.random.default_rng(7)
@@ -802,6 +822,12 @@ def _cpu_legs() -> dict:
         return (lambda: activations.gate_softplus(a, a_log, dt_bias),
                 8192 * 32 * 2 + 2 * 32 * 4 + 8192 * 32 * 4, "[8192, 32], whole", False)
 
+    def gated_leg():
+        run_swiglu, swiglu_bytes, _, _ = swiglu_leg()
+        run_softplus, softplus_bytes, _, _ = softplus_leg()
+        return (lambda: (run_swiglu(), run_softplus()), swiglu_bytes + softplus_bytes,
+                "64 of 8192 SwiGLU rows and the whole [8192, 32] gate", False)
+
     def router_leg():
         x, r, w = bf((256, 2048)), bf((256, 2048)), bf((2048,), 0.1, 1.0)
         gate = bf((128, 2048), 0.02)
@@ -916,6 +942,7 @@ def _cpu_legs() -> dict:
         "rope_epilogue_prefill": epilogue_leg,
         "swiglu": swiglu_leg,
         "gate_softplus": softplus_leg,
+        "gated_activations": gated_leg,
         "residual_rms_router": router_leg,
         "embed_atlas": embed_leg,
         "moe_gate_up_decode": lambda: moe_leg(False),

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 12
+#define OMNIA_ABI_VERSION 13
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -142,6 +142,20 @@ int32_t omnia_swiglu(const uint16_t* gate, int64_t gate_stride, const uint16_t* 
 int32_t omnia_gate_softplus(const uint16_t* a, int64_t a_stride, const float* a_log,
                             const float* dt_bias, float* out, int64_t rows, int64_t heads,
                             hipStream_t stream);
+
+/* Both gated activations in one dispatch: omnia_swiglu over gate/up -> y [rows, inner]
+ * and omnia_gate_softplus over a -> g [a_rows, heads], with the same arithmetic and
+ * results as the two entries. heads must be even, a's row stride even, a 4-byte and
+ * A_log, dt_bias, g 8-byte aligned; either part may be empty (rows or a_rows 0).
+ * Replaces: the pair of Core chains core/layers.py:249-250,284-287 (SwiGLU) and
+ * models/qwen3_5/layers/deltanet.py:222-224 (gate-softplus), issued as one launch; the
+ * reference has no fused form, so this is the one-dispatch answer to the gate-softplus's
+ * launch cost at small sizes. */
+int32_t omnia_gated_activations(const uint16_t* gate, int64_t gate_stride, const uint16_t* up,
+                                int64_t up_stride, uint16_t* y, int64_t rows, int64_t inner,
+                                const uint16_t* a, int64_t a_stride, const float* a_log,
+                                const float* dt_bias, float* g, int64_t a_rows, int64_t heads,
+                                hipStream_t stream);
 
 /* Softmax -> top-k -> renormalise over given router logits, one row per token:
  *   indices[r, :k] = the k largest bf16 logits of row r in descending order, an exact

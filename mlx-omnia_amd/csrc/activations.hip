@@ -163,6 +163,75 @@ unsigned blocks_for(int64_t items) {
   return static_cast<unsigned>((items + kBlock - 1) / kBlock);
 }
 
+// Both gated activations of a layer in one grid (the SwiGLU and the gate-softplus of
+// configs[3]): blocks [0, softplus_blocks) run the gate-softplus, one pair of heads per
+// lane as gate_softplus_kernel does; the rest stream the SwiGLU, one vector per lane as
+// swiglu_flat_kernel / swiglu_rows_kernel do. The gate-softplus blocks come first, so
+// their fp64 work runs beside the SwiGLU stream rather than after its last blocks.
+struct GatedArgs {
+  const uint16_t* gate;
+  int64_t gate_stride;
+  const uint16_t* up;
+  int64_t up_stride;
+  uint16_t* y;
+  int64_t rows;
+  uint32_t row_vectors;
+  int64_t vectors;
+  const uint16_t* a;
+  int64_t a_stride;
+  const float* a_log;
+  const float* dt_bias;
+  float* g;
+  int64_t a_rows;
+  int heads;
+  unsigned softplus_blocks;
+};
+
+// The gate-softplus blocks hold -exp(A_log) of up to kDecayHeads heads in LDS, each
+// computed once per block rather than once per element (one fp64 exp of three).
+constexpr int kDecayHeads = kBlock;
+
+template <bool kFlat>
+__global__ __launch_bounds__(kBlock) void gated_activations_kernel(GatedArgs p) {
+  if (blockIdx.x < p.softplus_blocks) {  // block-uniform
+    __shared__ float decay[kDecayHeads];
+    const bool cached = p.heads <= kDecayHeads;
+    if (cached && static_cast<int>(threadIdx.x) < p.heads) {
+      decay[threadIdx.x] = -static_cast<float>(exp(static_cast<double>(p.a_log[threadIdx.x])));
+    }
+    __syncthreads();
+    const int head_pairs = p.heads / 2;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= p.a_rows * head_pairs) return;
+    const int64_t r = i / head_pairs;
+    const int h = static_cast<int>(i - r * head_pairs) * 2;
+    const uint32_t x = *reinterpret_cast<const uint32_t*>(p.a + r * p.a_stride + h);
+    const f32x2 bb = *reinterpret_cast<const f32x2*>(p.dt_bias + h);
+    f32x2 o;
+    if (cached) {  // the same fp32 steps as gate_softplus1
+      o = f32x2{decay[h] * softplus_f32(bf16_lo(x) + bb.x), decay[h + 1] * softplus_f32(bf16_hi(x) + bb.y)};
+    } else {
+      const f32x2 la = *reinterpret_cast<const f32x2*>(p.a_log + h);
+      o = f32x2{gate_softplus1(bf16_lo(x), la.x, bb.x), gate_softplus1(bf16_hi(x), la.y, bb.y)};
+    }
+    *reinterpret_cast<f32x2*>(p.g + r * p.heads + h) = o;
+    return;
+  }
+  const int64_t i = static_cast<int64_t>(blockIdx.x - p.softplus_blocks) * kBlock + threadIdx.x;
+  if (i >= p.vectors) return;
+  if constexpr (kFlat) {
+    const u32x4 g = load_nt(reinterpret_cast<const u32x4*>(p.gate) + i);
+    const u32x4 u = load_nt(reinterpret_cast<const u32x4*>(p.up) + i);
+    store_nt(reinterpret_cast<u32x4*>(p.y) + i, swiglu8(g, u));
+  } else {
+    const int64_t r = i / p.row_vectors;
+    const int64_t c = (i - r * p.row_vectors) * 8;
+    const u32x4 g = load_nt(reinterpret_cast<const u32x4*>(p.gate + r * p.gate_stride + c));
+    const u32x4 u = load_nt(reinterpret_cast<const u32x4*>(p.up + r * p.up_stride + c));
+    store_nt(reinterpret_cast<u32x4*>(p.y + r * p.row_vectors * 8 + c), swiglu8(g, u));
+  }
+}
+
 }  // namespace
 }  // namespace omnia
 
@@ -221,4 +290,53 @@ extern "C" int32_t omnia_gate_softplus(const uint16_t* a, int64_t a_stride, cons
         a, a_stride, a_log, dt_bias, out, rows, static_cast<int>(heads));
   }
   return launched("gate_softplus");
+}
+
+extern "C" int32_t omnia_gated_activations(const uint16_t* gate, int64_t gate_stride,
+                                           const uint16_t* up, int64_t up_stride, uint16_t* y,
+                                           int64_t rows, int64_t inner, const uint16_t* a,
+                                           int64_t a_stride, const float* a_log,
+                                           const float* dt_bias, float* g, int64_t a_rows,
+                                           int64_t heads, hipStream_t stream) {
+  using namespace omnia;
+  OMNIA_REQUIRE(rows >= 0 && inner > 0 && inner % 8 == 0,
+                "gated_activations: inner must be a positive multiple of 8");
+  OMNIA_REQUIRE(gate_stride >= inner && up_stride >= inner && gate_stride % 8 == 0 &&
+                    up_stride % 8 == 0,
+                "gated_activations: row strides must be >= inner and multiples of 8");
+  OMNIA_REQUIRE(rows * (inner / 8) < (int64_t{1} << 40), "gated_activations: too large");
+  OMNIA_REQUIRE(inner / 8 < (int64_t{1} << 31), "gated_activations: rows too wide");
+  OMNIA_REQUIRE(a_rows >= 0 && heads > 0 && heads % 2 == 0 && heads <= (int64_t{1} << 20),
+                "gated_activations: heads must be even and positive");
+  OMNIA_REQUIRE(a_stride >= heads && a_stride % 2 == 0,
+                "gated_activations: a's row stride must be even and >= heads");
+  OMNIA_REQUIRE(a_rows * heads < (int64_t{1} << 40), "gated_activations: a too large");
+  if (rows == 0 && a_rows == 0) return 0;
+  OMNIA_REQUIRE(rows == 0 || (gate && up && y), "gated_activations: null SwiGLU pointer");
+  OMNIA_REQUIRE(a_rows == 0 || (a && a_log && dt_bias && g),
+                "gated_activations: null gate-softplus pointer");
+  OMNIA_REQUIRE(aligned16(gate) && aligned16(up) && aligned16(y),
+                "gated_activations: SwiGLU pointers must be 16-byte aligned");
+  const auto aligned = [](const void* p, uintptr_t n) {
+    return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0;
+  };
+  OMNIA_REQUIRE(aligned(a, 4) && aligned(a_log, 8) && aligned(dt_bias, 8) && aligned(g, 8),
+                "gated_activations: a must be 4-byte and A_log, dt_bias, g 8-byte aligned");
+  int32_t rc = check_device();
+  if (rc != 0) return rc;
+  const int64_t vectors = rows * (inner / 8);
+  const int64_t softplus_blocks = (a_rows * (heads / 2) + kBlock - 1) / kBlock;
+  const int64_t swiglu_blocks = (vectors + kBlock - 1) / kBlock;
+  OMNIA_REQUIRE(softplus_blocks + swiglu_blocks < (int64_t{1} << 31),
+                "gated_activations: grid too large");
+  const GatedArgs p{gate, gate_stride, up, up_stride, y, rows, static_cast<uint32_t>(inner / 8),
+                    vectors, a, a_stride, a_log, dt_bias, g, a_rows, static_cast<int>(heads),
+                    static_cast<unsigned>(softplus_blocks)};
+  const dim3 grid(static_cast<unsigned>(softplus_blocks + swiglu_blocks));
+  if (gate_stride == inner && up_stride == inner) {
+    gated_activations_kernel<true><<<grid, kBlock, 0, stream>>>(p);
+  } else {
+    gated_activations_kernel<false><<<grid, kBlock, 0, stream>>>(p);
+  }
+  return launched("gated_activations");
 }

@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libomnia_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -37,6 +37,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "omnia_swiglu": (_I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _P]),
     "omnia_gate_softplus": (_I32, [_P, _I64, _P, _P, _P, _I64, _I64, _P]),
+    "omnia_gated_activations": (
+        _I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _P]
+    ),
     "omnia_softmax_topk": (_I32, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "omnia_router_pack_bytes": (_I64, [_I64, _I64]),
     "omnia_pack_router_weight": (_I32, [_P, _I64, _I64, _P, _P]),

@@ -286,6 +286,47 @@ def gate_softplus(a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor, *
     return out
 
 
+def gated_activations(gate: torch.Tensor, up: torch.Tensor, a: torch.Tensor,
+                      a_log: torch.Tensor, dt_bias: torch.Tensor, *,
+                      y: torch.Tensor | None = None,
+                      g: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """`(swiglu(gate, up), gate_softplus(a, A_log, dt_bias))` in one dispatch; see
+    `omnia_gated_activations`. Same operand rules as `swiglu` and `gate_softplus`, plus
+    an even head count, an even row stride for `a` and 8-byte aligned A_log, dt_bias."""
+    _require(gate.shape == up.shape, "gated_activations: gate and up shapes differ")
+    inner = gate.shape[-1]
+    g2 = gate.reshape(-1, inner) if gate.is_contiguous() else gate
+    u2 = up.reshape(-1, inner) if up.is_contiguous() else up
+    if g2.dim() != 2 or u2.dim() != 2:
+        g2, u2 = gate.reshape(-1, inner), up.reshape(-1, inner)
+    heads = a.shape[-1]
+    a2 = a.reshape(-1, heads) if a.is_contiguous() else a
+    _require(a2.dim() == 2 and a2.dtype == BF16, "gated_activations: a must be bf16 [rows, heads]")
+    _require(a_log.shape == (heads,) and dt_bias.shape == (heads,), "gated_activations: [heads] params")
+    _dense(a_log, F32, "A_log")
+    _dense(dt_bias, F32, "dt_bias")
+    _require(a2.stride(-1) == 1, "gated_activations: heads axis must be contiguous")
+    _require(on_rocm(g2, u2, a2, a_log, dt_bias),
+             "gated_activations: tensors must share one ROCm device")
+    gs, us = _row_stride(g2, "gate"), _row_stride(u2, "up")
+    a_stride = heads if a2.shape[0] <= 1 else a2.stride(0)
+    y = _out(y, gate, gate.shape, BF16, "y")
+    g = _out(g, a, a.shape, F32, "g")
+    call("omnia_gated_activations", g2.data_ptr(), gs, u2.data_ptr(), us, y.data_ptr(),
+         g2.shape[0], inner, a2.data_ptr(), a_stride, a_log.data_ptr(), dt_bias.data_ptr(),
+         g.data_ptr(), a2.shape[0], heads, _stream(gate))
+    return y, g
+
+
+def gated_activations_applies(gate: torch.Tensor, up: torch.Tensor, a: torch.Tensor) -> bool:
+    """The operand conditions `omnia_gated_activations` adds to swiglu's and
+    gate_softplus's own: an even head count and even row stride for `a`, 4-byte alignment."""
+    heads = a.shape[-1] if a.dim() else 0
+    if heads == 0 or heads % 2 or a.stride(-1) != 1 or a.data_ptr() % 4:
+        return False
+    return a.dim() < 2 or a.shape[-2] <= 1 or a.stride(-2) % 2 == 0
+
+
 def softmax_topk(logits: torch.Tensor, k: int, *, indices: torch.Tensor | None = None,
                  weights: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """Top-k of bf16 router logits [..., E] (lowest index on ties) and the renormalised

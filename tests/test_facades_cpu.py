@@ -175,6 +175,28 @@ def test_gate_softplus_cpu_resolves_to_core_and_matches_oracle():
     np.testing.assert_allclose(got, want, rtol=2e-6, atol=0)
 
 
+def test_gated_activations_pair_on_cpu_resolves_to_core_chains():
+    from mlx_omnia_amd.kernels.gated import DefaultGatedActivations, GatedActivations
+    from mlx_omnia_amd.runtime.ops import gated_activations_applies
+
+    rng = np.random.default_rng(5)
+    gate_up = from_float(3 * rng.standard_normal((6, 2 * 40)))
+    a = from_float(4 * rng.standard_normal((6, 32)))
+    a_log = rng.uniform(0, 2.7, 32).astype(np.float32)
+    dt_bias = (0.5 * rng.standard_normal(32)).astype(np.float32)
+    pair = GatedActivations(torch.from_numpy(a_log), torch.from_numpy(dt_bias))
+    assert isinstance(pair.strategy, DefaultGatedActivations)  # CPU declaration: Core
+    y, g = pair(cpu(gate_up), None, cpu(a))
+    want_y = act.swiglu(gate_up[:, :40], gate_up[:, 40:])
+    assert ulp_distance(bits(y), want_y).max() <= 2
+    np.testing.assert_allclose(g.numpy(), act.gate_softplus(a, a_log, dt_bias), rtol=2e-6, atol=0)
+    # The fused kernel's operand conditions beyond the single kernels': even heads, an
+    # even row stride of `a`.
+    assert gated_activations_applies(cpu(gate_up), cpu(gate_up), cpu(a))
+    assert not gated_activations_applies(cpu(gate_up), cpu(gate_up), cpu(a[:, :7]))
+    assert not gated_activations_applies(cpu(gate_up), cpu(gate_up), torch.zeros(4, 9)[:, :8])
+
+
 # ---- Routing ------------------------------------------------------------------------
 
 
