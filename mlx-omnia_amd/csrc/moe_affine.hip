@@ -33,17 +33,22 @@
 // gate_up: a wave owns kPairsPerWave gate/up pairs of one slot (consecutive rows of the
 // interleaved matrix) and streams them together; x is read per 32-value chunk from L2, and
 // lane p runs pair p's activation. down_combine: a workgroup owns kDownRows output rows
-// with one wave per slot; kLanesPerRow lanes share a row, each taking every kLanesPerRow-th
-// chunk of it; the slots' terms meet in LDS and are summed in slot order.
+// with one wave per slot; 16, 32 or 64 lanes run across each row (the fewest that cover
+// its chunks, one chunk per lane), so each lane loads its chunk of the slot's activations
+// once for all the rows of its lane group; the slots' terms meet in LDS and are summed in
+// slot order.
 // Both issue a lane's loads (words, scale and bias bits each in a register of its own, the
 // activations) before the arithmetic, with no branch among them: a scale packed beside
 // another or a load inside a divergent branch makes the compiler wait on each load, one
-// round trip per chunk. The down kernel is compiled per step count, so a lane issues no
-// load past the row's end.
+// round trip per chunk. The down kernel is compiled per lane count, so a lane issues no
+// load past the row's end, and its row sums associate exactly as a 16-lane row summing a
+// lane's chunks in order would.
 // Measured at Qwen3-30B-A3B's routed MLP, 4 bits, groups of 64, one call: gate_up with 2
 // pairs per wave 6.0 us (before the load issue was fixed: 4 pairs 7.6, 8 pairs 8.7, 1 pair
-// 6.6 against 6.1 for 2); down with 16 lanes per row 5.4 us (before: 8 lanes 6.45, 8 lanes
-// and two rows per lane 8.8 against 5.9 for 16).
+// 6.6 against 6.1 for 2). down, A/B on one box: 16 lanes per row, each lane loading its
+// chunks' activations for its one row, 5.6 us; 32 lanes per row at inner 768 with the
+// activations held once for the lane group's rows, 5.1 us at 4 rows per workgroup, 5.0 at
+// 8 (6.5 at 16), bit-identical outputs.
 #include "common.hpp"
 #include "host.hpp"
 
@@ -53,12 +58,8 @@ namespace {
 constexpr int kChunk = 32;                // values per lane per step (`bits` words)
 constexpr int kPairsPerWave = 2;          // gate_up: gate/up pairs per wave
 constexpr int kGateWaves = 4;             // gate_up: waves per workgroup
-constexpr int kLanesPerRow = 16;          // down: lanes sharing an output row
-constexpr int kOctets = kWave / kLanesPerRow;
-constexpr int kRowsPerLane = 1;           // down: rows per lane (one activation load for all)
-constexpr int kDownRows = kOctets * kRowsPerLane;  // down: output rows per workgroup
-constexpr int kMaxInner = 1536;
-constexpr int kMaxDownSteps = kMaxInner / (32 * kLanesPerRow);  // down: chunks per lane
+constexpr int kDownRows = 8;              // down: output rows per workgroup
+constexpr int kMaxInner = 1536;           // down: at most 48 chunks, one per lane
 constexpr int kMaxDownSlots = 16;         // down: one wave per slot
 constexpr uint32_t kMagic = 0x43004300u;  // the bf16 pair (128, 128)
 constexpr uint32_t kOnes = 0x3F803F80u;   // the bf16 pair (1, 1)
@@ -190,12 +191,12 @@ __device__ __forceinline__ float chunk_term(float dot, float xsum, uint32_t scal
   return __builtin_fmaf(s, dot, shifted * xsum);
 }
 
-// Sum over each group of kLanesPerRow (8 or 16) aligned lanes, the same in each of them.
+// Sum over each 16-lane DPP row, the same in each of its lanes.
 __device__ __forceinline__ float octet_sum(float v) {
   v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
   v += __uint_as_float(dpp<kQuadSwap2>(__float_as_uint(v)));
   v += __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
-  if constexpr (kLanesPerRow == 16) v += __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
   return v;
 }
 
@@ -321,86 +322,106 @@ struct DownArgs {
   int slots;
 };
 
-// The dot products of the lane's rows (row0 + 8 q for q < kRowsPerLane, those with
-// live[q]) over the chunks part, part + 8, ... of the slot's activation row: every
-// weight word in flight before the first multiply, each activation chunk loaded once for
-// all the rows.
-template <int B, int kSteps>
-__device__ __forceinline__ void down_rows(const DownArgs& a, const Leaf& leaf, int64_t row0,
-                                          const bool (&live)[kRowsPerLane], int slot, int part,
-                                          float (&t)[kRowsPerLane]) {
+// The terms of one lane group's rows (rows group, group + kGroups, ... of the workgroup's
+// kDownRows) for the lane's chunk `part` of the slot's activation row: every load (each
+// row's words, scale and bias bits in registers of their own, the activation chunk, read
+// once for all the rows) goes out before any arithmetic, with no branch among them. A
+// lane past the row's last chunk re-reads that chunk and drops the term, and a row past
+// the last one re-reads the last (its sum is never used).
+template <int B, int kLanes>
+__device__ __forceinline__ void down_terms(const DownArgs& a, const Leaf& leaf, int64_t row_first,
+                                           int rows, int group, int part, int slot,
+                                           float (&t)[kDownRows * kLanes / kWave]) {
+  constexpr int kGroups = kWave / kLanes;
+  constexpr int kRowsPerGroup = kDownRows / kGroups;
   const int chunks = a.inner / kChunk;
   const int64_t words = static_cast<int64_t>(a.inner) * B / 32;
   const int groups = a.inner / leaf.group;
-  static_assert(kRowsPerLane == 1, "the caller checks the lane's one row for liveness");
-  // Every load (words, scale and bias bits in registers of their own, the activations)
-  // goes out before any arithmetic, with no branch among them: a lane past the row's
-  // last chunk re-reads that chunk and drops the term.
-  uint32_t w[kSteps][B];
-  uint32_t sb[kSteps], bb[kSteps];
-  u32x4 raw[kSteps][4];
+  const int c = min(part, chunks - 1);
+  uint32_t w[kRowsPerGroup][B];
+  uint32_t sb[kRowsPerGroup], bb[kRowsPerGroup];
+#pragma unroll
+  for (int q = 0; q < kRowsPerGroup; ++q) {
+    const int64_t row = row_first + min(group + kGroups * q, rows - 1);
+    load_words<B>(leaf.weight + row * words + static_cast<int64_t>(c) * B, w[q]);
+    const int64_t g = row * groups + (c * kChunk) / leaf.group;
+    sb[q] = leaf.scales[g];
+    bb[q] = leaf.biases[g];
+  }
+  u32x4 raw[4];
   const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
 #pragma unroll
-  for (int i = 0; i < kSteps; ++i) {
-    const int c = min(part + kLanesPerRow * i, chunks - 1);
-    load_words<B>(leaf.weight + row0 * words + static_cast<int64_t>(c) * B, w[i]);
-    const int64_t g = row0 * groups + (c * kChunk) / leaf.group;
-    sb[i] = leaf.scales[g];
-    bb[i] = leaf.biases[g];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) raw[i][j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
-  }
+  for (int j = 0; j < 4; ++j) raw[j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
   __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
-  t[0] = 0.0f;
+  uint32_t xq[16];
+  const float xsum = pair_x<B>(raw, xq);
+  const bool in_row = part < chunks;
 #pragma unroll
-  for (int i = 0; i < kSteps; ++i) {
-    uint32_t xq[16];
-    const float xsum = pair_x<B>(raw[i], xq);
-    const float term = t[0] + chunk_term<B>(chunk_dot<B>(w[i], xq), xsum, sb[i], bb[i]);
-    t[0] = part + kLanesPerRow * i < chunks ? term : t[0];
+  for (int q = 0; q < kRowsPerGroup; ++q) {
+    const float term = 0.0f + chunk_term<B>(chunk_dot<B>(w[q], xq), xsum, sb[q], bb[q]);
+    t[q] = in_row ? term : 0.0f;
   }
 }
 
-// kSteps = ceil(inner / (32 * kLanesPerRow)) chunks per lane.
-template <int kSteps>
+// A row's sum over its kLanes lanes, in every lane of the group, associated as a lane
+// of 16 summing chunks p, p + 16, p + 32 in that order and the 16 then meeting in the
+// DPP butterfly: the 16-lane rows of a group pair up first (rows 0 + 1, then + rows
+// 2 + 3), then the butterfly inside each row. Lanes holding no chunk hold +0.
+template <int kLanes>
+__device__ __forceinline__ float group_row_sum(float v) {
+  if constexpr (kLanes >= 32) {
+    uint32_t lo, hi;
+    row_pair(__float_as_uint(v), lo, hi);
+    v = __uint_as_float(lo) + __uint_as_float(hi);
+  }
+  if constexpr (kLanes == 64) {
+    uint32_t lo, hi;
+    half_pair(__float_as_uint(v), lo, hi);
+    v = __uint_as_float(lo) + __uint_as_float(hi);
+  }
+  return octet_sum(v);
+}
+
+// One wave per slot; kLanes lanes across each row (16, 32 or 64: the fewest that cover
+// the row's chunks), so each lane holds one activation chunk for the rows of its group.
+template <int kLanes>
 __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(DownArgs a) {
+  constexpr int kGroups = kWave / kLanes;
+  constexpr int kRowsPerGroup = kDownRows / kGroups;
   __shared__ float partial[kMaxDownSlots][kDownRows];
   const int lane = threadIdx.x % kWave;
   const int slot = threadIdx.x / kWave;   // one wave per slot
   const int row_base = blockIdx.x * kDownRows;
-  const int octet = lane / kLanesPerRow;
-  const int part = lane % kLanesPerRow;
+  const int rows = min(kDownRows, a.hidden - row_base);
+  const int group = lane / kLanes;
+  const int part = lane % kLanes;
   const bool shared = uses_shared(a.shared, slot, a.slots);
   const Leaf& leaf = shared ? a.shared : a.routed;
   bool valid = true;
-  int64_t row0 = row_base + octet;
+  int64_t row_first = row_base;
   if (!shared) {
     const int expert = a.chosen[slot];
-    valid = expert >= 0 && expert < a.experts;
-    row0 += static_cast<int64_t>(valid ? expert : 0) * a.hidden;
+    valid = expert >= 0 && expert < a.experts;   // uniform over the wave
+    row_first += static_cast<int64_t>(valid ? expert : 0) * a.hidden;
   }
-  bool live[kRowsPerLane];  // uniform over the lane's octet
+  float t[kRowsPerGroup];
 #pragma unroll
-  for (int q = 0; q < kRowsPerLane; ++q) live[q] = valid && row_base + octet + kOctets * q < a.hidden;
-  float t[kRowsPerLane];
-#pragma unroll
-  for (int q = 0; q < kRowsPerLane; ++q) t[q] = 0.0f;
-  if (live[0]) {
+  for (int q = 0; q < kRowsPerGroup; ++q) t[q] = 0.0f;
+  if (valid) {
     switch (leaf.bits) {  // wave-uniform
-      case 2: down_rows<2, kSteps>(a, leaf, row0, live, slot, part, t); break;
-      case 3: down_rows<3, kSteps>(a, leaf, row0, live, slot, part, t); break;
-      case 4: down_rows<4, kSteps>(a, leaf, row0, live, slot, part, t); break;
-      case 5: down_rows<5, kSteps>(a, leaf, row0, live, slot, part, t); break;
-      case 6: down_rows<6, kSteps>(a, leaf, row0, live, slot, part, t); break;
-      default: down_rows<8, kSteps>(a, leaf, row0, live, slot, part, t); break;
+      case 2: down_terms<2, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
+      case 3: down_terms<3, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
+      case 4: down_terms<4, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
+      case 5: down_terms<5, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
+      case 6: down_terms<6, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
+      default: down_terms<8, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
     }
   }
 #pragma unroll
-  for (int q = 0; q < kRowsPerLane; ++q) {
-    const float sum = octet_sum(t[q]);
-    if (part == 0) {
-      partial[slot][octet + kOctets * q] = valid ? round_bf16(round_bf16(sum) * a.weights[slot]) : 0.0f;
-    }
+  for (int q = 0; q < kRowsPerGroup; ++q) {
+    const float sum = group_row_sum<kLanes>(t[q]);
+    const int row = group + kGroups * q;
+    if (part == 0) partial[slot][row] = valid ? round_bf16(round_bf16(sum) * a.weights[slot]) : 0.0f;
   }
   __syncthreads();
   if (threadIdx.x < kDownRows && row_base + static_cast<int>(threadIdx.x) < a.hidden) {
@@ -492,11 +513,14 @@ extern "C" int32_t omnia_moe_down_combine_affine(
              static_cast<int>(inner), static_cast<int>(slots)};
   const dim3 grid(static_cast<unsigned>((hidden + kDownRows - 1) / kDownRows));
   const dim3 block(static_cast<unsigned>(slots * kWave));
-  static_assert(kMaxDownSteps == 3, "one instantiation per step count");
-  switch ((inner / kChunk + kLanesPerRow - 1) / kLanesPerRow) {
-    case 1: moe_down_affine_kernel<1><<<grid, block, 0, stream>>>(a); break;
-    case 2: moe_down_affine_kernel<2><<<grid, block, 0, stream>>>(a); break;
-    default: moe_down_affine_kernel<3><<<grid, block, 0, stream>>>(a); break;
+  static_assert(kMaxInner / kChunk <= kWave, "a row's chunks fit one wave");
+  const int64_t chunks = inner / kChunk;
+  if (chunks <= 16) {
+    moe_down_affine_kernel<16><<<grid, block, 0, stream>>>(a);
+  } else if (chunks <= 32) {
+    moe_down_affine_kernel<32><<<grid, block, 0, stream>>>(a);
+  } else {
+    moe_down_affine_kernel<64><<<grid, block, 0, stream>>>(a);
   }
   return launched("moe_down_combine_affine");
 }
