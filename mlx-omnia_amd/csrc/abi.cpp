@@ -24,11 +24,25 @@ int32_t fail(int32_t code, const std::string& message) {
   return code;
 }
 
-int32_t check_device() {
+int32_t check_device(hipStream_t stream) {
   int device = 0;
   hipError_t status = hipGetDevice(&device);
   if (status != hipSuccess) {
     return fail(-ENODEV, std::string("hipGetDevice: ") + hipGetErrorString(status));
+  }
+  if (stream != nullptr) {
+    // The kernels run on the stream's device and dereference the caller's pointers
+    // there; a stream of another device than the current one is a caller mistake.
+    hipDevice_t owner = 0;
+    status = hipStreamGetDevice(stream, &owner);
+    if (status != hipSuccess) {
+      return fail(-EINVAL, std::string("hipStreamGetDevice: ") + hipGetErrorString(status));
+    }
+    if (owner != device) {
+      return fail(-EINVAL, "the stream belongs to device " + std::to_string(owner) +
+                               " but device " + std::to_string(device) +
+                               " is current; make the stream's device current first");
+    }
   }
   if (device < 0 || device >= kMaxDevices) {
     return fail(-ENODEV, "device ordinal out of range");

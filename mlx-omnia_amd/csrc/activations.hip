@@ -249,7 +249,7 @@ extern "C" int32_t omnia_swiglu(const uint16_t* gate, int64_t gate_stride, const
   OMNIA_REQUIRE(gate && up && out, "swiglu: null pointer");
   OMNIA_REQUIRE(aligned16(gate) && aligned16(up) && aligned16(out),
                 "swiglu: pointers must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const int64_t vectors = rows * (inner / 8);
   OMNIA_REQUIRE(vectors / kBlock < (int64_t{1} << 31), "swiglu: grid too large");
@@ -275,7 +275,7 @@ extern "C" int32_t omnia_gate_softplus(const uint16_t* a, int64_t a_stride, cons
   OMNIA_REQUIRE(rows * heads < (int64_t{1} << 40), "gate_softplus: too large");
   if (rows == 0) return 0;
   OMNIA_REQUIRE(a && a_log && dt_bias && out, "gate_softplus: null pointer");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const auto aligned = [](const void* p, uintptr_t n) {
     return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0;
@@ -322,7 +322,7 @@ extern "C" int32_t omnia_gated_activations(const uint16_t* gate, int64_t gate_st
   };
   OMNIA_REQUIRE(aligned(a, 4) && aligned(a_log, 8) && aligned(dt_bias, 8) && aligned(g, 8),
                 "gated_activations: a must be 4-byte and A_log, dt_bias, g 8-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const int64_t vectors = rows * (inner / 8);
   const int64_t softplus_blocks = (a_rows * (heads / 2) + kBlock - 1) / kBlock;

@@ -116,7 +116,7 @@ extern "C" int32_t omnia_add_rms_norm(const uint16_t* x, const uint16_t* branch,
   OMNIA_REQUIRE(aligned16(x) && aligned16(branch) && aligned16(weight) &&
                     aligned16(summed) && aligned16(normalized),
                 "add_rms_norm: pointers must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
 
   const int vecs = static_cast<int>(hidden / 8);

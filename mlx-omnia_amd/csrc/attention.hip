@@ -634,7 +634,7 @@ int32_t attention_decode_checked(
                   "attention_decode: workspace smaller than omnia_attention_workspace_bytes()");
     OMNIA_REQUIRE(aligned16(workspace), "attention_decode: workspace must be 16-byte aligned");
   }
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   AttnArgs a{raw_queries, raw_keys, raw_values, query_weight, key_weight, angles, key_cache,
              value_cache, position, static_cast<float*>(workspace), out,
@@ -774,7 +774,7 @@ extern "C" int32_t omnia_attention_decode_noalloc(
                              std::to_string(kAttentionScratchBytes) +
                              " bytes; use omnia_attention_decode with a workspace");
   }
-  rc = check_device();
+  rc = check_device(stream);
   if (rc != 0) return rc;
   void* address = nullptr;
   rc = device_scratch(&address);

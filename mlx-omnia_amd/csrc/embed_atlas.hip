@@ -130,7 +130,7 @@ extern "C" int32_t omnia_embed_atlas(const int32_t* tokens, int64_t n_tokens,
   OMNIA_REQUIRE(aligned16(embedding) && aligned16(hidden_out) && aligned16(full_atlas) &&
                     aligned16(full_out) && aligned16(sliding_atlas) && aligned16(sliding_out),
                 "embed_atlas: pointers must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   EmbedArgs a{tokens,
               reinterpret_cast<const u32x4*>(embedding),

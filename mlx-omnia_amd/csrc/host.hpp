@@ -15,9 +15,11 @@ namespace omnia {
 // Records `message` as the calling thread's last error and returns `code`.
 int32_t fail(int32_t code, const std::string& message);
 
-// 0 when the current device is a gfx950, else -ENODEV (with the error text set).
-// The answer is cached per device ordinal after the first query.
-int32_t check_device();
+// 0 when `stream` belongs to the current device and that device is a gfx950.
+// A stream of another device gives -EINVAL, a device of another architecture
+// -ENODEV (with the error text set). The null stream stands for the current
+// device. The architecture is cached per device ordinal after the first query.
+int32_t check_device(hipStream_t stream);
 
 // Converts the status of the launch just made into the ABI's return code.
 int32_t launched(const char* kernel);

@@ -183,7 +183,7 @@ extern "C" int32_t omnia_dense_gate_up_swiglu(const uint16_t* x, const uint16_t*
   OMNIA_REQUIRE(x && fused_weight && activated, "dense_gate_up_swiglu: null pointer");
   OMNIA_REQUIRE(aligned16(x) && aligned16(fused_weight),
                 "dense_gate_up_swiglu: x and the weight must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const int vecs = static_cast<int>(hidden / 8);
   GateUpArgs a{reinterpret_cast<const u32x4*>(x), reinterpret_cast<const u32x4*>(fused_weight),
@@ -202,7 +202,7 @@ extern "C" int32_t omnia_dense_down_residual(const uint16_t* activated, const ui
   OMNIA_REQUIRE(activated && down_weight && residual && out, "dense_down_residual: null pointer");
   OMNIA_REQUIRE(aligned16(activated) && aligned16(down_weight),
                 "dense_down_residual: the activation and the weight must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   DownArgs a{reinterpret_cast<const u32x4*>(activated), reinterpret_cast<const u32x4*>(down_weight),
              residual, out, static_cast<int>(hidden), static_cast<int>(inner / 8)};

@@ -284,7 +284,7 @@ extern "C" int32_t omnia_moe_gate_up(const uint16_t* x, const uint16_t* weight, 
   if (k == 0) return 0;
   OMNIA_REQUIRE(x && weight && chosen && out, "moe_gate_up: null pointer");
   OMNIA_REQUIRE(aligned16(x) && aligned16(weight), "moe_gate_up: x and weight must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const int vecs = static_cast<int>(hidden / 8);
   GateUpArgs a{reinterpret_cast<const u32x4*>(x), weight, chosen, out, experts,
@@ -308,7 +308,7 @@ extern "C" int32_t omnia_moe_down_combine(const uint16_t* act, const uint16_t* w
   OMNIA_REQUIRE(act && weight && chosen && weights && out, "moe_down_combine: null pointer");
   OMNIA_REQUIRE(aligned16(act) && aligned16(weight),
                 "moe_down_combine: act and weight must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const int vecs = static_cast<int>(inner / 8);
   DownArgs a{act, weight, chosen, weights, residual, out, experts, static_cast<int>(hidden),

@@ -466,7 +466,7 @@ extern "C" int32_t omnia_moe_gate_up_affine(
                   "moe_gate_up_affine: bad shared width or group");
     OMNIA_REQUIRE(aligned16(shared_weight), "moe_gate_up_affine: the shared weight must be 16-byte aligned");
   }
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   GateUpArgs a{x,
                Leaf{weight, scales, biases, static_cast<int>(bits), static_cast<int>(group_size)},
@@ -503,7 +503,7 @@ extern "C" int32_t omnia_moe_down_combine_affine(
                   "moe_down_combine_affine: bad shared width or group");
     OMNIA_REQUIRE(aligned16(shared_weight), "moe_down_combine_affine: the shared weight must be 16-byte aligned");
   }
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   DownArgs a{act,
              Leaf{weight, scales, biases, static_cast<int>(bits), static_cast<int>(group_size)},

@@ -443,7 +443,7 @@ int32_t launch_gate_up(Fp4 format, const char* name, const uint16_t* x, const ui
   OMNIA_REQUIRE(aligned16(x) && aligned16(weight), std::string(name) + ": x and weight must be 16-byte aligned");
   OMNIA_REQUIRE(format == Fp4::kMx || reinterpret_cast<uintptr_t>(scales) % 2 == 0,
                 std::string(name) + ": the scales must be 2-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   GateUpArgs a{x, Stack{reinterpret_cast<const u32x4*>(weight), scales, bias}, chosen, keys, out, experts,
                static_cast<int>(hidden), static_cast<int>(inner), limit};
@@ -480,7 +480,7 @@ int32_t launch_down(Fp4 format, const char* name, const uint16_t* act, const uin
   OMNIA_REQUIRE(aligned16(act) && aligned16(weight), std::string(name) + ": act and weight must be 16-byte aligned");
   OMNIA_REQUIRE(format == Fp4::kMx || reinterpret_cast<uintptr_t>(scales) % 2 == 0,
                 std::string(name) + ": the scales must be 2-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   DownArgs a{act, Stack{reinterpret_cast<const u32x4*>(weight), scales, bias}, chosen, weights, residual, out,
              experts, static_cast<int>(hidden), static_cast<int>(inner), static_cast<int>(slots)};

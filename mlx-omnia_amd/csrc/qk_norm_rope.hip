@@ -591,7 +591,7 @@ extern "C" int32_t omnia_qk_norm_rope(
                     aligned16(key_weight) && aligned16(cos_table) && aligned16(sin_table) &&
                     aligned16(queries) && aligned16(keys),
                 "qk_norm_rope: pointers must be 16-byte aligned");
-  rc = check_device();
+  rc = check_device(stream);
   if (rc != 0) return rc;
   RopeArgs a{raw_queries, raw_keys, query_weight, key_weight, cos_table, sin_table,
              queries, keys, length, query_stride, key_stride, table_stride, offset,
@@ -621,7 +621,7 @@ extern "C" int32_t omnia_rope_epilogue(const uint16_t* fused, int64_t fused_stri
   OMNIA_REQUIRE(aligned16(fused) && aligned16(query_weight) && aligned16(key_weight) &&
                     aligned16(queries) && aligned16(keys),
                 "rope_epilogue: pointers must be 16-byte aligned");
-  rc = check_device();
+  rc = check_device(stream);
   if (rc != 0) return rc;
   RopeArgs a{fused, fused + query_heads * head_dim, query_weight, key_weight, nullptr,
              nullptr, queries, keys, length, fused_stride, fused_stride, 0, offset,

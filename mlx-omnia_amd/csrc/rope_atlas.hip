@@ -51,7 +51,7 @@ extern "C" int32_t omnia_rope_angle_atlas(const double* frequencies, int64_t pai
   OMNIA_REQUIRE(rows * pairs < (int64_t{1} << 40), "rope_angle_atlas: too many entries");
   if (rows == 0) return 0;
   OMNIA_REQUIRE(frequencies && atlas, "rope_angle_atlas: null pointer");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const int64_t blocks = (rows * pairs + kAtlasBlock - 1) / kAtlasBlock;
   OMNIA_REQUIRE(blocks < (int64_t{1} << 31), "rope_angle_atlas: too many rows");

@@ -1134,7 +1134,7 @@ extern "C" int32_t omnia_softmax_topk(const uint16_t* logits, int64_t stride, in
   OMNIA_REQUIRE(stride >= experts, "softmax_topk: row stride smaller than experts");
   if (rows == 0) return 0;
   OMNIA_REQUIRE(logits && indices && weights, "softmax_topk: null pointer");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   const int v = static_cast<int>((experts + kWave - 1) / kWave);
@@ -1165,7 +1165,7 @@ extern "C" int32_t omnia_pack_router_weight(const uint16_t* router_weight, int64
   OMNIA_REQUIRE(router_weight && packed, "pack_router_weight: null pointer");
   OMNIA_REQUIRE(aligned16(router_weight) && aligned16(packed),
                 "pack_router_weight: pointers must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const int chunks = static_cast<int>(experts * hidden / 8);
   const int chunk_blocks = (chunks + kPackBlock - 1) / kPackBlock;
@@ -1217,7 +1217,7 @@ extern "C" int32_t omnia_residual_rms_router(
   OMNIA_REQUIRE(aligned16(x) && aligned16(branch) && aligned16(norm_weight) &&
                     aligned16(packed_router) && aligned16(summed) && aligned16(normalized),
                 "residual_rms_router: pointers must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const uint16_t* packed = static_cast<const uint16_t*>(packed_router);
   RouterArgs a{reinterpret_cast<const u32x4*>(x), reinterpret_cast<const u32x4*>(branch),
@@ -1248,7 +1248,7 @@ extern "C" int32_t omnia_residual_rms_router_sigmoid(
   OMNIA_REQUIRE(aligned16(x) && aligned16(branch) && aligned16(norm_weight) &&
                     aligned16(packed_router) && aligned16(summed) && aligned16(normalized),
                 "residual_rms_router_sigmoid: pointers must be 16-byte aligned");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const uint16_t* packed = static_cast<const uint16_t*>(packed_router);
   RouterArgs a{reinterpret_cast<const u32x4*>(x), reinterpret_cast<const u32x4*>(branch),
@@ -1276,7 +1276,7 @@ extern "C" int32_t omnia_sigmoid_topk(const void* logits, int64_t stride, int32_
                 "sigmoid_topk: k must be in [1, min(experts, 64)]");
   if (rows == 0) return 0;
   OMNIA_REQUIRE(logits && bias && (keys || indices), "sigmoid_topk: null pointer");
-  int32_t rc = check_device();
+  int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   const int kk = indices ? static_cast<int>(k) : 0;
