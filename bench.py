@@ -554,6 +554,50 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.moe_down_combine_nvfp4(a["act"], a["dn"], a["ids"], a["w"], a["r"], out=a["o"]),
     ))
 
+    # The packed NVFP4 down/combine (core/kernels/down_combine/nvfp4_packed.py) at
+    # Qwen3-Next-80B-A3B's sparse block: hidden 2048, inner 512, 512 experts, top-10 plus
+    # the shared expert on the last slot, one token. Two layers' routed stacks (302 MB
+    # each) alternate, and every argument set holds its own shared stack, so nothing the
+    # timed loop reads stays in the 256 MB Infinity Cache between its visits.
+    nx_h, nx_i, nx_e, nx_k, nx_layers = 2048, 512, 512, 10, 2
+    nx_stacks: list = []
+
+    def setup_moe_nvfp4_shared(device, copies):
+        gen = torch.Generator(device=device).manual_seed(17)
+
+        def stack(*lead):
+            words = torch.randint(-2**31, 2**31, (*lead, nx_h, nx_i // 8), generator=gen, device=device,
+                                  dtype=torch.int32)
+            scales = torch.randint(0x18, 0x28, (*lead, nx_h, nx_i // 32), generator=gen, device=device,
+                                   dtype=torch.int32).to(torch.uint8).repeat_interleave(2, dim=-1)
+            return ops.Nvfp4Leaf(words, scales, None)
+
+        if not nx_stacks:
+            nx_stacks.extend(stack(nx_e) for _ in range(nx_layers))
+        rng = np.random.default_rng(18)
+        sets = []
+        for i in range(copies):
+            chosen = rng.choice(nx_e, size=nx_k, replace=False).astype(np.int32)[None]
+            sets.append(dict(dn=nx_stacks[i % nx_layers], sh=stack(1),
+                             ids=torch.from_numpy(chosen).to(device),
+                             act=_to_bf16_device(_normal(rng, (1, nx_k + 1, nx_i)), device),
+                             w=torch.from_numpy(rng.dirichlet(np.ones(nx_k)).astype(np.float32)[None]).to(device),
+                             r=_to_bf16_device(_normal(rng, (1, nx_h)), device),
+                             o=torch.empty((1, nx_h), dtype=torch.bfloat16, device=device)))
+        return sets
+
+    out.append(Workload(
+        name="moe_nvfp4_shared_down_combine_decode",
+        kernel="moe_down_nvfp4_shared_kernel",
+        description="activation [11, 512] x 10 of 512 experts' NVFP4 down stacks [2048, 512] and the "
+                    "shared expert's, bf16 routing sum, residual (Qwen3-Next-80B-A3B, T=1)",
+        bytes_per_launch=(nx_k + 1) * nx_h * nvfp4_row_bytes(nx_i) + (nx_k + 1) * nx_i * 2 + nx_k * 8
+        + 2 * nx_h * 2,
+        setup=setup_moe_nvfp4_shared,
+        launch=lambda a: ops.moe_down_combine_nvfp4_shared(a["act"], a["dn"], a["sh"], a["ids"], a["w"], a["r"],
+                                                           out=a["o"]),
+    ))
+
     # Next after the routed MLP: the dense SwiGLU MLP of a one-token step at Qwen3-4B's
     # shape (hidden 2560, inner 9728: config 4's inner dimension), bf16 weights, gate rows
     # first. Each argument set holds its own weights, as each layer of a model does.
@@ -912,6 +956,16 @@ def _cpu_legs() -> dict:
         return (lambda: nvfp4.gate_up(x, stack, np.arange(8)),
                 8 * 1536 * row_bytes + 2048 * 2 + 8 * 4 + 8 * 768 * 2, "the 8 routed experts", True)
 
+    def nvfp4_shared_leg():
+        stack = nvfp4.Stack(rng.integers(0, 2**32, (10, 2048, 64), dtype=np.uint32),
+                            rng.integers(0x18, 0x28, (10, 2048, 32), dtype=np.uint8))
+        shared = nvfp4.Stack(stack.weight[0], stack.scales[0])
+        act, res = bf((1, 11, 512)), bf((1, 2048))
+        weights = rng.dirichlet(np.ones(10)).astype(np.float32)[None]
+        return (lambda: nvfp4.down_combine_shared(act, stack, shared, np.arange(10)[None], weights, res),
+                11 * 2048 * 288 + 11 * 512 * 2 + 10 * 8 + 2 * 2048 * 2, "the 10 routed experts and the shared one",
+                True)
+
     def mlp_leg(down):
         if down:
             w, act, res = _bits(rng, (2560, 9728)), bf((9728,)), bf((2560,))
@@ -954,6 +1008,7 @@ def _cpu_legs() -> dict:
         "moe_nvfp4_gate_up_decode": lambda: nvfp4_leg(False),
         "moe_nvfp4_gate_up_ordinal_decode": lambda: nvfp4_leg(False, ordinal=True),
         "moe_nvfp4_down_combine_decode": lambda: nvfp4_leg(True),
+        "moe_nvfp4_shared_down_combine_decode": nvfp4_shared_leg,
         "dense_mlp_gate_up_decode": lambda: mlp_leg(False),
         "dense_mlp_down_decode": lambda: mlp_leg(True),
         "attention_decode_32k": lambda: attention_leg(32768),

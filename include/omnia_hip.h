@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 13
+#define OMNIA_ABI_VERSION 14
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -388,6 +388,29 @@ int32_t omnia_moe_down_combine_nvfp4(const uint16_t* act, const uint32_t* weight
                                      int64_t experts, int64_t hidden, int64_t inner, const int32_t* chosen,
                                      const float* weights, int64_t slots, const uint16_t* residual,
                                      uint16_t* out, hipStream_t stream);
+
+/* The packed NVFP4 down/combine: for each of `tokens` tokens, the routed down projections,
+ * the unrouted (shared) stack's and the residual add in one dispatch, with a bf16 epilogue:
+ *   d[t, s, n] = bf16(sum over groups of 16 of s * sum_i act[t, s, i] v[i])   fp32 sum
+ *                (slot s < top_k: expert chosen[t, s]; slot top_k: the shared stack)
+ *   total = bf16(bf16(d[t, s, n] * bf16(weights[t, s])) + total) over s < top_k in order
+ *   out[t, n] = bf16(residual[t, n] + bf16(total + d[t, top_k, n]))
+ * each operation in fp32. act [tokens, top_k + 1, inner] bf16; weight [experts, hidden,
+ * inner / 8] and shared_weight [hidden, inner / 8] uint32; scales and shared_scales the
+ * group-16 e4m3 planes [.., hidden, inner / 16] uint8, 2-byte aligned; chosen [tokens,
+ * top_k] int32 (an id outside [0, experts) gives zero rows); weights [tokens, top_k] fp32;
+ * residual, out [tokens, hidden] bf16. inner a multiple of 32, at most 2048; 0 <= top_k
+ * <= 31; tokens <= 65535.
+ * Replaces: core/kernels/down_combine/nvfp4_packed.py:38-138,224-270
+ * (`nvfp4_fused_down_residual`, Nvfp4PackedDownCombine.__call__). The reference reads a
+ * halved scale plane (shared/nvfp4/packed.py:126-164) that equals this group-16 plane
+ * wherever its build accepts the checkpoint; the caller checks that certificate. */
+int32_t omnia_moe_down_combine_nvfp4_shared(const uint16_t* act, const uint32_t* weight,
+                                            const uint8_t* scales, int64_t experts,
+                                            const uint32_t* shared_weight, const uint8_t* shared_scales,
+                                            int64_t hidden, int64_t inner, const int32_t* chosen,
+                                            const float* weights, int64_t tokens, int64_t top_k,
+                                            const uint16_t* residual, uint16_t* out, hipStream_t stream);
 
 /* Dense SwiGLU MLP of one token, first half: the fused gate||up projection with the
  * SwiGLU applied in bf16 steps,

@@ -185,6 +185,34 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return __uint_as_float(a) + __uint_as_float(b);
 }
 
+// Sum over each 16-lane DPP row, the same in each of its lanes.
+__device__ __forceinline__ float octet_sum(float v) {
+  v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kQuadSwap2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
+  return v;
+}
+
+// A row's sum over a group of kLanes consecutive lanes (16, 32 or 64), in every lane of
+// the group: the 16-lane DPP rows of the group pair up first (rows 0 + 1, then + rows
+// 2 + 3), then the butterfly inside each row. A lane holding no term holds +0.
+template <int kLanes>
+__device__ __forceinline__ float group_row_sum(float v) {
+  static_assert(kLanes == 16 || kLanes == 32 || kLanes == 64, "16, 32 or 64 lanes");
+  if constexpr (kLanes >= 32) {
+    uint32_t lo, hi;
+    row_pair(__float_as_uint(v), lo, hi);
+    v = __uint_as_float(lo) + __uint_as_float(hi);
+  }
+  if constexpr (kLanes == 64) {
+    uint32_t lo, hi;
+    half_pair(__float_as_uint(v), lo, hi);
+    v = __uint_as_float(lo) + __uint_as_float(hi);
+  }
+  return octet_sum(v);
+}
+
 // c + a.lo * b.lo + a.hi * b.hi over two packed bf16 pairs (v_dot2_f32_bf16), fp32.
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,

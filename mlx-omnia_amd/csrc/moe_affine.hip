@@ -191,15 +191,6 @@ __device__ __forceinline__ float chunk_term(float dot, float xsum, uint32_t scal
   return __builtin_fmaf(s, dot, shifted * xsum);
 }
 
-// Sum over each 16-lane DPP row, the same in each of its lanes.
-__device__ __forceinline__ float octet_sum(float v) {
-  v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));
-  v += __uint_as_float(dpp<kQuadSwap2>(__float_as_uint(v)));
-  v += __uint_as_float(dpp<kRowHalfMirror>(__float_as_uint(v)));
-  v += __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
-  return v;
-}
-
 __device__ __forceinline__ bool uses_shared(const Leaf& shared, int slot, int slots) {
   return shared.weight != nullptr && slot == slots - 1;
 }
@@ -361,25 +352,6 @@ __device__ __forceinline__ void down_terms(const DownArgs& a, const Leaf& leaf, 
     const float term = 0.0f + chunk_term<B>(chunk_dot<B>(w[q], xq), xsum, sb[q], bb[q]);
     t[q] = in_row ? term : 0.0f;
   }
-}
-
-// A row's sum over its kLanes lanes, in every lane of the group, associated as a lane
-// of 16 summing chunks p, p + 16, p + 32 in that order and the 16 then meeting in the
-// DPP butterfly: the 16-lane rows of a group pair up first (rows 0 + 1, then + rows
-// 2 + 3), then the butterfly inside each row. Lanes holding no chunk hold +0.
-template <int kLanes>
-__device__ __forceinline__ float group_row_sum(float v) {
-  if constexpr (kLanes >= 32) {
-    uint32_t lo, hi;
-    row_pair(__float_as_uint(v), lo, hi);
-    v = __uint_as_float(lo) + __uint_as_float(hi);
-  }
-  if constexpr (kLanes == 64) {
-    uint32_t lo, hi;
-    half_pair(__float_as_uint(v), lo, hi);
-    v = __uint_as_float(lo) + __uint_as_float(hi);
-  }
-  return octet_sum(v);
 }
 
 // One wave per slot; kLanes lanes across each row (16, 32 or 64: the fewest that cover

@@ -36,6 +36,10 @@
 // inside a divergent branch, or a scale byte packed beside another, makes the compiler
 // wait on it, one memory round trip per chunk.
 //
+// The packed NVFP4 form of down_combine (core/kernels/down_combine/nvfp4_packed.py) adds an
+// unrouted slot, several tokens per dispatch and a bf16 epilogue; it is described at its
+// kernel below.
+//
 // gate_up: a wave owns kPairsPerWave gate/up pairs of one slot and streams them together,
 // 64 lanes across each row; lane p runs pair p's activation. down_combine: a workgroup
 // owns kDownRows output rows with one wave per slot, 64 lanes across each row and the
@@ -424,6 +428,102 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_nvfp4_kernel(D
   down_body<Fp4::kNv, kSteps, kLanes>(a, partial);
 }
 
+// ---- down_combine with the unrouted slot (the packed NVFP4 form) --------------------
+//
+// core/kernels/down_combine/nvfp4_packed.py:38-138: every token's routed down
+// projections, the unrouted (shared) stack's, the routing sum and the residual in one
+// dispatch, for any number of tokens. Slot s < top_k runs expert chosen[t, s] over
+// act[t, s]; slot top_k runs the shared stack over act[t, top_k], unweighted. The scale
+// plane is the checkpoint's group-16 plane, which equals the reference's halved plane
+// with its patch restored wherever that plane is accepted (its certificate is the
+// caller's to check). The epilogue is bf16 at every step, in slot order:
+//   d_s = T(dot_s); total = T(T(d_s * T(w_s)) + total) over s < top_k;
+//   y = T(residual + T(total + d_top_k)), each operation in fp32.
+
+constexpr int kSharedRows = 8;         // output rows per workgroup
+constexpr int kSharedWaves = 16;       // slot s runs on wave s % 16
+constexpr int kMaxSharedSlots = 32;    // top_k + 1
+
+struct SharedDownArgs {
+  const uint16_t* act;        // [tokens, top_k + 1, inner]
+  Stack routed;               // [experts, hidden, ...]
+  Stack shared;               // [hidden, ...]
+  const int32_t* chosen;      // [tokens, top_k]
+  const float* weights;       // [tokens, top_k]
+  const uint16_t* residual;   // [tokens, hidden]
+  uint16_t* out;              // [tokens, hidden]
+  int64_t experts;
+  int hidden;
+  int inner;
+  int top_k;
+};
+
+// kLanes lanes run across each row (16, 32 or 64: the fewest that give each lane one
+// 32-value chunk), so a wave holds kWave / kLanes row groups, each taking every
+// (kWave / kLanes)-th row of the workgroup with the slot's activation chunk loaded once.
+template <int kLanes>
+__global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_kernel(SharedDownArgs a) {
+  constexpr int kGroups = kWave / kLanes;
+  constexpr int kRowsPerGroup = kSharedRows / kGroups;
+  __shared__ float term[kMaxSharedSlots][kSharedRows];
+  const int lane = threadIdx.x % kWave;
+  const int part = lane % kLanes;
+  const int group = lane / kLanes;
+  const int wave = threadIdx.x / kWave;
+  const int waves = blockDim.x / kWave;
+  const int64_t token = blockIdx.y;
+  const int row_base = blockIdx.x * kSharedRows;
+  const int rows = min(kSharedRows, a.hidden - row_base);
+  const int slots = a.top_k + 1;
+  const int chunks = a.inner / kChunk;
+  const int c = min(part, chunks - 1);   // a lane past the row's end re-reads its last chunk
+  const bool in_row = part < chunks;
+  for (int slot = wave; slot < slots; slot += waves) {   // uniform over the wave
+    const bool shared = slot == a.top_k;
+    const int expert = shared ? 0 : a.chosen[token * a.top_k + slot];
+    const bool valid = shared || (expert >= 0 && expert < a.experts);
+    const Stack& stack = shared ? a.shared : a.routed;
+    const int64_t row0 = (shared ? 0 : static_cast<int64_t>(valid ? expert : 0) * a.hidden) + row_base;
+    // Every load (the activation chunk, each row's codes and scale bits) goes out before
+    // any arithmetic, with no branch among them; a row past the last re-reads the last.
+    const u32x4* x = reinterpret_cast<const u32x4*>(
+        a.act + (token * slots + slot) * a.inner + static_cast<int64_t>(c) * kChunk);
+    u32x4 xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xv[j] = x[j];
+    u32x4 w[kRowsPerGroup];
+    uint32_t s[kRowsPerGroup];
+#pragma unroll
+    for (int q = 0; q < kRowsPerGroup; ++q) {
+      const int64_t at = (row0 + min(group + kGroups * q, rows - 1)) * chunks + c;
+      w[q] = load_nt(stack.weight + at);
+      s[q] = load_scales<Fp4::kNv>(stack.scales, at);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
+    float mine = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kRowsPerGroup; ++q) {
+      const float t = in_row ? chunk_value<Fp4::kNv>(s[q], w[q], xv, 0.0f) : 0.0f;
+      const float total = group_row_sum<kLanes>(t);
+      mine = part == q ? total : mine;
+    }
+    const int row = group + kGroups * part;
+    if (part < kRowsPerGroup && row < rows) term[slot][row] = valid ? round_bf16(mine) : 0.0f;
+  }
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) < rows) {
+    const int r = threadIdx.x;
+    const int64_t n = token * a.hidden + row_base + r;
+    float total = 0.0f;
+    for (int j = 0; j < a.top_k; ++j) {
+      const float weight = round_bf16(a.weights[token * a.top_k + j]);
+      total = round_bf16(round_bf16(term[j][r] * weight) + total);
+    }
+    const float joined = round_bf16(total + term[a.top_k][r]);
+    a.out[n] = f32_to_bf16(bf16_to_f32(a.residual[n]) + joined);
+  }
+}
+
 // Host side: shape checks and launches shared by both formats.
 
 int32_t launch_gate_up(Fp4 format, const char* name, const uint16_t* x, const uint32_t* weight,
@@ -501,8 +601,54 @@ int32_t launch_down(Fp4 format, const char* name, const uint16_t* act, const uin
   return launched(name);
 }
 
+int32_t launch_down_shared(const uint16_t* act, const uint32_t* weight, const uint8_t* scales,
+                           int64_t experts, const uint32_t* shared_weight, const uint8_t* shared_scales,
+                           int64_t hidden, int64_t inner, const int32_t* chosen, const float* weights,
+                           int64_t tokens, int64_t top_k, const uint16_t* residual, uint16_t* out,
+                           hipStream_t stream) {
+  const char* name = "moe_down_combine_nvfp4_shared";
+  OMNIA_REQUIRE(experts > 0 && experts < (int64_t{1} << 20), std::string(name) + ": bad expert count");
+  OMNIA_REQUIRE(hidden > 0 && hidden < (int64_t{1} << 24), std::string(name) + ": bad hidden size");
+  OMNIA_REQUIRE(inner > 0 && inner % kChunk == 0 && inner <= kChunk * kWave,
+                std::string(name) + ": inner must be a multiple of 32 in [32, 2048]");
+  OMNIA_REQUIRE(top_k >= 0 && top_k < kMaxSharedSlots, std::string(name) + ": top_k must be in [0, 31]");
+  OMNIA_REQUIRE(tokens >= 0 && tokens <= 65535, std::string(name) + ": tokens must be in [0, 65535]");
+  if (tokens == 0) return 0;
+  OMNIA_REQUIRE(act && weight && scales && shared_weight && shared_scales && residual && out &&
+                    (top_k == 0 || (chosen && weights)),
+                std::string(name) + ": null pointer");
+  OMNIA_REQUIRE(aligned16(act) && aligned16(weight) && aligned16(shared_weight),
+                std::string(name) + ": act and the weights must be 16-byte aligned");
+  OMNIA_REQUIRE(reinterpret_cast<uintptr_t>(scales) % 2 == 0 && reinterpret_cast<uintptr_t>(shared_scales) % 2 == 0,
+                std::string(name) + ": the scales must be 2-byte aligned");
+  int32_t rc = check_device(stream);
+  if (rc != 0) return rc;
+  SharedDownArgs a{act,
+                   Stack{reinterpret_cast<const u32x4*>(weight), scales, nullptr},
+                   Stack{reinterpret_cast<const u32x4*>(shared_weight), shared_scales, nullptr},
+                   chosen, weights, residual, out, experts, static_cast<int>(hidden), static_cast<int>(inner),
+                   static_cast<int>(top_k)};
+  const dim3 grid(static_cast<unsigned>((hidden + kSharedRows - 1) / kSharedRows), static_cast<unsigned>(tokens));
+  const int64_t waves = top_k + 1 < kSharedWaves ? top_k + 1 : kSharedWaves;
+  const dim3 block(static_cast<unsigned>(waves * kWave));
+  const int64_t chunks = inner / kChunk;
+  if (chunks <= 16) moe_down_nvfp4_shared_kernel<16><<<grid, block, 0, stream>>>(a);
+  else if (chunks <= 32) moe_down_nvfp4_shared_kernel<32><<<grid, block, 0, stream>>>(a);
+  else moe_down_nvfp4_shared_kernel<64><<<grid, block, 0, stream>>>(a);
+  return launched(name);
+}
+
 }  // namespace
 }  // namespace omnia
+
+extern "C" int32_t omnia_moe_down_combine_nvfp4_shared(
+    const uint16_t* act, const uint32_t* weight, const uint8_t* scales, int64_t experts,
+    const uint32_t* shared_weight, const uint8_t* shared_scales, int64_t hidden, int64_t inner,
+    const int32_t* chosen, const float* weights, int64_t tokens, int64_t top_k, const uint16_t* residual,
+    uint16_t* out, hipStream_t stream) {
+  return omnia::launch_down_shared(act, weight, scales, experts, shared_weight, shared_scales, hidden, inner,
+                                   chosen, weights, tokens, top_k, residual, out, stream);
+}
 
 extern "C" int32_t omnia_moe_gate_up_mxfp4(const uint16_t* x, const uint32_t* weight, const uint8_t* scales,
                                            const uint16_t* bias, int64_t experts, int64_t hidden,

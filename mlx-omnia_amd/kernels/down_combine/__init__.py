@@ -5,6 +5,15 @@ down-projected by its expert, routing-weighted, summed and residual-added.
 Mirrors core/kernels/down_combine/__init__.py and kernel.py (`DownCombine`,
 `DownCombineStrategy`, `Layout`).
 
+- `HipNvfp4PackedDownCombine` (`omnia_moe_down_combine_nvfp4_shared`, csrc/moe_fp4.hip)
+  serves what the reference's `Nvfp4PackedDownCombine` serves
+  (core/kernels/down_combine/nvfp4_packed.py:196-270): an NVFP4 stack under the
+  `interleaved` layout with a required NVFP4 shared expert (`QuantizedLinearLeaf`) of
+  the same width, inner 512, hidden a multiple of 4, no bias, and both scale planes
+  passing the halved plane's certificate (every odd byte of a group pair equal to the
+  even one except flat pair 0, every byte below 128; shared/nvfp4/packed.py:150-162);
+  any number of tokens, 1 to 31 routed slots. The shared stack runs on the last slot,
+  unweighted, and the epilogue is bf16 at every step.
 - `HipNvfp4DownCombine` (`omnia_moe_down_combine_nvfp4`, csrc/moe_fp4.hip) serves what
   the reference's `Nvfp4DownCombine` serves (core/kernels/down_combine/nvfp4.py:76-98): an
   NVFP4 stack under the `interleaved` layout, no bias or shared expert, hidden and inner
@@ -53,8 +62,8 @@ Layout = Literal["interleaved", "blocked"]
 MAX_SLOTS = 16
 
 __all__ = ["DefaultDownCombine", "DownCombine", "DownCombineStrategy", "HipAffineDownCombine",
-           "HipDenseDownCombine", "HipMxfp4DownCombine", "HipNvfp4DownCombine", "Layout", "affine_down_applies",
-           "dense_down_applies"]
+           "HipDenseDownCombine", "HipMxfp4DownCombine", "HipNvfp4DownCombine", "HipNvfp4PackedDownCombine",
+           "Layout", "affine_down_applies", "dense_down_applies", "packed_down_applies", "packed_plane_certified"]
 
 
 @runtime_checkable
@@ -237,8 +246,70 @@ class HipNvfp4DownCombine(DownCombineStrategy):
         )
 
 
-_STRATEGIES = (HipNvfp4DownCombine, HipMxfp4DownCombine, HipAffineDownCombine, HipDenseDownCombine,
-               DefaultDownCombine)
+def packed_plane_certified(scales: torch.Tensor) -> bool:
+    """Whether an e4m3 plane [..., in / 16] is one the reference's halved group-32 plane
+    accepts (shared/nvfp4/packed.py:150-162): read as byte pairs, every odd byte equals its
+    even partner except in flat pair 0 (the quantizer's first span), and no byte has its
+    sign bit set."""
+    if scales.dtype != torch.uint8 or scales.numel() == 0 or scales.shape[-1] % 2:
+        return False
+    pairs = scales.reshape(-1, 2)
+    differ = pairs[1:, 0] != pairs[1:, 1]
+    return not bool(differ.any()) and int(scales.max()) < 128
+
+
+def packed_down_applies(hidden: int, inner: int, top_k: int | None = None) -> bool:
+    """The reference's shape rule (nvfp4_packed.py:185-190): one 512-wide contraction,
+    hidden a multiple of 4, 1 to 31 routed slots."""
+    return hidden % 4 == 0 and hidden > 0 and inner == 512 and (top_k is None or 0 < top_k <= 31)
+
+
+@dataclass(frozen=True)
+class HipNvfp4PackedDownCombine(DownCombineStrategy):
+    leaf: "ops.Nvfp4Leaf"
+    shared: "ops.Nvfp4Leaf"
+
+    @classmethod
+    def build(cls, leaf, *, hidden, inner, bias, shared, layout) -> "HipNvfp4PackedDownCombine | None":
+        if layout != "interleaved" or bias is not None or not packed_down_applies(hidden, inner):
+            return None
+        view = nvfp4_leaf(leaf, hidden, inner)
+        if view is None:
+            return None
+        if (not isinstance(shared, QuantizedLinearLeaf) or shared.mode != "nvfp4" or shared.biases is not None
+                or shared.bits != 4 or shared.group_size != 16):
+            return None
+        shared_view = ops.Nvfp4Leaf(shared.weight[None], shared.scales[None], None)
+        try:
+            shared_view.check(hidden, inner, "nvfp4 shared leaf")
+        except ValueError:
+            return None
+        if not all(hip_device(t) for t in shared_view.tensors()):
+            return None
+        if not (packed_plane_certified(leaf.scales) and packed_plane_certified(shared.scales)):
+            return None
+        return cls(view, shared_view)
+
+    def __call__(self, act, chosen, weights, residual):
+        """act [..., top_k + 1, inner] (the shared slot last), chosen and weights
+        [..., top_k + 1] (the last entries unread), residual [..., hidden]."""
+        hidden = residual.shape[-1]
+        tokens = residual.numel() // hidden
+        slots = chosen.shape[-1]
+        if not packed_down_applies(hidden, self.leaf.features, slots - 1):
+            raise ValueError(f"packed NVFP4 down/combine: {slots - 1} routed slots, expected 1 to 31")
+        device = self.leaf.weight.device
+        out = ops.moe_down_combine_nvfp4_shared(
+            act.reshape(tokens, slots, -1).to(torch.bfloat16).contiguous(), self.leaf, self.shared,
+            chosen.reshape(tokens, slots)[:, :-1].to(device=device, dtype=torch.int32).contiguous(),
+            weights.reshape(tokens, slots)[:, :-1].to(device=device, dtype=torch.float32).contiguous(),
+            residual.reshape(tokens, hidden).to(torch.bfloat16).contiguous(),
+        )
+        return out.reshape(residual.shape)
+
+
+_STRATEGIES = (HipNvfp4PackedDownCombine, HipNvfp4DownCombine, HipMxfp4DownCombine, HipAffineDownCombine,
+               HipDenseDownCombine, DefaultDownCombine)
 
 
 class DownCombine(DownCombineStrategy):

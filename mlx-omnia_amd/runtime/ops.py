@@ -1056,3 +1056,48 @@ def moe_down_combine_nvfp4(
          hidden, inner, chosen.data_ptr(), weights.data_ptr(), slots,
          residual.data_ptr() if residual is not None else None, out.data_ptr(), _stream(act))
     return out
+
+
+def moe_down_combine_nvfp4_shared(
+    act: torch.Tensor,
+    leaf: Nvfp4Leaf,
+    shared: Nvfp4Leaf,
+    chosen: torch.Tensor,
+    weights: torch.Tensor,
+    residual: torch.Tensor,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The packed NVFP4 down/combine for `tokens` tokens: the routed down projections, the
+    shared stack's (the last activation row, unweighted) and the residual, with the bf16
+    epilogue; see `omnia_moe_down_combine_nvfp4_shared`. act [tokens, top_k + 1, inner]
+    bf16, leaf [experts, hidden, ...], shared [hidden, ...] (or [1, hidden, ...]), chosen
+    [tokens, top_k] int32, weights [tokens, top_k] fp32, residual [tokens, hidden] bf16 ->
+    [tokens, hidden] bf16."""
+    name = "moe_down_combine_nvfp4_shared"
+    _require(leaf.bias is None and shared.bias is None, f"{name}: NVFP4 stacks carry no bias")
+    _require(leaf.weight.dim() == 3, f"{name}: weight must be [experts, hidden, words]")
+    if shared.weight.dim() == 2:
+        shared = Nvfp4Leaf(shared.weight[None], shared.scales[None], None)
+    experts, hidden = leaf.weight.shape[0], leaf.weight.shape[1]
+    _require(act.dim() == 3, f"{name}: act must be [tokens, top_k + 1, inner]")
+    tokens, slots, inner = act.shape
+    top_k = slots - 1
+    _require(top_k >= 0, f"{name}: act needs the shared slot")
+    _dense(act, BF16, "act")
+    leaf.check(hidden, inner, name)
+    shared.check(hidden, inner, name)
+    _require(shared.weight.shape[0] == 1, f"{name}: the shared stack is one matrix")
+    _require(chosen.dtype == torch.int32 and chosen.is_contiguous() and tuple(chosen.shape) == (tokens, top_k),
+             f"{name}: chosen must be contiguous int32 [tokens, top_k]")
+    _require(weights.dtype == F32 and weights.is_contiguous() and tuple(weights.shape) == (tokens, top_k),
+             f"{name}: weights must be contiguous fp32 [tokens, top_k]")
+    _require(residual.dtype == BF16 and residual.is_contiguous() and tuple(residual.shape) == (tokens, hidden),
+             f"{name}: residual must be contiguous bf16 [tokens, hidden]")
+    _require(on_rocm(act, chosen, weights, residual, *leaf.tensors(), *shared.tensors()),
+             f"{name}: tensors must share one ROCm device")
+    out = _out(out, act, (tokens, hidden), BF16, "out")
+    call("omnia_moe_down_combine_nvfp4_shared", act.data_ptr(), leaf.weight.data_ptr(), leaf.scales.data_ptr(),
+         experts, shared.weight.data_ptr(), shared.scales.data_ptr(), hidden, inner, chosen.data_ptr(),
+         weights.data_ptr(), tokens, top_k, residual.data_ptr(), out.data_ptr(), _stream(act))
+    return out

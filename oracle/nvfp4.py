@@ -24,6 +24,17 @@ down_combine (core/kernels/down_combine/nvfp4.py:16-61):
     acc = sum over slots in order of T(fp32(T(t) * w))       fp32
     y   = T(fp32(T(acc) + residual))
 
+down_combine_shared, the packed form (core/kernels/down_combine/nvfp4_packed.py:108-138),
+for each token of a batch: slot s < k runs expert chosen[s], slot k the shared stack,
+unweighted; every step is bf16:
+
+    d_s   = T(t_s)                                           t_s the exact dot here
+    total = T(T(d_s * T(w_s)) + total)    s < k, in order   each op in fp32
+    y     = T(residual + T(total + d_k))
+
+halved_scales restates the halved group-32 plane and its certificate
+(core/kernels/shared/nvfp4/packed.py:126-164).
+
 An expert id outside [0, experts) contributes zero rows (the HIP kernels' guard).
 """
 
@@ -110,3 +121,46 @@ def down_combine(act_bits: np.ndarray, stack: Stack, chosen, weights,
     if residual_bits is not None:
         out = (out + to_f32(np.asarray(residual_bits).reshape(-1))).astype(np.float32)
     return from_float(out)
+
+
+PATCH_BYTES = 128   # shared/nvfp4/packed.py:63 (SCALE_PATCH_BYTES)
+
+
+def halved_scales(scales: np.ndarray, allowed_pairs=(0,)) -> np.ndarray | None:
+    """packed.py:126-164 `halved_group32_scales`: the plane read as [size / 2, 2] byte
+    pairs keeps each even byte behind a PATCH_BYTES header holding the odd bytes of the
+    allowed pairs; None unless every other odd byte equals its even partner and every byte
+    is below 128."""
+    flat = np.ascontiguousarray(scales, dtype=np.uint8).reshape(-1, 2)
+    allowed = list(allowed_pairs)
+    mismatch = flat[:, 0] != flat[:, 1]
+    mismatch[allowed] = False
+    if mismatch.any() or int(np.asarray(scales).max(initial=0)) >= 128:
+        return None
+    header = np.zeros(PATCH_BYTES, dtype=np.uint8)
+    header[: len(allowed)] = flat[allowed, 1]
+    return np.concatenate([header, flat[:, 0]])
+
+
+def down_combine_shared(act_bits: np.ndarray, stack: Stack, shared: Stack, chosen, weights,
+                        residual_bits: np.ndarray) -> np.ndarray:
+    """act [T, k + 1, I] bf16 bits (the shared slot last), stack [E, H, ...], shared
+    [H, ...], chosen [T, k] (or [T, k + 1], the last ignored), weights likewise fp32,
+    residual [T, H] bf16 bits -> [T, H] bf16 bits."""
+    act = to_f32(np.asarray(act_bits)).astype(np.float64)
+    tokens, slots = act.shape[0], act.shape[1]
+    k = slots - 1
+    chosen = np.asarray(chosen).reshape(tokens, -1)[:, :k]
+    weights = np.asarray(weights, dtype=np.float32).reshape(tokens, -1)[:, :k]
+    residual = to_f32(np.asarray(residual_bits).reshape(tokens, -1))
+    shared_matrix = dequantize(shared)
+    out = []
+    for t in range(tokens):
+        total = np.zeros(stack.weight.shape[1], dtype=np.float32)
+        for s in range(k):
+            d = _T((_slot(stack, int(chosen[t, s])) @ act[t, s]).astype(np.float32))
+            w = _T(weights[t, s])
+            total = _T(_T(d * w) + total)
+        d_shared = _T((shared_matrix @ act[t, k]).astype(np.float32))
+        out.append(from_float((residual[t] + _T(total + d_shared)).astype(np.float32)))
+    return np.stack(out)

@@ -166,6 +166,28 @@ def make_moe_nvfp4() -> dict[str, np.ndarray]:
     return arrays
 
 
+def make_moe_nvfp4_shared() -> dict[str, np.ndarray]:
+    """The packed NVFP4 down/combine: the reference test's shape (hidden 64, inner 512,
+    top-4 of 8 plus the shared expert), two tokens, paired scale planes."""
+    rng = np.random.default_rng(12)
+    experts, hidden, inner, k, tokens = 8, 64, 512, 4, 2
+
+    def stack(lead):
+        codes = rng.integers(0, 16, size=(*lead, hidden, inner))
+        scales = np.repeat(rng.integers(0x18, 0x28, size=(*lead, hidden, inner // 32)).astype(np.uint8), 2, axis=-1)
+        return nvfp4.Stack(nvfp4.pack(codes), scales)
+
+    down, shared = stack((experts,)), stack(())
+    act = from_float(rng.standard_normal((tokens, k + 1, inner)))
+    chosen = np.array([[0, 2, 5, 7], [3, 0, 5, 1]], dtype=np.int32)
+    weights = (rng.random((tokens, k)) * 2.5).astype(np.float32)
+    residual = from_float(rng.standard_normal((tokens, hidden)))
+    out = nvfp4.down_combine_shared(act, down, shared, chosen, weights, residual)
+    return dict(act=act, chosen=chosen, weights=weights, residual=residual, out=out,
+                down_weight=down.weight, down_scales=down.scales, shared_weight=shared.weight,
+                shared_scales=shared.scales)
+
+
 def make_mlp() -> dict[str, np.ndarray]:
     rng = np.random.default_rng(7)
     hidden, inner = 128, 192
@@ -203,7 +225,7 @@ def make_attention() -> dict[str, np.ndarray]:
 MAKERS = {"attention": make_attention, "add_norm": make_add_norm, "qk_norm_rope": make_qk_norm_rope, "embed": make_embed,
           "activations": make_activations, "route": make_route, "moe": make_moe, "mlp": make_mlp,
           "moe_affine": make_moe_affine, "moe_mxfp4": make_moe_mxfp4,
-          "moe_nvfp4": make_moe_nvfp4}
+          "moe_nvfp4": make_moe_nvfp4, "moe_nvfp4_shared": make_moe_nvfp4_shared}
 
 
 def main(names: list[str]) -> None:

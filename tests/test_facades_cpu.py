@@ -743,3 +743,42 @@ def test_nvfp4_ordinal_routing_core_chain_matches_a_stable_argsort():
     got = gate_up(cpu(x), torch.from_numpy(keys))
     chosen = list(np.argsort(keys.astype(np.uint64), kind="stable")[:5])
     assert ulp_distance(bits(got), nvfp4.gate_up(x, nvfp4.Stack(words, scales), chosen)).max() <= 1
+
+
+def test_packed_nvfp4_certificate_agrees_with_the_oracle_and_cpu_declines():
+    """The facade's certificate of the halved plane (kernels/down_combine) against the
+    oracle's restatement of shared/nvfp4/packed.py:126-164, and the packed binding's
+    shape rule (nvfp4_packed.py:185-190); on CPU tensors the declaration reaches Core."""
+    from mlx_omnia_amd.kernels.down_combine import (DefaultDownCombine, DownCombine, packed_down_applies,
+                                                    packed_plane_certified)
+    from mlx_omnia_amd.kernels.leaf import QuantizedLinearLeaf, QuantizedSwitchLinearLeaf
+    from oracle import nvfp4
+
+    rng = np.random.default_rng(40)
+    base = rng.integers(0, 0x7F, size=(3, 16, 32)).astype(np.uint8)
+    base[..., 1::2] = base[..., 0::2]
+    planes = [base]
+    first = base.copy()
+    first[0, 0, 1] ^= 0x11
+    planes.append(first)
+    other = base.copy()
+    other[2, 5, 7] ^= 0x01
+    planes.append(other)
+    signed = base.copy()
+    signed[1, 3, 4:6] = 0x85
+    planes.append(signed)
+    for plane in planes:
+        want = nvfp4.halved_scales(plane) is not None
+        assert packed_plane_certified(torch.from_numpy(plane)) == want
+    assert [packed_plane_certified(torch.from_numpy(p)) for p in planes] == [True, True, False, False]
+
+    assert packed_down_applies(64, 512, 4) and packed_down_applies(2048, 512, 31)
+    assert not packed_down_applies(64, 256, 4) and not packed_down_applies(66, 512, 4)
+    assert not packed_down_applies(64, 512, 32) and not packed_down_applies(64, 512, 0)
+
+    words = torch.from_numpy(rng.integers(0, 1 << 32, size=(3, 64, 64), dtype=np.uint64).astype(np.uint32).view(np.int32))
+    scales = torch.from_numpy(np.repeat(base[:, :, ::2], 2, axis=-1)[:, :4].repeat(16, axis=1)[:, :64])
+    leaf = QuantizedSwitchLinearLeaf(words, scales[..., :32], None, 16, 4, mode="nvfp4")
+    shared = QuantizedLinearLeaf(words[0], scales[0, :, :32], None, 16, 4, mode="nvfp4")
+    facade = DownCombine(leaf, hidden=64, inner=512, shared=shared)
+    assert isinstance(facade.strategy, DefaultDownCombine)

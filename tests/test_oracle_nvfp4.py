@@ -140,3 +140,129 @@ def test_planted_mistakes_fail(monkeypatch, name):
     _mutate(monkeypatch, name)
     with pytest.raises(AssertionError):
         assert_bf16_close(nvfp4.gate_up(x, case.stack, [1, 2]), want, min_exact=0.97)
+
+
+# ---- the packed form: the halved plane's certificate and the bf16 epilogue ------------
+#
+# core/kernels/down_combine/nvfp4_packed.py reads a halved group-32 plane
+# (shared/nvfp4/packed.py:126-164) and ends in a bf16 chain. Pinned here:
+# - the certificate and the halved plane's layout by hand;
+# - that reading the halved plane the reference's way (byte `lane >> 1` of the row's
+#   halved bytes, the header's byte for the second group of expert 0's row 0) decodes
+#   exactly what the checkpoint's group-16 plane decodes, for certified planes;
+# - down_combine_shared bit for bit against the reference test's own composition
+#   (tests/test_kernel_nvfp4_fused_down_residual.py:88-118) restated in torch: float64
+#   projections rounded to bf16, then `routed * w + total` and
+#   `residual + (total + shared)` as bf16 tensor ops;
+# - and that the comparison tells apart the mistakes an oracle could make (the shared
+#   slot weighted, an fp32 running sum, the weights not rounded to bf16, the slots summed
+#   in reverse).
+
+
+def _paired_case(rows, features, seed, experts=EXPERTS):
+    case = Case(rows, features, seed, experts)
+    case.s = case.s & 0x7F                   # the halved plane refuses sign bits
+    case.s[..., 1::2] = case.s[..., 0::2]    # mlx's quantizer writes both halves of a span alike
+    case.stack = nvfp4.Stack(case.stack.weight, case.s)
+    return case
+
+
+def test_halved_scales_by_hand():
+    plane = np.array([[[5, 5, 9, 9], [7, 7, 3, 3]]], np.uint8)
+    got = nvfp4.halved_scales(plane)
+    assert got.shape == (nvfp4.PATCH_BYTES + 4,)
+    assert got[:2].tolist() == [5, 0] and not got[1:nvfp4.PATCH_BYTES].any()
+    assert got[nvfp4.PATCH_BYTES:].tolist() == [5, 9, 7, 3]
+    first = plane.copy()
+    first[0, 0, 1] = 11          # flat pair 0 may differ: its odd byte goes to the header
+    assert nvfp4.halved_scales(first)[0] == 11
+    other = plane.copy()
+    other[0, 1, 3] = 4           # any other unequal pair refuses the plane
+    assert nvfp4.halved_scales(other) is None
+    signed = plane.copy()
+    signed[0, 1, :2] = 0x90      # so does a sign bit
+    assert nvfp4.halved_scales(signed) is None
+
+
+def _halved_read(halved, codes, expert, row_count, features, patched):
+    """Expert `expert`'s [rows, features] weights read through the halved plane as
+    nvfp4_packed.py:60-105 addresses it (one byte per 32 values; lane 1 of row 0 takes
+    the header's byte when `patched`)."""
+    per_row = features // 32
+    out = np.zeros((row_count, features))
+    for r in range(row_count):
+        for j in range(features):
+            at = nvfp4.PATCH_BYTES + (expert * row_count + r) * per_row + j // 32
+            byte = halved[0] if patched and r == 0 and 16 <= j < 32 else halved[at]
+            out[r, j] = nvfp4.E2M1[codes[expert, r, j]] * nvfp4.E4M3[byte]
+    return out
+
+
+def test_halved_read_decodes_what_the_group16_plane_decodes():
+    case = _paired_case(8, 64, seed=11, experts=3)
+    case.s[0, 0, 1] = 0x33       # the quantizer's first span, restored from the header
+    stack = nvfp4.Stack(case.stack.weight, case.s)
+    halved = nvfp4.halved_scales(case.s)
+    assert halved is not None
+    codes = nvfp4.codes(stack.weight)
+    for e in range(3):
+        want = nvfp4.dequantize(nvfp4.Stack(stack.weight[e], stack.scales[e]))
+        assert np.array_equal(_halved_read(halved, codes, e, 8, 64, patched=e == 0), want)
+
+
+def _packed_inputs(seed, tokens, k, hidden=HIDDEN, inner=512):
+    rng = np.random.default_rng(seed)
+    case = _paired_case(hidden, inner, seed, experts=6)
+    shared = _paired_case(hidden, inner, seed + 1, experts=1)
+    act = from_float(rng.standard_normal((tokens, k + 1, inner)))
+    chosen = np.concatenate([rng.integers(0, 6, size=(tokens, k)), np.full((tokens, 1), 99)], axis=1)
+    weights = np.concatenate([(rng.random((tokens, k)) * 2.5).astype(np.float32),
+                              np.full((tokens, 1), 7.0, np.float32)], axis=1)
+    residual = from_float(rng.standard_normal((tokens, hidden)))
+    return case, shared, act, chosen, weights, residual
+
+
+def _torch_packed(case, shared, act_bits, chosen, weights, residual_bits, *, weigh_shared=False,
+                  fp32_total=False, unrounded_weights=False, reverse=False):
+    out = []
+    tokens, slots = act_bits.shape[:2]
+    k = slots - 1
+    for t in range(tokens):
+        act = torch.from_numpy(to_f32(act_bits[t])).double()
+        routed = _bf16(torch.stack([case.torch_matrix(e) @ act[j] for j, e in enumerate(chosen[t, :k])]).float())
+        unrouted = _bf16((shared.torch_matrix(0) @ act[k]).float())
+        w = torch.from_numpy(weights[t, :k])
+        w = w if unrounded_weights else _bf16(w)
+        order = range(k - 1, -1, -1) if reverse else range(k)
+        if fp32_total:
+            total = torch.zeros(routed.shape[1])
+            for s in order:
+                total = total + _bf16(routed[s].float() * w[s].float()).float()
+            total = _bf16(total)
+        else:
+            total = torch.zeros(routed.shape[1], dtype=torch.bfloat16)
+            for s in order:
+                total = _bf16(routed[s].float() * w[s].float()) + total
+        if weigh_shared:
+            unrouted = _bf16(unrouted.float() * float(weights[t, k]))
+        residual = _bf16(torch.from_numpy(to_f32(residual_bits[t])))
+        out.append(_bits(residual + (total + unrouted)))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("tokens,k", [(1, 4), (2, 4), (3, 8)])
+def test_down_combine_shared_matches_the_reference_composition(tokens, k):
+    case, shared, act, chosen, weights, residual = _packed_inputs(20 + tokens, tokens, k)
+    got = nvfp4.down_combine_shared(act, case.stack, nvfp4.Stack(shared.stack.weight[0], shared.s[0]),
+                                    chosen, weights, residual)
+    assert got.shape == (tokens, HIDDEN)
+    assert np.array_equal(got, _torch_packed(case, shared, act, chosen, weights, residual))
+
+
+@pytest.mark.parametrize("mistake", ["weigh_shared", "fp32_total", "unrounded_weights", "reverse"])
+def test_down_combine_shared_comparison_tells_mistakes_apart(mistake):
+    case, shared, act, chosen, weights, residual = _packed_inputs(30, 3, 8)
+    got = nvfp4.down_combine_shared(act, case.stack, nvfp4.Stack(shared.stack.weight[0], shared.s[0]),
+                                    chosen, weights, residual)
+    wrong = _torch_packed(case, shared, act, chosen, weights, residual, **{mistake: True})
+    assert not np.array_equal(got, wrong)
