@@ -686,6 +686,38 @@ def workloads() -> list[Workload]:
                 workspace=a["ws"], out=a["o"]),
         ))
 
+    # The attention of a layer with learned sinks (core/kernels/attention/sink.py) at
+    # gpt-oss-120b's geometry: 64 query heads over 8 kv heads, head_dim 64, the full
+    # layer over 32,768 and 4,096 cached rows (the roped query in, the context out).
+    sk_h, sk_kv, sk_d = 64, 8, 64
+
+    def setup_attention_sink(device, copies, rows):
+        rng = np.random.default_rng(19)
+        gen = torch.Generator(device=device).manual_seed(20)
+        sinks = _to_bf16_device(_normal(rng, (sk_h,), 2.0), device)
+        workspace = torch.empty(max(ops.attention_sink_workspace_bytes(sk_h, sk_kv, rows) // 4, 1),
+                                dtype=torch.float32, device=device)
+        sets = []
+        for _ in range(copies):
+            shape = (1, sk_kv, rows, sk_d)
+            sets.append(dict(kc=torch.randn(shape, generator=gen, device=device).to(torch.bfloat16),
+                             vc=torch.randn(shape, generator=gen, device=device).to(torch.bfloat16),
+                             q=_to_bf16_device(_normal(rng, (sk_h, sk_d)), device), sinks=sinks, ws=workspace,
+                             o=torch.empty((sk_h, sk_d), dtype=torch.bfloat16, device=device)))
+        return sets
+
+    for rows, tag in ((32768, "32k"), (4096, "4k")):
+        out.append(Workload(
+            name=f"attention_sink_decode_{tag}",
+            kernel="sink_split_kernel",
+            description=f"one query per head, 64 heads over 8 kv heads, head_dim 64, learned sinks, attention "
+                        f"over {rows} cached rows [8, {rows}, 64] bf16 (gpt-oss-120b geometry)",
+            bytes_per_launch=2 * sk_kv * rows * sk_d * 2 + 2 * sk_h * sk_d * 2 + sk_h * 2,
+            setup=lambda device, copies, rows=rows: setup_attention_sink(device, copies, rows),
+            launch=lambda a: ops.attention_sink_decode(a["q"], a["kc"], a["vc"], a["sinks"], None, sk_d ** -0.5,
+                                                       workspace=a["ws"], out=a["o"]),
+        ))
+
     # Not a product kernel: a plain device-to-device copy of known size, the scale for
     # the FETCH_SIZE / WRITE_SIZE counters (run with --only copy_calibration).
     def setup_copy(device, copies, elements=64 * 2**20):
@@ -966,6 +998,12 @@ def _cpu_legs() -> dict:
                 11 * 2048 * 288 + 11 * 512 * 2 + 10 * 8 + 2 * 2048 * 2, "the 10 routed experts and the shared one",
                 True)
 
+    def sink_leg(rows):
+        q, sinks = bf((64, 64)), bf((64,), 2.0)
+        k, v = bf((8, rows, 64)), bf((8, rows, 64))
+        return (lambda: attention.sink_attend(q, k, v, sinks, None, 0.125),
+                2 * 8 * rows * 64 * 2 + 2 * 64 * 64 * 2 + 64 * 2, f"[8, {rows}, 64], whole", True)
+
     def mlp_leg(down):
         if down:
             w, act, res = _bits(rng, (2560, 9728)), bf((9728,)), bf((2560,))
@@ -1013,6 +1051,8 @@ def _cpu_legs() -> dict:
         "dense_mlp_down_decode": lambda: mlp_leg(True),
         "attention_decode_32k": lambda: attention_leg(32768),
         "attention_decode_4k": lambda: attention_leg(4096),
+        "attention_sink_decode_32k": lambda: sink_leg(32768),
+        "attention_sink_decode_4k": lambda: sink_leg(4096),
     }
 
 

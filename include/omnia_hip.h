@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define OMNIA_ABI_VERSION 14
+#define OMNIA_ABI_VERSION 15
 
 /* Version of this ABI (OMNIA_ABI_VERSION). Pure; touches no device. */
 int32_t omnia_abi_version(void);
@@ -478,6 +478,27 @@ int32_t omnia_attention_decode(const uint16_t* raw_queries, const uint16_t* raw_
 /* Bytes of the static device array omnia_attention_decode_noalloc keeps its per-chunk
  * softmax states in (one array per GPU, held until the process ends). */
 #define OMNIA_ATTENTION_SCRATCH_BYTES (4 * 1024 * 1024)
+
+/* Workspace bytes omnia_attention_sink_decode needs for `heads` query heads over
+ * `key_length` keys: the per-chunk softmax states; 0 when one chunk covers the keys.
+ * -EINVAL for a bad geometry. Pure; touches no device. */
+int64_t omnia_attention_sink_workspace_bytes(int64_t heads, int64_t kv_heads, int64_t key_length);
+
+/* One query per head against `key_length` cached rows, the learned sink logit in the
+ * softmax's denominator (head_dim 64):
+ *   s[h, j] = (q[h] . keys[h / gqa, j]) * scale + mask[j]   (keys with mask +-inf skipped)
+ *   out[h]  = sum_j exp(s[h, j] - M) values[h / gqa, j] / (exp(sink[h] - M) + sum_j exp(s[h, j] - M))
+ * in fp32, M the maximum of the sink and the scores, rounded once to bf16. queries [heads,
+ * 64] bf16 (normed and rotated); keys, values: head h, row j at h * head_stride + j * 64
+ * bf16 elements (rows packed, 16-byte aligned); mask [key_length] fp32 additive or null;
+ * sinks [heads] bf16; out [heads, 64] bf16; gqa = heads / kv_heads in {1, 2, 4, 8}.
+ * Replaces: core/kernels/attention/sink.py:60-166,227-244 (`sink_attention`, its partial
+ * and combine kernels), called by SinkAttentionStep.__call__ (:330-352). */
+int32_t omnia_attention_sink_decode(const uint16_t* queries, const uint16_t* keys, const uint16_t* values,
+                                    int64_t key_head_stride, int64_t value_head_stride, int64_t heads,
+                                    int64_t kv_heads, int64_t head_dim, int64_t key_length, const float* mask,
+                                    const uint16_t* sinks, float scale, void* workspace, int64_t workspace_bytes,
+                                    uint16_t* out, hipStream_t stream);
 
 /* omnia_attention_decode without a workspace argument: the same step, the same kernels
  * and the same results, with the per-chunk states in a static device array of

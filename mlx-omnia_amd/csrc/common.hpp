@@ -185,6 +185,19 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return __uint_as_float(a) + __uint_as_float(b);
 }
 
+// fp32 maximum over the wave, the same in every lane.
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, __uint_as_float(dpp<kRowRor8>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp<kRowRor4>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp<kRowRor2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp<kRowRor1>(__float_as_uint(v))));
+  uint32_t a, b;
+  row_pair(__float_as_uint(v), a, b);
+  v = fmaxf(__uint_as_float(a), __uint_as_float(b));
+  half_pair(__float_as_uint(v), a, b);
+  return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+
 // Sum over each 16-lane DPP row, the same in each of its lanes.
 __device__ __forceinline__ float octet_sum(float v) {
   v += __uint_as_float(dpp<kQuadSwap1>(__float_as_uint(v)));

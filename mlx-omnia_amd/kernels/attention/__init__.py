@@ -11,6 +11,12 @@ whose `build` accepts it serves the layer.
   q/k norm gains, a rotary table, no sinks; one fused step that writes the new K/V row
   into the cache and reads the position on the device. A prefill (T != 1) goes to the
   Core chain, as in the reference.
+- `HipSinkAttentionStep` (`omnia_attention_sink_decode`, csrc/attention_sink.hip) serves
+  what the reference's `SinkAttentionStep` serves (core/kernels/attention/sink.py:256-366):
+  a layer with learned sink logits over a growing `KVCache`, bf16, head_dim 64, 1, 2, 4
+  or 8 query heads per kv head; the norms, the rotation and the cache write run as in the
+  Core chain, then one split-K attention with the sink in the softmax's denominator. A
+  prefill goes to the Core chain, as in the reference.
 - `DefaultAttentionStep` is the Core chain (core/kernels/attention/default.py:85-156): the
   norms, the rotation, `cache.update_and_fetch` and attention in torch ops (fp32). It
   accepts everything, sinks included.
@@ -28,10 +34,11 @@ from .._device import hip_device
 from ..qkv_rope.atlas import AngleAtlas
 from ..qkv_rope.kernel import AngleTable
 from ..resolve import record_fallback, resolve
-from .cache import FixedKVCache, RingKVCache
+from .cache import FixedKVCache, KVCache, RingKVCache
 
 __all__ = ["AttentionStep", "AttentionStepStrategy", "DefaultAttentionStep", "FixedKVCache",
-           "HipAttentionStep", "RingKVCache", "attention_step_applies"]
+           "HipAttentionStep", "HipSinkAttentionStep", "KVCache", "RingKVCache", "attention_step_applies",
+           "sink_step_applies"]
 
 HEAD_DIM = 128
 
@@ -104,7 +111,9 @@ class DefaultAttentionStep(AttentionStepStrategy):
         theta = positions[:, None] * torch.exp(-torch.log(torch.tensor(self.base, dtype=torch.float64)) * index / pairs)
         return torch.cos(theta).float(), torch.sin(theta).float()
 
-    def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
+    def project(self, raw_queries, raw_keys, raw_values):
+        """The step up to the attention: the normed and rotated queries [1, heads, T, D],
+        and the cached keys and values once this step's rows are written."""
         position = self.cache.offset
         length = raw_queries.shape[1]
         q = _split_heads(raw_queries, self.heads, self.head_dim)
@@ -119,12 +128,25 @@ class DefaultAttentionStep(AttentionStepStrategy):
             q = _rotate(q, cos, sin, self.rotary_pairs, self.mscale)
             k = _rotate(k, cos, sin, self.rotary_pairs, self.mscale)
         keys, values = self.cache.update_and_fetch(k, v)
+        return q, keys, values
+
+    def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
+        q, keys, values = self.project(raw_queries, raw_keys, raw_values)
         gqa = self.heads // self.kv_heads
         kf = keys.float().repeat_interleave(gqa, dim=1)
         vf = values.float().repeat_interleave(gqa, dim=1)
         scores = (q.float() @ kf.transpose(-1, -2).contiguous()) * self.scale
-        if mask is not None and not isinstance(mask, str):
-            scores = scores + mask.float()
+        if isinstance(mask, str) and mask == "causal":
+            # Query i sits at row rows - T + i and sees the rows up to it.
+            rows, length = scores.shape[-1], scores.shape[-2]
+            seen = (torch.arange(rows, device=scores.device)[None]
+                    <= (rows - length + torch.arange(length, device=scores.device))[:, None])
+            scores = scores.masked_fill(~seen, float("-inf"))
+        elif mask is not None and not isinstance(mask, str):
+            # A boolean band attends where True (scaled_dot_product_attention's rule); a
+            # float mask is additive.
+            scores = (scores.masked_fill(~mask, float("-inf")) if mask.dtype == torch.bool
+                      else scores + mask.float())
         if self.sinks is not None:
             sink = self.sinks.float().reshape(1, -1, 1, 1).expand(*scores.shape[:-1], 1)
             probs = torch.softmax(torch.cat([sink, scores], dim=-1), dim=-1)[..., 1:]
@@ -218,7 +240,54 @@ class HipAttentionStep(AttentionStepStrategy):
         return out.reshape(1, self.heads, 1, HEAD_DIM)
 
 
-_STRATEGIES = (HipAttentionStep, DefaultAttentionStep)
+SINK_HEAD_DIM = 64
+
+
+def sink_step_applies(heads: int, kv_heads: int, head_dim: int) -> bool:
+    """head_dim 64; grouped queries 1, 2, 4 or 8 per kv head."""
+    return (head_dim == SINK_HEAD_DIM and kv_heads > 0 and heads % kv_heads == 0
+            and heads // kv_heads in (1, 2, 4, 8))
+
+
+@dataclass(frozen=True)
+class HipSinkAttentionStep(AttentionStepStrategy):
+    """The decode step of a layer with learned sinks over a growing `KVCache`: the norms,
+    the rotation and the cache write as the Core chain runs them (the reference's
+    SinkAttentionStep runs them in ops too, core/kernels/attention/sink.py:330-352), then
+    the attention on `omnia_attention_sink_decode`. A prefill goes to the Core chain."""
+
+    core: DefaultAttentionStep
+    sinks: torch.Tensor
+
+    @classmethod
+    def build(cls, cache, *, heads, kv_heads, head_dim, scale, dtype, query_weight, key_weight,
+              eps, rotary_pairs, mscale, angles, base, sinks) -> "HipSinkAttentionStep | None":
+        if not isinstance(cache, KVCache) or sinks is None or dtype != torch.bfloat16:
+            return None
+        if sinks.dtype != dtype or tuple(sinks.shape) != (heads,) or not hip_device(sinks):
+            return None
+        if not sink_step_applies(heads, kv_heads, head_dim):
+            return None
+        core = DefaultAttentionStep.build(
+            cache, heads=heads, kv_heads=kv_heads, head_dim=head_dim, scale=scale, dtype=dtype,
+            query_weight=query_weight, key_weight=key_weight, eps=eps, rotary_pairs=rotary_pairs,
+            mscale=mscale, angles=angles, base=base, sinks=sinks)
+        return cls(core, sinks.contiguous())
+
+    def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
+        if raw_queries.shape[1] != 1:
+            record_fallback(self, self.core)
+            return self.core(raw_queries, raw_keys, raw_values, mask)
+        q, keys, values = self.core.project(raw_queries, raw_keys, raw_values)
+        if q.dtype != torch.bfloat16 or not hip_device(q, keys, values):
+            raise ValueError("sink attention step: the projections must be bf16 on the sinks' device")
+        band = None if isinstance(mask, str) else mask
+        out = ops.attention_sink_decode(q.reshape(-1, SINK_HEAD_DIM).contiguous(), keys, values, self.sinks,
+                                        band, self.core.scale)
+        return out.reshape(1, self.core.heads, 1, SINK_HEAD_DIM)
+
+
+_STRATEGIES = (HipAttentionStep, HipSinkAttentionStep, DefaultAttentionStep)
 
 
 class AttentionStep(AttentionStepStrategy):

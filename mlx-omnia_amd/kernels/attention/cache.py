@@ -91,3 +91,45 @@ class RingKVCache(FixedKVCache):
         self.advance(1)
         rows = self.valid_rows()
         return self.keys[:, :, :rows], self.values[:, :, :rows]
+
+
+class KVCache:
+    """A growing buffer [1, kv_heads, capacity, head_dim] for keys and one for values, the
+    reference's `KVCache` (core/cache/kv.py:18-71): rows are appended at `offset`, and the
+    buffers grow in blocks of 256 rows (`reserve`, kv.py:309-323), the old rows copied
+    into the new ones. A sliding layer keeps every row too: its mask, not the cache,
+    drops the old ones. `update_and_fetch` returns the rows written so far as views of
+    the buffers, so the head stride is the capacity's."""
+
+    BLOCK = 256
+
+    def __init__(self, window: int | None = None) -> None:
+        self.window = window
+        self.offset = 0
+        self.keys: torch.Tensor | None = None
+        self.values: torch.Tensor | None = None
+
+    @property
+    def capacity(self) -> int:
+        return 0 if self.keys is None else self.keys.shape[2]
+
+    @classmethod
+    def _reserve(cls, buffer: torch.Tensor | None, needed: int, like: torch.Tensor) -> torch.Tensor:
+        if buffer is not None and buffer.shape[2] >= needed:
+            return buffer
+        shape = list(like.shape)
+        shape[2] = (needed + cls.BLOCK - 1) // cls.BLOCK * cls.BLOCK
+        grown = torch.zeros(shape, dtype=like.dtype, device=like.device)
+        if buffer is not None:
+            grown[:, :, : buffer.shape[2]] = buffer
+        return grown
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        """Append [1, kv_heads, T, D] rows; the rows written so far."""
+        needed = self.offset + keys.shape[2]
+        self.keys = self._reserve(self.keys, needed, keys)
+        self.values = self._reserve(self.values, needed, values)
+        self.keys[:, :, self.offset : needed] = keys
+        self.values[:, :, self.offset : needed] = values
+        self.offset = needed
+        return self.keys[:, :, :needed], self.values[:, :, :needed]

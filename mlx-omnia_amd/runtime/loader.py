@@ -14,7 +14,7 @@ import threading
 from pathlib import Path
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libomnia_hip.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -70,6 +70,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "omnia_moe_gate_up_nvfp4": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "omnia_moe_down_combine_nvfp4": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
+    "omnia_attention_sink_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "omnia_attention_sink_decode": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _F32, _P, _I64,
+                                           _P, _P]),
     "omnia_moe_down_combine_nvfp4_shared": (_I32, [_P, _P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _I64, _P,
                                                    _P, _P]),
     "omnia_moe_gate_up_nvfp4_ordinal": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P]),

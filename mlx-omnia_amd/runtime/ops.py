@@ -739,6 +739,73 @@ def attention_workspace_bytes(heads: int, kv_heads: int, head_dim: int, capacity
 ATTENTION_SCRATCH_BYTES = 4 * 1024 * 1024  # OMNIA_ATTENTION_SCRATCH_BYTES
 
 
+def attention_sink_workspace_bytes(heads: int, kv_heads: int, key_length: int) -> int:
+    """Bytes of workspace `attention_sink_decode` needs over `key_length` keys."""
+    nbytes = int(library().omnia_attention_sink_workspace_bytes(heads, kv_heads, key_length))
+    _require(nbytes >= 0, "attention_sink_workspace_bytes: geometry not served")
+    return nbytes
+
+
+def _head_rows(t: torch.Tensor, name: str) -> tuple[int, int, int]:
+    """(kv_heads, rows, head stride in elements) of a [1, kv_heads, rows, 64] or
+    [kv_heads, rows, 64] bf16 view whose rows are packed (a slice of a larger buffer)."""
+    _require(t.dtype == BF16, f"{name}: expected bfloat16")
+    view = t[0] if t.dim() == 4 else t
+    _require(view.dim() == 3 and view.shape[-1] == 64, f"{name}: expected [kv_heads, rows, 64]")
+    _require(view.stride(-1) == 1 and (view.shape[1] <= 1 or view.stride(-2) == 64),
+             f"{name}: rows must be packed")
+    stride = view.stride(0) if view.shape[0] > 1 else view.shape[1] * 64
+    _require(view.data_ptr() % 16 == 0 and stride % 8 == 0, f"{name}: must be 16-byte aligned")
+    return view.shape[0], view.shape[1], stride
+
+
+def attention_sink_decode(
+    queries: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    sinks: torch.Tensor,
+    mask: torch.Tensor | None,
+    scale: float,
+    *,
+    workspace: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One query per head against the cached rows with learned sink logits; see
+    `omnia_attention_sink_decode`. queries [heads, 64] (or [1, heads, 1, 64]) bf16, keys and
+    values [1, kv_heads, rows, 64] bf16 views with packed rows, sinks [heads] bf16, mask
+    None, a boolean band [rows] (True attends) or an additive fp32 [rows] -> [heads, 64]."""
+    q = queries.reshape(-1, 64)
+    heads = q.shape[0]
+    _dense(q, BF16, "queries")
+    kv_heads, rows, key_stride = _head_rows(keys, "keys")
+    v_heads, v_rows, value_stride = _head_rows(values, "values")
+    _require((v_heads, v_rows) == (kv_heads, rows), "attention_sink_decode: keys and values differ in shape")
+    _require(sinks.dtype == BF16 and sinks.is_contiguous() and sinks.numel() == heads,
+             "attention_sink_decode: sinks must be contiguous bf16 [heads]")
+    additive = None
+    if mask is not None:
+        flat = mask.reshape(-1)
+        _require(flat.numel() == rows, "attention_sink_decode: the mask must cover every row")
+        if flat.dtype == torch.bool:
+            additive = torch.where(flat, 0.0, float("-inf")).to(torch.float32)
+        else:
+            additive = flat.to(torch.float32).contiguous()
+    nbytes = attention_sink_workspace_bytes(heads, kv_heads, rows)
+    if workspace is None and nbytes:
+        workspace = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+    _require(workspace is None or workspace.numel() * workspace.element_size() >= nbytes,
+             "attention_sink_decode: workspace too small")
+    tensors = [q, keys, values, sinks] + ([additive] if additive is not None else []) + \
+        ([workspace] if workspace is not None else [])
+    _require(on_rocm(*tensors), "attention_sink_decode: tensors must share one ROCm device")
+    out = _out(out, q, (heads, 64), BF16, "out")
+    call("omnia_attention_sink_decode", q.data_ptr(), keys.data_ptr(), values.data_ptr(), key_stride, value_stride,
+         heads, kv_heads, 64, rows, additive.data_ptr() if additive is not None else None, sinks.data_ptr(),
+         float(scale), workspace.data_ptr() if workspace is not None else None,
+         workspace.numel() * workspace.element_size() if workspace is not None else 0, out.data_ptr(), _stream(q))
+    return out
+
+
 def _attention_checks(raw_queries, raw_keys, raw_values, query_weight, key_weight, atlas,
                       key_cache, value_cache, position, heads, kv_heads, extra=()):
     head_dim = 128

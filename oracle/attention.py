@@ -15,6 +15,10 @@ sliding.py:136-430 (a ring), whose Core chain is core/kernels/attention/default.
   evaluated in float64 and rounded once to bf16 (the kernels keep fp32 with an online
   softmax; their order is free). Query head h reads kv head h // (heads / kv_heads)
   (full.py:146-149).
+
+`sink_attend` restates the attention of a layer with learned sink logits
+(core/kernels/attention/sink.py:60-166): the roped query against the cached rows, the
+sink in the softmax's denominator only, a boolean band or an additive mask.
 """
 
 from __future__ import annotations
@@ -72,3 +76,34 @@ def decode_step(raw_q, raw_k, raw_v, q_weight, k_weight, angle_row, k_cache, v_c
     keys[:, write] = k
     values[:, write] = np.asarray(raw_v).reshape(kv_heads, HEAD_DIM)
     return attend(q, keys[:, :count], values[:, :count], scale), keys, values
+
+
+def sink_attend(q_bits: np.ndarray, k_rows: np.ndarray, v_rows: np.ndarray, sink_bits: np.ndarray,
+                mask, scale: float) -> np.ndarray:
+    """core/kernels/attention/sink.py:60-166 (`sink_attention`): q [heads, D], k/v
+    [kv_heads, rows, D] bf16 bits, sinks [heads] bf16 bits, mask None (every row), a
+    boolean band [rows] (True attends) or an additive float [rows] whose infinite entries
+    drop the row -> [heads, D] bf16 bits. In float64, rounded once to bf16:
+
+        s_r = scale * q . k_r + mask_r,  M = max(sink, max_r s_r)
+        o   = sum_r exp(s_r - M) v_r / (exp(sink - M) + sum_r exp(s_r - M))
+    """
+    heads, kv_heads, rows = q_bits.shape[0], k_rows.shape[0], k_rows.shape[1]
+    gqa = heads // kv_heads
+    if mask is None:
+        additive = np.zeros(rows)
+    else:
+        flat = np.asarray(mask).reshape(-1)
+        additive = np.where(flat, 0.0, -np.inf) if flat.dtype == np.bool_ else flat.astype(np.float64)
+    keep = ~np.isinf(additive)
+    q = to_f32(q_bits).astype(np.float64)
+    k = to_f32(k_rows).astype(np.float64)
+    v = to_f32(v_rows).astype(np.float64)
+    sinks = to_f32(np.asarray(sink_bits).reshape(-1)).astype(np.float64)
+    out = np.empty(q.shape, dtype=np.float64)
+    for h in range(heads):
+        s = (float(scale) * (k[h // gqa] @ q[h]) + additive)[keep]
+        top = max(sinks[h], s.max()) if s.size else sinks[h]
+        p = np.exp(s - top)
+        out[h] = (p @ v[h // gqa][keep]) / (np.exp(sinks[h] - top) + p.sum())
+    return f64_to_bf16(out)

@@ -782,3 +782,41 @@ def test_packed_nvfp4_certificate_agrees_with_the_oracle_and_cpu_declines():
     shared = QuantizedLinearLeaf(words[0], scales[0, :, :32], None, 16, 4, mode="nvfp4")
     facade = DownCombine(leaf, hidden=64, inner=512, shared=shared)
     assert isinstance(facade.strategy, DefaultDownCombine)
+
+
+def test_sink_attention_core_chain_matches_the_oracle_on_a_growing_cache():
+    """The Core chain with sinks over `KVCache` (no norms, no rotation, so the queries are
+    the raw rows): a causal prefill, then a decode step under a boolean band, each query
+    against oracle.attention.sink_attend over the rows it may see; on CPU tensors the
+    HIP sink binding declines."""
+    from mlx_omnia_amd.kernels.attention import AttentionStep, DefaultAttentionStep, KVCache
+    from oracle import attention as oracle_attention
+
+    rng = np.random.default_rng(50)
+    heads, kv_heads, length = 8, 2, 6
+    sinks = from_float(2.0 * rng.standard_normal(heads))
+    cache = KVCache()
+    step = AttentionStep(cache, heads=heads, kv_heads=kv_heads, head_dim=64, scale=0.125, dtype=torch.bfloat16,
+                         sinks=torch.from_numpy(to_f32(sinks)).to(torch.bfloat16))
+    assert isinstance(step.strategy, DefaultAttentionStep)
+
+    def raw(t, count):
+        return torch.from_numpy(rng.standard_normal((1, t, count * 64))).to(torch.bfloat16)
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    q, k, v = raw(length, heads), raw(length, kv_heads), raw(length, kv_heads)
+    out = step(q, k, v, mask="causal")
+    assert cache.offset == length and cache.capacity == KVCache.BLOCK
+    keys, values = bits(cache.keys[0, :, :length]), bits(cache.values[0, :, :length])
+    for i in range(length):
+        want = oracle_attention.sink_attend(bits(q[0, i].reshape(heads, 64)), keys, values, sinks,
+                                            np.arange(length) <= i, 0.125)
+        assert_bf16_close(bits(out[0, :, i]), want, min_exact=0.95)
+    q, k, v = raw(1, heads), raw(1, kv_heads), raw(1, kv_heads)
+    band = torch.arange(length + 1) >= 3
+    out = step(q, k, v, mask=band)
+    keys, values = bits(cache.keys[0, :, : length + 1]), bits(cache.values[0, :, : length + 1])
+    want = oracle_attention.sink_attend(bits(q[0, 0].reshape(heads, 64)), keys, values, sinks, band.numpy(), 0.125)
+    assert_bf16_close(bits(out[0, :, 0]), want, min_exact=0.95)

@@ -121,3 +121,90 @@ def test_planted_mistakes_fail(kind):
         plain[:, 30] = raw_k.reshape(2, D)
         bad = attn.attend(q, plain[:, :31], values[:, :31], scale)
     assert not np.array_equal(good, bad)
+
+
+# ---- sink_attend: the attention of a layer with learned sink logits --------------------
+#
+# Pinned against a formula of its own: torch float64 softmax over the scores with the
+# sink prepended as one more column, that column dropped, the rest times the values
+# (what mx.fast.scaled_dot_product_attention(sinks=...) computes, the reference's own
+# parity target, tests/test_kernel_sink_attention.py:118-132). Closed forms: no attended
+# row gives zeros; a sink far below the scores gives the plain softmax. Mistakes the
+# comparison catches: the sink left out, the mask left out, the scale applied to the
+# mask, kv head h % kv_heads.
+
+def _sink_case(seed, heads=8, kv_heads=2, rows=40, head_dim=64):
+    rng = np.random.default_rng(seed)
+    q = from_float(rng.standard_normal((heads, head_dim)))
+    k = from_float(rng.standard_normal((kv_heads, rows, head_dim)))
+    v = from_float(rng.standard_normal((kv_heads, rows, head_dim)))
+    sinks = from_float(2.0 * rng.standard_normal(heads))
+    return q, k, v, sinks
+
+
+def _torch_sink(q, k, v, sinks, mask, scale, *, drop_sink=False, drop_mask=False, scale_mask=False,
+                modulo=False):
+    heads, kv_heads, rows = q.shape[0], k.shape[0], k.shape[1]
+    gqa = heads // kv_heads
+    qt = torch.from_numpy(to_f32(q)).double()
+    kt = torch.from_numpy(to_f32(k)).double()
+    vt = torch.from_numpy(to_f32(v)).double()
+    st = torch.from_numpy(to_f32(sinks)).double()
+    if mask is None:
+        additive = torch.zeros(rows, dtype=torch.float64)
+    elif mask.dtype == np.bool_:
+        additive = torch.where(torch.from_numpy(mask), 0.0, float("-inf")).double()
+    else:
+        additive = torch.from_numpy(np.asarray(mask, dtype=np.float64))
+    if drop_mask:
+        additive = torch.zeros(rows, dtype=torch.float64)
+    out = []
+    for h in range(heads):
+        kvh = h % kv_heads if modulo else h // gqa
+        dots = kt[kvh] @ qt[h]
+        scores = (dots + additive) * scale if scale_mask else dots * scale + additive
+        if drop_sink:
+            probs = torch.softmax(scores, dim=0)
+        else:
+            probs = torch.softmax(torch.cat([st[h : h + 1], scores]), dim=0)[1:]
+        out.append(probs @ vt[kvh])
+    return torch.stack(out).numpy()
+
+
+def _band(rows, window):
+    return np.arange(rows) >= rows - window
+
+
+@pytest.mark.parametrize("mask_kind", ["none", "band", "additive"])
+def test_sink_attend_matches_torch_float64(mask_kind):
+    q, k, v, sinks = _sink_case(1)
+    rows = k.shape[1]
+    mask = {"none": None, "band": _band(rows, 16),
+            "additive": np.where(np.arange(rows) % 7 == 3, -np.inf, 0.25 * np.sin(np.arange(rows)))}[mask_kind]
+    got = attn.sink_attend(q, k, v, sinks, mask, 0.125)
+    want = _torch_sink(q, k, v, sinks, mask, 0.125)
+    assert np.abs(to_f32(got) - want).max() <= 2.0 ** -8 * np.abs(want).max()
+    assert np.mean(ulp_distance(got, from_float(want.astype(np.float32))) == 0) >= 0.99
+
+
+def test_sink_attend_closed_forms():
+    q, k, v, sinks = _sink_case(2)
+    rows = k.shape[1]
+    none = attn.sink_attend(q, k, v, sinks, np.zeros(rows, bool), 0.125)
+    assert not to_f32(none).any()
+    empty = attn.sink_attend(q, k[:, :0], v[:, :0], sinks, None, 0.125)
+    assert empty.shape == q.shape and not to_f32(empty).any()
+    low = from_float(np.full(q.shape[0], -1e30))
+    plain = attn.sink_attend(q, k, v, low, None, 0.125)
+    want = _torch_sink(q, k, v, low, None, 0.125, drop_sink=True)
+    assert np.abs(to_f32(plain) - want).max() <= 2.0 ** -8 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("mistake", ["drop_sink", "drop_mask", "scale_mask", "modulo"])
+def test_sink_attend_comparison_tells_mistakes_apart(mistake):
+    q, k, v, sinks = _sink_case(3)
+    rows = k.shape[1]
+    mask = np.where(np.arange(rows) % 5 == 0, -np.inf, 0.5 * np.cos(np.arange(rows)))
+    got = to_f32(attn.sink_attend(q, k, v, sinks, mask, 0.125))
+    wrong = _torch_sink(q, k, v, sinks, mask, 0.125, **{mistake: True})
+    assert np.abs(got - wrong).max() > 4 * 2.0 ** -8 * np.abs(wrong).max()
