@@ -1,0 +1,49 @@
+"""The `torch.library` registration (runtime/torch_ops.py) on the CPU: every operator is
+registered under `torch.ops.omnia`, and its fake implementation gives the shapes and
+dtypes the entry point writes, without a device (what torch.compile and export trace)."""
+
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+from mlx_omnia_amd.runtime import loader, torch_ops
+
+BF16 = torch.bfloat16
+
+
+def test_every_operator_is_registered():
+    for name in torch_ops.REGISTERED:
+        assert hasattr(torch.ops.omnia, name), name
+
+
+def test_fake_shapes_and_dtypes():
+    with FakeTensorMode():
+        x = torch.empty(4, 2560, dtype=BF16)
+        summed, normed = torch.ops.omnia.add_rms_norm(x, x, torch.empty(2560, dtype=BF16), 1e-6)
+        assert summed.shape == normed.shape == (4, 2560) and normed.dtype == BF16
+        q, k = torch.ops.omnia.qk_norm_rope(torch.empty(5, 32, 128, dtype=BF16), torch.empty(5, 8, 128, dtype=BF16),
+                                            torch.empty(128, dtype=BF16), torch.empty(128, dtype=BF16),
+                                            torch.empty(64, 64), torch.empty(64, 64), 0, 1e-6, 64, 1.0)
+        assert q.shape == (32, 5, 128) and k.shape == (8, 5, 128)
+        q, k = torch.ops.omnia.rope_epilogue(torch.empty(6, 48 * 128, dtype=BF16), torch.empty(128, dtype=BF16),
+                                             torch.empty(128, dtype=BF16), 32, 8, 128, 0, 20.0, 1e-6)
+        assert q.shape == (32, 6, 128) and k.shape == (8, 6, 128)
+        hidden, full, sliding = torch.ops.omnia.embed_atlas(torch.empty(2, 7, dtype=torch.int32),
+                                                            torch.empty(100, 64, dtype=BF16), torch.empty(50, 128),
+                                                            None, 3, 7)
+        assert hidden.shape == (2, 7, 64) and full.shape == (7, 128) and sliding.shape == (0, 0)
+        y = torch.ops.omnia.swiglu(torch.empty(3, 96, dtype=BF16), torch.empty(3, 96, dtype=BF16))
+        assert y.shape == (3, 96) and y.dtype == BF16
+        g = torch.ops.omnia.gate_softplus(torch.empty(3, 32, dtype=BF16), torch.empty(32), torch.empty(32))
+        assert g.shape == (3, 32) and g.dtype == torch.float32
+        y, g = torch.ops.omnia.gated_activations(torch.empty(3, 96, dtype=BF16), torch.empty(3, 96, dtype=BF16),
+                                                 torch.empty(3, 32, dtype=BF16), torch.empty(32), torch.empty(32))
+        assert y.shape == (3, 96) and g.shape == (3, 32)
+        for op in (lambda t: torch.ops.omnia.softmax_topk(t, 8),
+                   lambda t: torch.ops.omnia.sigmoid_topk(t, torch.empty(128), 8)):
+            idx, w = op(torch.empty(2, 5, 128, dtype=BF16))
+            assert idx.shape == w.shape == (2, 5, 8) and idx.dtype == torch.int32 and w.dtype == torch.float32
+        packed = torch.ops.omnia.pack_router_weight(torch.empty(128, 2048, dtype=BF16))
+        assert packed.shape == (loader.library().omnia_router_pack_bytes(128, 2048),)
+        s2, n2, idx, w = torch.ops.omnia.residual_rms_router(x[:, :2048], x[:, :2048], torch.empty(2048, dtype=BF16),
+                                                            packed, 128, 8, 1e-6)
+        assert s2.shape == (4, 2048) and idx.shape == (4, 8)
