@@ -11,26 +11,28 @@
 //
 // Layout. A workgroup (4 waves) owns one kv head and one chunk of keys, and serves every
 // query head of that kv head, so grouped queries share each key and value load. A wave
-// takes 64 keys at a time:
-// - scores on v_mfma_f32_16x16x32_bf16: the G query heads (padded to 16) are the A
-//   operand, held in registers for the whole chunk; 16 keys are the B operand, loaded
-//   straight from their rows (16 bytes per lane); four tiles of 16 keys, two steps each;
-// - lane l then holds heads 4 (l / 16) .. + 3 against key l % 16 of each tile, so a
-//   head's block maximum is a reduction inside one DPP row and its running maximum is
-//   uniform over that row;
-// - values: the weights (and each head's rescale factor) go through LDS to a second
-//   layout, lane (key group kg, slice g): keys 8 kg .. 8 kg + 7, elements 8 g .. 8 g + 7,
-//   so a value load instruction reads 1 KiB of contiguous cache and each lane
-//   accumulates G x 8 outputs in fp32.
-// Measured at gpt-oss-120b's geometry (32,768 / 4,096 rows, one call): scores on
-// v_dot2_f32_bf16 with the queries read from LDS 25.3 / 11.5 us, on MFMA 22.3 / 10.9 us;
-// the next block's loads issued ahead into a second register set (occupancy 1) 32.8 /
-// 12.1 us.
-// At the chunk's end the eight key groups add up across lanes (DPP, permlane swaps), the
-// four waves merge through LDS, and the chunk's (max, sum, context) state goes to the
-// workspace, or, with one chunk, straight to the output with the sink folded in. A chunk
-// whose mask hides every key does no loads. A second kernel merges the chunks of each
-// query head and folds in the sink.
+// takes 64 keys at a time, both products on v_mfma_f32_16x16x32_bf16:
+// - scores: the G query heads (padded to 16) are the A operand, held in registers for the
+//   whole chunk; 16 keys are the B operand, loaded straight from their rows (16 bytes per
+//   lane); four tiles of 16 keys, two steps each. Lane l then holds heads
+//   4 (l / 16) .. + 3 against key l % 16 of each tile, so a head's block maximum is a
+//   reduction inside one DPP row and its running maximum is uniform over that row;
+// - values: the fp32 weights, through LDS, become the A operand split into bf16 high and
+//   low parts (p = hi + lo to about 2^-17 of p); the block's values, loaded 1 KiB of
+//   contiguous cache per instruction and transposed through LDS, are the B operand. The
+//   context accumulates in fp32 in the MFMA's output layout, the same rows (heads) as
+//   the scores', so the online rescale needs no exchange.
+// At the chunk's end the sums add up inside each DPP row, the four waves merge through
+// LDS, and the chunk's (max, sum, context) state goes to the workspace, or, with one
+// chunk, straight to the output with the sink folded in. A chunk whose mask hides every
+// key does no loads. A second kernel merges the chunks of each query head and folds in
+// the sink.
+// Measured at gpt-oss-120b's geometry (32,768 / 4,096 rows, one call each): scores on
+// v_dot2_f32_bf16 and the value sum on VALU fp32 FMAs 25.3 / 11.5 us; scores on MFMA
+// 22.3 / 10.9 us; the value sum on MFMA as well 20.1 / 9.7 us, and with the LDS cut to
+// 45.5 KB (three workgroups per CU) 20.3 / 9.2 us. The next block's loads issued ahead
+// into a second register set were slower every time (32.8 / 12.1 over the first form,
+// 21.4 / 9.4 over the last), as were twice as many chunks (24.8 / 9.4).
 #include "common.hpp"
 #include "host.hpp"
 
@@ -87,20 +89,28 @@ __device__ __forceinline__ float with_sink(float m, float l, float o, float sink
 
 template <int G>
 __global__ __launch_bounds__(kThreads) void sink_split_kernel(SinkArgs a) {
-  __shared__ __align__(16) float p_lds[kWaves][G][kBlock];     // a block's weights
-  __shared__ __align__(16) float corr_lds[kWaves][G];          // a block's rescale factors
-  __shared__ float merge_lds[kWaves][G][kPartial];
+  constexpr int kPPitch = kBlock + 4;         // weight rows padded against bank conflicts
+  constexpr int kVPitch = kBlock + 8;         // transposed value rows (bf16), padded
+  // LDS: per wave a block's weights (G rows) and its values transposed; the waves'
+  // final states reuse the same memory.
+  constexpr int kWaveBytes = G * kPPitch * 4 + kD * kVPitch * 2;
+  static_assert(kWaves * G * kPartial * 4 <= kWaves * kWaveBytes, "merge fits");
+  __shared__ __align__(16) unsigned char lds[kWaves * kWaveBytes];
   __shared__ int live;
+  float (*p_lds)[kPPitch] = reinterpret_cast<float (*)[kPPitch]>(lds + (threadIdx.x / kWave) * kWaveBytes);
+  uint16_t (*vt_lds)[kVPitch] =
+      reinterpret_cast<uint16_t (*)[kVPitch]>(lds + (threadIdx.x / kWave) * kWaveBytes + G * kPPitch * 4);
+  float (*merge_lds)[G][kPartial] = reinterpret_cast<float (*)[G][kPartial]>(lds);
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int chunk = blockIdx.x;
   const int kvh = blockIdx.y;
   const int j0 = chunk * a.chunk;
   const int j1 = min(j0 + a.chunk, a.key_length);
-  const int n = lane % 16;    // score layout: key within a 16-key tile / query row
-  const int r = lane / 16;    // score layout: DPP row, heads 4 r .. 4 r + 3
-  const int kg = lane / 8;    // value layout: key group
-  const int g = lane % 8;     // value layout: element slice
+  const int n = lane % 16;    // MFMA layouts: key (scores) / query row (operands) / element
+  const int r = lane / 16;    // DPP row: heads 4 r .. 4 r + 3 of the outputs
+  const int kg = lane / 8;    // value loads: key group
+  const int g = lane % 8;     // value loads: element slice
 
   // The queries as the MFMA A operand: lane l holds head l % 16's elements
   // 8 (l / 16) + 32 kk .. + 8 (rows past the group's G heads are zero).
@@ -120,19 +130,16 @@ __global__ __launch_bounds__(kThreads) void sink_split_kernel(SinkArgs a) {
   if (any) live = 1;   // every writer stores the same value
   __syncthreads();
 
-  // Score-layout state of heads 4 r + i: the running maximum m (uniform over the DPP row)
-  // and the lane's part of the sum l. Value-layout state: o[h][d], element 8 g + d of
-  // head h over the lane's key group.
-  float m[4], l[4], o[G][8];
+  // State of heads 4 r + i (the MFMA output rows of the lane): the running maximum m
+  // (uniform over the DPP row), the lane's part of the sum l, and the context o[dt][i],
+  // element 16 dt + n.
+  float m[4], l[4];
+  f32x4 o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m[i] = -INFINITY;
     l[i] = 0.0f;
-  }
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
+    o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
   if (live) {
     const uint16_t* khead = a.keys + static_cast<int64_t>(kvh) * a.key_head_stride;
@@ -172,8 +179,20 @@ __global__ __launch_bounds__(kThreads) void sink_split_kernel(SinkArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) s[t][i] = valid ? (acc[i] * a.scale + mk[t]) * kLog2e : -INFINITY;
       }
+      // The values, transposed through LDS: element d of key j at vt_lds[d][j - base].
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const uint32_t a0 = (d & 1) ? (v[e][d / 2] >> 16) : (v[e][d / 2] & 0xFFFFu);
+          const uint32_t a1 = (d & 1) ? (v[e + 1][d / 2] >> 16) : (v[e + 1][d / 2] & 0xFFFFu);
+          w[e / 2] = a0 | (a1 << 16);
+        }
+        *reinterpret_cast<u32x4*>(&vt_lds[8 * g + d][8 * kg]) = u32x4{w[0], w[1], w[2], w[3]};
+      }
       // The block's maximum per head: over the four tiles in the lane, then over the
-      // sixteen keys of the DPP row.
+      // sixteen keys of the DPP row; then the weights and the rescale of the context.
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float top = fmaxf(fmaxf(s[0][i], s[1][i]), fmaxf(s[2][i], s[3][i]));
@@ -189,38 +208,46 @@ __global__ __launch_bounds__(kThreads) void sink_split_kernel(SinkArgs a) {
         for (int t = 0; t < 4; ++t) {
           const float p = s[t][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[t][i] - mx);
           sum += p;
-          if (4 * r + i < G) p_lds[wave][4 * r + i][16 * t + n] = p;
+          if (4 * r + i < G) p_lds[4 * r + i][16 * t + n] = p;
         }
         l[i] = l[i] * corr + sum;
-        if (4 * r + i < G && n == 0) corr_lds[wave][4 * r + i] = corr;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt][i] *= corr;
       }
       __builtin_amdgcn_wave_barrier();
+      // o += P V on the MFMA: P (head l % 16, keys 8 (l / 16) + 32 ks .. + 8) split into
+      // bf16 high and low parts as the A operand (rows past the G heads zero), the
+      // transposed values as the B operand.
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float corr = corr_lds[wave][h];
-        if (corr != 1.0f) {   // uniform over the wave
+      for (int ks = 0; ks < 2; ++ks) {
+        const int row = n < G ? n : 0;
+        const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4 p0 = n < G ? *reinterpret_cast<const f32x4*>(&p_lds[row][32 * ks + 8 * r]) : zero;
+        const f32x4 p1 = n < G ? *reinterpret_cast<const f32x4*>(&p_lds[row][32 * ks + 8 * r + 4]) : zero;
+        const float pf[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+        uint32_t hi[4], lo[4];
 #pragma unroll
-          for (int d = 0; d < 8; ++d) o[h][d] *= corr;
+        for (int e = 0; e < 8; e += 2) {
+          hi[e / 2] = pack_bf16(pf[e], pf[e + 1]);
+          lo[e / 2] = pack_bf16(pf[e] - bf16_lo(hi[e / 2]), pf[e + 1] - bf16_hi(hi[e / 2]));
+        }
+        const bf16x8 pa_hi = __builtin_bit_cast(bf16x8, u32x4{hi[0], hi[1], hi[2], hi[3]});
+        const bf16x8 pa_lo = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], lo[2], lo[3]});
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const u32x4 vb = *reinterpret_cast<const u32x4*>(&vt_lds[16 * dt + n][32 * ks + 8 * r]);
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_hi, __builtin_bit_cast(bf16x8, vb), o[dt], 0, 0, 0);
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, __builtin_bit_cast(bf16x8, vb), o[dt], 0, 0, 0);
         }
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float vf[8];
-        unpack8(v[e], vf);
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          const float p = p_lds[wave][h][8 * kg + e];
-#pragma unroll
-          for (int d = 0; d < 8; ++d) o[h][d] = __builtin_fmaf(p, vf[d], o[h][d]);
-        }
-      }
-      // The next block overwrites p_lds and corr_lds only after every lane has read them.
+      // The next block overwrites the weights and values only after every lane has read them.
       __builtin_amdgcn_wave_barrier();
     }
   }
 
-  // The wave's state. l: over the sixteen lanes of each DPP row; o: over the eight key
-  // groups (lanes g, g + 8, ...).
+  // The wave's state: l over the sixteen lanes of each DPP row; o is whole per lane. The
+  // states go to LDS the blocks used, once every wave is done with its blocks.
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float x = l[i];
@@ -228,26 +255,14 @@ __global__ __launch_bounds__(kThreads) void sink_split_kernel(SinkArgs a) {
     x += __uint_as_float(dpp<kRowRor4>(__float_as_uint(x)));
     x += __uint_as_float(dpp<kRowRor2>(__float_as_uint(x)));
     x += __uint_as_float(dpp<kRowRor1>(__float_as_uint(x)));
-    if (n == 0 && 4 * r + i < G) {
-      merge_lds[wave][4 * r + i][kD] = m[i];
-      merge_lds[wave][4 * r + i][kD + 1] = x;
-    }
-  }
+    const int h = 4 * r + i;
+    if (h < G) {
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      float x = o[h][d];
-      x += __uint_as_float(dpp<kRowRor8>(__float_as_uint(x)));
-      uint32_t lo, hi;
-      row_pair(__float_as_uint(x), lo, hi);
-      x = __uint_as_float(lo) + __uint_as_float(hi);
-      half_pair(__float_as_uint(x), lo, hi);
-      o[h][d] = __uint_as_float(lo) + __uint_as_float(hi);
-    }
-    if (lane < 8) {
-#pragma unroll
-      for (int d = 0; d < 8; ++d) merge_lds[wave][h][8 * lane + d] = o[h][d];
+      for (int dt = 0; dt < 4; ++dt) merge_lds[wave][h][16 * dt + n] = o[dt][i];
+      if (n == 0) {
+        merge_lds[wave][h][kD] = m[i];
+        merge_lds[wave][h][kD + 1] = x;
+      }
     }
   }
   __syncthreads();
