@@ -26,7 +26,8 @@ for elementwise numpy, the BLAS pool for legs that multiply matrices), the cores
 process may use and the thread environment.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only NAME[,NAME]]
-       python bench.py --phase-clocks   (the fused router's per-phase wall clocks)
+       python bench.py --phase-clocks [--phase-clocks-rows 4096,512]
+                                        (the fused router's per-phase wall clocks)
 """
 
 from __future__ import annotations
@@ -1100,14 +1101,15 @@ PHASES = ("entry", "row 0 done", "phase 1 done", "tile complete", "walk done",
           "logits complete", "selection + tasks", "task list complete", "recomputed", "written")
 
 
-def router_phase_clocks(device, stamped: int = 8, timed: int = 200) -> dict:
+def router_phase_clocks(device, rows: int = 4096, stamped: int = 8, timed: int = 200) -> dict:
     """Per-phase wall clocks of the fused residual router at configs[4] ([4096, 2048],
-    128 experts, k = 8), from `libomnia_router_clocks.so` (the same source compiled with
-    its phase marks on): each of `stamped` launches, taken in the rotation's steady state,
-    records the 100 MHz wall clock of every wave at ten phase boundaries; the summary is
-    each boundary's spread over the 256 workgroups (median over launches of each
-    statistic), in µs from the launch's earliest entry. `launch_us` is the event-timed
-    mean of `timed` back-to-back launches of the diagnostic build."""
+    128 experts, k = 8), or the same at fewer `rows` (a multiple of 16: one workgroup per
+    16 tokens, so fewer workgroups share the chip), from `libomnia_router_clocks.so` (the
+    same source compiled with its phase marks on): each of `stamped` launches, taken in the
+    rotation's steady state, records the 100 MHz wall clock of every wave at ten phase
+    boundaries; the summary is each boundary's spread over the workgroups (median over
+    launches of each statistic), in µs from the launch's earliest entry. `launch_us` is
+    the event-timed mean of `timed` back-to-back launches of the diagnostic build."""
     import ctypes
 
     import torch
@@ -1124,7 +1126,9 @@ def router_phase_clocks(device, stamped: int = 8, timed: int = 200) -> dict:
                                               + [ctypes.c_float] + [ctypes.c_void_p] * 6)
     lib.omnia_router_phase_clocks_set.argtypes = [ctypes.c_void_p]
     lib.omnia_last_error.restype = ctypes.c_char_p
-    rows, hidden, experts, k = 4096, 2048, 128, 8
+    if rows <= 0 or rows % 16:
+        raise ValueError(f"phase clocks: rows must be a positive multiple of 16, not {rows}")
+    hidden, experts, k = 2048, 128, 8
     groups, slots = rows // 16, len(PHASES)
     rng = np.random.default_rng(7)
     copies = 8  # 8 x 68 MB: past the 256 MB Infinity Cache
@@ -1189,7 +1193,8 @@ def router_phase_clocks(device, stamped: int = 8, timed: int = 200) -> dict:
     summary = {name: [round(float(np.median([s[name][q] for s in per_launch])), 2) for q in range(4)]
                for name in PHASES}
     return dict(kernel="residual_rms_router_split_kernel<128>",
-                workload="x, residual bf16 [4096, 2048], router [128, 2048], k = 8",
+                workload=f"x, residual bf16 [{rows}, 2048], router [128, 2048], k = 8",
+                workgroups=groups,
                 launch_us=round(launch_us, 3), stamped_launches=stamped,
                 columns=["p10", "median", "p90", "max"], unit="us from the launch's first entry",
                 phases=summary)
@@ -1220,6 +1225,8 @@ def main() -> int:
     parser.add_argument("--phase-clocks", action="store_true",
                         help="print the fused router's per-phase wall clocks (diagnostic "
                              "build) as one JSON line instead of the bench line")
+    parser.add_argument("--phase-clocks-rows", default="4096",
+                        help="comma-separated token counts for --phase-clocks (multiples of 16)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not run "
@@ -1237,7 +1244,8 @@ def main() -> int:
         return 1
     device = torch.device("cuda:0")
     if args.phase_clocks:
-        print(json.dumps(router_phase_clocks(device)), flush=True)
+        for rows in (int(n) for n in args.phase_clocks_rows.split(",") if n):
+            print(json.dumps(router_phase_clocks(device, rows)), flush=True)
         return 0
     only = [n for n in args.only.split(",") if n]
     selected = [w for w in workloads() if ((w.name in only) if only else w.default)]
