@@ -284,6 +284,76 @@ def workloads() -> list[Workload]:
             normalized=a["n"], indices=a["idx"], weights=a["wts"]),
     ))
 
+    # The routing of configs[4] on its own, in the softmax form and in the reference's
+    # sigmoid-with-bias form (route/softmax_topk.py, route/ordinal.py), and the fused
+    # router in that sigmoid form (route/residual.py): 4096 tokens, 128 experts, top-8.
+    def setup_route(device, copies, rows=4096, experts=128, k=8):
+        rng = np.random.default_rng(9)
+        bias = torch.from_numpy(_normal(rng, (experts,), 0.5)).to(device)
+        first = dict(logits=_to_bf16_device(_normal(rng, (rows, experts)), device), bias=bias,
+                     idx=torch.empty((rows, k), dtype=torch.int32, device=device),
+                     wts=torch.empty((rows, k), dtype=torch.float32, device=device))
+        sets = _copies(first, copies)
+        for entry in sets:
+            entry["bias"] = bias
+        return sets
+
+    out.append(Workload(
+        name="softmax_topk",
+        kernel="softmax_topk_kernel",
+        description="router logits bf16 [4096, 128] ~N(0,1) -> top-8 indices + renormalised fp32 "
+                    "softmax weights",
+        bytes_per_launch=4096 * 128 * 2 + 2 * 4096 * 8 * 4,
+        setup=setup_route,
+        launch=lambda a: ops.softmax_topk(a["logits"], 8, indices=a["idx"], weights=a["wts"]),
+    ))
+    out.append(Workload(
+        name="sigmoid_topk",
+        kernel="sigmoid_topk_kernel",
+        description="router logits bf16 [4096, 128] ~N(0,1), correction bias fp32 [128] -> ordinal "
+                    "top-8 indices + fp32 weights from the unbiased scores",
+        bytes_per_launch=4096 * 128 * 2 + 128 * 4 + 2 * 4096 * 8 * 4,
+        setup=setup_route,
+        launch=lambda a: ops.sigmoid_topk(a["logits"], a["bias"], 8, indices=a["idx"], weights=a["wts"]),
+    ))
+
+    def setup_router_sigmoid(device, copies):
+        sets = setup_router(device, copies)
+        bias = torch.from_numpy(_normal(np.random.default_rng(10), (128,), 0.5)).to(device)
+        for entry in sets:
+            entry["bias"] = bias
+        return sets
+
+    out.append(Workload(
+        name="residual_rms_router_sigmoid",
+        kernel="residual_rms_router_split_kernel",
+        description="configs[4]'s fused router in the sigmoid form: the same inputs and a correction "
+                    "bias fp32 [128] -> summed, normed, ordinal top-8 indices + fp32 weights",
+        bytes_per_launch=4 * 4096 * 2048 * 2 + 2048 * 2 + 128 * 2048 * 2 + 128 * 4 + 128 * 4
+        + 2 * 4096 * 8 * 4,
+        setup=setup_router_sigmoid,
+        launch=lambda a: ops.residual_rms_router_sigmoid(
+            a["x"], a["r"], a["w"], a["gate"], a["bias"], k=8, eps=1e-6, emit_logits=False,
+            emit_keys=False, select=True, summed=a["s"], normalized=a["n"], indices=a["idx"],
+            weights=a["wts"]),
+    ))
+
+    # The angle atlas the table-driven rotation reads (laguna/layers/attention.py:171-196):
+    # 40,960 positions x 64 pairs, cos || sin fp32, built on the device.
+    def setup_atlas(device, copies, rows=40960):
+        freqs = torch.from_numpy(np.exp(-np.log(1e6) * np.arange(pairs) / pairs)).to(device)
+        return [dict(f=freqs, out=torch.empty((rows, 2 * pairs), dtype=torch.float32, device=device))
+                for _ in range(copies)]
+
+    out.append(Workload(
+        name="rope_angle_atlas",
+        kernel="rope_atlas_kernel",
+        description="cos || sin atlas [40960, 2 x 64] fp32 from fp64 frequencies of theta=1e6",
+        bytes_per_launch=40960 * 2 * pairs * 4 + pairs * 8,
+        setup=setup_atlas,
+        launch=lambda a: ops.rope_angle_atlas(a["f"], 0, 40960, out=a["out"]),
+    ))
+
     # embedding gather + cos/sin atlas rows.
     def setup_embed(device, copies, vocab=151936, hidden=2560, batch=8, length=2048):
         rng = np.random.default_rng(4)
@@ -854,7 +924,7 @@ def _cpu_legs() -> dict:
     reference's Core chain) on a bounded sample of the workload's own shapes."""
     from oracle import activations, add_norm, attention, embed, mlp, moe, route, rope
     from oracle import affine, mxfp4, nvfp4
-    from oracle.bf16 import from_float
+    from oracle.bf16 import from_float, to_f32
 
     rng = np.random.default_rng(42)
 
@@ -911,6 +981,28 @@ def _cpu_legs() -> dict:
         return (lambda: route.residual_rms_router(x, r, w, gate, 1e-6, 8),
                 256 * (4 * 2048 * 2 + 2 * 8 * 4) + 2048 * 2 + 128 * 2048 * 2,
                 "256 of 4096 tokens", True)
+
+    def route_leg(sigmoid):
+        logits = bf((4096, 128))
+        if sigmoid:
+            bias = (0.5 * rng.standard_normal(128)).astype(np.float32)
+            scores = to_f32(logits)
+            return (lambda: route.sigmoid_topk(scores, bias, 8),
+                    4096 * 128 * 2 + 128 * 4 + 2 * 4096 * 8 * 4, "[4096, 128], whole", False)
+        return (lambda: route.softmax_topk(logits, 8), 4096 * 128 * 2 + 2 * 4096 * 8 * 4,
+                "[4096, 128], whole", False)
+
+    def router_sigmoid_leg():
+        x, r, w = bf((256, 2048)), bf((256, 2048)), bf((2048,), 0.1, 1.0)
+        gate = bf((128, 2048), 0.02)
+        bias = (0.5 * rng.standard_normal(128)).astype(np.float32)
+        return (lambda: route.residual_rms_router_sigmoid(x, r, w, gate, bias, 1e-6, 8),
+                256 * (4 * 2048 * 2 + 2 * 8 * 4) + 2048 * 2 + 128 * 2048 * 2 + 2 * 128 * 4,
+                "256 of 4096 tokens", True)
+
+    def atlas_leg():
+        return (lambda: rope.angle_table(40960, 64, 1e6), 40960 * 2 * 64 * 4 + 64 * 8,
+                "[40960, 2 x 64], whole", False)
 
     def embed_leg():
         table = np.full((151936, 2560), 0x3C00, dtype=np.uint16)  # a gather: values do not matter
@@ -1037,6 +1129,10 @@ def _cpu_legs() -> dict:
         "gate_softplus": softplus_leg,
         "gated_activations": gated_leg,
         "residual_rms_router": router_leg,
+        "softmax_topk": lambda: route_leg(False),
+        "sigmoid_topk": lambda: route_leg(True),
+        "residual_rms_router_sigmoid": router_sigmoid_leg,
+        "rope_angle_atlas": atlas_leg,
         "embed_atlas": embed_leg,
         "moe_gate_up_decode": lambda: moe_leg(False),
         "moe_down_combine_decode": lambda: moe_leg(True),

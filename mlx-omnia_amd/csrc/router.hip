@@ -49,9 +49,11 @@
 //      one bf16 value, that value is the correctly rounded logit; otherwise the logit is
 //      recomputed as an fp64 dot product from the LDS tile and W (the products of two
 //      bf16 values are exact in fp32) and rounded once. Recomputed are the unsure
-//      logits whose upper bound could reach the top k (all of them when the logits are
-//      written out), so the selection, the weights and any emitted logit equal those of
-//      the correctly rounded logits. Then the selection and the weights above.
+//      logits whose upper bound could reach the top k (all of them when the logits or
+//      the keys are written out), so the selection, the weights and any emitted logit
+//      equal those of the correctly rounded logits. Then the selection and the weights
+//      above. In the sigmoid form the bounds go through bounds of the sigmoid (below)
+//      to bounds of each ordinal key, which is monotone in the logit.
 #include "common.hpp"
 #include "host.hpp"
 
@@ -162,6 +164,20 @@ __device__ __forceinline__ void write_winners(uint32_t chosen, int k, int lane,
 __device__ __forceinline__ float sigmoid_rounded(float x) {
   const double y = 1.0 / (1.0 + exp(fabs(static_cast<double>(x))));
   return static_cast<float>(x < 0.0f ? y : 1.0 - y);
+}
+
+// lo <= sigmoid_rounded(x) <= hi from the hardware's single-precision 2^y (v_exp_f32) and
+// 1/y (v_rcp_f32), each within a few ulps; x * log2(e) rounded to fp32 moves exp(-x) by
+// at most |x| 2^-24 of itself. All of it stays below (|x| + 6) 2^-24 of the value, and the
+// slack taken is (1 + |x|) 2^-16 of it plus 2^-100 (where exp(-x) overflows, the true
+// value is below 2^-127). For the selection on bounds only: a wider interval costs
+// recomputations, never a different result.
+__device__ __forceinline__ void sigmoid_bounds(float x, float& lo, float& hi) {
+  const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+  const float s = __builtin_amdgcn_rcpf(1.0f + e);
+  const float slack = s * (0x1p-16f * (1.0f + fabsf(x))) + 0x1p-100f;
+  lo = fmaxf(s - slack, 0.0f);   // a NaN slack (s = 0 at x = -inf) leaves [0, 1]
+  hi = fminf(s + slack, 1.0f);
 }
 
 // ordinal.py:37-47 `router_key_ordinal`.
@@ -645,7 +661,8 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   const bool active = t < a.rows;  // wave-uniform; inactive waves still meet the barriers
   const bool emit = a.logits != nullptr;
   const bool sigmoid = a.bias != nullptr;
-  const bool exact_all = emit || sigmoid;  // every logit exact: no selection on the bounds
+  // Every logit exact (no selection on the bounds) when logits or keys are written out.
+  const bool exact_all = emit || (sigmoid && a.keys != nullptr);
   const float n_norm = row_norm[r];
   uint32_t bits[V], upper[V], keys[V];
   bool unsure[V];
@@ -659,8 +676,19 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
     const uint32_t hi = f32_to_bf16(logit + delta);
     bits[v] = lo;
     unsure[v] = lo != hi;
-    keys[v] = route_key(lo, e);
-    upper[v] = route_key(hi, e);
+    if (sigmoid) {
+      // The ordinal key falls as the logit rises: the worst key comes from the lower
+      // bound, the best from the upper. Inverted, so that select_topk's largest are the
+      // best (ties take one round together, which only lowers the threshold).
+      float worst, best, unused;
+      sigmoid_bounds(bf16_to_f32(static_cast<uint16_t>(lo)), worst, unused);
+      sigmoid_bounds(bf16_to_f32(static_cast<uint16_t>(hi)), unused, best);
+      keys[v] = ~ordinal_of(-(worst + bias[v]));
+      upper[v] = ~ordinal_of(-(best + bias[v]));
+    } else {
+      keys[v] = route_key(lo, e);
+      upper[v] = route_key(hi, e);
+    }
   }
   // Select on the lower bounds. A certain logit's lower bound is its value; an unsure
   // logit whose upper bound stays below the k-th selected key cannot be selected. If
@@ -1020,7 +1048,8 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   const bool active = t < a.rows;  // wave-uniform; inactive waves still meet the barriers
   const bool emit = a.logits != nullptr;
   const bool sigmoid = a.bias != nullptr;
-  const bool exact_all = emit || sigmoid;  // every logit exact: no selection on the bounds
+  // Every logit exact (no selection on the bounds) when logits or keys are written out.
+  const bool exact_all = emit || (sigmoid && a.keys != nullptr);
   const float n_norm = row_norm[r];
   uint32_t bits[V], upper[V], keys[V];
   bool unsure[V];
@@ -1034,8 +1063,19 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     const uint32_t hi = f32_to_bf16(logit + delta);
     bits[v] = lo;
     unsure[v] = lo != hi;
-    keys[v] = route_key(lo, e);
-    upper[v] = route_key(hi, e);
+    if (sigmoid) {
+      // The ordinal key falls as the logit rises: the worst key comes from the lower
+      // bound, the best from the upper. Inverted, so that select_topk's largest are the
+      // best (ties take one round together, which only lowers the threshold).
+      float worst, best, unused;
+      sigmoid_bounds(bf16_to_f32(static_cast<uint16_t>(lo)), worst, unused);
+      sigmoid_bounds(bf16_to_f32(static_cast<uint16_t>(hi)), unused, best);
+      keys[v] = ~ordinal_of(-(worst + bias[v]));
+      upper[v] = ~ordinal_of(-(best + bias[v]));
+    } else {
+      keys[v] = route_key(lo, e);
+      upper[v] = route_key(hi, e);
+    }
   }
   uint32_t chosen = 0;
   uint32_t threshold = 0xFFFFFFFFu;

@@ -461,10 +461,16 @@ def residual_rms_router_sigmoid(
     emit_logits: bool = True,
     emit_keys: bool = True,
     select: bool = False,
+    summed: torch.Tensor | None = None,
+    normalized: torch.Tensor | None = None,
+    logits: torch.Tensor | None = None,
+    keys: torch.Tensor | None = None,
+    indices: torch.Tensor | None = None,
+    weights: torch.Tensor | None = None,
 ):
     """The fused router's sigmoid form; see `omnia_residual_rms_router_sigmoid`.
     Returns (summed, normalized, logits or None, keys or None, indices or None,
-    weights or None)."""
+    weights or None); an output passed in is written in place."""
     hidden = norm_weight.numel()
     if not isinstance(router, PackedRouterWeight):
         _require(router.dim() == 2 and router.shape[-1] == hidden,
@@ -482,12 +488,12 @@ def residual_rms_router_sigmoid(
              "residual_rms_router_sigmoid: tensors must share one ROCm device")
     rows = x.numel() // hidden
     lead = x.shape[:-1]
-    summed = torch.empty_like(x)
-    normalized = torch.empty_like(x)
-    logits = torch.empty((*lead, experts), dtype=BF16, device=x.device) if emit_logits else None
-    keys = torch.empty((*lead, experts), dtype=torch.uint32, device=x.device) if emit_keys else None
-    indices = torch.empty((*lead, k), dtype=torch.int32, device=x.device) if select else None
-    weights = torch.empty((*lead, k), dtype=F32, device=x.device) if select else None
+    summed = _out(summed, x, x.shape, BF16, "summed")
+    normalized = _out(normalized, x, x.shape, BF16, "normalized")
+    logits = _out(logits, x, (*lead, experts), BF16, "logits") if emit_logits else None
+    keys = _out(keys, x, (*lead, experts), torch.uint32, "keys") if emit_keys else None
+    indices = _out(indices, x, (*lead, k), torch.int32, "indices") if select else None
+    weights = _out(weights, x, (*lead, k), F32, "weights") if select else None
     ptr = lambda t: t.data_ptr() if t is not None else None
     call("omnia_residual_rms_router_sigmoid", x.data_ptr(), branch.data_ptr(),
          norm_weight.data_ptr(), router.buffer.data_ptr(), bias.data_ptr(), rows, hidden,

@@ -183,6 +183,31 @@ def test_residual_router_sigmoid_matches_oracle(rows, hidden, experts, k):
     assert torch.equal(idx3, idx) and torch.equal(wts3, wts)
 
 
+@pytest.mark.parametrize("rows,hidden,experts,k,gate_scale,bias_scale", [
+    (512, 2048, 128, 8, 5e-4, 0.0), (512, 2048, 256, 8, 5e-4, 1e-3), (256, 4096, 128, 16, 5e-4, 0.0),
+    (512, 2048, 128, 8, 0.02, 1e-4),
+])
+def test_residual_router_sigmoid_selection_on_close_keys(rows, hidden, experts, k, gate_scale, bias_scale):
+    """The selection alone runs on bounds of the keys and recomputes only the contenders:
+    tiny logits (bf16 ties among many experts, scores within a few ulps) and biases of
+    the keys' own size make most keys near the k-th, and the indices and weights must
+    still be those of the exact chain."""
+    print(f"sigmoid selection on close keys rows={rows} hidden={hidden} experts={experts} k={k}", flush=True)
+    rng = np.random.default_rng(rows + hidden + experts + k)
+    x = from_float(rng.standard_normal((rows, hidden), dtype=np.float32))
+    r = from_float(rng.standard_normal((rows, hidden), dtype=np.float32))
+    w = from_float(1.0 + 0.1 * rng.standard_normal(hidden))
+    gate = from_float(gate_scale * rng.standard_normal((experts, hidden), dtype=np.float32))
+    bias = (bias_scale * rng.standard_normal(experts)).astype(np.float32)
+    _, _, _, _, idx, wts = ops.residual_rms_router_sigmoid(
+        to_device(x), to_device(r), to_device(w), to_device(gate), torch.from_numpy(bias).cuda(),
+        k=k, eps=1e-6, emit_logits=False, emit_keys=False, select=True)
+    torch.cuda.synchronize()
+    _, _, _, _, want_idx, want_w = route.residual_rms_router_sigmoid(x, r, w, gate, bias, 1e-6, k)
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    assert np.array_equal(wts.cpu().numpy(), want_w)
+
+
 @pytest.mark.parametrize("hidden,experts", [(2048, 256), (2048, 128)])
 def test_residual_router_key_permutation_property(hidden, experts):
     x, r, w, gate, _ = _router_inputs(1, hidden, experts, seed=55)
