@@ -317,8 +317,8 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.sigmoid_topk(a["logits"], a["bias"], 8, indices=a["idx"], weights=a["wts"]),
     ))
 
-    def setup_router_sigmoid(device, copies):
-        sets = setup_router(device, copies)
+    def setup_router_sigmoid(device, copies, rows=4096):
+        sets = setup_router(device, copies, rows=rows)
         bias = torch.from_numpy(_normal(np.random.default_rng(10), (128,), 0.5)).to(device)
         for entry in sets:
             entry["bias"] = bias
@@ -336,6 +336,40 @@ def workloads() -> list[Workload]:
             a["x"], a["r"], a["w"], a["gate"], a["bias"], k=8, eps=1e-6, emit_logits=False,
             emit_keys=False, select=True, summed=a["s"], normalized=a["n"], indices=a["idx"],
             weights=a["wts"]),
+    ))
+
+    # One token (a decode step), the reference's own case for the fused router
+    # (route/residual.py:117-299, T = 1): the softmax form with its selection, and the
+    # sigmoid form writing the bf16 logits and the ordinal keys as the reference does.
+    def setup_router_one(device, copies):
+        sets = setup_router_sigmoid(device, copies, rows=1)
+        for entry in sets:
+            entry["logits"] = torch.empty((1, 128), dtype=torch.bfloat16, device=device)
+            entry["keys"] = torch.empty((1, 128), dtype=torch.uint32, device=device)
+        return sets
+
+    out.append(Workload(
+        name="residual_rms_router_decode",
+        kernel="residual_rms_router",
+        description="one token: x, residual bf16 [1, 2048], router [128, 2048] (packed once) -> summed, "
+                    "normed, bf16 logits (the facade asks for them at a decode step), top-8 indices + "
+                    "fp32 weights",
+        bytes_per_launch=4 * 2048 * 2 + 2048 * 2 + 128 * 2048 * 2 + 128 * 4 + 128 * 2 + 2 * 8 * 4,
+        setup=setup_router_one,
+        launch=lambda a: ops.residual_rms_router(
+            a["x"], a["r"], a["w"], a["gate"], k=8, eps=1e-6, summed=a["s"],
+            normalized=a["n"], logits=a["logits"], indices=a["idx"], weights=a["wts"]),
+    ))
+    out.append(Workload(
+        name="residual_rms_router_sigmoid_decode",
+        kernel="residual_rms_router",
+        description="one token, sigmoid form with a correction bias fp32 [128]: summed, normed, bf16 "
+                    "logits and uint32 ordinal keys (the reference's outputs)",
+        bytes_per_launch=4 * 2048 * 2 + 2048 * 2 + 128 * 2048 * 2 + 128 * 4 + 128 * 4 + 128 * 2 + 128 * 4,
+        setup=setup_router_one,
+        launch=lambda a: ops.residual_rms_router_sigmoid(
+            a["x"], a["r"], a["w"], a["gate"], a["bias"], k=8, eps=1e-6, summed=a["s"],
+            normalized=a["n"], logits=a["logits"], keys=a["keys"]),
     ))
 
     # The angle atlas the table-driven rotation reads (laguna/layers/attention.py:171-196):
@@ -1000,6 +1034,18 @@ def _cpu_legs() -> dict:
                 256 * (4 * 2048 * 2 + 2 * 8 * 4) + 2048 * 2 + 128 * 2048 * 2 + 2 * 128 * 4,
                 "256 of 4096 tokens", True)
 
+    def router_one_leg(sigmoid):
+        x, r, w = bf((1, 2048)), bf((1, 2048)), bf((2048,), 0.1, 1.0)
+        gate = bf((128, 2048), 0.02)
+        if sigmoid:
+            bias = (0.5 * rng.standard_normal(128)).astype(np.float32)
+            return (lambda: route.residual_rms_router_sigmoid(x, r, w, gate, bias, 1e-6, 8),
+                    4 * 2048 * 2 + 2048 * 2 + 128 * 2048 * 2 + 128 * 4 + 128 * 4 + 128 * 2 + 128 * 4,
+                    "[1, 2048], whole", True)
+        return (lambda: route.residual_rms_router(x, r, w, gate, 1e-6, 8),
+                4 * 2048 * 2 + 2048 * 2 + 128 * 2048 * 2 + 128 * 4 + 128 * 2 + 2 * 8 * 4, "[1, 2048], whole",
+                True)
+
     def atlas_leg():
         return (lambda: rope.angle_table(40960, 64, 1e6), 40960 * 2 * 64 * 4 + 64 * 8,
                 "[40960, 2 x 64], whole", False)
@@ -1132,6 +1178,8 @@ def _cpu_legs() -> dict:
         "softmax_topk": lambda: route_leg(False),
         "sigmoid_topk": lambda: route_leg(True),
         "residual_rms_router_sigmoid": router_sigmoid_leg,
+        "residual_rms_router_decode": lambda: router_one_leg(False),
+        "residual_rms_router_sigmoid_decode": lambda: router_one_leg(True),
         "rope_angle_atlas": atlas_leg,
         "embed_atlas": embed_leg,
         "moe_gate_up_decode": lambda: moe_leg(False),

@@ -846,7 +846,7 @@ template <int VPL>
 __device__ __forceinline__ void router_row(const u32x4 (&xv)[VPL], const u32x4 (&bv)[VPL],
                                            const u32x4 (&wv)[VPL], bool live, int64_t t,
                                            float eps, int lane, const RouterArgs& a,
-                                           uint16_t* tile_row, float* norm_slot) {
+                                           uint16_t* tile_row, float* norm_slot, bool store = true) {
   constexpr int H = 512 * VPL;
   u32x4 sv[VPL];  // s = bf16(x + b), packed as stored
   double part[4] = {0.0, 0.0, 0.0, 0.0};
@@ -885,7 +885,7 @@ __device__ __forceinline__ void router_row(const u32x4 (&xv)[VPL], const u32x4 (
     const u32x4 packed = pack8(n);
     const int v = lane + i * kWave;
     *reinterpret_cast<u32x4*>(tile_row + v * 8) = live ? packed : u32x4{0u, 0u, 0u, 0u};
-    if (live) {
+    if (live && store) {
       store_nt(a.summed + t * (H / 8) + v, sv[i]);
       store_nt(a.normalized + t * (H / 8) + v, packed);
     }
@@ -1142,6 +1142,110 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   OMNIA_CLOCK(a, wave, lane, 9);  // token written
 }
 
+// ---- one to four tokens: the projection spread over the chip -------------------------
+//
+// At a decode step one workgroup would read all of W through one CU (512 KB at
+// H = 2048, about 4 us at the CU's ~120 GB/s). Here a workgroup of 4 waves owns 8
+// experts. Every wave first issues the row loads of phase 1 (the first `rows` waves use
+// them) and then its 2 experts' rows of W's row-major copy; the first `rows` waves run
+// phase 1 of one token each (only the first workgroup stores the summed and normalized
+// rows), and each wave then takes its experts' logits of every token as fp64 dot
+// products of exact fp32 products, rounded once: the correctly rounded logits, the
+// fused kernel's own. They go to the caller's logits output, and softmax_topk_kernel or
+// sigmoid_topk_kernel selects from there, with the same functions as the fused kernel's
+// phase 3.
+constexpr int kDecodeRows = 4;
+constexpr int kDecodeWaves = 4;
+constexpr int kDecodeExperts = 2;   // per wave
+
+template <int VPL>
+__global__ __launch_bounds__(kDecodeWaves * kWave) void router_decode_logits_kernel(RouterArgs a, int experts) {
+  constexpr int H = 512 * VPL;
+  __shared__ __align__(16) uint16_t tile[kDecodeRows][H];
+  __shared__ float norm_bound[kDecodeRows];   // phase 1 writes it; unused here
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int rows = static_cast<int>(a.rows);   // 1 .. kDecodeRows
+  const int e0 = (static_cast<int>(blockIdx.x) * kDecodeWaves + wave) * kDecodeExperts;
+  // Loads in the order they are used (results are counted in issue order), with no
+  // branch among them: a wave past the last token reads the last token's rows.
+  const int64_t row = wave < rows ? wave : rows - 1;
+  u32x4 xv[VPL], bv[VPL], nw[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int v = lane + i * kWave;
+    xv[i] = load_nt(a.x + row * (H / 8) + v);
+    bv[i] = load_nt(a.branch + row * (H / 8) + v);
+    nw[i] = a.norm_weight[v];
+  }
+  u32x4 w[kDecodeExperts][VPL];
+#pragma unroll
+  for (int j = 0; j < kDecodeExperts; ++j) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      w[j][i] = *reinterpret_cast<const u32x4*>(a.weight_rows + static_cast<int64_t>(e0 + j) * H +
+                                                (lane + i * kWave) * 8);
+    }
+  }
+  if (wave < rows) {
+    router_row<VPL>(xv, bv, nw, true, wave, a.eps, lane, a, tile[wave], &norm_bound[wave], blockIdx.x == 0);
+  }
+  __syncthreads();
+  double acc[kDecodeRows][kDecodeExperts];
+#pragma unroll
+  for (int t = 0; t < kDecodeRows; ++t) {
+#pragma unroll
+    for (int j = 0; j < kDecodeExperts; ++j) acc[t][j] = 0.0;
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int h0 = (lane + i * kWave) * 8;
+    float wf[kDecodeExperts][8];
+#pragma unroll
+    for (int j = 0; j < kDecodeExperts; ++j) unpack8(w[j][i], wf[j]);
+#pragma unroll
+    for (int t = 0; t < kDecodeRows; ++t) {
+      if (t < rows) {   // uniform
+        float n[8];
+        unpack8(*reinterpret_cast<const u32x4*>(&tile[t][h0]), n);
+#pragma unroll
+        for (int j = 0; j < kDecodeExperts; ++j) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[t][j] += static_cast<double>(n[q] * wf[j][q]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kDecodeRows; ++t) {
+    if (t < rows) {
+#pragma unroll
+      for (int j = 0; j < kDecodeExperts; ++j) {
+        const uint32_t bits = f64_to_bf16(wave_sum_f64(acc[t][j]));
+        if (lane == 0) a.logits[static_cast<int64_t>(t) * experts + e0 + j] = static_cast<uint16_t>(bits);
+      }
+    }
+  }
+}
+
+// The decode path: rows <= kDecodeRows with the logits written out.
+template <int VPL, int E>
+int32_t launch_decode(const RouterArgs& a, hipStream_t stream) {
+  router_decode_logits_kernel<VPL><<<dim3(E / (kDecodeWaves * kDecodeExperts)), kDecodeWaves * kWave, 0, stream>>>(
+      a, E);
+  const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
+  constexpr int V = E / kWave;
+  if (a.bias != nullptr) {
+    if (a.keys != nullptr || a.indices != nullptr) {
+      sigmoid_topk_kernel<V, false><<<grid, 256, 0, stream>>>(a.logits, E, a.bias, a.rows, E, a.k, a.keys,
+                                                               a.indices, a.weights);
+    }
+  } else {
+    softmax_topk_kernel<V><<<grid, 256, 0, stream>>>(a.logits, E, a.rows, E, a.k, a.indices, a.weights);
+  }
+  return launched("residual_rms_router");
+}
+
 template <int E>
 int32_t launch_split(const RouterArgs& a, hipStream_t stream) {
   constexpr size_t lds = SplitShape<E>::kLds;
@@ -1230,6 +1334,10 @@ int32_t launch_router(RouterArgs a, int64_t hidden, int64_t experts, hipStream_t
 #ifdef OMNIA_PHASE_CLOCKS
   a.clocks = hidden == 2048 ? phase_clocks : nullptr;
 #endif
+  if (a.rows <= kDecodeRows && a.logits != nullptr) {
+    if (hidden == 2048) return experts == 128 ? launch_decode<4, 128>(a, stream) : launch_decode<4, 256>(a, stream);
+    return experts == 128 ? launch_decode<8, 128>(a, stream) : launch_decode<8, 256>(a, stream);
+  }
   if (hidden == 2048) {
     return experts == 128 ? launch_split<128>(a, stream) : launch_split<256>(a, stream);
   }

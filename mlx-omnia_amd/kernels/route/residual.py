@@ -90,16 +90,19 @@ class HipResidualRouter(ResidualRouterStrategy):
                    routing)
 
     def __call__(self, x, projected):
+        # A few tokens (a decode step) take the library's decode path, which needs the
+        # logits written out; more tokens run the one fused dispatch without them.
+        decode = x.numel() // x.shape[-1] <= ops.ROUTER_DECODE_ROWS
         if self.routing.bias is not None:
             summed, normalized, _, _, indices, weights = ops.residual_rms_router_sigmoid(
                 x.contiguous(), projected.contiguous(), self.norm_weight, self.gate,
                 self.routing.bias.contiguous(), k=self.routing.k, eps=self.eps,
-                emit_logits=False, emit_keys=False, select=True,
+                emit_logits=decode, emit_keys=False, select=True,
             )
             return summed, normalized, indices, weights
         summed, normalized, _, indices, weights = ops.residual_rms_router(
             x.contiguous(), projected.contiguous(), self.norm_weight, self.gate,
-            k=self.routing.k, eps=self.eps,
+            k=self.routing.k, eps=self.eps, emit_logits=decode,
         )
         return summed, normalized, indices, weights
 

@@ -370,6 +370,11 @@ def pack_router_weight(router_weight: torch.Tensor) -> PackedRouterWeight:
     return PackedRouterWeight(buffer, int(experts), int(hidden))
 
 
+# At most this many rows with the logits written out take the fused router's decode
+# path: the projection spread over the chip, then the selection kernel (two dispatches).
+ROUTER_DECODE_ROWS = 4
+
+
 def residual_rms_router(
     x: torch.Tensor,
     branch: torch.Tensor,

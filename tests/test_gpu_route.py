@@ -89,6 +89,43 @@ def test_residual_router_matches_oracle(rows, hidden, experts, k):
     np.testing.assert_allclose(wts2.cpu().numpy(), want_w, rtol=1e-5, atol=1e-7)
 
 
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("hidden,experts,k", [(2048, 128, 8), (4096, 256, 8), (2048, 256, 16), (4096, 128, 64)])
+def test_decode_path_equals_the_fused_dispatch(rows, hidden, experts, k):
+    """Up to four rows with the logits written take two dispatches (the projection
+    spread over the chip, then the selection kernel); without the logits the one fused
+    dispatch runs. Both forms give the same bits, and the oracle's."""
+    print(f"router decode path rows={rows} hidden={hidden} experts={experts} k={k}", flush=True)
+    x, r, w, gate = _router_inputs(rows, hidden, experts, seed=7 * rows + hidden + experts + k)
+    xd, rd, wd = to_device(x), to_device(r), to_device(w)
+    packed = ops.pack_router_weight(to_device(gate))
+    s1, n1, logits, idx1, w1 = ops.residual_rms_router(xd, rd, wd, packed, k=k, eps=1e-6, emit_logits=True)
+    s2, n2, none, idx2, w2 = ops.residual_rms_router(xd, rd, wd, packed, k=k, eps=1e-6)
+    torch.cuda.synchronize()
+    assert none is None
+    for a, b in ((s1, s2), (n1, n2), (idx1, idx2), (w1, w2)):
+        assert torch.equal(a, b)
+    want_s, want_n, want_logits, want_idx, want_w = route.residual_rms_router(x, r, w, gate, 1e-6, k)
+    assert np.array_equal(bits_of(s1), want_s)
+    assert_bf16_close(bits_of(n1), want_n)
+    assert np.array_equal(bits_of(logits), want_logits)
+    assert np.array_equal(idx1.cpu().numpy(), want_idx)
+    bias = torch.from_numpy((0.1 * np.random.default_rng(rows).standard_normal(experts)).astype(np.float32)).cuda()
+    s3, n3, logits3, keys3, idx3, w3 = ops.residual_rms_router_sigmoid(xd, rd, wd, packed, bias, k=k, eps=1e-6,
+                                                                       select=True)
+    _, _, none, keys4, idx4, w4 = ops.residual_rms_router_sigmoid(xd, rd, wd, packed, bias, k=k, eps=1e-6,
+                                                                  emit_logits=False, select=True)
+    torch.cuda.synchronize()
+    assert none is None
+    assert torch.equal(s3, s1) and torch.equal(n3, n1) and torch.equal(logits3, logits)
+    assert torch.equal(keys3.view(torch.int32), keys4.view(torch.int32))
+    assert torch.equal(idx3, idx4) and torch.equal(w3, w4)
+    want = route.residual_rms_router_sigmoid(x, r, w, gate, bias.cpu().numpy(), 1e-6, k)
+    assert np.array_equal(keys3.cpu().numpy(), want[3])
+    assert np.array_equal(idx3.cpu().numpy(), want[4])
+    assert np.array_equal(w3.cpu().numpy(), want[5])
+
+
 @pytest.mark.parametrize("experts,hidden", [(128, 2048), (256, 4096), (32, 96)])
 def test_pack_router_weight_layout_and_norms(experts, hidden):
     rng = np.random.default_rng(experts + hidden)
