@@ -197,7 +197,7 @@ int32_t omnia_pack_router_weight(const uint16_t* router_weight, int64_t experts,
  * x, branch [rows, hidden] bf16; norm_weight [hidden] bf16; packed_router: the router
  * weight [experts, hidden] bf16 as omnia_pack_router_weight wrote it.
  * hidden in {2048, 4096}, experts in {128, 256}; k <= 64.
- * With rows <= 4 and `logits` given (a decode step) the launch is two dispatches: the
+ * With rows <= 16 and `logits` given (decode steps) the launch is two dispatches: the
  * projection spread over many workgroups, every logit an fp64 dot product rounded once,
  * then the selection of omnia_softmax_topk over the written logits. The outputs are
  * the same bits either way.
@@ -236,7 +236,7 @@ int32_t omnia_sigmoid_topk(const void* logits, int64_t stride, int32_t logits_fp
  *   logits [rows, experts] bf16 or null; keys [rows, experts] uint32 or null;
  *   indices [rows, k] int32 and weights [rows, k] fp32, both or neither.
  * Every logit is the correctly rounded bf16 of the exact dot product, so the keys and
- * the selection equal those computed from the exact logits. With rows <= 4 and `logits`
+ * the selection equal those computed from the exact logits. With rows <= 16 and `logits`
  * given the launch is the two dispatches of omnia_residual_rms_router's decode path,
  * the second omnia_sigmoid_topk over the written logits.
  * Replaces: core/kernels/route/residual.py:117-299 (`residual_rms_router` with its

@@ -1142,34 +1142,37 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   OMNIA_CLOCK(a, wave, lane, 9);  // token written
 }
 
-// ---- one to four tokens: the projection spread over the chip -------------------------
+// ---- up to 16 tokens: the projection spread over the chip ----------------------------
 //
 // At a decode step one workgroup would read all of W through one CU (512 KB at
-// H = 2048, about 4 us at the CU's ~120 GB/s). Here a workgroup of 4 waves owns 8
-// experts. Every wave first issues the row loads of phase 1 (the first `rows` waves use
-// them) and then its 2 experts' rows of W's row-major copy; the first `rows` waves run
-// phase 1 of one token each (only the first workgroup stores the summed and normalized
-// rows), and each wave then takes its experts' logits of every token as fp64 dot
-// products of exact fp32 products, rounded once: the correctly rounded logits, the
-// fused kernel's own. They go to the caller's logits output, and softmax_topk_kernel or
-// sigmoid_topk_kernel selects from there, with the same functions as the fused kernel's
-// phase 3.
-constexpr int kDecodeRows = 4;
+// H = 2048, about 4 us at the CU's ~120 GB/s; 2 MB at 4096 x 256). Here a workgroup of 4
+// waves owns 8 experts and up to 4 tokens (grid: experts / 8 by tokens / 4). Every wave
+// first issues the token rows' loads (the first `rows` waves use them) and then its 2
+// experts' rows of W's row-major copy; the first `rows` waves run phase 1 of one token
+// each (only the workgroups of the first expert group store the summed and normalized
+// rows), and each wave then takes its experts' logits of the group's tokens as fp64 dot
+// products (each product of two bf16 values exact, each fused add rounded once), rounded
+// to bf16 once: the correctly rounded logits, the fused kernel's own. They go to the
+// caller's logits output, and softmax_topk_kernel or sigmoid_topk_kernel selects from
+// there, with the same functions as the fused kernel's phase 3.
+constexpr int kDecodeRows = 16;      // the path's limit
+constexpr int kDecodeGroupRows = 4;  // tokens per workgroup
 constexpr int kDecodeWaves = 4;
-constexpr int kDecodeExperts = 2;   // per wave
+constexpr int kDecodeExperts = 2;    // per wave
 
 template <int VPL>
 __global__ __launch_bounds__(kDecodeWaves * kWave) void router_decode_logits_kernel(RouterArgs a, int experts) {
   constexpr int H = 512 * VPL;
-  __shared__ __align__(16) uint16_t tile[kDecodeRows][H];
-  __shared__ float norm_bound[kDecodeRows];   // phase 1 writes it; unused here
+  __shared__ __align__(16) uint16_t tile[kDecodeGroupRows][H];
+  __shared__ float norm_bound[kDecodeGroupRows];   // phase 1 writes it; unused here
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  const int rows = static_cast<int>(a.rows);   // 1 .. kDecodeRows
+  const int row0 = static_cast<int>(blockIdx.y) * kDecodeGroupRows;
+  const int rows = min(kDecodeGroupRows, static_cast<int>(a.rows) - row0);   // 1 .. 4
   const int e0 = (static_cast<int>(blockIdx.x) * kDecodeWaves + wave) * kDecodeExperts;
   // Loads in the order they are used (results are counted in issue order), with no
-  // branch among them: a wave past the last token reads the last token's rows.
-  const int64_t row = wave < rows ? wave : rows - 1;
+  // branch among them: a wave past the group's last token reads that token's rows.
+  const int64_t row = row0 + (wave < rows ? wave : rows - 1);
   u32x4 xv[VPL], bv[VPL], nw[VPL];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
@@ -1188,41 +1191,47 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void router_decode_logits_ker
     }
   }
   if (wave < rows) {
-    router_row<VPL>(xv, bv, nw, true, wave, a.eps, lane, a, tile[wave], &norm_bound[wave], blockIdx.x == 0);
+    router_row<VPL>(xv, bv, nw, true, row, a.eps, lane, a, tile[wave], &norm_bound[wave], blockIdx.x == 0);
   }
   __syncthreads();
-  double acc[kDecodeRows][kDecodeExperts];
+  double acc[kDecodeGroupRows][kDecodeExperts];
 #pragma unroll
-  for (int t = 0; t < kDecodeRows; ++t) {
+  for (int t = 0; t < kDecodeGroupRows; ++t) {
 #pragma unroll
     for (int j = 0; j < kDecodeExperts; ++j) acc[t][j] = 0.0;
   }
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int h0 = (lane + i * kWave) * 8;
-    float wf[kDecodeExperts][8];
+    double wd[kDecodeExperts][8];
 #pragma unroll
-    for (int j = 0; j < kDecodeExperts; ++j) unpack8(w[j][i], wf[j]);
+    for (int j = 0; j < kDecodeExperts; ++j) {
+      float wf[8];
+      unpack8(w[j][i], wf);
 #pragma unroll
-    for (int t = 0; t < kDecodeRows; ++t) {
+      for (int q = 0; q < 8; ++q) wd[j][q] = wf[q];
+    }
+#pragma unroll
+    for (int t = 0; t < kDecodeGroupRows; ++t) {
       if (t < rows) {   // uniform
         float n[8];
         unpack8(*reinterpret_cast<const u32x4*>(&tile[t][h0]), n);
 #pragma unroll
-        for (int j = 0; j < kDecodeExperts; ++j) {
+        for (int q = 0; q < 8; ++q) {
+          const double nq = n[q];
 #pragma unroll
-          for (int q = 0; q < 8; ++q) acc[t][j] += static_cast<double>(n[q] * wf[j][q]);
+          for (int j = 0; j < kDecodeExperts; ++j) acc[t][j] = __builtin_fma(nq, wd[j][q], acc[t][j]);
         }
       }
     }
   }
 #pragma unroll
-  for (int t = 0; t < kDecodeRows; ++t) {
+  for (int t = 0; t < kDecodeGroupRows; ++t) {
     if (t < rows) {
 #pragma unroll
       for (int j = 0; j < kDecodeExperts; ++j) {
         const uint32_t bits = f64_to_bf16(wave_sum_f64(acc[t][j]));
-        if (lane == 0) a.logits[static_cast<int64_t>(t) * experts + e0 + j] = static_cast<uint16_t>(bits);
+        if (lane == 0) a.logits[static_cast<int64_t>(row0 + t) * experts + e0 + j] = static_cast<uint16_t>(bits);
       }
     }
   }
@@ -1231,8 +1240,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void router_decode_logits_ker
 // The decode path: rows <= kDecodeRows with the logits written out.
 template <int VPL, int E>
 int32_t launch_decode(const RouterArgs& a, hipStream_t stream) {
-  router_decode_logits_kernel<VPL><<<dim3(E / (kDecodeWaves * kDecodeExperts)), kDecodeWaves * kWave, 0, stream>>>(
-      a, E);
+  const dim3 groups(E / (kDecodeWaves * kDecodeExperts),
+                    static_cast<unsigned>((a.rows + kDecodeGroupRows - 1) / kDecodeGroupRows));
+  router_decode_logits_kernel<VPL><<<groups, kDecodeWaves * kWave, 0, stream>>>(a, E);
   const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
   constexpr int V = E / kWave;
   if (a.bias != nullptr) {

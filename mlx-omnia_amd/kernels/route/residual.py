@@ -90,7 +90,7 @@ class HipResidualRouter(ResidualRouterStrategy):
                    routing)
 
     def __call__(self, x, projected):
-        # A few tokens (a decode step) take the library's decode path, which needs the
+        # Up to 16 tokens (decode steps) take the library's decode path, which needs the
         # logits written out; more tokens run the one fused dispatch without them.
         decode = x.numel() // x.shape[-1] <= ops.ROUTER_DECODE_ROWS
         if self.routing.bias is not None:

@@ -372,7 +372,7 @@ def pack_router_weight(router_weight: torch.Tensor) -> PackedRouterWeight:
 
 # At most this many rows with the logits written out take the fused router's decode
 # path: the projection spread over the chip, then the selection kernel (two dispatches).
-ROUTER_DECODE_ROWS = 4
+ROUTER_DECODE_ROWS = 16
 
 
 def residual_rms_router(
