@@ -495,8 +495,10 @@ def residual_rms_router_sigmoid(
     lead = x.shape[:-1]
     summed = _out(summed, x, x.shape, BF16, "summed")
     normalized = _out(normalized, x, x.shape, BF16, "normalized")
-    logits = _out(logits, x, (*lead, experts), BF16, "logits") if emit_logits else None
-    keys = _out(keys, x, (*lead, experts), torch.uint32, "keys") if emit_keys else None
+    # An output passed in is written whatever its flag says.
+    logits = _out(logits, x, (*lead, experts), BF16, "logits") if emit_logits or logits is not None else None
+    keys = _out(keys, x, (*lead, experts), torch.uint32, "keys") if emit_keys or keys is not None else None
+    select = select or indices is not None or weights is not None
     indices = _out(indices, x, (*lead, k), torch.int32, "indices") if select else None
     weights = _out(weights, x, (*lead, k), F32, "weights") if select else None
     ptr = lambda t: t.data_ptr() if t is not None else None
