@@ -284,6 +284,21 @@ def workloads() -> list[Workload]:
             normalized=a["n"], indices=a["idx"], weights=a["wts"]),
     ))
 
+    # configs[4]'s step at Qwen3-235B-A22B's width (hidden 4096, 128 experts, top-8): the
+    # fused router's other kernel (phases one after another). Run when named by --only.
+    out.append(Workload(
+        name="residual_rms_router_h4096",
+        kernel="residual_rms_router_kernel",
+        description="x, residual bf16 [4096, 4096] ~N(0,1), norm weight 1+N(0,0.1), router [128, 4096] "
+                    "~N(0,0.02) (packed once) -> summed, normed, top-8 indices + fp32 weights",
+        bytes_per_launch=4 * 4096 * 4096 * 2 + 4096 * 2 + 128 * 4096 * 2 + 128 * 4 + 2 * 4096 * 8 * 4,
+        setup=lambda device, copies: setup_router(device, copies, hidden=4096),
+        launch=lambda a: ops.residual_rms_router(
+            a["x"], a["r"], a["w"], a["gate"], k=8, eps=1e-6, summed=a["s"],
+            normalized=a["n"], indices=a["idx"], weights=a["wts"]),
+        default=False,
+    ))
+
     # The routing of configs[4] on its own, in the softmax form and in the reference's
     # sigmoid-with-bias form (route/softmax_topk.py, route/ordinal.py), and the fused
     # router in that sigmoid form (route/residual.py): 4096 tokens, 128 experts, top-8.
