@@ -8,7 +8,9 @@ calling `ops` directly.
 
 Registered: add_rms_norm, qk_norm_rope, rope_epilogue, embed_atlas, swiglu,
 gate_softplus, gated_activations, softmax_topk, sigmoid_topk, pack_router_weight,
-residual_rms_router.
+residual_rms_router, residual_rms_router_sigmoid; and the steps either side of the path:
+moe_gate_up, moe_down_combine (dense bf16 stacks), dense_gate_up_swiglu,
+dense_down_residual, attention_sink_decode.
 """
 
 from __future__ import annotations
@@ -201,5 +203,88 @@ def _residual_rms_router_fake(x, branch, norm_weight, packed, experts, k, eps):
 
 residual_rms_router = _op("residual_rms_router", _residual_rms_router, _residual_rms_router_fake)
 
+def _residual_rms_router_sigmoid(x: torch.Tensor, branch: torch.Tensor, norm_weight: torch.Tensor,
+                                 packed: torch.Tensor, bias: torch.Tensor, experts: int, k: int,
+                                 eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The reference's outputs (route/residual.py:268-299): summed, normalized, bf16 logits,
+    uint32 ordinal keys; `packed` as for residual_rms_router."""
+    router = ops.PackedRouterWeight(packed, int(experts), int(x.shape[-1]))
+    summed, normalized, logits, keys, _, _ = ops.residual_rms_router_sigmoid(x, branch, norm_weight, router, bias,
+                                                                          k=k, eps=eps)
+    return summed, normalized, logits, keys
+
+
+def _residual_rms_router_sigmoid_fake(x, branch, norm_weight, packed, bias, experts, k, eps):
+    shape = (*x.shape[:-1], experts)
+    return (torch.empty_like(x), torch.empty_like(x), x.new_empty(shape, dtype=BF16),
+            x.new_empty(shape, dtype=torch.uint32))
+
+
+residual_rms_router_sigmoid = _op("residual_rms_router_sigmoid", _residual_rms_router_sigmoid,
+                                  _residual_rms_router_sigmoid_fake)
+
+
+# the steps either side of the path ----------------------------------------------------
+
+def _moe_gate_up(x: torch.Tensor, weight: torch.Tensor, chosen: torch.Tensor) -> torch.Tensor:
+    return ops.moe_gate_up(x, weight, chosen)
+
+
+def _moe_gate_up_fake(x, weight, chosen):
+    return x.new_empty((chosen.numel(), weight.shape[1]), dtype=BF16)
+
+
+moe_gate_up = _op("moe_gate_up", _moe_gate_up, _moe_gate_up_fake)
+
+
+def _moe_down_combine(act: torch.Tensor, weight: torch.Tensor, chosen: torch.Tensor, weights: torch.Tensor,
+                      residual: torch.Tensor | None) -> torch.Tensor:
+    return ops.moe_down_combine(act, weight, chosen, weights, residual)
+
+
+def _moe_down_combine_fake(act, weight, chosen, weights, residual):
+    return act.new_empty((weight.shape[1],), dtype=BF16)
+
+
+moe_down_combine = _op("moe_down_combine", _moe_down_combine, _moe_down_combine_fake)
+
+
+def _dense_gate_up_swiglu(x: torch.Tensor, fused_weight: torch.Tensor) -> torch.Tensor:
+    return ops.dense_gate_up_swiglu(x, fused_weight)
+
+
+def _dense_gate_up_swiglu_fake(x, fused_weight):
+    return x.new_empty((fused_weight.shape[0] // 2,), dtype=BF16)
+
+
+dense_gate_up_swiglu = _op("dense_gate_up_swiglu", _dense_gate_up_swiglu, _dense_gate_up_swiglu_fake)
+
+
+def _dense_down_residual(activated: torch.Tensor, down_weight: torch.Tensor,
+                         residual: torch.Tensor) -> torch.Tensor:
+    return ops.dense_down_residual(activated, down_weight, residual)
+
+
+def _dense_down_residual_fake(activated, down_weight, residual):
+    return activated.new_empty((down_weight.shape[0],), dtype=BF16)
+
+
+dense_down_residual = _op("dense_down_residual", _dense_down_residual, _dense_down_residual_fake)
+
+
+def _attention_sink_decode(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, sinks: torch.Tensor,
+                           mask: torch.Tensor | None, scale: float) -> torch.Tensor:
+    """The cache views are read, not written; the workspace is allocated per call."""
+    return ops.attention_sink_decode(queries, keys, values, sinks, mask, scale)
+
+
+def _attention_sink_decode_fake(queries, keys, values, sinks, mask, scale):
+    return queries.new_empty((queries.numel() // 64, 64), dtype=BF16)
+
+
+attention_sink_decode = _op("attention_sink_decode", _attention_sink_decode, _attention_sink_decode_fake)
+
 REGISTERED = ("add_rms_norm", "qk_norm_rope", "rope_epilogue", "embed_atlas", "swiglu", "gate_softplus",
-              "gated_activations", "softmax_topk", "sigmoid_topk", "pack_router_weight", "residual_rms_router")
+              "gated_activations", "softmax_topk", "sigmoid_topk", "pack_router_weight", "residual_rms_router",
+              "residual_rms_router_sigmoid", "moe_gate_up", "moe_down_combine", "dense_gate_up_swiglu",
+              "dense_down_residual", "attention_sink_decode")

@@ -60,6 +60,37 @@ def test_each_operator_equals_its_entry_point():
     assert all(_same(p, q) for p, q in zip(got, (want[0], want[1], want[3], want[4])))
 
 
+def test_the_steps_either_side_equal_their_entry_points():
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    x, r = _bf16(gen, 5, 2048), _bf16(gen, 5, 2048)
+    w, gate = _bf16(gen, 2048, scale=0.1, shift=1.0), _bf16(gen, 128, 2048, scale=0.02)
+    bias = 0.1 * torch.randn(128, generator=gen, device="cuda")
+    packed = torch.ops.omnia.pack_router_weight(gate)
+    got = torch.ops.omnia.residual_rms_router_sigmoid(x, r, w, packed, bias, 128, 8, 1e-6)
+    want = ops.residual_rms_router_sigmoid(x, r, w, gate, bias, k=8, eps=1e-6)
+    assert all(_same(p, q) for p, q in zip(got[:3], want[:3]))
+    assert _same(got[3].view(torch.int32), want[3].view(torch.int32))
+    experts, hidden, inner, k = 16, 2048, 768, 4
+    token = _bf16(gen, hidden)
+    gate_up, down = _bf16(gen, experts, 2 * inner, hidden, scale=0.02), _bf16(gen, experts, hidden, inner, scale=0.02)
+    chosen = torch.tensor([3, 0, 15, 7], dtype=torch.int32, device="cuda")
+    weights = torch.tensor([0.4, 0.3, 0.2, 0.1], device="cuda")
+    act = torch.ops.omnia.moe_gate_up(token, gate_up, chosen)
+    assert _same(act, ops.moe_gate_up(token, gate_up, chosen))
+    assert _same(torch.ops.omnia.moe_down_combine(act, down, chosen, weights, token),
+                 ops.moe_down_combine(act, down, chosen, weights, token))
+    fused, down2 = _bf16(gen, 2 * inner, hidden, scale=0.02), _bf16(gen, hidden, inner, scale=0.02)
+    y = torch.ops.omnia.dense_gate_up_swiglu(token, fused)
+    assert _same(y, ops.dense_gate_up_swiglu(token, fused))
+    assert _same(torch.ops.omnia.dense_down_residual(y, down2, token), ops.dense_down_residual(y, down2, token))
+    q, sinks = _bf16(gen, 64, 64), _bf16(gen, 64, scale=2.0)
+    cache_k, cache_v = _bf16(gen, 1, 8, 300, 64), _bf16(gen, 1, 8, 300, 64)
+    band = torch.arange(300, device="cuda") >= 44
+    for mask in (None, band):
+        assert _same(torch.ops.omnia.attention_sink_decode(q, cache_k, cache_v, sinks, mask, 0.125),
+                     ops.attention_sink_decode(q, cache_k, cache_v, sinks, mask, 0.125))
+
+
 def test_a_compiled_chain_matches_eager():
     gen = torch.Generator(device="cuda").manual_seed(1)
     x, r, w = _bf16(gen, 4, 2048), _bf16(gen, 4, 2048), _bf16(gen, 2048, scale=0.1, shift=1.0)

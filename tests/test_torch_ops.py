@@ -47,3 +47,21 @@ def test_fake_shapes_and_dtypes():
         s2, n2, idx, w = torch.ops.omnia.residual_rms_router(x[:, :2048], x[:, :2048], torch.empty(2048, dtype=BF16),
                                                             packed, 128, 8, 1e-6)
         assert s2.shape == (4, 2048) and idx.shape == (4, 8)
+        s3, n3, logits, keys = torch.ops.omnia.residual_rms_router_sigmoid(
+            x[:, :2048], x[:, :2048], torch.empty(2048, dtype=BF16), packed, torch.empty(128), 128, 8, 1e-6)
+        assert logits.shape == (4, 128) and logits.dtype == BF16 and keys.dtype == torch.uint32
+        act = torch.ops.omnia.moe_gate_up(torch.empty(2048, dtype=BF16), torch.empty(16, 1536, 2048, dtype=BF16),
+                                          torch.empty(4, dtype=torch.int32))
+        assert act.shape == (4, 1536) and act.dtype == BF16
+        out = torch.ops.omnia.moe_down_combine(act, torch.empty(16, 2048, 768, dtype=BF16),
+                                               torch.empty(4, dtype=torch.int32), torch.empty(4), None)
+        assert out.shape == (2048,) and out.dtype == BF16
+        y = torch.ops.omnia.dense_gate_up_swiglu(torch.empty(2048, dtype=BF16), torch.empty(1536, 2048, dtype=BF16))
+        assert y.shape == (768,)
+        z = torch.ops.omnia.dense_down_residual(y, torch.empty(2048, 768, dtype=BF16), torch.empty(2048, dtype=BF16))
+        assert z.shape == (2048,)
+        ctx = torch.ops.omnia.attention_sink_decode(torch.empty(64, 64, dtype=BF16),
+                                                    torch.empty(1, 8, 300, 64, dtype=BF16),
+                                                    torch.empty(1, 8, 300, 64, dtype=BF16),
+                                                    torch.empty(64, dtype=BF16), None, 0.125)
+        assert ctx.shape == (64, 64) and ctx.dtype == BF16
