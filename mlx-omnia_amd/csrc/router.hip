@@ -484,6 +484,68 @@ __device__ __forceinline__ void sigmoid_finish(const uint32_t (&bits)[V], const 
   if (a.indices) ordinal_topk_write<V>(keys, scores, E, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
 }
 
+// The sigmoid form's last step when it only selects. The contenders are the experts whose
+// best-case key reaches the threshold of the bounds: every winner is one, and by now each
+// has its exact logit. They are packed into the first lanes through `slots` (64 words of
+// this wave's own). Each lane takes one contender's exact score and key and ranks it among
+// the others, (key, expert) ascending. The first k write their expert and their score over
+// the winners' fp32 sum, taken in winner order, as ordinal_topk_write does. Too many
+// contenders (keys tied everywhere, NaN keys) or too few go to sigmoid_finish.
+template <int V, int E>
+__device__ __forceinline__ void sigmoid_select_contenders(const uint32_t (&bits)[V], const uint32_t (&upper)[V],
+                                                          uint32_t threshold, const float (&bias)[V],
+                                                          const RouterArgs& a, int64_t t, int lane, uint32_t* slots) {
+  uint64_t mask[V];
+  int count = 0;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    mask[v] = __ballot(upper[v] >= threshold);
+    count += __popcll(mask[v]);
+  }
+  if (count > kWave || count < a.k) {   // uniform
+    sigmoid_finish<V, E>(bits, bias, a, t, lane);
+    return;
+  }
+  int base = 0;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    if (upper[v] >= threshold) {
+      const int at = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                static_cast<uint32_t>(mask[v] >> 32),
+                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask[v]), 0)));
+      slots[at] = (static_cast<uint32_t>(lane + v * kWave) << 16) | (bits[v] & 0xFFFFu);
+    }
+    base += __popcll(mask[v]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  uint32_t key = 0xFFFFFFFFu;
+  int expert = 0xFFFF;
+  float score = 0.0f;
+  if (lane < count) {
+    const uint32_t slot = slots[lane];
+    expert = static_cast<int>(slot >> 16);
+    score = sigmoid_rounded(bf16_to_f32(static_cast<uint16_t>(slot & 0xFFFFu)));
+    key = ordinal_of(-(score + a.bias[expert]));
+  }
+  int rank = 0;
+  for (int j = 0; j < count; ++j) {   // uniform
+    const uint32_t other = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), j));
+    const int other_expert = __builtin_amdgcn_readlane(expert, j);
+    rank += (other < key || (other == key && other_expert < expert)) ? 1 : 0;
+  }
+  const bool winner = lane < count && rank < a.k;
+  float total = 0.0f;
+  for (int r = 0; r < a.k; ++r) {   // uniform
+    const uint64_t who = __ballot(winner && rank == r);
+    const int owner = static_cast<int>(__builtin_ctzll(who));
+    total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score), owner)) + total;
+  }
+  if (winner) {
+    a.indices[t * a.k + rank] = expert;
+    a.weights[t * a.k + rank] = score / total;
+  }
+}
+
 template <int VPL, int E>
 __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArgs a) {
   using S = FusedShape<VPL, E>;
@@ -742,7 +804,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
 #pragma unroll
     for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
   }
-  if (sigmoid) {
+  if (sigmoid) {   // the contenders' ranking (split kernel) would spill registers here
     sigmoid_finish<V, E>(bits, bias, a, t, lane);
     return;
   }
@@ -1129,7 +1191,12 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
   }
   if (sigmoid) {
-    sigmoid_finish<V, E>(bits, bias, a, t, lane);
+    if (exact_all) {
+      sigmoid_finish<V, E>(bits, bias, a, t, lane);
+    } else {
+      sigmoid_select_contenders<V, E>(bits, upper, threshold, bias, a, t, lane,
+                                      reinterpret_cast<uint32_t*>(tasks) + r * kWave);
+    }
     OMNIA_CLOCK(a, wave, lane, 9);  // token written
     return;
   }
