@@ -77,6 +77,17 @@ __device__ __forceinline__ float round_bf16(float value) {
   return bf16_to_f32(f32_to_bf16(value));
 }
 
+// The bits of a bf16 value an epilogue needs (a residual, a projection bias), loaded at
+// a kernel's start together with its other loads, instead of after its last wait or
+// barrier where it would be one more dependent round trip: src[index], or any[0] (which
+// must be a valid bf16 address) when `src` is null, the caller then ignoring it. The
+// load is unconditional and the caller widens the bits where it uses them: a select on
+// the value would let the compiler sink the load into a branch and wait on it there.
+__device__ __forceinline__ uint32_t early_bf16_bits(const uint16_t* src, int64_t index, const uint16_t* any) {
+  const bool have = src != nullptr;
+  return (have ? src : any)[have ? index : 0];
+}
+
 // Eight bf16 values held in one 16-byte vector, unpacked to fp32.
 __device__ __forceinline__ void unpack8(const u32x4& v, float out[8]) {
   out[0] = bf16_lo(v.x); out[1] = bf16_hi(v.x);

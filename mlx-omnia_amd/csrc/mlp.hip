@@ -120,6 +120,9 @@ __global__ __launch_bounds__(kDownSplit * kWave) void dense_down_residual_kernel
   const int lane = threadIdx.x % kWave;
   const int part = threadIdx.x / kWave;
   const int row = blockIdx.x;  // the grid is exactly `hidden` workgroups
+  // The residual, loaded ahead of the row (every thread reads the same value; thread 0
+  // uses it after the barrier).
+  const uint16_t resid_raw = a.residual[row];
   const int per = (a.vecs + kDownSplit - 1) / kDownSplit;
   const int lo = part * per;
   const int hi = min(a.vecs, lo + per);
@@ -153,7 +156,7 @@ __global__ __launch_bounds__(kDownSplit * kWave) void dense_down_residual_kernel
     float sum = partial[0];
 #pragma unroll
     for (int p = 1; p < kDownSplit; ++p) sum += partial[p];
-    a.out[row] = f32_to_bf16(bf16_to_f32(a.residual[row]) + round_bf16(sum));
+    a.out[row] = f32_to_bf16(bf16_to_f32(resid_raw) + round_bf16(sum));
   }
 }
 

@@ -144,13 +144,19 @@ template <int VPL>
 __global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a) {
   __shared__ float partial[kMaxSlots][kDownRows];
   const int lane = threadIdx.x % kWave;
-  const int slot = threadIdx.x / kWave;  // one wave per chosen expert; blockDim = k waves
+  // One wave per chosen expert (blockDim = k waves); uniform, so its routing entries
+  // are scalar loads.
+  const int slot = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
   const int half = lane / 32;
   const int hl = lane % 32;
   const int row_base = blockIdx.x * kDownRows;
   const int64_t expert = a.chosen[slot];
   const bool valid = expert >= 0 && expert < a.experts;  // wave-uniform
   const float scale = a.weights[slot];
+  // The residual of the output row this thread writes at the end (rows past the last
+  // read the last).
+  const uint32_t resid = early_bf16_bits(
+      a.residual, min(row_base + static_cast<int>(threadIdx.x % kDownRows), a.hidden - 1), a.act);
 
   // The lane's slice of the pair block (elements (hl + 32 i) * 8 + j of I) is loaded
   // first, then the first group of weight rows; the activation is computed while the
@@ -238,7 +244,7 @@ __global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a)
       float sum = 0.0f;
       for (int j = 0; j < a.k; ++j) sum += partial[j][threadIdx.x];
       float out = round_bf16(sum);
-      if (a.residual != nullptr) out = out + bf16_to_f32(a.residual[n]);
+      if (a.residual != nullptr) out = out + bf16_to_f32(resid);
       a.out[n] = f32_to_bf16(out);
     }
   }

@@ -362,11 +362,17 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(
   constexpr int kRowsPerGroup = kDownRows / kGroups;
   __shared__ float partial[kMaxDownSlots][kDownRows];
   const int lane = threadIdx.x % kWave;
-  const int slot = threadIdx.x / kWave;   // one wave per slot
+  // One wave per slot; uniform, so its routing entries are scalar loads.
+  const int slot = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
   const int row_base = blockIdx.x * kDownRows;
   const int rows = min(kDownRows, a.hidden - row_base);
   const int group = lane / kLanes;
   const int part = lane % kLanes;
+  // The epilogue's operands, loaded ahead of the weights: the slot's routing weight and
+  // the residual of the output row this thread writes (rows past the last read the last).
+  const float route_weight = a.weights[slot];
+  const uint32_t resid = early_bf16_bits(
+      a.residual, row_base + min(static_cast<int>(threadIdx.x % kDownRows), rows - 1), a.act);
   const bool shared = uses_shared(a.shared, slot, a.slots);
   const Leaf& leaf = shared ? a.shared : a.routed;
   bool valid = true;
@@ -393,7 +399,7 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(
   for (int q = 0; q < kRowsPerGroup; ++q) {
     const float sum = group_row_sum<kLanes>(t[q]);
     const int row = group + kGroups * q;
-    if (part == 0) partial[slot][row] = valid ? round_bf16(round_bf16(sum) * a.weights[slot]) : 0.0f;
+    if (part == 0) partial[slot][row] = valid ? round_bf16(round_bf16(sum) * route_weight) : 0.0f;
   }
   __syncthreads();
   if (threadIdx.x < kDownRows && row_base + static_cast<int>(threadIdx.x) < a.hidden) {
@@ -401,7 +407,7 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(
     float sum = 0.0f;
     for (int j = 0; j < a.slots; ++j) sum += partial[j][threadIdx.x];
     float out = round_bf16(sum);
-    if (a.residual != nullptr) out = out + bf16_to_f32(a.residual[n]);
+    if (a.residual != nullptr) out = out + bf16_to_f32(resid);
     a.out[n] = f32_to_bf16(out);
   }
 }

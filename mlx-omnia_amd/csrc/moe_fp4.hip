@@ -332,13 +332,21 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
   const int lane = threadIdx.x % kWave;
   const int part = lane % kLanes;
   const int group = lane / kLanes;
-  const int slot = threadIdx.x / kWave;   // one wave per slot
+  // One wave per slot; uniform, so its routing entries are scalar loads.
+  const int slot = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
   const int row_base = blockIdx.x * kDownRows;
   const int rows = min(kDownRows, a.hidden - row_base);
   const int expert = a.chosen[slot];
   const bool valid = expert >= 0 && expert < a.experts;   // uniform over the wave
   const int64_t row0 = static_cast<int64_t>(valid ? expert : 0) * a.hidden + row_base;
   const int chunks = a.inner / kChunk;
+  // The epilogue's operands, loaded ahead of the codes: the slot's routing weight, the
+  // projection bias of the row lane i takes, and the residual of the output row this
+  // thread writes (rows past the last read the last).
+  const float route_weight = a.weights[slot];
+  const uint32_t bias = early_bf16_bits(a.stack.bias, row0 + min(lane, rows - 1), a.act);
+  const uint32_t resid = early_bf16_bits(
+      a.residual, row_base + min(static_cast<int>(threadIdx.x % kDownRows), rows - 1), a.act);
   float t[kRowsPerGroup];
 #pragma unroll
   for (int q = 0; q < kRowsPerGroup; ++q) t[q] = 0.0f;
@@ -400,8 +408,8 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
   if (lane < rows) {
     float term = 0.0f;
     if (valid) {
-      const float bias = a.stack.bias != nullptr ? bf16_to_f32(a.stack.bias[row0 + lane]) : 0.0f;
-      term = round_bf16(round_bf16(mine + bias) * a.weights[slot]);
+      const float b = a.stack.bias != nullptr ? bf16_to_f32(bias) : 0.0f;
+      term = round_bf16(round_bf16(mine + b) * route_weight);
     }
     partial[slot][lane] = term;
   }
@@ -411,7 +419,7 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
     float sum = 0.0f;
     for (int j = 0; j < a.slots; ++j) sum += partial[j][threadIdx.x];
     float out = round_bf16(sum);
-    if (a.residual != nullptr) out = out + bf16_to_f32(a.residual[n]);
+    if (a.residual != nullptr) out = out + bf16_to_f32(resid);
     a.out[n] = f32_to_bf16(out);
   }
 }
@@ -466,10 +474,12 @@ __global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_ke
   constexpr int kGroups = kWave / kLanes;
   constexpr int kRowsPerGroup = kSharedRows / kGroups;
   __shared__ float term[kMaxSharedSlots][kSharedRows];
+  __shared__ float route_weight[kMaxSharedSlots];
   const int lane = threadIdx.x % kWave;
   const int part = lane % kLanes;
   const int group = lane / kLanes;
-  const int wave = threadIdx.x / kWave;
+  // Uniform, so each slot's expert id is a scalar load.
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
   const int waves = blockDim.x / kWave;
   const int64_t token = blockIdx.y;
   const int row_base = blockIdx.x * kSharedRows;
@@ -478,6 +488,14 @@ __global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_ke
   const int chunks = a.inner / kChunk;
   const int c = min(part, chunks - 1);   // a lane past the row's end re-reads its last chunk
   const bool in_row = part < chunks;
+  // The epilogue's operands, loaded ahead of the codes: the residual of the output row
+  // this thread writes (rows past the last read the last), and the token's routing
+  // weights, thread j holding weight j (kept in LDS for the epilogue).
+  const uint16_t resid_raw =
+      a.residual[token * a.hidden + row_base + min(static_cast<int>(threadIdx.x % kSharedRows), rows - 1)];
+  const float my_weight =   // no routed slots: the weights may be null
+      a.top_k > 0 ? a.weights[token * a.top_k + min(static_cast<int>(threadIdx.x % kMaxSharedSlots), a.top_k - 1)]
+                  : 0.0f;
   for (int slot = wave; slot < slots; slot += waves) {   // uniform over the wave
     const bool shared = slot == a.top_k;
     const int expert = shared ? 0 : a.chosen[token * a.top_k + slot];
@@ -510,17 +528,18 @@ __global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_ke
     const int row = group + kGroups * part;
     if (part < kRowsPerGroup && row < rows) term[slot][row] = valid ? round_bf16(mine) : 0.0f;
   }
+  if (static_cast<int>(threadIdx.x) < a.top_k) route_weight[threadIdx.x] = my_weight;
   __syncthreads();
   if (static_cast<int>(threadIdx.x) < rows) {
     const int r = threadIdx.x;
     const int64_t n = token * a.hidden + row_base + r;
     float total = 0.0f;
     for (int j = 0; j < a.top_k; ++j) {
-      const float weight = round_bf16(a.weights[token * a.top_k + j]);
+      const float weight = round_bf16(route_weight[j]);
       total = round_bf16(round_bf16(term[j][r] * weight) + total);
     }
     const float joined = round_bf16(total + term[a.top_k][r]);
-    a.out[n] = f32_to_bf16(bf16_to_f32(a.residual[n]) + joined);
+    a.out[n] = f32_to_bf16(bf16_to_f32(resid_raw) + joined);
   }
 }
 

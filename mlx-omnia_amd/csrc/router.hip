@@ -158,6 +158,51 @@ __device__ __forceinline__ void write_winners(uint32_t chosen, int k, int lane,
   }
 }
 
+// The final top k of a row whose selection on bounds was refined, ranked among its
+// contenders only: the experts whose upper-bound key reaches `threshold` (the k-th
+// best lower-bound key). Every expert of the exact top k is one of them, since its
+// exact key is at least the k-th exact key, which is at least the threshold. There are
+// about k contenders; they are packed into the first lanes through `slots` (64 words of
+// LDS owned by this wave), each counts the contenders with a larger exact key (keys
+// are distinct), and the winners land in rank order: lane j < k holds the j-th
+// winner's key, as select_topk leaves it. Returns false (nothing written) when the
+// contenders do not fit one wave.
+template <int V>
+__device__ __forceinline__ bool rank_contenders(const uint32_t (&exact)[V], const uint32_t (&upper)[V],
+                                                uint32_t threshold, int k, int lane, uint32_t* slots,
+                                                uint32_t& chosen) {
+  uint64_t mask[V];
+  int count = 0;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    mask[v] = __ballot(upper[v] >= threshold);
+    count += __popcll(mask[v]);
+  }
+  if (count > kWave || count < k) return false;   // uniform
+  int base = 0;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    if (upper[v] >= threshold) {
+      const int at = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                static_cast<uint32_t>(mask[v] >> 32),
+                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask[v]), 0)));
+      slots[at] = exact[v];
+    }
+    base += __popcll(mask[v]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t key = lane < count ? slots[lane] : 0u;
+  int rank = 0;
+  for (int j = 0; j < count; ++j) {   // uniform
+    rank += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), j)) > key ? 1 : 0;
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (lane < count && rank < k) slots[rank] = key;
+  __builtin_amdgcn_wave_barrier();
+  chosen = lane < k ? slots[lane] : 0u;
+  return true;
+}
+
 // ---- sigmoid scores, ordinal keys and their selection ---------------------------------
 
 // Correctly rounded fp32 sigmoid of an fp32 value.
@@ -811,7 +856,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   if (refined || exact_all) {
 #pragma unroll
     for (int v = 0; v < V; ++v) keys[v] = route_key(bits[v], lane + v * kWave);
-    select_topk<V>(keys, a.k, lane, chosen);
+    select_topk<V>(keys, a.k, lane, chosen);   // ranking the contenders spills here
   }
   write_winners(chosen, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
 }
@@ -893,6 +938,7 @@ struct SplitShape {
   static_assert(kSteps == 4 * kGroup, "four groups of steps per (tile, slice)");
   static_assert(kTiles * kSlices % kWalkers == 0 && kWalkers % kSlices == 0, "shape");
   static_assert(kTileTokens == 2 * kRowWaves, "two rows per row wave");
+  static_assert(kTileTokens * E * 2 >= kWaves * kWave * 4, "64 contender slots per wave in the task list");
 };
 
 // Phase 1 of one token row, for a row wave: residual add + RMSNorm (the arithmetic of
@@ -1203,7 +1249,12 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   if (refined || exact_all) {
 #pragma unroll
     for (int v = 0; v < V; ++v) keys[v] = route_key(bits[v], lane + v * kWave);
-    select_topk<V>(keys, a.k, lane, chosen);
+    // A refined selection ranks its few contenders; with every logit exact (or more
+    // contenders than lanes) the k rounds over the whole row run.
+    if (exact_all || !rank_contenders<V>(keys, upper, threshold, a.k, lane,
+                                         reinterpret_cast<uint32_t*>(tasks) + r * kWave, chosen)) {
+      select_topk<V>(keys, a.k, lane, chosen);
+    }
   }
   write_winners(chosen, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
   OMNIA_CLOCK(a, wave, lane, 9);  // token written
