@@ -82,9 +82,9 @@ struct StepRows {
   int count;                  // rows [0, count) are attended
 };
 
-__device__ __forceinline__ StepRows step_rows(const AttnArgs& a) {
+__device__ __forceinline__ StepRows step_rows(const AttnArgs& a, int position) {
   StepRows r;
-  r.position = *a.position;
+  r.position = position;
   if (r.position < 0) {
     r.write = -1;
     r.count = 0;
@@ -99,6 +99,7 @@ __device__ __forceinline__ StepRows step_rows(const AttnArgs& a) {
   if (r.write >= r.count) r.write = -1;
   return r;
 }
+__device__ __forceinline__ StepRows step_rows(const AttnArgs& a) { return step_rows(a, *a.position); }
 
 __device__ __forceinline__ float row16_fsum(float v) {
   v += __uint_as_float(dpp<kRowRor8>(__float_as_uint(v)));
@@ -362,17 +363,15 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   // cache rows, bounded by max_rows (rows past the attended count are masked when the
   // block is consumed; the write row is read stale and replaced from LDS before use).
   // Measured at 32k and 4k rows: 0.4-0.5 us less than loading after the position.
+  // The item's loads carry no branch (in a divergent branch the compiler waits for one
+  // branch's load before the other's, a round trip ahead of the cache rows): items past
+  // GQA + 1 read the value row as well and leave it unused.
   const int item = wave * 4 + drow;
   const bool is_q = item < GQA;
-  u32x4 raw = u32x4{0u, 0u, 0u, 0u}, wgt = u32x4{0u, 0u, 0u, 0u};
-  if (item <= GQA) {
-    const uint16_t* row = is_q ? a.raw_q + static_cast<int64_t>(kvh * GQA + item) * kD
-                               : a.raw_k + static_cast<int64_t>(kvh) * kD;
-    raw = *reinterpret_cast<const u32x4*>(row + 8 * c);
-    wgt = *reinterpret_cast<const u32x4*>((is_q ? a.q_weight : a.k_weight) + 8 * c);
-  } else if (item == GQA + 1) {
-    raw = *reinterpret_cast<const u32x4*>(a.raw_v + static_cast<int64_t>(kvh) * kD + 8 * c);
-  }
+  const uint16_t* row = is_q ? a.raw_q + static_cast<int64_t>(kvh * GQA + min(item, GQA - 1)) * kD
+                             : (item == GQA ? a.raw_k : a.raw_v) + static_cast<int64_t>(kvh) * kD;
+  const u32x4 raw = *reinterpret_cast<const u32x4*>(row + 8 * c);
+  const u32x4 wgt = *reinterpret_cast<const u32x4*>((is_q ? a.q_weight : a.k_weight) + 8 * c);
   u32x4 kcur[8], vcur[8];
   int b0 = c0 + wave * kBlockRows;
   load_block(a, head_base, b0, min(c0 + a.chunk, a.max_rows), drow, c, kcur, vcur);
@@ -546,18 +545,39 @@ __global__ __launch_bounds__(kCombineWaves * kWave) void attention_combine_kerne
   const int g = head % GQA;
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  const StepRows rows = step_rows(a);
-  const int used = min(a.splits, (rows.count + a.chunk - 1) / a.chunk);
   const float* base = a.partial + (static_cast<int64_t>(kvh) * a.splits * GQA + g) * kPartial;
   const int64_t stride = static_cast<int64_t>(GQA) * kPartial;  // between chunks
 
+  // A wave merges chunks wave, wave + kCombineWaves, ... in that order. Their states are
+  // loaded kAhead at a time over every chunk of the split, not only the `used` ones, so
+  // no load waits for the position read on the device; the unused ones (stale, from an
+  // earlier step) are loaded and dropped. The position itself is a vector load issued
+  // first (vector loads complete in order, so waiting for it leaves the states in flight;
+  // a scalar load would be waited on with the kernel arguments, before any state load).
+  constexpr int kAhead = 4;
+  const int position = __hip_atomic_load(a.position, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float2 v[kAhead], ml[kAhead];
+  auto load_states = [&](int s0) {
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) {
+      const float* slot = base + min(s0 + kCombineWaves * i, a.splits - 1) * stride;
+      v[i] = *reinterpret_cast<const float2*>(slot + 2 * lane);
+      ml[i] = *reinterpret_cast<const float2*>(slot + kD);
+    }
+  };
+  load_states(wave);
+  const StepRows rows = step_rows(a, position);
+  const int used = min(a.splits, (rows.count + a.chunk - 1) / a.chunk);
   float m = -INFINITY, l = 0.0f, o[2] = {0.0f, 0.0f};
-#pragma unroll 4
-  for (int s = wave; s < used; s += kCombineWaves) {
-    const float* slot = base + s * stride;
-    const float2 v = *reinterpret_cast<const float2*>(slot + 2 * lane);
-    const float o2[2] = {v.x, v.y};
-    merge_state(m, l, o, slot[kD], slot[kD + 1], o2);
+  for (int s0 = wave; s0 < a.splits; s0 += kCombineWaves * kAhead) {   // uniform
+    if (s0 != wave) load_states(s0);
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) {
+      if (s0 + kCombineWaves * i < used) {   // uniform
+        const float o2[2] = {v[i].x, v[i].y};
+        merge_state(m, l, o, ml[i].x, ml[i].y, o2);
+      }
+    }
   }
   wave_o[wave][lane] = float2{o[0], o[1]};
   if (lane == 0) {

@@ -121,14 +121,19 @@ __global__ __launch_bounds__(kThreads) void sink_split_kernel(SinkArgs a) {
                           : u32x4{0u, 0u, 0u, 0u};
     qa[kk] = __builtin_bit_cast(bf16x8, q);
   }
-  if (threadIdx.x == 0) live = 0;
-  __syncthreads();
-  bool any = false;
-  for (int j = j0 + static_cast<int>(threadIdx.x); j < j1; j += kThreads) {
-    any |= a.mask == nullptr || !__builtin_isinf(a.mask[j]);
+  // Whether any row of the chunk is unmasked: always without a mask (no check, so the
+  // queries' loads stay in flight into the first block's); with one, through LDS behind
+  // barriers that order LDS only.
+  bool attends = true;
+  if (a.mask != nullptr) {   // uniform
+    if (threadIdx.x == 0) live = 0;
+    lds_barrier();
+    bool any = false;
+    for (int j = j0 + static_cast<int>(threadIdx.x); j < j1; j += kThreads) any |= !__builtin_isinf(a.mask[j]);
+    if (any) live = 1;   // every writer stores the same value
+    lds_barrier();
+    attends = live != 0;
   }
-  if (any) live = 1;   // every writer stores the same value
-  __syncthreads();
 
   // State of heads 4 r + i (the MFMA output rows of the lane): the running maximum m
   // (uniform over the DPP row), the lane's part of the sum l, and the context o[dt][i],
@@ -141,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void sink_split_kernel(SinkArgs a) {
     l[i] = 0.0f;
     o[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  if (live) {
+  if (attends) {
     const uint16_t* khead = a.keys + static_cast<int64_t>(kvh) * a.key_head_stride;
     const uint16_t* vhead = a.values + static_cast<int64_t>(kvh) * a.value_head_stride;
     for (int base = j0 + wave * kBlock; base < j1; base += kWaves * kBlock) {   // uniform over the wave
@@ -309,30 +314,46 @@ __global__ __launch_bounds__(kThreads) void sink_combine_kernel(SinkArgs a) {
   const int wave = threadIdx.x / kWave;
   const float* base = a.partial + (static_cast<int64_t>(kvh) * a.chunks * G + h) * kPartial;
   const int64_t stride = static_cast<int64_t>(G) * kPartial;   // between chunks
-  if (wave == 0) {
-    const float sink = bf16_to_f32(a.sinks[head]) * kLog2e;
-    float top = sink;
-    for (int c = lane; c < a.chunks; c += kWave) top = fmaxf(top, base[c * stride + kD]);
-    top = wave_max_f32(top);
-    float total = 0.0f;
-    for (int c = lane; c < a.chunks; c += kWave) {
-      const float mc = base[c * stride + kD];
-      const float f = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - top);
-      factor[c] = f;
-      total = __builtin_fmaf(base[c * stride + kD + 1], f, total);
-    }
-    total = wave_sum_f32(total) + __builtin_amdgcn_exp2f(sink - top);
-    if (lane == 0) shared_total = total;
-  }
-  __syncthreads();
+  // Every load goes out before anything waits, in the order they are used: each lane's
+  // first chunk (max, sum) pair and the sink, then the wave's first batch of context
+  // values (wave w sums chunks w, w + kWaves, ... in that order, kBatch a pass). Every
+  // wave computes the factors (so no load is used on one wave's path alone, where the
+  // compiler would sink it); wave 0 stores them.
+  const float2 first_ms = *reinterpret_cast<const float2*>(base + min(lane, a.chunks - 1) * stride + kD);
+  const uint16_t sink_bits = a.sinks[head];
   constexpr int kBatch = 8;
+  float values[kBatch];
+  auto load_values = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) values[i] = base[min(c0 + kWaves * i, a.chunks - 1) * stride + lane];
+  };
+  load_values(wave);
+  // The running maximum over the sink and the chunks, lane by lane in chunk order.
+  const float sink = bf16_to_f32(sink_bits) * kLog2e;
+  float top = sink;
+  if (lane < a.chunks) top = fmaxf(top, first_ms.x);
+  for (int c = lane + kWave; c < a.chunks; c += kWave) top = fmaxf(top, base[c * stride + kD]);
+  top = wave_max_f32(top);
+  const float first_f =
+      lane < a.chunks && first_ms.x != -INFINITY ? __builtin_amdgcn_exp2f(first_ms.x - top) : 0.0f;
+  float total = lane < a.chunks ? __builtin_fmaf(first_ms.y, first_f, 0.0f) : 0.0f;
+  if (wave == 0 && lane < a.chunks) factor[lane] = first_f;
+  for (int c = lane + kWave; c < a.chunks; c += kWave) {   // past 64 chunks
+    const float mc = base[c * stride + kD];
+    const float f = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - top);
+    if (wave == 0) factor[c] = f;
+    total = __builtin_fmaf(base[c * stride + kD + 1], f, total);
+  }
+  total = wave_sum_f32(total) + __builtin_amdgcn_exp2f(sink - top);
+  if (wave == 0 && lane == 0) shared_total = total;
+  __syncthreads();
   float acc = 0.0f;
   for (int c0 = wave; c0 < a.chunks; c0 += kWaves * kBatch) {   // uniform over the wave
-    float values[kBatch], factors[kBatch];
+    if (c0 != wave) load_values(c0);
+    float factors[kBatch];
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       const int c = min(c0 + kWaves * i, a.chunks - 1);
-      values[i] = base[c * stride + lane];
       factors[i] = c0 + kWaves * i < a.chunks ? factor[c] : 0.0f;
     }
 #pragma unroll

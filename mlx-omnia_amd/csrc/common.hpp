@@ -88,6 +88,16 @@ __device__ __forceinline__ uint32_t early_bf16_bits(const uint16_t* src, int64_t
   return (have ? src : any)[have ? index : 0];
 }
 
+// A workgroup barrier ordering LDS traffic only. __syncthreads() also drains each wave's
+// outstanding global loads and stores (its fence waits for vmcnt(0)); this one lets them
+// stay in flight across it, for barriers that guard LDS data alone (no wave reads global
+// memory another wave of the workgroup wrote).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Eight bf16 values held in one 16-byte vector, unpacked to fp32.
 __device__ __forceinline__ void unpack8(const u32x4& v, float out[8]) {
   out[0] = bf16_lo(v.x); out[1] = bf16_hi(v.x);

@@ -222,6 +222,14 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   const int rows = 2 * pairs;
   const int64_t row0 = static_cast<int64_t>(expert) * 2 * a.inner + 2 * static_cast<int64_t>(pair0);
   const int chunks = a.hidden / kChunk;
+  // The projection bias of the pair this lane activates (its gate and up rows), loaded
+  // ahead of the codes.
+  uint32_t gate_bias_bits = 0, up_bias_bits = 0;
+  if constexpr (F == Fp4::kMx) {
+    const int64_t at = row0 + 2 * min(lane, pairs - 1);
+    gate_bias_bits = early_bf16_bits(a.stack.bias, at, a.x);
+    up_bias_bits = early_bf16_bits(a.stack.bias, at + 1, a.x);
+  }
   constexpr int kBatch = kTrips > 0 ? kTrips : kGateBatch;
   const int trips = kTrips > 0 ? kTrips : (chunks + kWave - 1) / kWave;
   float r[kRows];
@@ -270,8 +278,8 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   if constexpr (F == Fp4::kMx) {
     float gate_bias = 0.0f, up_bias = 0.0f;
     if (a.stack.bias != nullptr) {
-      gate_bias = bf16_to_f32(a.stack.bias[row0 + 2 * lane]);
-      up_bias = bf16_to_f32(a.stack.bias[row0 + 2 * lane + 1]);
+      gate_bias = bf16_to_f32(gate_bias_bits);
+      up_bias = bf16_to_f32(up_bias_bits);
     }
     float g = round_bf16(gate_sum + gate_bias);
     float u = round_bf16(up_sum + up_bias);

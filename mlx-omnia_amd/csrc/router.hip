@@ -888,15 +888,9 @@ int32_t launch_fused(const RouterArgs& a, hipStream_t stream) {
 // waves' stores drain. A store counts in the issuing wave's vmcnt until it completes,
 // so only walkers, which store nothing before the end, load anything after phase 1:
 // the walk and the exact recomputations.
-// A workgroup barrier ordering LDS traffic only. __syncthreads() also drains each
-// wave's outstanding global loads and stores (its fence waits for vmcnt(0)), which would
-// make every wave wait for the row waves' stores; nothing here reads global memory
-// another wave of the workgroup wrote.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
+// The barriers below are lds_barrier() (common.hpp): __syncthreads() would make every
+// wave wait for the row waves' stores; nothing here reads global memory another wave of
+// the workgroup wrote.
 
 template <int E>
 struct SplitShape {
