@@ -196,17 +196,22 @@ __global__ __launch_bounds__(kBlock) void gated_activations_kernel(GatedArgs p) 
   if (blockIdx.x < p.softplus_blocks) {  // block-uniform
     __shared__ float decay[kDecayHeads];
     const bool cached = p.heads <= kDecayHeads;
+    // The thread's inputs go out before the decay table's load and barrier (a thread
+    // past the end reads the last pair and leaves before any store), so the two loads
+    // overlap instead of following each other.
+    const int head_pairs = p.heads / 2;
+    const int64_t n = p.a_rows * head_pairs;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const int64_t ic = i < n ? i : n - 1;
+    const int64_t r = ic / head_pairs;
+    const int h = static_cast<int>(ic - r * head_pairs) * 2;
+    const uint32_t x = *reinterpret_cast<const uint32_t*>(p.a + r * p.a_stride + h);
+    const f32x2 bb = *reinterpret_cast<const f32x2*>(p.dt_bias + h);
     if (cached && static_cast<int>(threadIdx.x) < p.heads) {
       decay[threadIdx.x] = -static_cast<float>(exp(static_cast<double>(p.a_log[threadIdx.x])));
     }
-    __syncthreads();
-    const int head_pairs = p.heads / 2;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (i >= p.a_rows * head_pairs) return;
-    const int64_t r = i / head_pairs;
-    const int h = static_cast<int>(i - r * head_pairs) * 2;
-    const uint32_t x = *reinterpret_cast<const uint32_t*>(p.a + r * p.a_stride + h);
-    const f32x2 bb = *reinterpret_cast<const f32x2*>(p.dt_bias + h);
+    lds_barrier();   // the table is LDS; the loads above stay in flight
+    if (i >= n) return;
     f32x2 o;
     if (cached) {  // the same fp32 steps as gate_softplus1
       o = f32x2{decay[h] * softplus_f32(bf16_lo(x) + bb.x), decay[h + 1] * softplus_f32(bf16_hi(x) + bb.y)};
