@@ -98,6 +98,18 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// XCD-aware block order. The part hands workgroups to its 8 XCDs in turn (workgroup b
+// to XCD b % 8), and each XCD has its own L2. This maps them so that each XCD takes one
+// contiguous run of blocks (the first blocks % 8 XCDs one more than the others), which
+// keeps the cache lines neighbouring blocks share (quantization scales, for instance) in
+// one L2 instead of fetching them from HBM for two. A bijection on [0, blocks) for any
+// count, so every block is still computed exactly once.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_contiguous_block(int b, int blocks) {
+  const int xcd = b % kXcds, k = b / kXcds;
+  return xcd * (blocks / kXcds) + min(xcd, blocks % kXcds) + k;
+}
+
 // Eight bf16 values held in one 16-byte vector, unpacked to fp32.
 __device__ __forceinline__ void unpack8(const u32x4& v, float out[8]) {
   out[0] = bf16_lo(v.x); out[1] = bf16_hi(v.x);

@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(
   const int lane = threadIdx.x % kWave;
   // One wave per slot; uniform, so its routing entries are scalar loads.
   const int slot = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-  const int row_base = blockIdx.x * kDownRows;
+  const int row_base = xcd_contiguous_block(blockIdx.x, gridDim.x) * kDownRows;
   const int rows = min(kDownRows, a.hidden - row_base);
   const int group = lane / kLanes;
   const int part = lane % kLanes;

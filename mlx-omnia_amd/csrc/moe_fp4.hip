@@ -342,7 +342,7 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
   const int group = lane / kLanes;
   // One wave per slot; uniform, so its routing entries are scalar loads.
   const int slot = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-  const int row_base = blockIdx.x * kDownRows;
+  const int row_base = xcd_contiguous_block(blockIdx.x, gridDim.x) * kDownRows;
   const int rows = min(kDownRows, a.hidden - row_base);
   const int expert = a.chosen[slot];
   const bool valid = expert >= 0 && expert < a.experts;   // uniform over the wave
@@ -490,7 +490,7 @@ __global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_ke
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
   const int waves = blockDim.x / kWave;
   const int64_t token = blockIdx.y;
-  const int row_base = blockIdx.x * kSharedRows;
+  const int row_base = xcd_contiguous_block(blockIdx.x, gridDim.x) * kSharedRows;
   const int rows = min(kSharedRows, a.hidden - row_base);
   const int slots = a.top_k + 1;
   const int chunks = a.inner / kChunk;
