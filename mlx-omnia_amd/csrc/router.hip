@@ -301,20 +301,26 @@ __global__ __launch_bounds__(256) void sigmoid_topk_kernel(const void* __restric
   const int lane = threadIdx.x % kWave;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
   if (row >= rows) return;
+  // Every load first, from a clamped index and with no branch (a load in a branch is
+  // waited on there, one round trip per value); lanes past the experts then drop theirs.
+  float x[V], b[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int e = min(lane + v * kWave, experts - 1);
+    x[v] = kF32 ? static_cast<const float*>(logits)[row * stride + e]
+                : bf16_to_f32(static_cast<const uint16_t*>(logits)[row * stride + e]);
+    b[v] = bias[e];
+  }
   uint32_t keys[V];
   float scores[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int e = lane + v * kWave;
-    keys[v] = 0xFFFFFFFFu;
-    scores[v] = 0.0f;
-    if (e < experts) {
-      const float x = kF32 ? static_cast<const float*>(logits)[row * stride + e]
-                           : bf16_to_f32(static_cast<const uint16_t*>(logits)[row * stride + e]);
-      scores[v] = sigmoid_rounded(x);
-      keys[v] = ordinal_of(-(scores[v] + bias[e]));
-      if (keys_out) keys_out[row * experts + e] = keys[v];
-    }
+    const float score = sigmoid_rounded(x[v]);
+    const uint32_t key = ordinal_of(-(score + b[v]));
+    keys[v] = e < experts ? key : 0xFFFFFFFFu;
+    scores[v] = e < experts ? score : 0.0f;
+    if (keys_out && e < experts) keys_out[row * experts + e] = key;
   }
   if (indices) ordinal_topk_write<V>(keys, scores, experts, k, lane, indices + row * k, weights + row * k);
 }
@@ -330,11 +336,17 @@ __global__ __launch_bounds__(256) void softmax_topk_kernel(const uint16_t* __res
   const int lane = threadIdx.x % kWave;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
   if (row >= rows) return;
+  // Every load first, from a clamped index and with no branch; lanes past the experts
+  // then drop theirs.
+  uint16_t raw[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) raw[v] = logits[row * stride + min(lane + v * kWave, experts - 1)];
   uint32_t keys[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int e = lane + v * kWave;
-    keys[v] = e < experts ? route_key(logits[row * stride + e], e) : 0u;
+    const uint32_t key = route_key(raw[v], e);
+    keys[v] = e < experts ? key : 0u;
   }
   uint32_t chosen;
   select_topk<V>(keys, k, lane, chosen);
