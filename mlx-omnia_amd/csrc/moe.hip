@@ -77,7 +77,10 @@ struct GateUpArgs {
 template <int VPL>
 __global__ __launch_bounds__(kWavesPerBlock * kWave) void moe_gate_up_kernel(GateUpArgs a) {
   const int lane = threadIdx.x % kWave;
-  const int wave = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  // Uniform, so the slot's expert id is a scalar load, waited on without the
+  // activation loads issued beside it.
+  const int wave = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave));
   const int slot = wave / a.waves_per_slot;
   if (slot >= a.k) return;  // whole wave; no barrier follows
   const int row0 = (wave - slot * a.waves_per_slot) * kRowsPerWave;
@@ -89,9 +92,10 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void moe_gate_up_kernel(Gat
   constexpr int kGroup = VPL <= 8 ? kRowsPerWave : 1;
   u32x4 xv[VPL];
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) {
+  for (int i = 0; i < VPL; ++i) {   // branch-free: a lane past the row reads its last vector
     const int v = lane + i * kWave;
-    xv[i] = v < a.vecs ? a.x[v] : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 loaded = a.x[min(v, a.vecs - 1)];
+    xv[i] = v < a.vecs ? loaded : u32x4{0u, 0u, 0u, 0u};
   }
 #pragma unroll
   for (int r0 = 0; r0 < kRowsPerWave; r0 += kGroup) {
