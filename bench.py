@@ -21,11 +21,14 @@ Method, per kernel:
 The CPU baseline is the repo's numpy oracle (a port of the reference's Core chains;
 MLX does not exist on these machines), timed on this host for every workload on a
 bounded sample of that workload's own shapes (about 0.8 s each, 3 s for the headline).
-Each `kernels[...]` entry carries its own `cpu_baseline` with the threads it used (one
-for elementwise numpy, the BLAS pool for legs that multiply matrices), the cores this
-process may use and the thread environment.
+
+Output: one compact JSON line on stdout (the headline's figures, roofline and CPU
+baseline, and `kernels`: name -> [us, fraction of peak, CPU oracle GB/s] for every
+workload), and the full record (each workload's description, rotation copies, launch
+mode, CPU sample, threads used and thread environment) in the `--results` file.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only NAME[,NAME]]
+                       [--results bench_results.json]
        python bench.py --phase-clocks [--phase-clocks-rows 4096,512]
                                         (the fused router's per-phase wall clocks)
 """
@@ -1275,7 +1278,9 @@ def router_phase_clocks(device, rows: int = 4096, stamped: int = 8, timed: int =
 
     path = REPO / "mlx-omnia_amd" / "libomnia_router_clocks.so"
     if not path.exists():
-        raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build()")
+        raise FileNotFoundError(f"{path} is not built (a diagnostic, built on request): run "
+                                "`python mlx-omnia_amd/build.py --clocks` or build() with "
+                                "OMNIA_BUILD_CLOCKS=1 first")
     lib = ctypes.CDLL(str(path))
     lib.omnia_router_pack_bytes.restype = ctypes.c_int64
     lib.omnia_router_pack_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64]
@@ -1371,6 +1376,51 @@ def _traffic(kernel_name: str) -> int | None:
     return None
 
 
+def bench_line(results: dict, head_name: str, steps: int, warmup: int) -> dict:
+    """The one stdout JSON line: the headline's figures, its roofline and CPU baseline, and
+    a compact map of every workload -> [us, fraction of peak, CPU oracle GB/s]. The full
+    per-workload record (descriptions, copies, CPU samples) goes to the results file; the
+    line stays a few KB whatever the number of workloads."""
+    head = results[head_name]
+    cpu = head.get("cpu_baseline")
+    baseline = None if not cpu else {
+        "value": cpu["value"], "unit": cpu["unit"], "cores": cpu["cores"],
+        "kind": cpu["kind"], "sample": cpu["sample"],
+        "us_per_launch": cpu["us_per_launch"], "affinity_cores": cpu["affinity_cores"]}
+    kernels = {}
+    for name, r in results.items():
+        leg = r.get("cpu_baseline")
+        kernels[name] = [r["us"], r["frac"], leg["value"] if leg else None]
+    return {
+        "metric": METRIC,
+        "value": head["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(head["us"] / 1000.0, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded numpy normal draws rounded to bf16 (RNE), resident in HBM",
+        "config": {"workload": f"{head_name}: {head['workload']}",
+                   "us_per_launch": head["us"], "frac_of_peak": head["frac"],
+                   "bytes_per_launch": head["bytes"], "launch": head["launch"]},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": head["GBps"],
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": head["frac"],
+            "traffic": _traffic(head_name),
+        },
+        "cpu_baseline": baseline,
+        "kernels_fields": ["us", "frac_of_peak", "cpu_oracle_GBps"],
+        "kernels": kernels,
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -1384,6 +1434,8 @@ def main() -> int:
     parser.add_argument("--phase-clocks", action="store_true",
                         help="print the fused router's per-phase wall clocks (diagnostic "
                              "build) as one JSON line instead of the bench line")
+    parser.add_argument("--results", default="bench_results.json",
+                        help="file for the full per-workload record ('' for none)")
     parser.add_argument("--phase-clocks-rows", default="4096",
                         help="comma-separated token counts for --phase-clocks (multiples of 16)")
     args = parser.parse_args()
@@ -1409,8 +1461,7 @@ def main() -> int:
     only = [n for n in args.only.split(",") if n]
     selected = [w for w in workloads() if ((w.name in only) if only else w.default)]
     results = {}
-    for w in selected:
-        print(f"[bench] {w.name}: {w.description}", file=sys.stderr, flush=True)
+    for index, w in enumerate(selected, 1):
         direct = time_workload(w, args.steps, args.warmup, device, False)
         # Small kernels outrun a Python launch loop; a graph replay then gives the
         # tighter figure. Either way the number is events over `steps` launches.
@@ -1418,59 +1469,29 @@ def main() -> int:
             args.graph or direct["us"] < 12.0) else None
         results[w.name] = min((r for r in (direct, graphed) if r), key=lambda r: r["us"])
         r = results[w.name]
-        print(f"[bench] {w.name}: {r['us']} us  {r['GBps']} GB/s  ({100 * r['frac']:.1f}% of peak)",
-              file=sys.stderr, flush=True)
+        note = ""
         if args.ceiling:
             ceiling = time_workload(copy_ceiling(w.bytes_per_launch), args.steps, args.warmup,
                                     device, False)
             r["copy_ceiling"] = {k: ceiling[k] for k in ("us", "GBps", "frac", "workload")}
-            print(f"[bench] {w.name}: plain copy of the same bytes {ceiling['us']} us "
-                  f"{ceiling['GBps']} GB/s", file=sys.stderr, flush=True)
+            note = f" copy {ceiling['us']}"
+        print(f"[bench] {index}/{len(selected)} {w.name} {r['us']} us{note}",
+              file=sys.stderr, flush=True)
 
-    head = results.get(HEADLINE) or next(iter(results.values()))
     head_name = HEADLINE if HEADLINE in results else next(iter(results))
-    baseline = None
     if not args.no_cpu:
         # The numpy oracle on each workload's own shapes (bounded samples), after the GPU
         # timing; the headline's sample runs longest.
         for name, r in results.items():
             seconds = 3.0 if name == head_name else 0.8
             r["cpu_baseline"] = cpu_baseline(name, r["bytes"], seconds)
-            if r["cpu_baseline"]:
-                print(f"[bench] {name}: CPU oracle {r['cpu_baseline']['value']} GB/s "
-                      f"({r['cpu_baseline']['us_per_launch']} us per launch, "
-                      f"{r['cpu_baseline']['cores']} core(s))", file=sys.stderr, flush=True)
-        baseline = results[head_name].get("cpu_baseline")
-    line = {
-        "metric": METRIC,
-        "value": head["GBps"],
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(head["us"] / 1000.0, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: seeded numpy normal draws rounded to bf16 (RNE), resident in HBM",
-        "config": {"workload": f"{head_name}: {head['workload']}",
-                   "us_per_launch": head["us"], "frac_of_peak": head["frac"]},
-        "roofline": {
-            "bound": "hbm",
-            "achieved": head["GBps"],
-            "peak": PEAK_GBS,
-            "unit": "GB/s",
-            "frac": head["frac"],
-            "traffic": _traffic(head_name),
-            "traffic_source": "profiles/hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, "
-                              "WRITE_SIZE of this workload, scaled by a copy of known size); "
-                              "not measured in this run",
-        },
-        "cpu_baseline": baseline,
-        "kernels": results,
-    }
-    print(json.dumps(line), flush=True)
+        print(f"[bench] CPU oracle legs done ({len(results)})", file=sys.stderr, flush=True)
+    line = bench_line(results, head_name, args.steps, args.warmup)
+    if args.results:
+        record = dict(line, kernels=results)
+        Path(args.results).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.results).write_text(json.dumps(record, indent=1) + "\n")
+    print(json.dumps(line, separators=(",", ":")), flush=True)
     return 0
 
 

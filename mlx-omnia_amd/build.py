@@ -77,29 +77,44 @@ def _link(objects: list[Path], target: Path) -> None:
     os.replace(staged, target)
 
 
-def build_library(verbose: bool = True) -> Path:
-    """Compile every source under `csrc/` and link `libomnia_hip.so` (and the router's
-    phase-clock diagnostic library); returns the product library's path."""
+def build_library(verbose: bool = True, clocks: bool | None = None) -> Path:
+    """Compile every source under `csrc/` and link `libomnia_hip.so`; returns its path.
+
+    `clocks` (default: the environment variable OMNIA_BUILD_CLOCKS=1) also builds the
+    router's phase-clock diagnostic library, which only `bench.py --phase-clocks` loads
+    (see `build_clocks_library`)."""
+    if clocks is None:
+        clocks = os.environ.get("OMNIA_BUILD_CLOCKS", "") == "1"
     OBJDIR.mkdir(exist_ok=True)
     sources = sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.cpp")])
     if not sources:
         raise FileNotFoundError(f"no sources under {CSRC}")
-    clock_sources = [CSRC / name for name in CLOCKS_SOURCES]
-    workers = min(len(sources) + len(clock_sources), max(1, (os.cpu_count() or 2) // 2), 8)
+    workers = min(len(sources), max(1, (os.cpu_count() or 2) // 2), 8)
     with ThreadPoolExecutor(max_workers=workers) as pool:
-        product = [pool.submit(_compile, source) for source in sources]
-        clocks = [pool.submit(_compile, source, ("-DOMNIA_PHASE_CLOCKS",), ".clocks")
-                  for source in clock_sources]
-        objects = [job.result() for job in product]
-        clock_objects = [job.result() for job in clocks]
+        objects = list(pool.map(_compile, sources))
     _link(objects, LIBRARY)
-    _link(clock_objects, CLOCKS_LIBRARY)
     if verbose:
-        print(f"built {LIBRARY.relative_to(REPO)} from {len(sources)} sources "
-              f"(and {CLOCKS_LIBRARY.name})", flush=True)
+        print(f"built {LIBRARY.relative_to(REPO)} from {len(sources)} sources", flush=True)
+    if clocks:
+        build_clocks_library(verbose)
     return LIBRARY
 
 
+def build_clocks_library(verbose: bool = True) -> Path:
+    """The router and the ABI bookkeeping compiled with the phase-clock marks on, linked
+    into `libomnia_router_clocks.so` beside the product library (never loaded by the
+    package)."""
+    OBJDIR.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(max_workers=len(CLOCKS_SOURCES)) as pool:
+        objects = list(pool.map(
+            lambda name: _compile(CSRC / name, ("-DOMNIA_PHASE_CLOCKS",), ".clocks"),
+            CLOCKS_SOURCES))
+    _link(objects, CLOCKS_LIBRARY)
+    if verbose:
+        print(f"built {CLOCKS_LIBRARY.relative_to(REPO)} (diagnostic)", flush=True)
+    return CLOCKS_LIBRARY
+
+
 if __name__ == "__main__":
-    build_library(verbose=True)
+    build_library(verbose=True, clocks="--clocks" in sys.argv[1:] or None)
     sys.exit(0)

@@ -155,6 +155,28 @@ class DefaultAttentionStep(AttentionStepStrategy):
         return (probs @ vf).to(raw_queries.dtype)
 
 
+def capture_covered(cache: FixedKVCache, atlas_rows: int) -> None:
+    """Refuse a capture whose replays could rotate at a position past the angle table.
+
+    A replay advances the device position the host never sees. A fixed cache bounds it
+    by the capacity, so the table must cover every row. A ring's position keeps rising
+    past the window, so the capture needs `replay_limit` (the last position a replay
+    reaches, declared with `prepare_capture`) and a table that covers it; without that
+    the kernel would rotate late replays with the table's last row and no error."""
+    if cache.window == 0:
+        if atlas_rows < cache.capacity:
+            raise ValueError(f"a captured step needs an angle table covering the cache's "
+                             f"{cache.capacity} rows, not {atlas_rows}")
+        return
+    limit = cache.replay_limit
+    if limit is None or limit < cache.offset:
+        raise ValueError("a captured step over a ring cache needs the last position its "
+                         "replays reach: call prepare_capture(last_position) first")
+    if limit >= atlas_rows:
+        raise ValueError(f"a captured step's replays reach position {limit}, past the "
+                         f"angle table's {atlas_rows} rows")
+
+
 @dataclass(frozen=True)
 class HipAttentionStep(AttentionStepStrategy):
     cache: FixedKVCache
@@ -206,6 +228,17 @@ class HipAttentionStep(AttentionStepStrategy):
         return cls(cache, heads, kv_heads, scale, eps, mscale, query_weight.contiguous(),
                    key_weight.contiguous(), atlas, growable, workspace, fallback)
 
+    def prepare_capture(self, last_position: int) -> None:
+        """Declare the last position a captured step's replays will reach, before the
+        capture: a growable atlas is grown to cover it (it cannot grow inside a capture)
+        and the cache records it. Replays past it are outside the contract."""
+        if last_position < self.cache.offset:
+            raise ValueError(f"last position {last_position} is before the cache's "
+                             f"position {self.cache.offset}")
+        if self.growable is not None:
+            self.growable.ensure(last_position)
+        self.cache.replay_limit = last_position
+
     def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
         if raw_queries.shape[1] != 1:
             record_fallback(self, self.fallback)
@@ -226,9 +259,8 @@ class HipAttentionStep(AttentionStepStrategy):
             atlas = self.growable.atlas
         if cache.offset >= atlas.shape[0]:
             raise ValueError(f"position {cache.offset} is past the angle table's {atlas.shape[0]} rows")
-        if capturing and cache.window == 0 and atlas.shape[0] < cache.capacity:
-            raise ValueError(f"a captured step needs an angle table covering the cache's "
-                             f"{cache.capacity} rows, not {atlas.shape[0]}")
+        if capturing:
+            capture_covered(cache, atlas.shape[0])
         keys, values = cache.fetch()
         max_rows = cache.capacity if capturing else min(cache.offset + 1, cache.capacity)
         out = ops.attention_decode(
@@ -305,6 +337,13 @@ class AttentionStep(AttentionStepStrategy):
             query_weight=query_weight, key_weight=key_weight, eps=eps,
             rotary_pairs=rotary_pairs, mscale=mscale, angles=angles, base=base, sinks=sinks,
         )
+
+    def prepare_capture(self, last_position: int) -> None:
+        """Before capturing a step over a ring cache: the last position its replays reach
+        (the binding grows what it must to cover it)."""
+        prepare = getattr(self.strategy, "prepare_capture", None)
+        if prepare is not None:  # the other bindings run their replays in torch ops
+            prepare(last_position)
 
     def __call__(self, raw_queries, raw_keys, raw_values, mask=None):
         return self.strategy(raw_queries, raw_keys, raw_values, mask)

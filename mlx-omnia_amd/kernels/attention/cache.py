@@ -18,6 +18,10 @@ class FixedKVCache:
         self.keys, self.values = keys, values
         self.offset = position
         self.position = torch.tensor([position], dtype=torch.int32, device=keys.device)
+        # The last position a captured step's replays may reach (None: not declared). A
+        # fixed cache is bounded by its capacity; a ring's position has no bound of its
+        # own, so a step over it is captured only after this is declared.
+        self.replay_limit: int | None = None
 
     @classmethod
     def empty(cls, kv_heads: int, capacity: int, head_dim: int, *, dtype=torch.bfloat16,

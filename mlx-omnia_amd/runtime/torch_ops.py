@@ -91,8 +91,11 @@ def _embed_atlas(tokens: torch.Tensor, embedding: torch.Tensor, full_atlas: torc
     """Gathered rows, then the full and sliding atlas rows ([0, 0] for an atlas not given)."""
     hidden, full, sliding = ops.embed_atlas(tokens, embedding, full_atlas, sliding_atlas, position=position,
                                             n_positions=n_positions)
-    empty = embedding.new_empty((0, 0), dtype=torch.float32)
-    return hidden, empty if full is None else full, empty if sliding is None else sliding
+    # A missing atlas gets an empty tensor of its own: custom ops may not return one
+    # tensor twice (the outputs would alias).
+    def rows(atlas):
+        return embedding.new_empty((0, 0), dtype=torch.float32) if atlas is None else atlas
+    return hidden, rows(full), rows(sliding)
 
 
 def _embed_atlas_fake(tokens, embedding, full_atlas, sliding_atlas, position, n_positions):

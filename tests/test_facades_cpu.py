@@ -577,6 +577,28 @@ def test_attention_predicates_and_declines():
                       DefaultAttentionStep)
 
 
+def test_captured_step_refuses_replays_past_the_angle_table():
+    """A capture over a ring cache needs the last position its replays reach, covered by
+    the table; a fixed cache needs the table to cover its capacity."""
+    from mlx_omnia_amd.kernels.attention import FixedKVCache, RingKVCache, capture_covered
+
+    fixed = FixedKVCache.empty(2, 64, 128)
+    capture_covered(fixed, 64)
+    with pytest.raises(ValueError, match="covering the cache's 64 rows"):
+        capture_covered(fixed, 63)
+    ring = RingKVCache.empty(2, 16, 128)
+    ring.offset = 40
+    with pytest.raises(ValueError, match="prepare_capture"):
+        capture_covered(ring, 4096)                  # no bound declared
+    ring.replay_limit = 39
+    with pytest.raises(ValueError, match="prepare_capture"):
+        capture_covered(ring, 4096)                  # a bound behind the position
+    ring.replay_limit = 100
+    capture_covered(ring, 101)
+    with pytest.raises(ValueError, match="past the angle table's 100 rows"):
+        capture_covered(ring, 100)
+
+
 def test_attention_core_chain_matches_oracle_on_cpu():
     from mlx_omnia_amd.kernels.attention import AttentionStep, FixedKVCache, RingKVCache
     from mlx_omnia_amd.kernels.qkv_rope import AngleTable

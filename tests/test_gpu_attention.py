@@ -266,6 +266,8 @@ def test_facade_step_captured_and_replayed(ring):
     cache.position.fill_(start)
     keys.copy_(case.kc.unsqueeze(0))
     values.copy_(case.vc.unsqueeze(0))
+    if ring:
+        step.prepare_capture(start + 7)             # the last position a replay reaches
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         out = step(q, k, v)

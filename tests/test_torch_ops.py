@@ -65,3 +65,20 @@ def test_fake_shapes_and_dtypes():
                                                     torch.empty(1, 8, 300, 64, dtype=BF16),
                                                     torch.empty(64, dtype=BF16), None, 0.125)
         assert ctx.shape == (64, 64) and ctx.dtype == BF16
+
+
+def test_embed_atlas_without_atlases_returns_distinct_empties(monkeypatch):
+    """A gather-only call (both atlases None) runs the real operator body: the two empty
+    atlas outputs are distinct tensors (custom ops refuse outputs that alias). The C-ABI
+    gather is replaced by a torch gather, so no device is needed."""
+    def gather_only(tokens, embedding, full, sliding, *, position, n_positions):
+        assert full is None and sliding is None
+        return embedding[tokens.long()], None, None
+
+    monkeypatch.setattr(torch_ops.ops, "embed_atlas", gather_only)
+    tokens = torch.tensor([[3, 1, 4]], dtype=torch.int32)
+    table = torch.arange(5 * 8, dtype=torch.float32).reshape(5, 8).to(BF16)
+    hidden, full, sliding = torch.ops.omnia.embed_atlas(tokens, table, None, None, 0, 3)
+    assert torch.equal(hidden, table[tokens.long()])
+    assert full.shape == sliding.shape == (0, 0)
+    assert full.data_ptr() != sliding.data_ptr() or full is not sliding
