@@ -12,7 +12,9 @@ Method, per kernel:
 - the launch cycles through enough copies of inputs and outputs that one cycle touches
   >= 512 MB (twice the 256 MB Infinity Cache), so no launch is served from cache;
 - `--warmup` launches, then exactly `--steps` launches between two HIP events recorded
-  on the stream the kernels run on, with a device synchronise on both sides. Each launch
+  on the stream the kernels run on, with a device synchronise on both sides; a ~100 us
+  spin is queued ahead of the start event, so the host's latency in issuing the first
+  launch falls outside the timed region. Each launch
   is a direct call of the C-ABI entry point with its arguments bound in advance (about a
   microsecond of host time), so back-to-back launches keep the GPU queue fed without
   the per-node gap a HIP graph replay adds; `--graph` times a captured graph instead;
@@ -324,6 +326,24 @@ def workloads() -> list[Workload]:
         bytes_per_launch=4096 * 128 * 2 + 2 * 4096 * 8 * 4,
         setup=setup_route,
         launch=lambda a: ops.softmax_topk(a["logits"], 8, indices=a["idx"], weights=a["wts"]),
+    ))
+
+    def setup_route_shared(device, copies, rows=4096, experts=128, k=8):
+        rng = np.random.default_rng(19)
+        first = dict(logits=_to_bf16_device(_normal(rng, (rows, experts + 1)), device),
+                     idx=torch.empty((rows, k + 1), dtype=torch.int32, device=device),
+                     wts=torch.empty((rows, k + 1), dtype=torch.float32, device=device))
+        return _copies(first, copies)
+
+    out.append(Workload(
+        name="softmax_topk_shared",
+        kernel="softmax_topk_kernel",
+        description="router logits bf16 [4096, 128 + 1 shared gate] -> top-8 indices + fp32 softmax "
+                    "probabilities (normalize=False) + the shared slot's sigmoid (Qwen3.5 / Qwen3 forms)",
+        bytes_per_launch=4096 * 129 * 2 + 2 * 4096 * 9 * 4,
+        setup=setup_route_shared,
+        launch=lambda a: ops.softmax_topk(a["logits"], 8, normalize=False, shared=True,
+                                          indices=a["idx"], weights=a["wts"]),
     ))
     out.append(Workload(
         name="sigmoid_topk",
@@ -905,6 +925,31 @@ def _bound_launch(w: Workload, argset):
     return run
 
 
+_PREROLL_CYCLES: list[int] = []
+
+
+def _preroll(stream) -> None:
+    """Queue about 100 us of spin on `stream` ahead of the start event, so the timed
+    launches find the queue already running: the host's latency in issuing the first
+    launch is not inside the timed region (it would add several us to a 20-launch
+    region). The spin's length in clock cycles is calibrated once with events."""
+    import torch
+
+    if not _PREROLL_CYCLES:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(1000)
+            start.record(stream)
+            torch.cuda._sleep(1_000_000)
+            end.record(stream)
+        torch.cuda.synchronize()
+        us = max(start.elapsed_time(end) * 1000.0, 1.0)
+        _PREROLL_CYCLES.append(max(1000, min(int(1_000_000 * 100.0 / us), 50_000_000)))
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(_PREROLL_CYCLES[0])
+
+
 def time_workload(w: Workload, steps: int, warmup: int, device, graph_mode: bool) -> dict:
     import torch
 
@@ -931,6 +976,7 @@ def time_workload(w: Workload, steps: int, warmup: int, device, graph_mode: bool
                     w.launch(sets[i % copies])
             graph.replay()  # untimed: first replay uploads the graph
             torch.cuda.synchronize(device)
+            _preroll(stream)
             start.record(stream)
             graph.replay()
             end.record(stream)
@@ -942,6 +988,7 @@ def time_workload(w: Workload, steps: int, warmup: int, device, graph_mode: bool
                 runs[i % copies]()
             torch.cuda.synchronize(device)
             codes = 0
+            _preroll(stream)
             start.record(stream)
             for i in range(steps):
                 codes |= runs[i % copies]()
@@ -1043,6 +1090,11 @@ def _cpu_legs() -> dict:
                     4096 * 128 * 2 + 128 * 4 + 2 * 4096 * 8 * 4, "[4096, 128], whole", False)
         return (lambda: route.softmax_topk(logits, 8), 4096 * 128 * 2 + 2 * 4096 * 8 * 4,
                 "[4096, 128], whole", False)
+
+    def route_shared_leg():
+        logits = bf((4096, 129))
+        return (lambda: route.softmax_topk_slots(logits, 8, normalize=False, shared=True),
+                4096 * 129 * 2 + 2 * 4096 * 9 * 4, "[4096, 129], whole", False)
 
     def router_sigmoid_leg():
         x, r, w = bf((256, 2048)), bf((256, 2048)), bf((2048,), 0.1, 1.0)
@@ -1194,6 +1246,7 @@ def _cpu_legs() -> dict:
         "gated_activations": gated_leg,
         "residual_rms_router": router_leg,
         "softmax_topk": lambda: route_leg(False),
+        "softmax_topk_shared": route_shared_leg,
         "sigmoid_topk": lambda: route_leg(True),
         "residual_rms_router_sigmoid": router_sigmoid_leg,
         "residual_rms_router_decode": lambda: router_one_leg(False),

@@ -171,6 +171,25 @@ int32_t omnia_softmax_topk(const uint16_t* logits, int64_t stride, int64_t rows,
                            int64_t experts, int64_t k, int32_t* indices, float* weights,
                            hipStream_t stream);
 
+/* The same selection with the two other softmax declarations of the reference's Route:
+ *   normalize = 1: weights as omnia_softmax_topk (renormalised over the kept experts);
+ *   normalize = 0: weights[r, j] = softmax(logits[r, :experts])[indices[r, j]], the
+ *                  probability over the whole row (Route(..., normalize=False));
+ *   shared = 1:    the row holds experts + 1 logits, the last the shared expert's gate;
+ *                  slot k of each output row is the shared expert: index `experts`,
+ *                  weight sigmoid(logit) in fp32 (correctly rounded), after the k routed
+ *                  slots (Route(..., shared=True)).
+ * indices, weights [rows, k + shared]; stride >= experts + shared; k <= 63 with a shared
+ * slot, 64 without; the other limits as omnia_softmax_topk.
+ * Replaces: core/kernels/route/softmax_topk.py:20-75 (`moe_softmax_topk` with SHARED)
+ * and 295-336 (the declarations SoftmaxTopkRoute.build serves), and the Core chain
+ * core/kernels/route/default.py:44-69 for `normalize=False` (its `if routing.normalize`
+ * and `if routing.shared` arms), as models/qwen3_5/layers/moe.py:157-162 (shared) and
+ * models/qwen3/layers/moe.py:50-52 (normalize=norm_topk) declare them. */
+int32_t omnia_softmax_topk_slots(const uint16_t* logits, int64_t stride, int64_t rows,
+                                 int64_t experts, int64_t k, int32_t normalize, int32_t shared,
+                                 int32_t* indices, float* weights, hipStream_t stream);
+
 /* Bytes of the packed router weight for [experts, hidden] (experts a multiple of 16,
  * hidden of 32), or -EINVAL. Pure; touches no device. */
 int64_t omnia_router_pack_bytes(int64_t experts, int64_t hidden);

@@ -325,9 +325,36 @@ __global__ __launch_bounds__(256) void sigmoid_topk_kernel(const void* __restric
   if (indices) ordinal_topk_write<V>(keys, scores, experts, k, lane, indices + row * k, weights + row * k);
 }
 
-// ---- softmax -> top-k over given bf16 logits: one wave per row --------------------
-
+// Writes the winners' indices and their softmax probabilities over the whole row (no
+// renormalisation over the kept experts): p_j = exp(l_j - l_1) / sum_e exp(l_e - l_1),
+// l_1 the largest logit, the denominator summed over every expert of the row.
 template <int V>
+__device__ __forceinline__ void write_winners_unnormalised(uint32_t chosen, const uint16_t (&raw)[V],
+                                                           int experts, int k, int lane,
+                                                           int32_t* indices, float* weights) {
+  const float top = key_logit(static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(chosen), 0)));
+  float part = 0.0f;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const float e = expf(bf16_to_f32(raw[v]) - top);
+    part += lane + v * kWave < experts ? e : 0.0f;
+  }
+  const float total = wave_sum(part);
+  if (lane < k) {
+    indices[lane] = static_cast<int32_t>(0xFFFFu - (chosen & 0xFFFFu));
+    weights[lane] = expf(key_logit(chosen) - top) / total;
+  }
+}
+
+// ---- softmax -> top-k over given bf16 logits: one wave per row --------------------
+//
+// kNormalize: the kept probabilities renormalised over themselves (write_winners), or
+// the probabilities themselves (write_winners_unnormalised). kShared: the row holds one
+// more logit after the routed ones, the shared expert's; slot k gets index `experts`
+// and weight sigmoid(logit), correctly rounded to fp32. The output row is k + kShared
+// slots long.
+template <int V, bool kNormalize, bool kShared>
 __global__ __launch_bounds__(256) void softmax_topk_kernel(const uint16_t* __restrict__ logits,
                                                            int64_t stride, int64_t rows,
                                                            int experts, int k,
@@ -341,6 +368,7 @@ __global__ __launch_bounds__(256) void softmax_topk_kernel(const uint16_t* __res
   uint16_t raw[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) raw[v] = logits[row * stride + min(lane + v * kWave, experts - 1)];
+  const uint16_t shared_raw = kShared ? logits[row * stride + experts] : uint16_t{0};
   uint32_t keys[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
@@ -350,7 +378,17 @@ __global__ __launch_bounds__(256) void softmax_topk_kernel(const uint16_t* __res
   }
   uint32_t chosen;
   select_topk<V>(keys, k, lane, chosen);
-  write_winners(chosen, k, lane, indices + row * k, weights + row * k);
+  const int slots = k + (kShared ? 1 : 0);
+  if (kNormalize) {
+    write_winners(chosen, k, lane, indices + row * slots, weights + row * slots);
+  } else {
+    write_winners_unnormalised<V>(chosen, raw, experts, k, lane, indices + row * slots,
+                                  weights + row * slots);
+  }
+  if (kShared && lane == k) {
+    indices[row * slots + k] = experts;
+    weights[row * slots + k] = sigmoid_rounded(bf16_to_f32(shared_raw));
+  }
 }
 
 // ---- packed router weight --------------------------------------------------------
@@ -1375,7 +1413,8 @@ int32_t launch_decode(const RouterArgs& a, hipStream_t stream) {
                                                                a.indices, a.weights);
     }
   } else {
-    softmax_topk_kernel<V><<<grid, 256, 0, stream>>>(a.logits, E, a.rows, E, a.k, a.indices, a.weights);
+    softmax_topk_kernel<V, true, false><<<grid, 256, 0, stream>>>(a.logits, E, a.rows, E, a.k, a.indices,
+                                                                  a.weights);
   }
   return launched("residual_rms_router");
 }
@@ -1402,27 +1441,55 @@ bool fused_shape(int64_t hidden, int64_t experts) {
 }  // namespace
 }  // namespace omnia
 
-extern "C" int32_t omnia_softmax_topk(const uint16_t* logits, int64_t stride, int64_t rows,
-                                      int64_t experts, int64_t k, int32_t* indices,
-                                      float* weights, hipStream_t stream) {
+namespace omnia {
+namespace {
+
+template <bool kNormalize, bool kShared>
+void launch_softmax_topk(const uint16_t* logits, int64_t stride, int64_t rows, int64_t experts,
+                         int64_t k, int32_t* indices, float* weights, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  const int e = static_cast<int>(experts), top = static_cast<int>(k);
+  switch ((experts + kWave - 1) / kWave) {
+    case 1: softmax_topk_kernel<1, kNormalize, kShared><<<grid, 256, 0, stream>>>(logits, stride, rows, e, top, indices, weights); break;
+    case 2: softmax_topk_kernel<2, kNormalize, kShared><<<grid, 256, 0, stream>>>(logits, stride, rows, e, top, indices, weights); break;
+    case 3: softmax_topk_kernel<3, kNormalize, kShared><<<grid, 256, 0, stream>>>(logits, stride, rows, e, top, indices, weights); break;
+    default: softmax_topk_kernel<4, kNormalize, kShared><<<grid, 256, 0, stream>>>(logits, stride, rows, e, top, indices, weights); break;
+  }
+}
+
+}  // namespace
+}  // namespace omnia
+
+extern "C" int32_t omnia_softmax_topk_slots(const uint16_t* logits, int64_t stride, int64_t rows,
+                                            int64_t experts, int64_t k, int32_t normalize,
+                                            int32_t shared, int32_t* indices, float* weights,
+                                            hipStream_t stream) {
   using namespace omnia;
   OMNIA_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), "softmax_topk: bad row count");
   OMNIA_REQUIRE(experts > 0 && experts <= 4 * kWave, "softmax_topk: experts must be in [1, 256]");
-  OMNIA_REQUIRE(k > 0 && k <= experts && k <= kMaxTopK, "softmax_topk: k must be in [1, min(experts, 64)]");
-  OMNIA_REQUIRE(stride >= experts, "softmax_topk: row stride smaller than experts");
+  OMNIA_REQUIRE(k > 0 && k <= experts && k < kMaxTopK + (shared ? 0 : 1),
+                "softmax_topk: k must be in [1, min(experts, 64)] (63 with a shared slot)");
+  OMNIA_REQUIRE(normalize == 0 || normalize == 1, "softmax_topk: normalize must be 0 or 1");
+  OMNIA_REQUIRE(shared == 0 || shared == 1, "softmax_topk: shared must be 0 or 1");
+  OMNIA_REQUIRE(stride >= experts + shared, "softmax_topk: row stride smaller than the row's logits");
   if (rows == 0) return 0;
   OMNIA_REQUIRE(logits && indices && weights, "softmax_topk: null pointer");
   int32_t rc = check_device(stream);
   if (rc != 0) return rc;
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
-  const int v = static_cast<int>((experts + kWave - 1) / kWave);
-  switch (v) {
-    case 1: softmax_topk_kernel<1><<<grid, 256, 0, stream>>>(logits, stride, rows, experts, k, indices, weights); break;
-    case 2: softmax_topk_kernel<2><<<grid, 256, 0, stream>>>(logits, stride, rows, experts, k, indices, weights); break;
-    case 3: softmax_topk_kernel<3><<<grid, 256, 0, stream>>>(logits, stride, rows, experts, k, indices, weights); break;
-    default: softmax_topk_kernel<4><<<grid, 256, 0, stream>>>(logits, stride, rows, experts, k, indices, weights); break;
+  if (normalize) {
+    if (shared) launch_softmax_topk<true, true>(logits, stride, rows, experts, k, indices, weights, stream);
+    else launch_softmax_topk<true, false>(logits, stride, rows, experts, k, indices, weights, stream);
+  } else {
+    if (shared) launch_softmax_topk<false, true>(logits, stride, rows, experts, k, indices, weights, stream);
+    else launch_softmax_topk<false, false>(logits, stride, rows, experts, k, indices, weights, stream);
   }
   return launched("softmax_topk");
+}
+
+extern "C" int32_t omnia_softmax_topk(const uint16_t* logits, int64_t stride, int64_t rows,
+                                      int64_t experts, int64_t k, int32_t* indices,
+                                      float* weights, hipStream_t stream) {
+  return omnia_softmax_topk_slots(logits, stride, rows, experts, k, 1, 0, indices, weights, stream);
 }
 
 extern "C" int64_t omnia_router_pack_bytes(int64_t experts, int64_t hidden) {

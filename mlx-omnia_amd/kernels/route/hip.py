@@ -1,11 +1,13 @@
 """The HIP routing strategies (csrc/router.hip), over logits from the stock matmul or
 the caller:
 
-- `HipSoftmaxTopkRoute` (`omnia_softmax_topk`): softmax -> top-k -> renormalise, the
+- `HipSoftmaxTopkRoute` (`omnia_softmax_topk_slots`): softmax -> top-k, the
   declarations core/kernels/route/softmax_topk.py:295-336 (`SoftmaxTopkRoute.build`)
-  serves for the softmax family (no bias, renormalise with no epsilon, no scale, no
-  softcap), without a shared slot, with the lowest-index tie rule, up to 256 experts and
-  k <= 64;
+  serves for the softmax family (no bias, no scale, no softcap), renormalised with no
+  epsilon, with or without the shared expert's sigmoid slot (softmax_topk.py:67-72,
+  Qwen3.5's declaration), and also `normalize=False` (the Core chain's arm,
+  core/kernels/route/default.py:62-63, Qwen3's `normalize=norm_topk`), with the
+  lowest-index tie rule, up to 256 experts and k <= 64 (63 with the shared slot);
 - `HipOrdinalRoute` (`omnia_sigmoid_topk`): sigmoid scoring with a correction bias,
   ordinal keys, lower-index ties and weights from the unbiased scores, where
   core/kernels/route/ordinal.py:265-286 (`OrdinalRoute.build`) binds: renormalise with
@@ -29,8 +31,8 @@ from .default import DefaultRoute
 from .kernel import RouteStrategy, Routing, gate_logits
 
 
-def softmax_topk_applies(experts: int, k: int) -> bool:
-    return 0 < experts <= 256 and 0 < k <= min(experts, 64)
+def softmax_topk_applies(experts: int, k: int, shared: bool = False) -> bool:
+    return 0 < experts <= 256 and 0 < k <= min(experts, 63 if shared else 64)
 
 
 @dataclass(frozen=True)
@@ -41,19 +43,22 @@ class HipSoftmaxTopkRoute(RouteStrategy):
 
     @classmethod
     def build(cls, gate, *, routing: Routing) -> "HipSoftmaxTopkRoute | None":
-        if not routing.plain_softmax() or not softmax_topk_applies(routing.experts, routing.k):
+        if not routing.softmax_slots() or not softmax_topk_applies(routing.experts, routing.k,
+                                                                    routing.shared):
             return None
         if gate is not None and not hip_device(gate):
             return None
         return cls(gate, routing, DefaultRoute(gate, routing))
 
     def __call__(self, row, *, logits=None, ids=None):
+        routing = self.routing
         values = gate_logits(self.gate, row, logits)
-        if (values.dtype != torch.bfloat16 or values.shape[-1] != self.routing.experts
-                or not hip_device(values)):
+        width = routing.experts + (1 if routing.shared else 0)
+        if values.dtype != torch.bfloat16 or values.shape[-1] != width or not hip_device(values):
             record_fallback(self, self.fallback)
             return self.fallback(row, logits=values)
-        return ops.softmax_topk(values, self.routing.k)
+        return ops.softmax_topk(values, routing.k, normalize=routing.normalize,
+                                shared=routing.shared)
 
     def rows(self, logits: torch.Tensor):
         return self(logits, logits=logits)

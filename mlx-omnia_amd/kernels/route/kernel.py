@@ -38,11 +38,17 @@ class Routing:
         return self.k + (1 if self.shared else 0)
 
     def plain_softmax(self) -> bool:
-        """softmax -> top-k -> renormalise, nothing else (what the HIP kernels compute)."""
+        """softmax -> top-k -> renormalise, nothing else (what the fused router computes)."""
+        return self.softmax_slots() and self.normalize and not self.shared
+
+    def softmax_slots(self) -> bool:
+        """Softmax scoring with no bias, scale, softcap or hash table and the lower-index
+        tie rule; renormalised with no epsilon or not at all; with or without the shared
+        slot (what `omnia_softmax_topk_slots` computes)."""
         return (
-            self.scoring == "softmax" and self.bias is None and self.normalize
-            and self.norm_eps == 0.0 and self.scale == 1.0 and self.softcap == 0.0
-            and not self.shared and self.hash_table is None and self.ties == "lower"
+            self.scoring == "softmax" and self.bias is None and self.norm_eps == 0.0
+            and self.scale == 1.0 and self.softcap == 0.0 and self.hash_table is None
+            and self.ties == "lower"
         )
 
 

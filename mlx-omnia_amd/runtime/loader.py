@@ -41,6 +41,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I32, [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _P]
     ),
     "omnia_softmax_topk": (_I32, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "omnia_softmax_topk_slots": (_I32, [_P, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P]),
     "omnia_router_pack_bytes": (_I64, [_I64, _I64]),
     "omnia_pack_router_weight": (_I32, [_P, _I64, _I64, _P, _P]),
     "omnia_residual_rms_router": (

@@ -327,21 +327,31 @@ def gated_activations_applies(gate: torch.Tensor, up: torch.Tensor, a: torch.Ten
     return a.dim() < 2 or a.shape[-2] <= 1 or a.stride(-2) % 2 == 0
 
 
-def softmax_topk(logits: torch.Tensor, k: int, *, indices: torch.Tensor | None = None,
+def softmax_topk(logits: torch.Tensor, k: int, *, normalize: bool = True, shared: bool = False,
+                 indices: torch.Tensor | None = None,
                  weights: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """Top-k of bf16 router logits [..., E] (lowest index on ties) and the renormalised
-    softmax weights; see `omnia_softmax_topk`. Returns int32 and fp32 [..., k]."""
-    experts = logits.shape[-1]
-    rows2 = logits.reshape(-1, experts) if logits.is_contiguous() else logits
+    """Top-k of bf16 router logits [..., E] (lowest index on ties) and their softmax
+    weights, renormalised over the kept experts unless `normalize` is False; with
+    `shared` the last logit of each row is the shared expert's gate and slot k carries
+    (E - 1, its fp32 sigmoid). See `omnia_softmax_topk` / `omnia_softmax_topk_slots`.
+    Returns int32 and fp32 [..., k + shared]."""
+    width = logits.shape[-1]
+    experts = width - (1 if shared else 0)
+    rows2 = logits.reshape(-1, width) if logits.is_contiguous() else logits
     _require(rows2.dim() == 2 and rows2.dtype == BF16 and rows2.stride(-1) == 1,
              "softmax_topk: logits must be bf16 [rows, experts] with unit inner stride")
     _require(on_rocm(rows2), "softmax_topk: logits must be on a ROCm device")
-    stride = experts if rows2.shape[0] <= 1 else rows2.stride(0)
-    shape = (*logits.shape[:-1], k)
+    stride = width if rows2.shape[0] <= 1 else rows2.stride(0)
+    shape = (*logits.shape[:-1], k + (1 if shared else 0))
     indices = _out(indices, logits, shape, torch.int32, "indices")
     weights = _out(weights, logits, shape, F32, "weights")
-    call("omnia_softmax_topk", rows2.data_ptr(), stride, rows2.shape[0], experts, int(k),
-         indices.data_ptr(), weights.data_ptr(), _stream(logits))
+    if normalize and not shared:
+        call("omnia_softmax_topk", rows2.data_ptr(), stride, rows2.shape[0], experts, int(k),
+             indices.data_ptr(), weights.data_ptr(), _stream(logits))
+    else:
+        call("omnia_softmax_topk_slots", rows2.data_ptr(), stride, rows2.shape[0], experts,
+             int(k), int(bool(normalize)), int(bool(shared)), indices.data_ptr(),
+             weights.data_ptr(), _stream(logits))
     return indices, weights
 
 

@@ -148,12 +148,13 @@ gated_activations = _op("gated_activations", _gated_activations, _gated_activati
 
 # routing --------------------------------------------------------------------------------
 
-def _softmax_topk(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
-    return ops.softmax_topk(logits, k)
+def _softmax_topk(logits: torch.Tensor, k: int, normalize: bool = True,
+                  shared: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    return ops.softmax_topk(logits, k, normalize=normalize, shared=shared)
 
 
-def _softmax_topk_fake(logits, k):
-    shape = (*logits.shape[:-1], k)
+def _softmax_topk_fake(logits, k, normalize=True, shared=False):
+    shape = (*logits.shape[:-1], k + (1 if shared else 0))
     return logits.new_empty(shape, dtype=torch.int32), logits.new_empty(shape, dtype=torch.float32)
 
 

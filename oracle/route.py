@@ -29,6 +29,18 @@ Sigmoid routing with a correction bias (core/kernels/route/ordinal.py:200-286,
   (ordinal.py:183-193), divided in float32.
 
 NaN in the softmax chain ranks last as well, the place ordinal.py gives a NaN score.
+
+The two other softmax declarations of the reference's `Route` (`softmax_topk_slots`):
+
+- `normalize=False` (core/kernels/route/default.py:61-63 skips the division;
+  models/qwen3/layers/moe.py:50-52 declares `normalize=norm_topk`): the weights are
+  the kept float32 probabilities themselves, p[sel];
+- `shared=True` (core/kernels/route/softmax_topk.py:67-72 and default.py:65-68;
+  models/qwen3_5/layers/moe.py:157-162): the row carries one more logit after the
+  routed experts, the shared expert's gate; the selection runs over the routed logits
+  only, and one more slot follows the k routed ones: index `experts`, weight the
+  float32 sigmoid of that logit (the kernel's stable form, `sigmoid_f32` below,
+  correctly rounded; the reference rounds it to the logits' dtype, bf16).
 """
 
 from __future__ import annotations
@@ -73,6 +85,35 @@ def renormalised_weights(logit_bits: np.ndarray, indices: np.ndarray) -> np.ndar
 def softmax_topk(logit_bits: np.ndarray, k: int):
     indices = select(logit_bits, k)
     return indices, renormalised_weights(logit_bits, indices)
+
+
+def softmax_probabilities(logit_bits: np.ndarray) -> np.ndarray:
+    """softmax of the bf16 logits over the row, in float32 (default.py:46)."""
+    logits = to_f32(logit_bits)
+    shifted = logits - logits.max(axis=-1, keepdims=True)
+    e = np.exp(shifted, dtype=np.float32)
+    return (e / e.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
+
+
+def softmax_topk_slots(logit_bits: np.ndarray, k: int, *, normalize: bool = True,
+                       shared: bool = False):
+    """(indices [..., k + shared] int32, weights fp32) of the softmax declaration with
+    or without renormalisation and with or without the shared slot (default.py:44-69,
+    softmax_topk.py:20-75)."""
+    logit_bits = np.asarray(logit_bits, dtype=np.uint16)
+    experts = logit_bits.shape[-1] - (1 if shared else 0)
+    routed = logit_bits[..., :experts]
+    indices = select(routed, k)
+    if normalize:
+        weights = renormalised_weights(routed, indices)
+    else:
+        weights = np.take_along_axis(softmax_probabilities(routed), indices.astype(np.int64), axis=-1)
+    if shared:
+        slot = np.full((*indices.shape[:-1], 1), experts, dtype=np.int32)
+        gate = sigmoid_f32(to_f32(logit_bits[..., experts:]))
+        indices = np.concatenate([indices, slot], axis=-1)
+        weights = np.concatenate([weights, gate.astype(np.float32)], axis=-1)
+    return indices, weights.astype(np.float32)
 
 
 def residual_rms_router(x_bits, branch_bits, norm_bits, router_bits, eps: float, k: int):

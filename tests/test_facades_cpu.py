@@ -20,7 +20,7 @@ from mlx_omnia_amd.kernels.gate_up import (DefaultGateUpActivation, GateUpActiva
 from mlx_omnia_amd.kernels.leaf import RMSNormLeaf
 from mlx_omnia_amd.kernels.qkv_rope import (AngleTable, DefaultQkvRope, QkvRope, qk_norm_rope_applies,
                                             rope_core, rope_epilogue_applies)
-from mlx_omnia_amd.kernels.route import (DefaultResidualRouter, DefaultRoute, ResidualRouter, Route,
+from mlx_omnia_amd.kernels.route import (HipSoftmaxTopkRoute, DefaultResidualRouter, DefaultRoute, ResidualRouter, Route,
                                          Routing, residual_router_applies, softmax_topk_applies)
 from oracle import activations as act
 from oracle import embed as oracle_embed
@@ -206,12 +206,19 @@ def test_route_predicates_and_declines():
     assert residual_router_applies(2048, 128, 8) and residual_router_applies(4096, 256, 8)
     assert not residual_router_applies(2560, 128, 8) and not residual_router_applies(2048, 64, 8)
     assert Routing(experts=128, k=8).plain_softmax()
-    for knob in (dict(scoring="sigmoid"), dict(bias=torch.zeros(128)), dict(normalize=False),
-                 dict(scale=2.5), dict(softcap=30.0), dict(shared=True), dict(ties="higher"),
-                 dict(norm_eps=1e-20)):
+    for knob in (dict(scoring="sigmoid"), dict(bias=torch.zeros(128)), dict(scale=2.5),
+                 dict(softcap=30.0), dict(ties="higher"), dict(norm_eps=1e-20)):
         routing = Routing(experts=128, k=8, **knob)
-        assert not routing.plain_softmax(), knob
+        assert not routing.plain_softmax() and not routing.softmax_slots(), knob
         assert isinstance(Route(None, experts=128, k=8, **knob).strategy, DefaultRoute), knob
+    # The shared slot and the unnormalised weights: not the fused router's declaration,
+    # but the softmax top-k kernel's (Qwen3.5's shared=True, Qwen3's normalize=norm_topk).
+    for knob in (dict(normalize=False), dict(shared=True), dict(normalize=False, shared=True)):
+        routing = Routing(experts=128, k=8, **knob)
+        assert not routing.plain_softmax() and routing.softmax_slots(), knob
+        assert isinstance(Route(None, experts=128, k=8, **knob).strategy, HipSoftmaxTopkRoute), knob
+    assert softmax_topk_applies(128, 63, shared=True) and not softmax_topk_applies(128, 64, shared=True)
+    assert isinstance(Route(None, experts=128, k=64, shared=True).strategy, DefaultRoute)
 
 
 def test_route_core_chain_matches_oracle_and_reference_tie_fixture():
@@ -231,6 +238,28 @@ def test_route_core_chain_matches_oracle_and_reference_tie_fixture():
     higher, _ = Route(None, experts=128, k=8, ties="higher").rows(cpu(row))
     assert lower.numpy()[0].tolist() == [0, 1, 2, 3, 11, 35, 67, 99]
     assert higher.numpy()[0].tolist() == [127, 120, 99, 67, 35, 11, 3, 2]
+
+
+@pytest.mark.parametrize("normalize,shared", [(True, True), (False, False), (False, True)])
+def test_route_core_chain_shared_slot_and_unnormalised(normalize, shared):
+    """The Core chain's shared slot and unnormalised weights against the oracle; the HIP
+    binding, given CPU logits, hands the call to that chain and records it."""
+    from mlx_omnia_amd.kernels.resolve import FALLBACKS
+
+    rng = np.random.default_rng(7)
+    logits = from_float(rng.standard_normal((40, 128 + shared)) * 2)
+    want_idx, want_w = oracle_route.softmax_topk_slots(logits, 8, normalize=normalize, shared=shared)
+    core = Route(None, experts=128, k=8, normalize=normalize, shared=shared, reference=True)
+    idx, w = core.rows(cpu(logits))
+    assert np.array_equal(idx.numpy(), want_idx)
+    np.testing.assert_allclose(w.numpy(), want_w, rtol=1e-5, atol=1e-7)
+    hip = Route(None, experts=128, k=8, normalize=normalize, shared=shared)
+    assert isinstance(hip.strategy, HipSoftmaxTopkRoute)
+    name = "HipSoftmaxTopkRoute -> DefaultRoute"
+    before = FALLBACKS.get(name, 0)
+    idx2, w2 = hip.rows(cpu(logits))
+    assert FALLBACKS.get(name, 0) == before + 1
+    assert np.array_equal(idx2.numpy(), want_idx)
 
 
 def test_residual_router_cpu_resolves_to_core_and_matches_oracle():

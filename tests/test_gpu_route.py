@@ -54,6 +54,71 @@ def test_softmax_topk_tie_fixture_via_facade(experts):
     assert abs(float(w.sum()) - 1.0) < 1e-6
 
 
+@pytest.mark.parametrize("experts,k,normalize,shared", [
+    (128, 8, True, True), (128, 8, False, False), (128, 8, False, True), (256, 8, False, True),
+    (64, 4, True, True), (100, 16, False, True), (32, 32, False, False), (128, 63, True, True),
+    (256, 64, False, False),
+])
+def test_softmax_topk_slots_matches_oracle(experts, k, normalize, shared):
+    """The shared sigmoid slot and the unnormalised weights: indices bit-exact, the
+    shared weight bit-exact (both correctly rounded), routed weights within rtol 1e-5."""
+    print(f"softmax_topk_slots experts={experts} k={k} normalize={normalize} shared={shared}", flush=True)
+    rng = np.random.default_rng(experts * 7 + k)
+    logits = from_float(rng.standard_normal((777, experts + shared)) * 2)
+    logits[:10] = from_float(rng.integers(-3, 3, (10, experts + shared)) * 0.5)  # heavy ties
+    if shared:
+        logits[10:20, experts] = from_float(np.array([0.0, -0.0, 1.5, -1.5, 30.0, -30.0, 90.0, -90.0,
+                                                      1e-3, -7.25]))
+    idx, w = ops.softmax_topk(to_device(logits), k, normalize=normalize, shared=shared)
+    want_idx, want_w = route.softmax_topk_slots(logits, k, normalize=normalize, shared=shared)
+    assert idx.shape == (777, k + shared) and idx.dtype == torch.int32
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    got = w.cpu().numpy()
+    np.testing.assert_allclose(got[:, :k], want_w[:, :k], rtol=1e-5, atol=1e-7)
+    if shared:
+        assert np.array_equal(got[:, k], want_w[:, k])
+
+
+def test_softmax_topk_slots_strided_rows():
+    """Rows read from a wider buffer (the row stride larger than the row's logits)."""
+    rng = np.random.default_rng(91)
+    wide = from_float(rng.standard_normal((300, 160)))
+    view = to_device(wide)[:, :129]
+    idx, w = ops.softmax_topk(view, 8, normalize=False, shared=True)
+    want_idx, want_w = route.softmax_topk_slots(wide[:, :129], 8, normalize=False, shared=True)
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(w.cpu().numpy(), want_w, rtol=1e-5, atol=1e-7)
+
+
+def test_shared_slot_fixture_via_facade():
+    """The reference's shared-slot fixture (tests/test_kernel_moe_route.py:152-177 with
+    shared=True), lowest-index ties: Route(..., shared=True) binds the HIP kernel."""
+    facade = Route(None, experts=128, k=8, shared=True)
+    assert isinstance(facade.strategy, HipSoftmaxTopkRoute)
+    logits = np.concatenate([_tied(128), from_float(np.array([[1.5]]))], axis=-1)
+    idx, w = facade.rows(to_device(logits))
+    assert idx.cpu().numpy()[0].tolist() == KAT_EXPECTED + [128]
+    got = w.cpu().numpy()[0]
+    assert got[8] == np.float32(1.0 - 1.0 / (1.0 + np.exp(1.5)))
+    assert abs(float(got[:8].sum()) - 1.0) < 1e-6
+
+
+def test_unnormalised_decode_step_via_facade():
+    """Qwen3's decode declaration with norm_topk off: the gate on the device, one row of
+    logits handed in by the caller (models/qwen3/layers/moe.py:50-64)."""
+    rng = np.random.default_rng(92)
+    gate = to_device(from_float(0.02 * rng.standard_normal((128, 2048))))
+    x = to_device(from_float(rng.standard_normal(2048)))
+    facade = Route(gate, experts=128, k=8, normalize=False)
+    assert isinstance(facade.strategy, HipSoftmaxTopkRoute)
+    logits = x @ gate.T
+    idx, w = facade(x, logits=logits)
+    want_idx, want_w = route.softmax_topk_slots(bits_of(logits)[None, :], 8, normalize=False)
+    assert np.array_equal(idx.cpu().numpy(), want_idx[0])
+    np.testing.assert_allclose(w.cpu().numpy(), want_w[0], rtol=1e-5, atol=1e-7)
+    assert float(w.sum()) < 1.0
+
+
 def _router_inputs(rows, hidden, experts, seed):
     rng = np.random.default_rng(seed)
     return (

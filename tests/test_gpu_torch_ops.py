@@ -50,6 +50,8 @@ def test_each_operator_equals_its_entry_point():
                                            ops.gated_activations(g, u, a, a_log, dt_bias)))
     logits, bias = _bf16(gen, 3, 128), 0.1 * torch.randn(128, generator=gen, device="cuda")
     assert all(_same(p, q) for p, q in zip(torch.ops.omnia.softmax_topk(logits, 8), ops.softmax_topk(logits, 8)))
+    assert all(_same(p, q) for p, q in zip(torch.ops.omnia.softmax_topk(logits, 8, False, True),
+                                           ops.softmax_topk(logits, 8, normalize=False, shared=True)))
     assert all(_same(p, q) for p, q in zip(torch.ops.omnia.sigmoid_topk(logits, bias, 8),
                                            ops.sigmoid_topk(logits, bias, 8)[:2]))
     gate = _bf16(gen, 128, 2048, scale=0.02)

@@ -13,6 +13,17 @@
   score);
 - planted mistakes (upward ties, no renormalisation, ascending order) fail.
 
+The shared slot and `normalize=False` (`softmax_topk_slots`):
+
+- the reference's shared-slot fixture (tests/test_kernel_moe_route.py:152-177 with
+  shared=True: the tie fixture plus a shared logit of 1.5), restated with the
+  lowest-index rule: [0, 1, 2, 3, 11, 35, 67, 99, 128];
+- the shared weight against scipy's float64 `expit` rounded to float32, for logits of
+  both signs (a planted mistake, the stable form's negative branch dropped, fails);
+- the shared logit never enters the selection or the routed weights, however large;
+- unnormalised weights against torch's float64 softmax of the whole row, summing below
+  one, and equal to the renormalised weights times their own sum.
+
 Sigmoid routing with a correction bias (route/ordinal.py:200-286):
 
 - the ordinal map against float order itself (a stable sort of the floats), over
@@ -277,3 +288,61 @@ def test_sigmoid_planted_mistakes_fail():
     nan_first = np.argsort(np.where(np.isnan(np.array([1.0, np.nan], np.float32)), 0, 1))
     assert nan_first.tolist() != route.sigmoid_topk(np.array([[1.0, np.nan]], np.float32),
                                                     np.zeros(2, np.float32), 2)[0][0].tolist()
+
+
+# ---- the shared slot and normalize=False --------------------------------------------
+
+
+def test_reference_shared_slot_fixture_lowest_index():
+    logits = np.concatenate([tied_logits(128), from_float(np.array([[1.5]]))], axis=-1)
+    idx, w = route.softmax_topk_slots(logits, 8, shared=True)
+    assert idx[0].tolist() == KAT_EXPECTED + [128]
+    assert w[0, 8] == np.float32(1.0 - 1.0 / (1.0 + np.exp(1.5)))
+    routed_idx, routed_w = route.softmax_topk(tied_logits(128), 8)
+    assert np.array_equal(idx[:, :8], routed_idx) and np.array_equal(w[:, :8], routed_w)
+
+
+def test_shared_weight_is_the_rounded_sigmoid_on_both_sides():
+    from scipy.special import expit
+
+    rng = np.random.default_rng(21)
+    gate = from_float(np.concatenate([rng.standard_normal(400) * 6, [0.0, -0.0, 30.0, -30.0, 90.0, -90.0]]))
+    logits = np.concatenate([from_float(rng.standard_normal((gate.size, 64))), gate[:, None]], axis=-1)
+    _, w = route.softmax_topk_slots(logits, 4, shared=True)
+    want = expit(to_f32(gate).astype(np.float64)).astype(np.float32)
+    assert np.array_equal(w[:, 4], want)
+    negative = to_f32(gate) < 0
+    assert (w[negative, 4] < 0.5).all() and (w[~negative, 4] >= 0.5).all()
+    # planted: the stable form without its negative branch (y for every sign)
+    x = to_f32(gate).astype(np.float64)
+    dropped = (1.0 / (1.0 + np.exp(np.abs(x)))).astype(np.float32)
+    assert not np.array_equal(dropped, w[:, 4])
+
+
+def test_shared_logit_never_selects_or_weighs_the_routed_slots():
+    rng = np.random.default_rng(22)
+    routed = from_float(rng.standard_normal((50, 128)))
+    base_idx, base_w = route.softmax_topk_slots(routed, 8)
+    for value in (-80.0, 0.0, 3.0, 80.0):
+        logits = np.concatenate([routed, from_float(np.full((50, 1), value))], axis=-1)
+        for normalize in (True, False):
+            idx, w = route.softmax_topk_slots(logits, 8, normalize=normalize, shared=True)
+            want_idx, want_w = route.softmax_topk_slots(routed, 8, normalize=normalize)
+            assert np.array_equal(idx[:, :8], want_idx) and np.array_equal(w[:, :8], want_w)
+            assert (idx[:, 8] == 128).all()
+    assert np.array_equal(base_idx, route.select(routed, 8))
+
+
+def test_unnormalised_weights_are_the_row_probabilities():
+    rng = np.random.default_rng(23)
+    logits = from_float(rng.standard_normal((300, 128)) * 2)
+    idx, w = route.softmax_topk_slots(logits, 8, normalize=False)
+    assert np.array_equal(idx, route.select(logits, 8))
+    p = torch.softmax(torch.from_numpy(to_f32(logits)).double(), -1)
+    want = torch.gather(p, -1, torch.from_numpy(idx.astype(np.int64))).numpy()
+    np.testing.assert_allclose(w, want, rtol=2e-6)
+    assert (w.sum(-1) < 1.0).all() and (np.diff(w, axis=-1) <= 0).all()
+    _, renormalised = route.softmax_topk_slots(logits, 8)
+    np.testing.assert_allclose(renormalised, w / w.sum(-1, keepdims=True), rtol=2e-6)
+    # planted: renormalising anyway is a different answer
+    assert not np.allclose(renormalised, w, rtol=1e-3)

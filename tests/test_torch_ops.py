@@ -42,6 +42,8 @@ def test_fake_shapes_and_dtypes():
                    lambda t: torch.ops.omnia.sigmoid_topk(t, torch.empty(128), 8)):
             idx, w = op(torch.empty(2, 5, 128, dtype=BF16))
             assert idx.shape == w.shape == (2, 5, 8) and idx.dtype == torch.int32 and w.dtype == torch.float32
+        idx, w = torch.ops.omnia.softmax_topk(torch.empty(3, 129, dtype=BF16), 8, False, True)
+        assert idx.shape == w.shape == (3, 9)
         packed = torch.ops.omnia.pack_router_weight(torch.empty(128, 2048, dtype=BF16))
         assert packed.shape == (loader.library().omnia_router_pack_bytes(128, 2048),)
         s2, n2, idx, w = torch.ops.omnia.residual_rms_router(x[:, :2048], x[:, :2048], torch.empty(2048, dtype=BF16),
