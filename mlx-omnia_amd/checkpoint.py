@@ -1,199 +1,255 @@
-"""Weight layouts for the fused kernels, built from safetensors checkpoints.
+"""Weight layouts the fused kernels read, built from a checkpoint's flat tensor dict.
 
-The dict side of the reference's loader (mlx_omnia/engine/checkpoint.py:277-444, and the
-LFM2 expert stacking in models/lfm2/moe/checkpoint.py:43-60), over torch tensors: the
-fusions take a flat `{name: tensor}` dict and return it with the projections the kernels
-read fused, the sources removed so that only one copy stays resident.
+A layout is a tuple of declarative rules over the checkpoint's key space, and one
+engine (`apply`) runs them. Every key is parsed into (module, leaf, suffix):
+`model.layers.3.self_attn.q_proj.weight` is module `model.layers.3.self_attn`, leaf
+`q_proj`, suffix `weight` (a quantised leaf adds `scales` and `biases` suffixes). The
+rules:
 
-- `fuse_qkv` (checkpoint.py:303-330): q/k/v concatenated on the output axis for every
-  suffix they carry (weight, bias, and a quantised leaf's scales/biases); leaves of
-  different formats move under `qkv_proj.{q,k,v}_proj.*` instead of into one matrix.
-- `concat_gate_up` (:333-347): a dense trunk's gate and up concatenated, gate rows first,
-  the `SwiGLU` leaf's `gate_up_proj` (what `omnia_dense_gate_up_swiglu` reads).
-- `stack_experts` (:350-373): per-expert leaves stacked into `[experts, out, in]` under
-  `switch_mlp.*`, the `SwitchLinear` layout.
-- `block_gate_up`: each expert's gate and up concatenated on the output axis,
-  `[experts, 2 * inner, in]`, the "blocked" layout `omnia_moe_gate_up` reads (LFM2's `w13`,
-  models/lfm2/moe/checkpoint.py:43-60); `interleave_gate_up` (:410-426) builds the row
-  interleave the Core chain's `SwitchGLU` reads.
-- `split_stacked_gate_up` (:376-394), `fold_norm_scales` (:397-407), `drop_tied_head`
-  (:440-444), `reject_dtype_cast` (:446-451) and `prepare_weights` (:617-636) as there.
+- `Join`: in every module whose path ends with `scope`, the `parts` leaves become one
+  leaf `into`, each suffix arranged as the kernel reads it: "rows" (stacked on the output
+  axis: q, k, v for `omnia_qk_norm_rope`'s fused projection, gate then up for
+  `omnia_dense_gate_up_swiglu`), "blocked" (per expert, gate rows then up rows on axis 1:
+  `omnia_moe_gate_up`'s layout) or "interleaved" (per expert, gate and up rows
+  alternating: the Core `SwitchGLU` order). Parts whose formats differ (a format being
+  the set of suffixes with their dtypes and trailing shapes) are nested under
+  `into.part` instead, as separate leaves;
+- `Stack`: per-expert modules `<owner>.experts.<i>` become one module
+  `<owner>.<into>` whose leaves are stacked over the expert index ([experts, out, in],
+  the `SwitchLinear` layout); the expert count is read off the keys;
+- `Halves`: a stacked [experts, in, 2 * inner] leaf stored without suffix (gate and up
+  as halves of the last axis) becomes two [experts, inner, in] leaves, and its partner
+  down leaf [experts, inner, in] the transposed [experts, in, inner];
+- `Shift` adds a constant to the matching keys (norm gains stored centred on zero);
+  `Drop` removes them (a tied head serialised anyway).
 
-`load_shards` reads every `model*.safetensors` of a directory with safetensors' own
-loader (it executes nothing from the file), straight onto `device` when one is given:
-on an MI355X the fusions then run on the GPU and the fused tensors are born contiguous
-and 16-byte aligned, ready for the kernels. Each fusion frees its sources as it goes, so
-the peak stays near one extra layer's worth of memory.
+`prepare` casts (refused for a quantised checkpoint, whose packed words cannot be
+cast), drops a tied head, then applies a layout. `LAYOUTS` names the layout each kernel
+family reads. Every rule removes its sources as it builds its target, so only one copy
+of each weight stays resident.
+
+The layouts, key names and the cases handled are those of the reference's loader
+(mlx_omnia/engine/checkpoint.py:277-451 and 617-636: q/k/v fusion with the mixed-format
+fallback, gate||up concatenation, expert stacking, stacked gate_up halves, norm
+folding, tied heads, the quantised-cast refusal) and of LFM2's blocked `w13`
+(models/lfm2/moe/checkpoint.py:43-60).
+
+`read_checkpoint` reads every `model*.safetensors` shard of a directory with
+safetensors' own loader (it executes nothing from the file), straight onto `device`
+when one is given: the rules then run on the GPU and every fused tensor is born
+contiguous and 16-byte aligned, as the kernels require.
 """
 
 from __future__ import annotations
 
+import re
+from collections import defaultdict
+from dataclasses import dataclass
 from pathlib import Path
-from typing import Callable, Iterable, Mapping, Sequence
+from typing import Literal, Mapping, Protocol, Sequence
 
 import torch
 
-QKV = ("q", "k", "v")
-QKV_SUFFIXES = ("weight", "scales", "biases", "bias")
-FORMAT_SUFFIXES = ("weight", "scales", "biases")
-
 Weights = dict[str, torch.Tensor]
-Fusion = Callable[[Weights], Weights]
+Arrangement = Literal["rows", "blocked", "interleaved"]
 
 __all__ = [
-    "block_gate_up", "concat_gate_up", "drop_tied_head", "fold_norm_scales", "fusible",
-    "fuse_qkv", "interleave_gate_up", "load_shards", "prepare_weights", "reject_dtype_cast",
-    "split_stacked_gate_up", "stack_experts",
+    "Drop", "Halves", "Join", "LAYOUTS", "Shift", "Stack", "apply", "leaf_format", "prepare",
+    "read_checkpoint",
 ]
 
 
-def load_shards(directory: Path | str, device: torch.device | str | None = None) -> Weights:
-    """Every `model*.safetensors` shard of `directory`, merged (the index file only says
-    which shard holds what)."""
+class Rule(Protocol):
+    def __call__(self, weights: Weights) -> None: ...
+
+
+def _parse(key: str) -> tuple[str, str, str]:
+    """(module, leaf, suffix) of a dotted key; a key of two parts has no module."""
+    head, _, suffix = key.rpartition(".")
+    module, _, leaf = head.rpartition(".")
+    return module, leaf, suffix
+
+
+def _key(module: str, leaf: str, suffix: str) -> str:
+    return ".".join(part for part in (module, leaf, suffix) if part)
+
+
+def _scope(pattern: str) -> re.Pattern:
+    """A module path ending with the dotted components `pattern` matches."""
+    return re.compile(rf"(?:^|\.)(?:{pattern})$")
+
+
+def _leaves(weights: Mapping[str, torch.Tensor]) -> dict[tuple[str, str], dict[str, str]]:
+    """(module, leaf) -> {suffix: key} over the whole dict."""
+    table: dict[tuple[str, str], dict[str, str]] = defaultdict(dict)
+    for key in weights:
+        module, leaf, suffix = _parse(key)
+        table[(module, leaf)][suffix] = key
+    return table
+
+
+def leaf_format(weights: Mapping[str, torch.Tensor], keys: Mapping[str, str]) -> frozenset:
+    """The format of one leaf: its suffixes, each with the dtype and trailing shape of its
+    tensor. Leaves of one format can share a matrix; others cannot."""
+    return frozenset((suffix, weights[key].dtype, tuple(weights[key].shape[1:]))
+                     for suffix, key in keys.items())
+
+
+def _arrange(parts: list[torch.Tensor], how: Arrangement) -> torch.Tensor:
+    if how == "rows":
+        return torch.cat(parts, dim=0).contiguous()
+    if how == "blocked":
+        return torch.cat(parts, dim=1).contiguous()
+    stacked = torch.stack(parts, dim=2)            # [experts, rows, parts, ...]
+    experts, rows = stacked.shape[:2]
+    return stacked.reshape(experts, rows * len(parts), *stacked.shape[3:]).contiguous()
+
+
+@dataclass(frozen=True)
+class Join:
+    scope: str
+    parts: tuple[str, ...]
+    into: str
+    arrange: Arrangement = "rows"
+
+    def __call__(self, weights: Weights) -> None:
+        scope = _scope(self.scope)
+        table = _leaves(weights)
+        owners = {module for (module, leaf) in table if leaf in self.parts and scope.search(module)}
+        for module in sorted(owners):
+            members = [table.get((module, part)) for part in self.parts]
+            if any(not keys or "weight" not in keys for keys in members):
+                continue                     # a leaf missing: nothing to fuse here
+            formats = {leaf_format(weights, keys) for keys in members}
+            if len(formats) > 1:             # mixed formats: one leaf each, under `into`
+                for part, keys in zip(self.parts, members):
+                    for suffix, key in keys.items():
+                        weights[_key(f"{module}.{self.into}", part, suffix)] = weights.pop(key)
+                continue
+            for suffix in members[0]:
+                tensors = [weights.pop(keys[suffix]) for keys in members]
+                weights[_key(module, self.into, suffix)] = _arrange(tensors, self.arrange)
+                del tensors
+
+
+@dataclass(frozen=True)
+class Stack:
+    scope: str
+    into: str = "switch_mlp"
+
+    def __call__(self, weights: Weights) -> None:
+        pattern = re.compile(rf"^(?P<owner>(?:.*\.)?(?:{self.scope}))\.experts\.(?P<index>\d+)$")
+        groups: dict[tuple[str, str, str], dict[int, str]] = defaultdict(dict)
+        for key in list(weights):
+            module, leaf, suffix = _parse(key)
+            found = pattern.match(module)
+            if found:
+                groups[(found["owner"], leaf, suffix)][int(found["index"])] = key
+        for (owner, leaf, suffix), members in sorted(groups.items()):
+            count = max(members) + 1
+            if len(members) != count:
+                raise ValueError(f"{owner}.experts: {leaf}.{suffix} is missing for experts "
+                                 f"{sorted(set(range(count)) - set(members))}")
+            tensors = [weights.pop(members[index]) for index in range(count)]
+            weights[_key(f"{owner}.{self.into}", leaf, suffix)] = torch.stack(tensors).contiguous()
+            del tensors
+
+
+@dataclass(frozen=True)
+class Halves:
+    scope: str
+    fused: str = "gate_up_proj"
+    down: str = "down_proj"
+    source: str = "experts"
+    into: str = "switch_mlp"
+    names: tuple[str, str] = ("gate_proj", "up_proj")
+
+    def __call__(self, weights: Weights) -> None:
+        scope = _scope(self.scope)
+        owners = sorted({module for module, leaf, _ in map(_parse, weights)
+                         if leaf == self.source and scope.search(module)})
+        for owner in owners:
+            fused = weights.pop(f"{owner}.{self.source}.{self.fused}", None)
+            if fused is None:
+                continue
+            middle = fused.shape[-1] // 2
+            for name, half in zip(self.names, (fused[..., :middle], fused[..., middle:])):
+                weights[f"{owner}.{self.into}.{name}.weight"] = half.transpose(-2, -1).contiguous()
+            del fused
+            down = weights.pop(f"{owner}.{self.source}.{self.down}")
+            weights[f"{owner}.{self.into}.{self.down}.weight"] = down.transpose(-2, -1).contiguous()
+
+
+@dataclass(frozen=True)
+class Shift:
+    pattern: str
+    by: float = 1.0
+
+    def __call__(self, weights: Weights) -> None:
+        pattern = re.compile(self.pattern)
+        for key in [key for key in weights if pattern.search(key)]:
+            weights[key] = weights[key] + self.by
+
+
+@dataclass(frozen=True)
+class Drop:
+    pattern: str
+
+    def __call__(self, weights: Weights) -> None:
+        pattern = re.compile(self.pattern)
+        for key in [key for key in weights if pattern.search(key)]:
+            del weights[key]
+
+
+FOLD_NORMS = Shift(r"(?:layernorm|q_norm|k_norm)\.weight$|^model\.norm\.weight$")
+TIED_HEAD = Drop(r"^lm_head\.(?:weight|scales|biases)$")
+
+LAYOUTS: dict[str, tuple[Rule, ...]] = {
+    # omnia_qk_norm_rope / omnia_rope_epilogue read q, k, v as one projection.
+    "qkv": (Join("self_attn", ("q_proj", "k_proj", "v_proj"), "qkv_proj"),),
+    # omnia_dense_gate_up_swiglu: gate rows, then up rows, one matrix.
+    "dense_gate_up": (Join("mlp", ("gate_proj", "up_proj"), "gate_up_proj"),),
+    # omnia_moe_gate_up (layout="blocked"): experts stacked, each gate||up on axis 1.
+    "moe_blocked": (Stack("mlp"), Join("switch_mlp", ("gate_proj", "up_proj"), "gate_up_proj", "blocked")),
+    # The Core SwitchGLU order: experts stacked, gate and up rows alternating.
+    "moe_interleaved": (Stack("mlp"), Join("switch_mlp", ("gate_proj", "up_proj"), "gate_up_proj",
+                                           "interleaved")),
+    # Experts stored pre-stacked with gate and up as halves of one [E, in, 2 * inner].
+    "moe_halves": (Halves("mlp"), Join("switch_mlp", ("gate_proj", "up_proj"), "gate_up_proj", "blocked")),
+    "fold_norms": (FOLD_NORMS,),
+}
+
+
+def apply(weights: Weights, rules: Sequence[Rule]) -> Weights:
+    """Runs the rules in order over `weights` (changed in place, and returned)."""
+    for rule in rules:
+        rule(weights)
+    return weights
+
+
+def prepare(weights: Weights, rules: Sequence[Rule], *, dtype: torch.dtype | None = None,
+            tie_word_embeddings: bool = False) -> Weights:
+    """Casts (not a quantised checkpoint: its packed words are not numbers of a dtype),
+    drops a tied head, then applies `rules`."""
+    if dtype is not None:
+        if any(key.endswith(".scales") for key in weights):
+            raise ValueError("a quantised checkpoint (it carries .scales) cannot be cast to "
+                             f"{dtype}")
+        weights = {key: value.to(dtype) for key, value in weights.items()}
+    if tie_word_embeddings:
+        TIED_HEAD(weights)
+    return apply(weights, rules)
+
+
+def read_checkpoint(directory: Path | str, device: torch.device | str | None = None) -> Weights:
+    """Every `model*.safetensors` shard of `directory`, merged, on `device` (the CPU when
+    None)."""
     from safetensors.torch import load_file
 
-    weights: Weights = {}
     shards = sorted(Path(directory).glob("model*.safetensors"))
     if not shards:
         raise FileNotFoundError(f"no model*.safetensors under {directory}")
-    target = "cpu" if device is None else str(device)
+    weights: Weights = {}
     for shard in shards:
-        weights.update(load_file(str(shard), device=target))
-    return weights
-
-
-def fusible(weights: Mapping[str, torch.Tensor], keys: Sequence[str]) -> bool:
-    """Whether leaves sharing an input carry one format, read off the tensors: the same
-    trailing shape and dtype for all of them, or none of them present."""
-    present = [key for key in keys if key in weights]
-    if not present:
-        return True
-    if len(present) != len(keys):
-        return False
-    return len({(tuple(weights[key].shape[1:]), weights[key].dtype) for key in present}) == 1
-
-
-def _cat(parts: Iterable[torch.Tensor], dim: int = 0) -> torch.Tensor:
-    return torch.cat(list(parts), dim=dim).contiguous()
-
-
-def fuse_qkv(weights: Weights, layers: int) -> Weights:
-    for layer in range(layers):
-        prefix = f"model.layers.{layer}.self_attn."
-        if not all(f"{prefix}{name}_proj.weight" in weights for name in QKV):
-            continue
-        same = all(fusible(weights, [f"{prefix}{name}_proj.{suffix}" for name in QKV])
-                   for suffix in QKV_SUFFIXES)
-        if not same:
-            for name in QKV:
-                for suffix in QKV_SUFFIXES:
-                    key = f"{prefix}{name}_proj.{suffix}"
-                    if key in weights:
-                        weights[f"{prefix}qkv_proj.{name}_proj.{suffix}"] = weights.pop(key)
-            continue
-        for suffix in QKV_SUFFIXES:
-            keys = [f"{prefix}{name}_proj.{suffix}" for name in QKV]
-            if all(key in weights for key in keys):
-                weights[f"{prefix}qkv_proj.{suffix}"] = _cat(weights.pop(key) for key in keys)
-    return weights
-
-
-def concat_gate_up(weights: Weights, layers: int, *, prefix: str = "mlp") -> Weights:
-    for layer in range(layers):
-        leaf = f"model.layers.{layer}.{prefix}."
-        for suffix in FORMAT_SUFFIXES:
-            keys = [f"{leaf}{name}_proj.{suffix}" for name in ("gate", "up")]
-            if all(key in weights for key in keys):
-                weights[f"{leaf}gate_up_proj.{suffix}"] = _cat(weights.pop(key) for key in keys)
-    return weights
-
-
-def stack_experts(weights: Weights, layers: int, experts: int, *, prefix: str = "mlp") -> Weights:
-    for layer in range(layers):
-        source = f"model.layers.{layer}.{prefix}.experts."
-        target = f"model.layers.{layer}.{prefix}.switch_mlp."
-        for name in ("gate_proj", "up_proj", "down_proj"):
-            for suffix in FORMAT_SUFFIXES:
-                if f"{source}0.{name}.{suffix}" not in weights:
-                    continue
-                parts = [weights.pop(f"{source}{expert}.{name}.{suffix}") for expert in range(experts)]
-                weights[f"{target}{name}.{suffix}"] = torch.stack(parts).contiguous()
-                del parts
-    return weights
-
-
-def block_gate_up(weights: Weights, layers: int, *, prefix: str = "mlp") -> Weights:
-    """`switch_mlp.{gate,up}_proj` [E, inner, in] -> `switch_mlp.gate_up_proj`
-    [E, 2 * inner, in]: each expert's gate rows, then its up rows."""
-    for layer in range(layers):
-        leaf = f"model.layers.{layer}.{prefix}.switch_mlp."
-        for suffix in FORMAT_SUFFIXES:
-            keys = [f"{leaf}{name}_proj.{suffix}" for name in ("gate", "up")]
-            if all(key in weights for key in keys):
-                weights[f"{leaf}gate_up_proj.{suffix}"] = _cat((weights.pop(key) for key in keys), dim=1)
-    return weights
-
-
-def interleave_gate_up(weights: Weights, layers: int, *, prefix: str = "mlp") -> Weights:
-    """[E, inner, in] gate and up -> [E, 2 * inner, in] rows g0, u0, g1, u1, ..."""
-    for layer in range(layers):
-        leaf = f"model.layers.{layer}.{prefix}.switch_mlp."
-        for suffix in FORMAT_SUFFIXES:
-            keys = [f"{leaf}{name}_proj.{suffix}" for name in ("gate", "up")]
-            if not all(key in weights for key in keys):
-                continue
-            parts = [weights.pop(key) for key in keys]
-            experts, rows, cols = parts[0].shape
-            weights[f"{leaf}gate_up_proj.{suffix}"] = torch.stack(parts, dim=2).reshape(
-                experts, 2 * rows, cols).contiguous()
-    return weights
-
-
-def split_stacked_gate_up(weights: Weights, layers: int) -> Weights:
-    """`experts.gate_up_proj` [E, in, 2 * inner] (gate and up in halves) and
-    `experts.down_proj` [E, inner, in] -> `switch_mlp.*` in the [E, out, in] layout."""
-    for layer in range(layers):
-        source = f"model.layers.{layer}.mlp.experts."
-        target = f"model.layers.{layer}.mlp.switch_mlp."
-        fused = weights.pop(f"{source}gate_up_proj", None)
-        if fused is None:
-            continue
-        middle = fused.shape[-1] // 2
-        weights[f"{target}gate_proj.weight"] = fused[..., :middle].transpose(-2, -1).contiguous()
-        weights[f"{target}up_proj.weight"] = fused[..., middle:].transpose(-2, -1).contiguous()
-        del fused
-        weights[f"{target}down_proj.weight"] = weights.pop(f"{source}down_proj").transpose(-2, -1).contiguous()
-    return weights
-
-
-def fold_norm_scales(weights: Weights) -> Weights:
-    """Norm weights stored centred on zero (`scale = 1 + w`) folded to plain gains."""
-    for key, value in weights.items():
-        if key.endswith(("layernorm.weight", "q_norm.weight", "k_norm.weight")) or key == "model.norm.weight":
-            weights[key] = value + 1
-    return weights
-
-
-def drop_tied_head(weights: Weights) -> None:
-    """Tied checkpoints still serialise lm_head; it is dropped."""
-    for suffix in FORMAT_SUFFIXES:
-        weights.pop(f"lm_head.{suffix}", None)
-
-
-def reject_dtype_cast(dtype: torch.dtype | None, weights: Mapping[str, torch.Tensor]) -> None:
-    """A quantised checkpoint (it carries `.scales`) cannot be cast to a float dtype."""
-    if dtype is not None and any(key.endswith(".scales") for key in weights):
-        raise ValueError("dtype= cannot be applied to a quantized checkpoint")
-
-
-def prepare_weights(weights: Weights, fusions: Sequence[Fusion], *, dtype: torch.dtype | None = None,
-                    tie_word_embeddings: bool = False) -> Weights:
-    """Reject a cast over packed tensors, cast, drop the tied head, fuse in order."""
-    reject_dtype_cast(dtype, weights)
-    if dtype is not None:
-        weights = {key: value.to(dtype) for key, value in weights.items()}
-    if tie_word_embeddings:
-        drop_tied_head(weights)
-    for fuse in fusions:
-        weights = fuse(weights)
+        weights.update(load_file(str(shard), device="cpu" if device is None else str(device)))
     return weights

@@ -24,9 +24,10 @@ pytestmark = pytest.mark.gpu
 def test_device_load_fuse_and_run(tmp_path):
     print("checkpoint: load to cuda, fuse, run dense MLP and routed experts", flush=True)
     source = {k: bits_of(v) for k, v in make(tmp_path / "ckpt").items()}
-    weights = ckpt.load_shards(tmp_path / "ckpt", device="cuda")
+    weights = ckpt.read_checkpoint(tmp_path / "ckpt", device="cuda")
     assert all(t.device.type == "cuda" for t in weights.values())
-    weights = ckpt.block_gate_up(ckpt.stack_experts(ckpt.concat_gate_up(ckpt.fuse_qkv(weights, 2), 2), 2, EXPERTS), 2)
+    layouts = ckpt.LAYOUTS
+    weights = ckpt.apply(weights, layouts["qkv"] + layouts["dense_gate_up"] + layouts["moe_blocked"])
     fused = weights["model.layers.0.mlp.gate_up_proj.weight"]
     assert fused.is_contiguous() and fused.data_ptr() % 16 == 0
 
