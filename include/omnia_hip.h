@@ -48,6 +48,18 @@ const char* omnia_last_error(void);
 int32_t omnia_rope_angle_atlas(const double* frequencies, int64_t pairs, int64_t first,
                                int64_t rows, float* atlas, int64_t stride, hipStream_t stream);
 
+/* The same atlas in the fp32 order of the reference's builder:
+ *   theta[r, i] = fp32(fp32(first + r) / inverse_frequencies[i]),
+ *   atlas[r, i] = fp32(cos(theta)), atlas[r, pairs + i] = fp32(sin(theta)),
+ * every operation correctly rounded (quotient formed in fp64 and rounded once; cos and
+ * sin of the fp32 angle evaluated in fp64 and rounded once). inverse_frequencies [pairs]
+ * fp32: base ** (2i / D) as fp32 operations (or a YaRN table). Limits as above.
+ * Replaces: models/laguna/layers/attention.py:236-243 (`_angle_atlas`: theta =
+ * arange(rows, fp32) / inverse, then cos, sin and a concatenate), one launch. */
+int32_t omnia_rope_angle_atlas_fp32(const float* inverse_frequencies, int64_t pairs,
+                                    int64_t first, int64_t rows, float* atlas, int64_t stride,
+                                    hipStream_t stream);
+
 /* Residual add + RMSNorm over `rows` rows of `hidden` bf16 values.
  *   summed[r]     = bf16(x[r] + branch[r])
  *   normalized[r] = bf16(weight * bf16(summed[r] * rsqrt(mean(summed[r]^2) + eps)))

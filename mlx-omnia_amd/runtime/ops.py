@@ -66,6 +66,22 @@ def rope_angle_atlas(frequencies: torch.Tensor, first: int, rows: int, *,
     return out
 
 
+def rope_angle_atlas_fp32(inverse_frequencies: torch.Tensor, first: int, rows: int, *,
+                          out: torch.Tensor | None = None) -> torch.Tensor:
+    """Atlas rows [rows, 2 * pairs] fp32 (cos || sin) in the fp32 order: theta =
+    fp32(position) / inverse, from fp32 inverse frequencies [pairs] on the device; see
+    `omnia_rope_angle_atlas_fp32`."""
+    _dense(inverse_frequencies, F32, "inverse_frequencies")
+    pairs = inverse_frequencies.numel()
+    out = _out(out, inverse_frequencies, (rows, 2 * pairs), F32, "atlas")
+    _require(out.dim() == 2 and out.stride(-1) == 1 and out.shape == (rows, 2 * pairs),
+             "rope_angle_atlas: out must be [rows, 2 * pairs] with unit column stride")
+    _require(on_rocm(inverse_frequencies, out), "rope_angle_atlas: tensors must share one ROCm device")
+    call("omnia_rope_angle_atlas_fp32", inverse_frequencies.data_ptr(), pairs, int(first), int(rows),
+         out.data_ptr(), out.stride(0), _stream(inverse_frequencies))
+    return out
+
+
 def add_rms_norm(
     x: torch.Tensor,
     branch: torch.Tensor,

@@ -38,6 +38,27 @@ def angle_table(rows: int, pairs: int, base: float, first: int = 0):
     return np.cos(theta).astype(np.float32), np.sin(theta).astype(np.float32)
 
 
+def laguna_inverse(pairs: int, base: float) -> np.ndarray:
+    """`base ** (arange(0, D, 2, fp32) / D)` of models/laguna/layers/attention.py:238-239 as
+    fp32 operations, each correctly rounded (the power evaluated in float64 from the fp32
+    operands and rounded once)."""
+    exponents = np.arange(0, 2 * pairs, 2, dtype=np.float32) / np.float32(2 * pairs)
+    return np.power(np.float64(np.float32(base)), exponents.astype(np.float64)).astype(np.float32)
+
+
+def laguna_angle_table(rows: int, pairs: int, base: float | None = None, first: int = 0,
+                       inverse: np.ndarray | None = None):
+    """(cos, sin) float32 [rows, pairs] in the fp32 order of models/laguna/layers/
+    attention.py:236-243: theta = arange(fp32) / inverse as an fp32 quotient (formed in
+    float64 and rounded once), cos and sin of that fp32 angle in float64, rounded once.
+    `inverse` is the YaRN table when given (used as is), else `laguna_inverse`."""
+    inverse = laguna_inverse(pairs, base) if inverse is None else np.asarray(inverse, np.float32)
+    positions = np.arange(first, first + rows, dtype=np.float64).astype(np.float32)
+    theta = (positions.astype(np.float64)[:, None] / inverse.astype(np.float64)[None, :]).astype(np.float32)
+    wide = theta.astype(np.float64)
+    return np.cos(wide).astype(np.float32), np.sin(wide).astype(np.float32)
+
+
 def epilogue_angles(positions: np.ndarray, pairs: int, base: float):
     """(cos, sin) float32 [len(positions), pairs] by the in-kernel derivation of
     core/kernels/qkv_rope/epilogue.py:57-63."""

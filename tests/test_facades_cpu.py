@@ -100,6 +100,23 @@ def test_angle_atlas_on_cpu_matches_oracle_and_grows():
         AngleAtlas(64)
 
 
+def test_angle_atlas_fp32_order_on_cpu_matches_oracle():
+    """Laguna's fp32 op order (models/laguna/layers/attention.py:236-243), on the CPU."""
+    from mlx_omnia_amd.kernels.qkv_rope import AngleAtlas
+    from mlx_omnia_amd.kernels.qkv_rope.atlas import rope_inverse_fp32
+
+    assert np.array_equal(rope_inverse_fp32(64, 1e6), oracle_rope.laguna_inverse(64, 1e6))
+    atlas = AngleAtlas(64, base=1e6, rows=300, arithmetic="fp32")
+    atlas.ensure(40000)
+    cos, sin = oracle_rope.laguna_angle_table(atlas.rows, 64, 1e6)
+    got = atlas.atlas.numpy()
+    ulp = np.spacing(np.float32(1.0))
+    assert np.abs(got[:, :64] - cos).max() <= ulp and np.abs(got[:, 64:] - sin).max() <= ulp
+    assert np.mean(got[:, :64] == cos) > 0.9999
+    with pytest.raises(ValueError):
+        AngleAtlas(64, base=1e6, arithmetic="fp16")
+
+
 def test_angle_table_contract_and_atlas_view():
     cos, sin = oracle_rope.angle_table(32, 8, 1e4)
     atlas = torch.from_numpy(np.concatenate([cos, sin], axis=-1))

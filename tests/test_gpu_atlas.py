@@ -44,6 +44,27 @@ def test_growth_keeps_old_rows_and_matches_oracle():
     assert rows.shape == (3, 64) and atlas.rows >= 6003
 
 
+def test_fp32_order_bit_equal_to_oracle_and_grows():
+    """Laguna's fp32 op order (models/laguna/layers/attention.py:236-243) at the config's
+    40,960 x 64, then grown past its last row (old rows kept), and a YaRN inverse row."""
+    print("atlas fp32 order 40960 x 64 theta 1e6", flush=True)
+    atlas = AngleAtlas(64, base=1e6, rows=40960, device="cuda", arithmetic="fp32")
+    cos, sin = rope.laguna_angle_table(40960, 64, 1e6)
+    got = atlas.atlas.cpu().numpy()
+    assert np.array_equal(got[:, :64], cos) and np.array_equal(got[:, 64:], sin)
+    kept = atlas.atlas.clone()
+    atlas.ensure(70000)
+    assert torch.equal(atlas.atlas[:40960], kept)
+    cos, sin = rope.laguna_angle_table(atlas.rows, 64, 1e6)
+    got = atlas.atlas.cpu().numpy()
+    assert np.array_equal(got[:, :64], cos) and np.array_equal(got[:, 64:], sin)
+    freqs = (1e4 ** (np.arange(0, 64, 2) / 64) * np.linspace(1.0, 8.0, 32)).astype(np.float32)
+    yarn = AngleAtlas(32, inverse_frequencies=freqs, rows=4096, device="cuda", arithmetic="fp32")
+    cos, sin = rope.laguna_angle_table(4096, 32, inverse=freqs)
+    got = yarn.atlas.cpu().numpy()
+    assert np.array_equal(got[:, :32], cos) and np.array_equal(got[:, 32:], sin)
+
+
 def test_yarn_frequencies():
     pairs = 32
     freqs = 1e4 ** (np.arange(0, 2 * pairs, 2) / (2 * pairs)) * np.linspace(1.0, 8.0, pairs)

@@ -164,3 +164,55 @@ def test_planted_mistakes_fail_the_complex_check(kind):
     out = _planted(kind)(raw, weight, cos[20:29], sin[20:29], EPS, 64)
     want = _complex_reference(raw, weight, cos[20:29], sin[20:29], 64)
     assert ulp_distance(out, want).max() > 2
+
+
+# ---- the atlas in Laguna's fp32 order ---------------------------------------------------
+
+
+def test_laguna_inverse_row_against_fp32_libraries():
+    """The fp32 power against torch's and numpy's own fp32 power (each within an ulp of
+    the correctly rounded value), and the exponent against a brute-force fraction."""
+    for pairs, base in ((64, 1e6), (32, 10000.0), (16, 500000.0)):
+        got = rope.laguna_inverse(pairs, base)
+        torch_row = torch.pow(torch.tensor(base, dtype=torch.float32),
+                              torch.arange(0, 2 * pairs, 2, dtype=torch.float32) / (2 * pairs)).numpy()
+        numpy_row = np.power(np.float32(base), np.arange(0, 2 * pairs, 2, dtype=np.float32) / np.float32(2 * pairs))
+        for other in (torch_row, numpy_row):
+            gap = np.abs(got.view(np.int32).astype(np.int64) - other.astype(np.float32).view(np.int32))
+            assert gap.max() <= 1
+        assert got[0] == 1.0
+        assert abs(float(got[-1]) / base ** ((2 * pairs - 2) / (2 * pairs)) - 1.0) < 2 ** -23
+
+
+def test_laguna_angles_are_fp32_quotients():
+    """theta equals numpy's own fp32 division (IEEE, correctly rounded), which pins the
+    float64-then-round formation; column 0 (inverse 1) is the plain fp64 table's."""
+    rows, pairs, base = 40960, 64, 1e6
+    inverse = rope.laguna_inverse(pairs, base)
+    cos, sin = rope.laguna_angle_table(rows, pairs, base)
+    positions = np.arange(rows, dtype=np.float32)
+    theta = positions[:, None] / inverse[None, :]
+    assert theta.dtype == np.float32
+    np.testing.assert_array_equal(cos, np.cos(theta.astype(np.float64)).astype(np.float32))
+    np.testing.assert_array_equal(sin, np.sin(theta.astype(np.float64)).astype(np.float32))
+    cos64, sin64 = rope.angle_table(rows, pairs, base)
+    assert np.array_equal(cos[:, 0], cos64[:, 0]) and np.array_equal(sin[:, 0], sin64[:, 0])
+    assert (cos[0] == 1.0).all() and (sin[0] == 0.0).all()
+    # against numpy's float32 cos and sin, a different evaluation: within 2 fp32 ulps
+    gap = np.abs(np.cos(theta).view(np.int32).astype(np.int64) - cos.view(np.int32))
+    assert np.percentile(gap, 99.9) <= 2
+
+
+def test_fp32_and_fp64_atlases_differ_by_the_angle_rounding():
+    """The two arithmetics at the config's 40,960 x 64, base 1e6: they agree at small
+    positions and part by up to half an fp32 ulp of theta (about 4e-3 rad near 40,960)."""
+    cos32, sin32 = rope.laguna_angle_table(40960, 64, 1e6)
+    cos64, sin64 = rope.angle_table(40960, 64, 1e6)
+    dcos, dsin = np.abs(cos32 - cos64), np.abs(sin32 - sin64)
+    print(f"max |dcos| {dcos.max():.3e} max |dsin| {dsin.max():.3e}; "
+          f"rows < 4096: {dcos[:4096].max():.3e} {dsin[:4096].max():.3e}")
+    assert 1e-3 < max(dcos.max(), dsin.max()) < 5e-3
+    assert max(dcos[:256].max(), dsin[:256].max()) < 2e-5
+    # the bound: half an ulp of the largest angle plus the inverse row's own rounding
+    theta_max = 40959.0
+    assert max(dcos.max(), dsin.max()) <= theta_max * 2.0 ** -24 * 2 + 1e-6
