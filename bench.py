@@ -29,8 +29,14 @@ baseline, and `kernels`: name -> [us, fraction of peak, CPU oracle GB/s] for eve
 workload), and the full record (each workload's description, rotation copies, launch
 mode, CPU sample, threads used and thread environment) in the `--results` file.
 
+The headline also carries `roofline.copy_us`: the calibration copy (`omnia_stream_copy`,
+16-byte nontemporal loads and stores, the best of 1, 2 and 4 vectors per thread) of the
+same bytes, timed in the same run, the practical ceiling at that size. `--ceiling` adds
+that copy and torch's `copy_` beside every workload.
+
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--only NAME[,NAME]]
-                       [--results bench_results.json]
+                       [--results bench_results.json] [--ceiling]
+       python bench.py --copy-sweep     (the calibration copy from 32 MB to 1.2 GB moved)
        python bench.py --phase-clocks [--phase-clocks-rows 4096,512]
                                         (the fused router's per-phase wall clocks)
 """
@@ -289,6 +295,27 @@ def workloads() -> list[Workload]:
             normalized=a["n"], indices=a["idx"], weights=a["wts"]),
     ))
 
+    # configs[4] with the bf16 logits written as well (BASELINE.md prices them at +1 MiB):
+    # every logit made exact, the unsure ones recomputed in fp64 by their token's wave.
+    def setup_router_logits(device, copies):
+        sets = setup_router(device, copies)
+        for entry in sets:
+            entry["l"] = torch.empty((4096, 128), dtype=torch.bfloat16, device=device)
+        return sets
+
+    out.append(Workload(
+        name="residual_rms_router_logits",
+        kernel="residual_rms_router_split_kernel",
+        description="configs[4]'s fused router writing its bf16 logits [4096, 128] too (every "
+                    "logit the correctly rounded dot product)",
+        bytes_per_launch=4 * 4096 * 2048 * 2 + 2048 * 2 + 128 * 2048 * 2 + 128 * 4
+        + 2 * 4096 * 8 * 4 + 4096 * 128 * 2,
+        setup=setup_router_logits,
+        launch=lambda a: ops.residual_rms_router(
+            a["x"], a["r"], a["w"], a["gate"], k=8, eps=1e-6, summed=a["s"],
+            normalized=a["n"], logits=a["l"], indices=a["idx"], weights=a["wts"]),
+    ))
+
     # configs[4]'s step at Qwen3-235B-A22B's width (hidden 4096, 128 experts, top-8): the
     # fused router's other kernel (phases one after another). Run when named by --only.
     out.append(Workload(
@@ -373,6 +400,27 @@ def workloads() -> list[Workload]:
         launch=lambda a: ops.residual_rms_router_sigmoid(
             a["x"], a["r"], a["w"], a["gate"], a["bias"], k=8, eps=1e-6, emit_logits=False,
             emit_keys=False, select=True, summed=a["s"], normalized=a["n"], indices=a["idx"],
+            weights=a["wts"]),
+    ))
+
+    def setup_router_sigmoid_keys(device, copies):
+        sets = setup_router_sigmoid(device, copies)
+        for entry in sets:
+            entry["l"] = torch.empty((4096, 128), dtype=torch.bfloat16, device=device)
+            entry["k"] = torch.empty((4096, 128), dtype=torch.uint32, device=device)
+        return sets
+
+    out.append(Workload(
+        name="residual_rms_router_sigmoid_keys",
+        kernel="residual_rms_router_split_kernel",
+        description="the sigmoid form writing the reference's outputs too: bf16 logits and uint32 "
+                    "ordinal keys [4096, 128], with the top-8 selection",
+        bytes_per_launch=4 * 4096 * 2048 * 2 + 2048 * 2 + 128 * 2048 * 2 + 128 * 4 + 128 * 4
+        + 2 * 4096 * 8 * 4 + 4096 * 128 * (2 + 4),
+        setup=setup_router_sigmoid_keys,
+        launch=lambda a: ops.residual_rms_router_sigmoid(
+            a["x"], a["r"], a["w"], a["gate"], a["bias"], k=8, eps=1e-6, select=True,
+            summed=a["s"], normalized=a["n"], logits=a["l"], keys=a["k"], indices=a["idx"],
             weights=a["wts"]),
     ))
 
@@ -870,6 +918,16 @@ def workloads() -> list[Workload]:
 
     out.append(Workload(
         name="copy_calibration",
+        kernel="stream_copy_kernel",
+        description="omnia_stream_copy of 128 MiB (one 16-byte vector per thread): 128 MiB read "
+                    "+ 128 MiB written",
+        bytes_per_launch=2 * 64 * 2**20 * 2,
+        setup=setup_copy,
+        launch=lambda a: ops.stream_copy(a["src"], a["dst"]),
+        default=False,
+    ))
+    out.append(Workload(
+        name="copy_calibration_torch",
         kernel="copy",
         description="torch copy_ of 128 MiB bf16 (64 Mi elements): 128 MiB read + 128 MiB written",
         bytes_per_launch=2 * 64 * 2**20 * 2,
@@ -880,10 +938,14 @@ def workloads() -> list[Workload]:
     return out
 
 
-def copy_ceiling(moved: int) -> Workload:
-    """A plain device-to-device copy (torch `copy_`) that reads and writes `moved` / 2 bytes:
-    what the same HBM traffic costs with no arithmetic, the practical ceiling at that size."""
+def copy_ceiling(moved: int, kind: str = "stream", vectors: int = 1) -> Workload:
+    """A plain device-to-device copy that reads and writes `moved` / 2 bytes: what the same
+    HBM traffic costs with no arithmetic, the practical ceiling at that size. `kind`
+    "stream" is the calibration copy `omnia_stream_copy` (`vectors` 16-byte vectors per
+    thread), "torch" is torch's `copy_`."""
     import torch
+
+    from mlx_omnia_amd.runtime import ops
 
     elements = max(8, (moved // 2) // 2 // 8 * 8)
 
@@ -892,11 +954,30 @@ def copy_ceiling(moved: int) -> Workload:
                      dst=torch.empty(elements, dtype=torch.bfloat16, device=device))
         return _copies(first, copies)
 
+    if kind == "torch":
+        return Workload(
+            name="copy_ceiling_torch", kernel="copy",
+            description=f"torch copy_ of {elements * 2} bytes ({elements * 4} bytes moved)",
+            bytes_per_launch=elements * 4, setup=setup,
+            launch=lambda a: a["dst"].copy_(a["src"]), default=False)
     return Workload(
-        name="copy_ceiling", kernel="copy",
-        description=f"torch copy_ of {elements * 2} bytes ({elements * 4} bytes moved)",
+        name=f"copy_ceiling_stream{vectors}", kernel="stream_copy_kernel",
+        description=f"omnia_stream_copy of {elements * 2} bytes ({elements * 4} bytes moved), "
+                    f"{vectors} vector(s) per thread",
         bytes_per_launch=elements * 4, setup=setup,
-        launch=lambda a: a["dst"].copy_(a["src"]), default=False)
+        launch=lambda a: ops.stream_copy(a["src"], a["dst"], vectors_per_thread=vectors),
+        default=False)
+
+
+def best_copy(moved: int, steps: int, warmup: int, device) -> dict:
+    """The calibration copy of `moved` bytes at 1, 2 and 4 vectors per thread; the fastest."""
+    runs = [time_workload(copy_ceiling(moved, "stream", v), steps, warmup, device, False)
+            for v in (1, 2, 4)]
+    best = min(runs, key=lambda r: r["us"])
+    return dict(best, vectors=(1, 2, 4)[runs.index(best)], all_us=[r["us"] for r in runs])
+
+
+COPY_SWEEP_BYTES = (32 * 10**6, 85_983_744, 169_934_848, 320 * 10**6, 640 * 10**6, 1_200 * 10**6)
 
 
 def _bound_launch(w: Workload, argset):
@@ -1074,12 +1155,13 @@ def _cpu_legs() -> dict:
         return (lambda: (run_swiglu(), run_softplus()), swiglu_bytes + softplus_bytes,
                 "64 of 8192 SwiGLU rows and the whole [8192, 32] gate", False)
 
-    def router_leg():
+    def router_leg(logits=False):
+        # The oracle's chain forms every logit exactly either way; written, they add bytes.
         x, r, w = bf((256, 2048)), bf((256, 2048)), bf((2048,), 0.1, 1.0)
         gate = bf((128, 2048), 0.02)
         return (lambda: route.residual_rms_router(x, r, w, gate, 1e-6, 8),
-                256 * (4 * 2048 * 2 + 2 * 8 * 4) + 2048 * 2 + 128 * 2048 * 2,
-                "256 of 4096 tokens", True)
+                256 * (4 * 2048 * 2 + 2 * 8 * 4 + (128 * 2 if logits else 0)) + 2048 * 2
+                + 128 * 2048 * 2, "256 of 4096 tokens", True)
 
     def route_leg(sigmoid):
         logits = bf((4096, 128))
@@ -1096,13 +1178,13 @@ def _cpu_legs() -> dict:
         return (lambda: route.softmax_topk_slots(logits, 8, normalize=False, shared=True),
                 4096 * 129 * 2 + 2 * 4096 * 9 * 4, "[4096, 129], whole", False)
 
-    def router_sigmoid_leg():
+    def router_sigmoid_leg(keys=False):
         x, r, w = bf((256, 2048)), bf((256, 2048)), bf((2048,), 0.1, 1.0)
         gate = bf((128, 2048), 0.02)
         bias = (0.5 * rng.standard_normal(128)).astype(np.float32)
         return (lambda: route.residual_rms_router_sigmoid(x, r, w, gate, bias, 1e-6, 8),
-                256 * (4 * 2048 * 2 + 2 * 8 * 4) + 2048 * 2 + 128 * 2048 * 2 + 2 * 128 * 4,
-                "256 of 4096 tokens", True)
+                256 * (4 * 2048 * 2 + 2 * 8 * 4 + (128 * 6 if keys else 0)) + 2048 * 2
+                + 128 * 2048 * 2 + 2 * 128 * 4, "256 of 4096 tokens", True)
 
     def router_one_leg(sigmoid):
         x, r, w = bf((1, 2048)), bf((1, 2048)), bf((2048,), 0.1, 1.0)
@@ -1245,10 +1327,12 @@ def _cpu_legs() -> dict:
         "gate_softplus": softplus_leg,
         "gated_activations": gated_leg,
         "residual_rms_router": router_leg,
+        "residual_rms_router_logits": lambda: router_leg(logits=True),
         "softmax_topk": lambda: route_leg(False),
         "softmax_topk_shared": route_shared_leg,
         "sigmoid_topk": lambda: route_leg(True),
         "residual_rms_router_sigmoid": router_sigmoid_leg,
+        "residual_rms_router_sigmoid_keys": lambda: router_sigmoid_leg(keys=True),
         "residual_rms_router_decode": lambda: router_one_leg(False),
         "residual_rms_router_sigmoid_decode": lambda: router_one_leg(True),
         "rope_angle_atlas": atlas_leg,
@@ -1316,7 +1400,8 @@ PHASES = ("entry", "row 0 done", "phase 1 done", "tile complete", "walk done",
           "logits complete", "selection + tasks", "task list complete", "recomputed", "written")
 
 
-def router_phase_clocks(device, rows: int = 4096, stamped: int = 8, timed: int = 200) -> dict:
+def router_phase_clocks(device, rows: int = 4096, stamped: int = 8, timed: int = 200,
+                        logits: bool = False) -> dict:
     """Per-phase wall clocks of the fused residual router at configs[4] ([4096, 2048],
     128 experts, k = 8), or the same at fewer `rows` (a multiple of 16: one workgroup per
     16 tokens, so fewer workgroups share the chip), from `libomnia_router_clocks.so` (the
@@ -1324,7 +1409,8 @@ def router_phase_clocks(device, rows: int = 4096, stamped: int = 8, timed: int =
     rotation's steady state, records the 100 MHz wall clock of every wave at ten phase
     boundaries; the summary is each boundary's spread over the workgroups (median over
     launches of each statistic), in µs from the launch's earliest entry. `launch_us` is
-    the event-timed mean of `timed` back-to-back launches of the diagnostic build."""
+    the event-timed mean of `timed` back-to-back launches of the diagnostic build. With
+    `logits` the launch also writes the bf16 logits (every logit exact)."""
     import ctypes
 
     import torch
@@ -1355,7 +1441,9 @@ def router_phase_clocks(device, rows: int = 4096, stamped: int = 8, timed: int =
     gate = _to_bf16_device(_normal(rng, (experts, hidden), 0.02), device)
     outs = [dict(s=torch.empty_like(xs[0]), n=torch.empty_like(xs[0]),
                  i=torch.empty((rows, k), dtype=torch.int32, device=device),
-                 w=torch.empty((rows, k), dtype=torch.float32, device=device)) for _ in range(copies)]
+                 w=torch.empty((rows, k), dtype=torch.float32, device=device),
+                 l=torch.empty((rows, experts), dtype=torch.bfloat16, device=device) if logits else None)
+            for _ in range(copies)]
     stream = torch.cuda.current_stream(device)
     handle = ctypes.c_void_p(stream.cuda_stream)
     packed = torch.empty(lib.omnia_router_pack_bytes(experts, hidden), dtype=torch.uint8,
@@ -1368,7 +1456,8 @@ def router_phase_clocks(device, rows: int = 4096, stamped: int = 8, timed: int =
         if lib.omnia_residual_rms_router(xs[c].data_ptr(), rs[c].data_ptr(), w.data_ptr(),
                                          packed.data_ptr(), rows, hidden, experts, k,
                                          ctypes.c_float(1e-6), o["s"].data_ptr(), o["n"].data_ptr(),
-                                         None, o["i"].data_ptr(), o["w"].data_ptr(), handle):
+                                         o["l"].data_ptr() if logits else None, o["i"].data_ptr(),
+                                         o["w"].data_ptr(), handle):
             raise RuntimeError(lib.omnia_last_error().decode())
 
     for i in range(400):
@@ -1410,7 +1499,8 @@ def router_phase_clocks(device, rows: int = 4096, stamped: int = 8, timed: int =
     summary = {name: [round(float(np.median([s[name][q] for s in per_launch])), 2) for q in range(4)]
                for name in PHASES}
     return dict(kernel="residual_rms_router_split_kernel<128>",
-                workload=f"x, residual bf16 [{rows}, 2048], router [128, 2048], k = 8",
+                workload=f"x, residual bf16 [{rows}, 2048], router [128, 2048], k = 8"
+                         + (", logits written" if logits else ""),
                 workgroups=groups,
                 launch_us=round(launch_us, 3), stamped_launches=stamped,
                 columns=["p10", "median", "p90", "max"], unit="us from the launch's first entry",
@@ -1467,6 +1557,7 @@ def bench_line(results: dict, head_name: str, steps: int, warmup: int) -> dict:
             "unit": "GB/s",
             "frac": head["frac"],
             "traffic": _traffic(head_name),
+            "copy_us": head.get("copy_ceiling", {}).get("us"),
         },
         "cpu_baseline": baseline,
         "kernels_fields": ["us", "frac_of_peak", "cpu_oracle_GBps"],
@@ -1483,12 +1574,18 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--graph", action="store_true", help="also time a captured HIP graph")
     parser.add_argument("--ceiling", action="store_true",
-                        help="also time a plain device copy moving each workload's bytes")
+                        help="also time the calibration copy and torch's copy_ moving each "
+                             "workload's bytes")
     parser.add_argument("--phase-clocks", action="store_true",
                         help="print the fused router's per-phase wall clocks (diagnostic "
                              "build) as one JSON line instead of the bench line")
+    parser.add_argument("--copy-sweep", action="store_true",
+                        help="time the calibration copy over a range of sizes (one JSON line "
+                             "each) instead of the bench line")
     parser.add_argument("--results", default="bench_results.json",
                         help="file for the full per-workload record ('' for none)")
+    parser.add_argument("--phase-clocks-logits", action="store_true",
+                        help="--phase-clocks with the logits written (every logit exact)")
     parser.add_argument("--phase-clocks-rows", default="4096",
                         help="comma-separated token counts for --phase-clocks (multiples of 16)")
     args = parser.parse_args()
@@ -1509,7 +1606,15 @@ def main() -> int:
     device = torch.device("cuda:0")
     if args.phase_clocks:
         for rows in (int(n) for n in args.phase_clocks_rows.split(",") if n):
-            print(json.dumps(router_phase_clocks(device, rows)), flush=True)
+            print(json.dumps(router_phase_clocks(device, rows, logits=args.phase_clocks_logits)),
+                  flush=True)
+        return 0
+    if args.copy_sweep:
+        for moved in COPY_SWEEP_BYTES:
+            r = best_copy(moved, args.steps, args.warmup, device)
+            print(json.dumps({"copy_bytes_moved": r["bytes"], "us": r["us"],
+                              "TBps": round(r["GBps"] / 1000.0, 3), "frac": r["frac"],
+                              "vectors": r["vectors"], "us_by_vectors": r["all_us"]}), flush=True)
         return 0
     only = [n for n in args.only.split(",") if n]
     selected = [w for w in workloads() if ((w.name in only) if only else w.default)]
@@ -1523,11 +1628,16 @@ def main() -> int:
         results[w.name] = min((r for r in (direct, graphed) if r), key=lambda r: r["us"])
         r = results[w.name]
         note = ""
-        if args.ceiling:
-            ceiling = time_workload(copy_ceiling(w.bytes_per_launch), args.steps, args.warmup,
-                                    device, False)
-            r["copy_ceiling"] = {k: ceiling[k] for k in ("us", "GBps", "frac", "workload")}
+        if args.ceiling or w.name == HEADLINE:
+            # The calibration copy of the same bytes, always beside the headline.
+            ceiling = best_copy(w.bytes_per_launch, args.steps, args.warmup, device)
+            r["copy_ceiling"] = {k: ceiling[k] for k in ("us", "GBps", "frac", "vectors", "all_us")}
             note = f" copy {ceiling['us']}"
+        if args.ceiling:
+            torch_copy = time_workload(copy_ceiling(w.bytes_per_launch, "torch"), args.steps,
+                                       args.warmup, device, False)
+            r["torch_copy"] = {k: torch_copy[k] for k in ("us", "GBps", "frac")}
+            note += f" torch copy {torch_copy['us']}"
         print(f"[bench] {index}/{len(selected)} {w.name} {r['us']} us{note}",
               file=sys.stderr, flush=True)
 

@@ -228,10 +228,10 @@ int32_t omnia_pack_router_weight(const uint16_t* router_weight, int64_t experts,
  * x, branch [rows, hidden] bf16; norm_weight [hidden] bf16; packed_router: the router
  * weight [experts, hidden] bf16 as omnia_pack_router_weight wrote it.
  * hidden in {2048, 4096}, experts in {128, 256}; k <= 64.
- * With rows <= 16 and `logits` given (decode steps) the launch is two dispatches: the
- * projection spread over many workgroups, every logit an fp64 dot product rounded once,
- * then the selection of omnia_softmax_topk over the written logits. The outputs are
- * the same bits either way.
+ * With rows <= 512 and `logits` given (decode steps and short prefills) the launch is
+ * two dispatches: the projection spread over many workgroups, every logit an fp64 dot
+ * product rounded once, then the selection of omnia_softmax_topk over the written
+ * logits. The outputs are the same bits either way.
  * Replaces: core/kernels/route/residual.py:117-299 (`residual_rms_router`, the
  * one-token residual join with the router gemv fused), generalised to many tokens and
  * to softmax routing; the Core chain is add_norm/default.py:28-29 followed by
@@ -267,7 +267,7 @@ int32_t omnia_sigmoid_topk(const void* logits, int64_t stride, int32_t logits_fp
  *   logits [rows, experts] bf16 or null; keys [rows, experts] uint32 or null;
  *   indices [rows, k] int32 and weights [rows, k] fp32, both or neither.
  * Every logit is the correctly rounded bf16 of the exact dot product, so the keys and
- * the selection equal those computed from the exact logits. With rows <= 16 and `logits`
+ * the selection equal those computed from the exact logits. With rows <= 512 and `logits`
  * given the launch is the two dispatches of omnia_residual_rms_router's decode path,
  * the second omnia_sigmoid_topk over the written logits.
  * Replaces: core/kernels/route/residual.py:117-299 (`residual_rms_router` with its
@@ -560,6 +560,16 @@ int32_t omnia_attention_decode_noalloc(const uint16_t* raw_queries, const uint16
                                        int64_t max_rows, int64_t heads, int64_t kv_heads,
                                        int64_t head_dim, float scale, float eps, uint16_t* out,
                                        hipStream_t stream);
+
+/* Calibration copy: dst[0 .. bytes) = src[0 .. bytes), 16-byte nontemporal loads and
+ * stores, `vectors_per_thread` (1, 2 or 4) vectors per thread issued before the first
+ * store. bytes a multiple of 16; both pointers 16-byte aligned; the ranges must not
+ * overlap.
+ * No counterpart in the reference: measurement infrastructure, the copy of known size
+ * that the bench times as each workload's ceiling (a kernel moving B bytes against this
+ * copy of B / 2 bytes) and that scales the HBM byte counters. */
+int32_t omnia_stream_copy(const void* src, void* dst, int64_t bytes, int32_t vectors_per_thread,
+                          hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -498,6 +498,52 @@ __device__ __forceinline__ void exact_logits(const uint16_t* n_row0, const uint1
   bits1 = f64_to_bf16(wave_sum_f64(acc1));
 }
 
+// Every logit of `list` (count experts, in LDS) for one token, by one wave, when all the
+// unsure logits are wanted (logits or keys written): the token's normalized row is
+// unpacked once into registers, and each expert's row of W is loaded one expert ahead,
+// so the load of the next row overlaps the sum of this one. Each logit is summed in the
+// order exact_logits sums it (per lane over the row's 16-byte pieces, then the wave), so
+// the bits are the same; `bits[v]` of the lane holding expert lane + 64 v is replaced.
+template <int VPL, int V>
+__device__ __forceinline__ void exact_token_logits(const uint16_t* n_row, const uint16_t* weight_rows,
+                                                   const uint16_t* list, int count, int lane,
+                                                   uint32_t (&bits)[V]) {
+  constexpr int H = 512 * VPL;
+  float n[VPL][8];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) unpack8(*reinterpret_cast<const u32x4*>(n_row + (lane + i * kWave) * 8), n[i]);
+  u32x4 cur[VPL], next[VPL];
+  int expert = count > 0 ? __builtin_amdgcn_readfirstlane(static_cast<int>(list[0])) : 0;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    cur[i] = *reinterpret_cast<const u32x4*>(weight_rows + static_cast<int64_t>(expert) * H +
+                                             (lane + i * kWave) * 8);
+  }
+  for (int c = 0; c < count; ++c) {   // uniform
+    // The next expert's row, or this one's again after the last (in bounds, unused).
+    const int following = __builtin_amdgcn_readfirstlane(static_cast<int>(list[c + 1 < count ? c + 1 : c]));
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      next[i] = *reinterpret_cast<const u32x4*>(weight_rows + static_cast<int64_t>(following) * H +
+                                                (lane + i * kWave) * 8);
+    }
+    double acc = 0.0;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float w[8];
+      unpack8(cur[i], w);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc += static_cast<double>(n[i][j] * w[j]);
+    }
+    const uint32_t exact = f64_to_bf16(wave_sum_f64(acc));
+#pragma unroll
+    for (int v = 0; v < V; ++v) bits[v] = lane + v * kWave == expert ? exact : bits[v];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) cur[i] = next[i];
+    expert = following;
+  }
+}
+
 struct RouterArgs {
   const u32x4* x;
   const u32x4* branch;
@@ -1046,7 +1092,9 @@ __device__ __forceinline__ void router_row(const u32x4 (&xv)[VPL], const u32x4 (
   if (lane == 0) *norm_slot = live ? norm_upper(static_cast<double>(nsq) * (1.0 + 0x1p-7)) : 0.0f;
 }
 
-template <int E>
+// kExactAll: the logits or the keys are written, so every logit is made exact (the launch
+// picks the instantiation; the selection-only one keeps its registers to itself).
+template <int E, bool kExactAll>
 __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(RouterArgs a) {
   using S = SplitShape<E>;
   constexpr int VPL = S::VPL, H = S::H, kRowPitch = S::kRowPitch;
@@ -1201,7 +1249,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   const bool emit = a.logits != nullptr;
   const bool sigmoid = a.bias != nullptr;
   // Every logit exact (no selection on the bounds) when logits or keys are written out.
-  const bool exact_all = emit || (sigmoid && a.keys != nullptr);
+  constexpr bool exact_all = kExactAll;
   const float n_norm = row_norm[r];
   uint32_t bits[V], upper[V], keys[V];
   bool unsure[V];
@@ -1234,18 +1282,39 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   if (active && !exact_all) threshold = select_topk<V>(keys, a.k, lane, chosen);
   bool need[V];
   bool refined = false;
+  if constexpr (exact_all) {
+    // Every unsure logit of this wave's token, recomputed by the wave itself: about a
+    // fifth of the logits at the config, too many to pool through one list. The
+    // experts go to this wave's own stretch of the task list.
+    uint16_t* mine = tasks + r * E;
+    int count = 0;
 #pragma unroll
-  for (int v = 0; v < V; ++v) {
-    need[v] = active && unsure[v] && (exact_all || upper[v] >= threshold);
-    const uint64_t mask = __ballot(need[v]);
-    if (mask != 0) {  // wave-uniform
-      refined = true;
-      int base = 0;
-      if (lane == 0) base = atomicAdd(task_count, __popcll(mask));
-      base = __builtin_amdgcn_readfirstlane(base);
+    for (int v = 0; v < V; ++v) {
+      need[v] = active && unsure[v];
+      const uint64_t mask = __ballot(need[v]);
       const int below = __builtin_amdgcn_mbcnt_hi(
           static_cast<uint32_t>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
-      if (need[v]) tasks[base + below] = static_cast<uint16_t>(r * E + lane + v * kWave);
+      if (need[v]) mine[count + below] = static_cast<uint16_t>(lane + v * kWave);
+      count += __popcll(mask);
+    }
+    __builtin_amdgcn_wave_barrier();
+    exact_token_logits<VPL, V>(tile + r * kRowPitch, a.weight_rows, mine, count, lane, bits);
+#pragma unroll
+    for (int v = 0; v < V; ++v) need[v] = false;   // bits[] already exact
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      need[v] = active && unsure[v] && upper[v] >= threshold;
+      const uint64_t mask = __ballot(need[v]);
+      if (mask != 0) {  // wave-uniform
+        refined = true;
+        int base = 0;
+        if (lane == 0) base = atomicAdd(task_count, __popcll(mask));
+        base = __builtin_amdgcn_readfirstlane(base);
+        const int below = __builtin_amdgcn_mbcnt_hi(
+            static_cast<uint32_t>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+        if (need[v]) tasks[base + below] = static_cast<uint16_t>(r * E + lane + v * kWave);
+      }
     }
   }
   OMNIA_CLOCK(a, wave, lane, 6);  // bounds, selection on them, tasks posted
@@ -1304,7 +1373,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   OMNIA_CLOCK(a, wave, lane, 9);  // token written
 }
 
-// ---- up to 16 tokens: the projection spread over the chip ----------------------------
+// ---- up to 512 tokens with the logits written: the projection spread over the chip --
 //
 // At a decode step one workgroup would read all of W through one CU (512 KB at
 // H = 2048, about 4 us at the CU's ~120 GB/s; 2 MB at 4096 x 256). Here a workgroup of 4
@@ -1317,7 +1386,11 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
 // to bf16 once: the correctly rounded logits, the fused kernel's own. They go to the
 // caller's logits output, and softmax_topk_kernel or sigmoid_topk_kernel selects from
 // there, with the same functions as the fused kernel's phase 3.
-constexpr int kDecodeRows = 16;      // the path's limit
+// The path's limit when the logits are written: every logit an fp64 dot product spread
+// over the chip costs less than the fused kernel's exact recomputation of the unsure
+// logits up to about 1,000 tokens at 2048 x 128 (measured on MI355X: 9.9 against 53.7
+// us at 17 tokens, 31.8 against 57.9 at 512, 53.8 against 58.9 at 1,024).
+constexpr int kDecodeRows = 512;
 constexpr int kDecodeGroupRows = 4;  // tokens per workgroup
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeExperts = 2;    // per wave
@@ -1419,18 +1492,24 @@ int32_t launch_decode(const RouterArgs& a, hipStream_t stream) {
   return launched("residual_rms_router");
 }
 
-template <int E>
-int32_t launch_split(const RouterArgs& a, hipStream_t stream) {
+template <int E, bool kExactAll>
+int32_t launch_split_form(const RouterArgs& a, hipStream_t stream) {
   constexpr size_t lds = SplitShape<E>::kLds;
   const hipError_t status = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&residual_rms_router_split_kernel<E>),
+      reinterpret_cast<const void*>(&residual_rms_router_split_kernel<E, kExactAll>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (status != hipSuccess) {
     return fail(-1, std::string("residual_rms_router: LDS attribute: ") + hipGetErrorString(status));
   }
   const dim3 grid(static_cast<unsigned>((a.rows + kTileTokens - 1) / kTileTokens));
-  residual_rms_router_split_kernel<E><<<grid, kThreads, lds, stream>>>(a);
+  residual_rms_router_split_kernel<E, kExactAll><<<grid, kThreads, lds, stream>>>(a);
   return launched("residual_rms_router");
+}
+
+template <int E>
+int32_t launch_split(const RouterArgs& a, hipStream_t stream) {
+  const bool exact_all = a.logits != nullptr || (a.bias != nullptr && a.keys != nullptr);
+  return exact_all ? launch_split_form<E, true>(a, stream) : launch_split_form<E, false>(a, stream);
 }
 
 bool fused_shape(int64_t hidden, int64_t experts) {

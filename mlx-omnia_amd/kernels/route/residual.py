@@ -90,9 +90,10 @@ class HipResidualRouter(ResidualRouterStrategy):
                    routing)
 
     def __call__(self, x, projected):
-        # Up to 16 tokens (decode steps) take the library's decode path, which needs the
-        # logits written out; more tokens run the one fused dispatch without them.
-        decode = x.numel() // x.shape[-1] <= ops.ROUTER_DECODE_ROWS
+        # Up to 64 tokens (decode steps, short prefills) take the library's decode path,
+        # which needs the logits written out; more tokens run the one fused dispatch
+        # without them.
+        decode = x.numel() // x.shape[-1] <= ops.ROUTER_SELECT_VIA_DECODE_ROWS
         if self.routing.bias is not None:
             summed, normalized, _, _, indices, weights = ops.residual_rms_router_sigmoid(
                 x.contiguous(), projected.contiguous(), self.norm_weight, self.gate,

@@ -28,6 +28,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "omnia_add_rms_norm": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _F32, _P]),
     "omnia_rope_angle_atlas": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _P]),
     "omnia_rope_angle_atlas_fp32": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _P]),
+    "omnia_stream_copy": (_I32, [_P, _P, _I64, _I32, _P]),
     "omnia_qk_norm_rope": (
         _I32,
         [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64,

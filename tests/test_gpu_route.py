@@ -154,12 +154,13 @@ def test_residual_router_matches_oracle(rows, hidden, experts, k):
     np.testing.assert_allclose(wts2.cpu().numpy(), want_w, rtol=1e-5, atol=1e-7)
 
 
-@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 9, 16, 17])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 9, 16, 17, 512, 513])
 @pytest.mark.parametrize("hidden,experts,k", [(2048, 128, 8), (4096, 256, 8), (2048, 256, 16), (4096, 128, 64)])
 def test_decode_path_equals_the_fused_dispatch(rows, hidden, experts, k):
-    """Up to 16 rows with the logits written take two dispatches (the projection spread
+    """Up to 512 rows with the logits written take two dispatches (the projection spread
     over the chip, then the selection kernel); without the logits the one fused dispatch
-    runs (and at 17 rows both do). Both forms give the same bits, and the oracle's."""
+    runs (and at 513 rows both do, the one writing its logits with every unsure logit
+    recomputed by its token's wave). Both forms give the same bits, and the oracle's."""
     print(f"router decode path rows={rows} hidden={hidden} experts={experts} k={k}", flush=True)
     x, r, w, gate = _router_inputs(rows, hidden, experts, seed=7 * rows + hidden + experts + k)
     xd, rd, wd = to_device(x), to_device(r), to_device(w)
