@@ -376,32 +376,41 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   int b0 = c0 + wave * kBlockRows;
   load_block(a, head_base, b0, min(c0 + a.chunk, a.max_rows), drow, c, kcur, vcur);
 
+  // The angle row at the host's bound (max_rows - 1, the position whenever the host
+  // knows it) goes out before the position is read; a different position reloads.
+  const int lanes = a.pairs / 8;
+  const int aoff = 8 * (c < lanes ? c : (c < 2 * lanes ? c - lanes : 0));
+  const int guess = min(a.max_rows - 1, a.angle_rows - 1);
+  f32x4 ga[4];
+  {
+    const float* angle = a.angles + static_cast<int64_t>(guess) * 2 * a.pairs + aoff;
+    ga[0] = *reinterpret_cast<const f32x4*>(angle);
+    ga[1] = *reinterpret_cast<const f32x4*>(angle + 4);
+    ga[2] = *reinterpret_cast<const f32x4*>(angle + a.pairs);
+    ga[3] = *reinterpret_cast<const f32x4*>(angle + a.pairs + 4);
+  }
   const StepRows rows = step_rows(a);
   if (c0 >= rows.count) return;         // whole workgroup, before any barrier
   const int c1 = min(c0 + a.chunk, rows.count);
   const bool writer = rows.write >= c0 && rows.write < c1;
   const bool norm_item = is_q || (item == GQA && writer);
   const bool value_item = item == GQA + 1 && writer;
+  const int arow = min(max(rows.position, 0), a.angle_rows - 1);
+  if (arow != guess) {                  // uniform: the position is the same everywhere
+    const float* angle = a.angles + static_cast<int64_t>(arow) * 2 * a.pairs + aoff;
+    ga[0] = *reinterpret_cast<const f32x4*>(angle);
+    ga[1] = *reinterpret_cast<const f32x4*>(angle + 4);
+    ga[2] = *reinterpret_cast<const f32x4*>(angle + a.pairs);
+    ga[3] = *reinterpret_cast<const f32x4*>(angle + a.pairs + 4);
+  }
   float cs[8], sn[8];
+  const bool rotates = norm_item && c < 2 * lanes;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) cs[j] = sn[j] = 0.0f;
-  if (norm_item) {
-    const int lanes = a.pairs / 8;
-    if (c < 2 * lanes) {
-      const int arow = min(rows.position, a.angle_rows - 1);
-      const float* angle = a.angles + static_cast<int64_t>(arow) * 2 * a.pairs + 8 * (c < lanes ? c : c - lanes);
-      const f32x4 c0v = *reinterpret_cast<const f32x4*>(angle);
-      const f32x4 c1v = *reinterpret_cast<const f32x4*>(angle + 4);
-      const f32x4 s0v = *reinterpret_cast<const f32x4*>(angle + a.pairs);
-      const f32x4 s1v = *reinterpret_cast<const f32x4*>(angle + a.pairs + 4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        cs[j] = c0v[j];
-        cs[4 + j] = c1v[j];
-        sn[j] = s0v[j];
-        sn[4 + j] = s1v[j];
-      }
-    }
+  for (int j = 0; j < 4; ++j) {
+    cs[j] = rotates ? ga[0][j] : 0.0f;
+    cs[4 + j] = rotates ? ga[1][j] : 0.0f;
+    sn[j] = rotates ? ga[2][j] : 0.0f;
+    sn[4 + j] = rotates ? ga[3][j] : 0.0f;
   }
 
   if (norm_item) {
