@@ -164,7 +164,7 @@ def workloads() -> list[Workload]:
 
         out.append(Workload(
             name=f"qk_norm_rope_{tag}",
-            kernel="qk_norm_rope_kernel",
+            kernel="qk_norm_rope_pairs_kernel",
             description=(f"q [{length},{hq},{d}], k [{length},{hkv},{d}] bf16, cos/sin "
                          f"[{table_rows},{pairs}] fp32 theta=1e6, offset ~U[0,32768)"),
             bytes_per_launch=length * (2 * (hq + hkv) * d * 2 + 2 * pairs * 4) + 2 * d * 2,
@@ -193,7 +193,7 @@ def workloads() -> list[Workload]:
 
     out.append(Workload(
         name="rope_epilogue_prefill",
-        kernel="qk_norm_rope_kernel",
+        kernel="qk_norm_rope_pairs_kernel",
         description="fused qkv [4096, 48*128] bf16 -> q [32,4096,128], k [8,4096,128]; "
                     "angles in-kernel, theta=1e6",
         bytes_per_launch=4096 * (2 * 40 * 128 * 2) + 2 * 128 * 2,
@@ -436,7 +436,7 @@ def workloads() -> list[Workload]:
 
     out.append(Workload(
         name="residual_rms_router_decode",
-        kernel="residual_rms_router",
+        kernel="router_decode_logits_kernel",
         description="one token: x, residual bf16 [1, 2048], router [128, 2048] (packed once) -> summed, "
                     "normed, bf16 logits (the facade asks for them at a decode step), top-8 indices + "
                     "fp32 weights",
@@ -448,7 +448,7 @@ def workloads() -> list[Workload]:
     ))
     out.append(Workload(
         name="residual_rms_router_sigmoid_decode",
-        kernel="residual_rms_router",
+        kernel="router_decode_logits_kernel",
         description="one token, sigmoid form with a correction bias fp32 [128]: summed, normed, bf16 "
                     "logits and uint32 ordinal keys (the reference's outputs)",
         bytes_per_launch=4 * 2048 * 2 + 2048 * 2 + 128 * 2048 * 2 + 128 * 4 + 128 * 4 + 128 * 2 + 128 * 4,
@@ -1492,6 +1492,8 @@ def router_phase_clocks(device, rows: int = 4096, stamped: int = 8, timed: int =
                 col = rel[:, walkers, j]   # walkers only
             elif j == 9:
                 col = rel[:, :, j].max(axis=1)  # a workgroup's last wave
+            elif j >= 6:
+                col = rel[:, 8, j]         # phase 3: a walker (row waves may have left)
             else:
                 col = rel[:, 0, j]         # barrier exits: every wave alike
             stats[name] = [float(np.percentile(col, q)) for q in (10, 50, 90)] + [float(col.max())]
@@ -1620,6 +1622,7 @@ def main() -> int:
     selected = [w for w in workloads() if ((w.name in only) if only else w.default)]
     results = {}
     for index, w in enumerate(selected, 1):
+        window = [time.monotonic_ns(), time.time_ns()]   # host clocks around the workload
         direct = time_workload(w, args.steps, args.warmup, device, False)
         # Small kernels outrun a Python launch loop; a graph replay then gives the
         # tighter figure. Either way the number is events over `steps` launches.
@@ -1638,6 +1641,9 @@ def main() -> int:
                                        args.warmup, device, False)
             r["torch_copy"] = {k: torch_copy[k] for k in ("us", "GBps", "frac")}
             note += f" torch copy {torch_copy['us']}"
+        torch.cuda.synchronize(device)
+        r["host_window_ns"] = dict(monotonic=[window[0], time.monotonic_ns()],
+                                   realtime=[window[1], time.time_ns()])
         print(f"[bench] {index}/{len(selected)} {w.name} {r['us']} us{note}",
               file=sys.stderr, flush=True)
 

@@ -635,7 +635,8 @@ __device__ __forceinline__ void sigmoid_finish(const uint32_t (&bits)[V], const 
 template <int V, int E>
 __device__ __forceinline__ void sigmoid_select_contenders(const uint32_t (&bits)[V], const uint32_t (&upper)[V],
                                                           uint32_t threshold, const float (&bias)[V],
-                                                          const RouterArgs& a, int64_t t, int lane, uint32_t* slots) {
+                                                          const RouterArgs& a, int64_t t, int lane, uint32_t* slots,
+                                                          const float* bias_table) {
   uint64_t mask[V];
   int count = 0;
 #pragma unroll
@@ -666,7 +667,7 @@ __device__ __forceinline__ void sigmoid_select_contenders(const uint32_t (&bits)
     const uint32_t slot = slots[lane];
     expert = static_cast<int>(slot >> 16);
     score = sigmoid_rounded(bf16_to_f32(static_cast<uint16_t>(slot & 0xFFFFu)));
-    key = ordinal_of(-(score + a.bias[expert]));
+    key = ordinal_of(-(score + bias_table[expert]));
   }
   int rank = 0;
   for (int j = 0; j < count; ++j) {   // uniform
@@ -977,13 +978,21 @@ int32_t launch_fused(const RouterArgs& a, hipStream_t stream) {
 //
 // Every CU holds one 16-token workgroup at the config (4096 tokens, 256 CUs), so the
 // phases cannot overlap across workgroups; here they overlap inside one. Waves
-// [0, kRowWaves) are row waves: phase 1 for two token rows each, whose summed and
-// normalized rows they store as soon as they are formed. Waves [kRowWaves, 16) are
-// walkers: at launch they load the first kRing blocks of their share of W (from L2)
-// into registers, while the rows stream from HBM, then run the MFMA walk while the row
-// waves' stores drain. A store counts in the issuing wave's vmcnt until it completes,
-// so only walkers, which store nothing before the end, load anything after phase 1:
-// the walk and the exact recomputations.
+// [0, kRowWaves) are row waves: phase 1 for two token rows each. Waves [kRowWaves, 16)
+// are walkers: at launch they load the first kRing blocks of their share of W (from L2)
+// into registers, while the rows stream from HBM, then run the MFMA walk.
+// Where the summed and normalized rows are stored decides where HBM's time goes. In
+// the selection-only form at E = 128 (kDeferStores) the row waves keep both rows in LDS
+// and store them only once the walk is done: the launch's reads then have HBM to
+// themselves (the last tile completes about 4.5 us sooner), the walk has the CU's path
+// to L2 to itself (stores issued during the walk slowed it from 3.8 to 7.4 us), and the
+// writes drain during phase 3. Issuing 16 KB of stores takes a wave a while once HBM
+// backs up, so the row waves then leave, and the walkers run phase 3 for two tokens
+// each: its barriers count only the waves still running. Otherwise (every logit exact,
+// or E = 256, where the second tile does not fit in LDS) the row waves store each row
+// as soon as it is formed. A store counts in the issuing wave's vmcnt until it
+// completes, so only walkers, which store nothing before the end, load anything after
+// phase 1: the walk and the exact recomputations.
 // The barriers below are lds_barrier() (common.hpp): __syncthreads() would make every
 // wave wait for the row waves' stores; nothing here reads global memory another wave of
 // the workgroup wrote.
@@ -1007,8 +1016,12 @@ struct SplitShape {
   // the task list [16 * E] of uint16.
   static constexpr size_t kTileBytes = static_cast<size_t>(kTileTokens) * kRowPitch * 2;
   static constexpr size_t kLogitBytes = static_cast<size_t>(kTileTokens) * E * 4;
-  static constexpr size_t kLds = kTileBytes + kSlices * kLogitBytes + kTileTokens * 4 + 16 +
-                                 static_cast<size_t>(kTileTokens) * E * 2;
+  // The selection-only form at E = 128 also keeps the summed rows, to store them after
+  // the walk (the tile's pitch).
+  static constexpr bool kDeferStores = E == 128;
+  static constexpr size_t kLdsCore = kTileBytes + kSlices * kLogitBytes + kTileTokens * 4 + 16 +
+                                     static_cast<size_t>(kTileTokens) * E * 2 + E * 4;
+  static constexpr size_t kLds = kLdsCore + (kDeferStores ? kTileBytes : 0);
   // Each 32-wide step is one v_mfma_f32_16x16x32_bf16 with a zero accumulator, summing
   // 32 exact products with at most 31 roundings, counted at a full ulp (62 half-ulps of
   // a partial bounded by the step's Cauchy-Schwarz product; those sum to at most A).
@@ -1044,9 +1057,10 @@ template <int VPL>
 __device__ __forceinline__ void router_row(const u32x4 (&xv)[VPL], const u32x4 (&bv)[VPL],
                                            const u32x4 (&wv)[VPL], bool live, int64_t t,
                                            float eps, int lane, const RouterArgs& a,
-                                           uint16_t* tile_row, float* norm_slot, bool store = true) {
+                                           uint16_t* tile_row, float* norm_slot, bool store,
+                                           u32x4 (&sv)[VPL]) {
   constexpr int H = 512 * VPL;
-  u32x4 sv[VPL];  // s = bf16(x + b), packed as stored
+  // sv: s = bf16(x + b), packed as stored (kept for the caller when `store` is false)
   double part[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
@@ -1092,6 +1106,15 @@ __device__ __forceinline__ void router_row(const u32x4 (&xv)[VPL], const u32x4 (
   if (lane == 0) *norm_slot = live ? norm_upper(static_cast<double>(nsq) * (1.0 + 0x1p-7)) : 0.0f;
 }
 
+template <int VPL>
+__device__ __forceinline__ void router_row(const u32x4 (&xv)[VPL], const u32x4 (&bv)[VPL],
+                                           const u32x4 (&wv)[VPL], bool live, int64_t t,
+                                           float eps, int lane, const RouterArgs& a,
+                                           uint16_t* tile_row, float* norm_slot, bool store = true) {
+  u32x4 sv[VPL];
+  router_row<VPL>(xv, bv, wv, live, t, eps, lane, a, tile_row, norm_slot, store, sv);
+}
+
 // kExactAll: the logits or the keys are written, so every logit is made exact (the launch
 // picks the instantiation; the selection-only one keeps its registers to itself).
 template <int E, bool kExactAll>
@@ -1107,6 +1130,9 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   float* row_norm = reinterpret_cast<float*>(smem + S::kTileBytes + S::kSlices * S::kLogitBytes);
   int* task_count = reinterpret_cast<int*>(row_norm + kTileTokens);
   uint16_t* tasks = reinterpret_cast<uint16_t*>(task_count + 4);
+  float* bias_lds = reinterpret_cast<float*>(tasks + kTileTokens * E);   // the sigmoid form's bias
+  uint16_t* summed_tile = reinterpret_cast<uint16_t*>(smem + S::kLdsCore);  // deferred form only
+  constexpr bool kDefer = S::kDeferStores && !kExactAll;
   if (threadIdx.x == 0) *task_count = 0;  // ordered before phase 3 by the barriers below
 
   // The wave index through readfirstlane: the compiler then knows the role branches are
@@ -1138,9 +1164,14 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   float bias[V];                // the sigmoid form's correction bias, loaded with them
 #pragma unroll
   for (int v = 0; v < V; ++v) bias[v] = a.bias ? a.bias[lane + v * kWave] : 0.0f;
+  if (wave == 0) {              // an LDS copy for phase 3, which loads nothing from memory
+#pragma unroll
+    for (int v = 0; v < V; ++v) bias_lds[lane + v * kWave] = bias[v];
+  }
 
   OMNIA_CLOCK(a, wave, lane, 0);  // entry
   u32x4 ring[kRing];
+
   if (walker) {
 #pragma unroll
     for (int i = 0; i < kRing; ++i) ring[i] = *reinterpret_cast<const u32x4*>(block_at(i));
@@ -1171,10 +1202,27 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     }
     // Keeps the scheduler from sinking row 1's loads below row 0's arithmetic.
     __builtin_amdgcn_sched_barrier(0);
-    router_row<VPL>(x0, b0, wv, live0, t0, a.eps, lane, a, tile + r0 * kRowPitch, row_norm + r0);
-    OMNIA_CLOCK(a, wave, lane, 1);  // row 0 normalized and stored
+    // The selection-only form keeps the summed rows in registers and stores both rows'
+    // outputs once the tile is complete: the launch's reads then have HBM to themselves,
+    // and its writes drain while the walk streams W from L2. The form that writes every
+    // exact logit stores at once (its row waves load W rows later, and a load waits for
+    // the wave's earlier stores).
+    u32x4 held[VPL];
+    router_row<VPL>(x0, b0, wv, live0, t0, a.eps, lane, a, tile + r0 * kRowPitch, row_norm + r0,
+                    !kDefer, held);
+    if constexpr (kDefer) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i)
+        *reinterpret_cast<u32x4*>(summed_tile + r0 * kRowPitch + (lane + i * kWave) * 8) = held[i];
+    }
+    OMNIA_CLOCK(a, wave, lane, 1);  // row 0 normalized
     router_row<VPL>(x1, b1, wv, live1, t1, a.eps, lane, a, tile + (r0 + 1) * kRowPitch,
-                    row_norm + r0 + 1);
+                    row_norm + r0 + 1, !kDefer, held);
+    if constexpr (kDefer) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i)
+        *reinterpret_cast<u32x4*>(summed_tile + (r0 + 1) * kRowPitch + (lane + i * kWave) * 8) = held[i];
+    }
   }
   OMNIA_CLOCK(a, wave, lane, 2);  // phase 1 done (walkers: ring issued)
   lds_barrier();
@@ -1240,80 +1288,113 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   }
   lds_barrier();
   OMNIA_CLOCK(a, wave, lane, 5);  // logits complete
+  if constexpr (kDefer) {
+    if (!walker) {
+      // The row waves' outputs, stored now that the walk no longer needs the CU's path
+      // to L2; the row waves then leave. Issuing 16 KB of stores takes a wave a while
+      // once HBM backs up, so the walkers run phase 3 for all 16 tokens, two each, and
+      // its barriers wait for them alone (a barrier counts the waves still running).
+      const int r0 = 2 * wave;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int64_t tq = first + r0 + q;
+        if (tq < a.rows) {
+#pragma unroll
+          for (int i = 0; i < VPL; ++i) {
+            const int v = lane + i * kWave;
+            store_nt(a.summed + tq * (H / 8) + v,
+                     *reinterpret_cast<const u32x4*>(summed_tile + (r0 + q) * kRowPitch + v * 8));
+            store_nt(a.normalized + tq * (H / 8) + v,
+                     *reinterpret_cast<const u32x4*>(tile + (r0 + q) * kRowPitch + v * 8));
+          }
+        }
+      }
+      return;
+    }
+  }
 
-  // Phase 3: as in residual_rms_router_kernel, one token per wave; the recomputations
-  // go to the walkers only.
-  const int r = wave;
-  const int64_t t = first + r;
-  const bool active = t < a.rows;  // wave-uniform; inactive waves still meet the barriers
+  // Phase 3: as in residual_rms_router_kernel, one token per wave (two per walker when
+  // the row waves have left); the recomputations go to the walkers.
+  constexpr int kTokens = kDefer ? 2 : 1;
   const bool emit = a.logits != nullptr;
   const bool sigmoid = a.bias != nullptr;
   // Every logit exact (no selection on the bounds) when logits or keys are written out.
   constexpr bool exact_all = kExactAll;
-  const float n_norm = row_norm[r];
-  uint32_t bits[V], upper[V], keys[V];
-  bool unsure[V];
+  int rr[kTokens];
+  bool active[kTokens];
+  uint32_t bits[kTokens][V], upper[kTokens][V], keys[kTokens][V];
+  bool need[kTokens][V];
+  bool refined[kTokens];
+  uint32_t chosen[kTokens], threshold[kTokens];
 #pragma unroll
-  for (int v = 0; v < V; ++v) {
-    const int e = lane + v * kWave;
-    const float logit = logit_tile[r * E + e] + logit_tile1[r * E + e];
-    const float w_norm = weight_norm[v];
-    const float delta = S::kDelta * (n_norm * w_norm) + kDeltaFloor * (n_norm + w_norm + 1.0f);
-    const uint32_t lo = f32_to_bf16(logit - delta);
-    const uint32_t hi = f32_to_bf16(logit + delta);
-    bits[v] = lo;
-    unsure[v] = lo != hi;
-    if (sigmoid) {
-      // The ordinal key falls as the logit rises: the worst key comes from the lower
-      // bound, the best from the upper. Inverted, so that select_topk's largest are the
-      // best (ties take one round together, which only lowers the threshold).
-      float worst, best, unused;
-      sigmoid_bounds(bf16_to_f32(static_cast<uint16_t>(lo)), worst, unused);
-      sigmoid_bounds(bf16_to_f32(static_cast<uint16_t>(hi)), unused, best);
-      keys[v] = ~ordinal_of(-(worst + bias[v]));
-      upper[v] = ~ordinal_of(-(best + bias[v]));
-    } else {
-      keys[v] = route_key(lo, e);
-      upper[v] = route_key(hi, e);
-    }
-  }
-  uint32_t chosen = 0;
-  uint32_t threshold = 0xFFFFFFFFu;
-  if (active && !exact_all) threshold = select_topk<V>(keys, a.k, lane, chosen);
-  bool need[V];
-  bool refined = false;
-  if constexpr (exact_all) {
-    // Every unsure logit of this wave's token, recomputed by the wave itself: about a
-    // fifth of the logits at the config, too many to pool through one list. The
-    // experts go to this wave's own stretch of the task list.
-    uint16_t* mine = tasks + r * E;
-    int count = 0;
+  for (int u = 0; u < kTokens; ++u) {
+    const int r = kDefer ? wk + S::kWalkers * u : wave;
+    rr[u] = r;
+    const int64_t t = first + r;
+    active[u] = t < a.rows;  // wave-uniform; inactive waves still meet the barriers
+    const float n_norm = row_norm[r];
+    bool unsure[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-      need[v] = active && unsure[v];
-      const uint64_t mask = __ballot(need[v]);
-      const int below = __builtin_amdgcn_mbcnt_hi(
-          static_cast<uint32_t>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
-      if (need[v]) mine[count + below] = static_cast<uint16_t>(lane + v * kWave);
-      count += __popcll(mask);
+      const int e = lane + v * kWave;
+      const float logit = logit_tile[r * E + e] + logit_tile1[r * E + e];
+      const float w_norm = weight_norm[v];
+      const float delta = S::kDelta * (n_norm * w_norm) + kDeltaFloor * (n_norm + w_norm + 1.0f);
+      const uint32_t lo = f32_to_bf16(logit - delta);
+      const uint32_t hi = f32_to_bf16(logit + delta);
+      bits[u][v] = lo;
+      unsure[v] = lo != hi;
+      if (sigmoid) {
+        // The ordinal key falls as the logit rises: the worst key comes from the lower
+        // bound, the best from the upper. Inverted, so that select_topk's largest are the
+        // best (ties take one round together, which only lowers the threshold).
+        float worst, best, unused;
+        sigmoid_bounds(bf16_to_f32(static_cast<uint16_t>(lo)), worst, unused);
+        sigmoid_bounds(bf16_to_f32(static_cast<uint16_t>(hi)), unused, best);
+        keys[u][v] = ~ordinal_of(-(worst + bias[v]));
+        upper[u][v] = ~ordinal_of(-(best + bias[v]));
+      } else {
+        keys[u][v] = route_key(lo, e);
+        upper[u][v] = route_key(hi, e);
+      }
     }
-    __builtin_amdgcn_wave_barrier();
-    exact_token_logits<VPL, V>(tile + r * kRowPitch, a.weight_rows, mine, count, lane, bits);
+    chosen[u] = 0;
+    threshold[u] = 0xFFFFFFFFu;
+    if (active[u] && !exact_all) threshold[u] = select_topk<V>(keys[u], a.k, lane, chosen[u]);
+    refined[u] = false;
+    if constexpr (exact_all) {
+      // Every unsure logit of this wave's token, recomputed by the wave itself: about a
+      // fifth of the logits at the config, too many to pool through one list. The
+      // experts go to this wave's own stretch of the task list.
+      uint16_t* mine = tasks + r * E;
+      int count = 0;
 #pragma unroll
-    for (int v = 0; v < V; ++v) need[v] = false;   // bits[] already exact
-  } else {
-#pragma unroll
-    for (int v = 0; v < V; ++v) {
-      need[v] = active && unsure[v] && upper[v] >= threshold;
-      const uint64_t mask = __ballot(need[v]);
-      if (mask != 0) {  // wave-uniform
-        refined = true;
-        int base = 0;
-        if (lane == 0) base = atomicAdd(task_count, __popcll(mask));
-        base = __builtin_amdgcn_readfirstlane(base);
+      for (int v = 0; v < V; ++v) {
+        need[u][v] = active[u] && unsure[v];
+        const uint64_t mask = __ballot(need[u][v]);
         const int below = __builtin_amdgcn_mbcnt_hi(
             static_cast<uint32_t>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
-        if (need[v]) tasks[base + below] = static_cast<uint16_t>(r * E + lane + v * kWave);
+        if (need[u][v]) mine[count + below] = static_cast<uint16_t>(lane + v * kWave);
+        count += __popcll(mask);
+      }
+      __builtin_amdgcn_wave_barrier();
+      exact_token_logits<VPL, V>(tile + r * kRowPitch, a.weight_rows, mine, count, lane, bits[u]);
+#pragma unroll
+      for (int v = 0; v < V; ++v) need[u][v] = false;   // bits[] already exact
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        need[u][v] = active[u] && unsure[v] && upper[u][v] >= threshold[u];
+        const uint64_t mask = __ballot(need[u][v]);
+        if (mask != 0) {  // wave-uniform
+          refined[u] = true;
+          int base = 0;
+          if (lane == 0) base = atomicAdd(task_count, __popcll(mask));
+          base = __builtin_amdgcn_readfirstlane(base);
+          const int below = __builtin_amdgcn_mbcnt_hi(
+              static_cast<uint32_t>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+          if (need[u][v]) tasks[base + below] = static_cast<uint16_t>(r * E + lane + v * kWave);
+        }
       }
     }
   }
@@ -1338,39 +1419,45 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   }
   lds_barrier();
   OMNIA_CLOCK(a, wave, lane, 8);  // recomputations done
-  if (!active) return;  // no barrier follows
-  if (refined) {
+  // No barrier follows.
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-      if (need[v]) bits[v] = exact_bits[r * E + lane + v * kWave];
-    }
-  }
-  if (emit) {
+  for (int u = 0; u < kTokens; ++u) {
+    if (!active[u]) continue;
+    const int r = rr[u];
+    const int64_t t = first + r;
+    if (refined[u]) {
 #pragma unroll
-    for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
-  }
-  if (sigmoid) {
-    if (exact_all) {
-      sigmoid_finish<V, E>(bits, bias, a, t, lane);
-    } else {
-      sigmoid_select_contenders<V, E>(bits, upper, threshold, bias, a, t, lane,
-                                      reinterpret_cast<uint32_t*>(tasks) + r * kWave);
+      for (int v = 0; v < V; ++v) {
+        if (need[u][v]) bits[u][v] = exact_bits[r * E + lane + v * kWave];
+      }
     }
-    OMNIA_CLOCK(a, wave, lane, 9);  // token written
-    return;
-  }
-  if (refined || exact_all) {
+    if (emit) {
 #pragma unroll
-    for (int v = 0; v < V; ++v) keys[v] = route_key(bits[v], lane + v * kWave);
-    // A refined selection ranks its few contenders; with every logit exact (or more
-    // contenders than lanes) the k rounds over the whole row run.
-    if (exact_all || !rank_contenders<V>(keys, upper, threshold, a.k, lane,
-                                         reinterpret_cast<uint32_t*>(tasks) + r * kWave, chosen)) {
-      select_topk<V>(keys, a.k, lane, chosen);
+      for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[u][v]);
     }
+    if (sigmoid) {
+      if (exact_all) {
+        sigmoid_finish<V, E>(bits[u], bias, a, t, lane);
+      } else {
+        sigmoid_select_contenders<V, E>(bits[u], upper[u], threshold[u], bias, a, t, lane,
+                                        reinterpret_cast<uint32_t*>(tasks) + r * kWave, bias_lds);
+      }
+      continue;
+    }
+    uint32_t chosen_u = chosen[u];
+    if (refined[u] || exact_all) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) keys[u][v] = route_key(bits[u][v], lane + v * kWave);
+      // A refined selection ranks its few contenders; with every logit exact (or more
+      // contenders than lanes) the k rounds over the whole row run.
+      if (exact_all || !rank_contenders<V>(keys[u], upper[u], threshold[u], a.k, lane,
+                                           reinterpret_cast<uint32_t*>(tasks) + r * kWave, chosen_u)) {
+        select_topk<V>(keys[u], a.k, lane, chosen_u);
+      }
+    }
+    write_winners(chosen_u, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
   }
-  write_winners(chosen, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
-  OMNIA_CLOCK(a, wave, lane, 9);  // token written
+  OMNIA_CLOCK(a, wave, lane, 9);  // tokens written
 }
 
 // ---- up to 512 tokens with the logits written: the projection spread over the chip --
