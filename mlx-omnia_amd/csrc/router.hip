@@ -498,34 +498,47 @@ __device__ __forceinline__ void exact_logits(const uint16_t* n_row0, const uint1
   bits1 = f64_to_bf16(wave_sum_f64(acc1));
 }
 
-// Every logit of `list` (count experts, in LDS) for one token, by one wave, when all the
-// unsure logits are wanted (logits or keys written): the token's normalized row is
-// unpacked once into registers, and each expert's row of W is loaded one expert ahead,
-// so the load of the next row overlaps the sum of this one. Each logit is summed in the
-// order exact_logits sums it (per lane over the row's 16-byte pieces, then the wave), so
-// the bits are the same; `bits[v]` of the lane holding expert lane + 64 v is replaced.
-template <int VPL, int V>
-__device__ __forceinline__ void exact_token_logits(const uint16_t* n_row, const uint16_t* weight_rows,
-                                                   const uint16_t* list, int count, int lane,
-                                                   uint32_t (&bits)[V]) {
+// The exact logits of tasks[lo, hi) (each task r * E + e: token r of the tile, expert e),
+// by one wave, when every unsure logit is wanted (logits or keys written). The tasks of a
+// token are contiguous in the list, so the wave holds the current token's normalized row
+// in fp64 registers and widens it again only when the token changes; each expert's row of
+// W is loaded one task ahead, so the next load overlaps this sum. Each logit is summed
+// in the order exact_logits sums it (per lane over the row's 16-byte pieces, then the
+// wave: fma(n, w, acc) adds the exact product n * w as acc + n * w does), so the bits are
+// the same; lane 0 writes them to exact_bits[task].
+template <int VPL, int E>
+__device__ __forceinline__ void exact_task_run(const uint16_t* tile, int row_pitch,
+                                               const uint16_t* weight_rows, const uint16_t* tasks,
+                                               int lo, int hi, int lane, uint32_t* exact_bits) {
   constexpr int H = 512 * VPL;
-  float n[VPL][8];
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) unpack8(*reinterpret_cast<const u32x4*>(n_row + (lane + i * kWave) * 8), n[i]);
+  if (lo >= hi) return;  // wave-uniform
+  double nd[VPL][8];
+  int row = -1;
+  int task = __builtin_amdgcn_readfirstlane(static_cast<int>(tasks[lo]));
   u32x4 cur[VPL], next[VPL];
-  int expert = count > 0 ? __builtin_amdgcn_readfirstlane(static_cast<int>(list[0])) : 0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    cur[i] = *reinterpret_cast<const u32x4*>(weight_rows + static_cast<int64_t>(expert) * H +
+    cur[i] = *reinterpret_cast<const u32x4*>(weight_rows + static_cast<int64_t>(task % E) * H +
                                              (lane + i * kWave) * 8);
   }
-  for (int c = 0; c < count; ++c) {   // uniform
-    // The next expert's row, or this one's again after the last (in bounds, unused).
-    const int following = __builtin_amdgcn_readfirstlane(static_cast<int>(list[c + 1 < count ? c + 1 : c]));
+  for (int c = lo; c < hi; ++c) {   // uniform
+    // The next task's row of W, or this one's again after the last (in bounds, unused).
+    const int following = __builtin_amdgcn_readfirstlane(static_cast<int>(tasks[c + 1 < hi ? c + 1 : c]));
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      next[i] = *reinterpret_cast<const u32x4*>(weight_rows + static_cast<int64_t>(following) * H +
+      next[i] = *reinterpret_cast<const u32x4*>(weight_rows + static_cast<int64_t>(following % E) * H +
                                                 (lane + i * kWave) * 8);
+    }
+    const int r = task / E;
+    if (r != row) {  // uniform: the token changed
+      row = r;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        float n[8];
+        unpack8(*reinterpret_cast<const u32x4*>(tile + r * row_pitch + (lane + i * kWave) * 8), n);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) nd[i][j] = static_cast<double>(n[j]);
+      }
     }
     double acc = 0.0;
 #pragma unroll
@@ -533,14 +546,13 @@ __device__ __forceinline__ void exact_token_logits(const uint16_t* n_row, const 
       float w[8];
       unpack8(cur[i], w);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc += static_cast<double>(n[i][j] * w[j]);
+      for (int j = 0; j < 8; ++j) acc = __builtin_fma(nd[i][j], static_cast<double>(w[j]), acc);
     }
     const uint32_t exact = f64_to_bf16(wave_sum_f64(acc));
-#pragma unroll
-    for (int v = 0; v < V; ++v) bits[v] = lane + v * kWave == expert ? exact : bits[v];
+    if (lane == 0) exact_bits[task] = exact;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) cur[i] = next[i];
-    expert = following;
+    task = following;
   }
 }
 
@@ -1344,7 +1356,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
       const uint32_t hi = f32_to_bf16(logit + delta);
       bits[u][v] = lo;
       unsure[v] = lo != hi;
-      if (sigmoid) {
+      if (sigmoid && !exact_all) {
         // The ordinal key falls as the logit rises: the worst key comes from the lower
         // bound, the best from the upper. Inverted, so that select_topk's largest are the
         // best (ties take one round together, which only lowers the threshold).
@@ -1363,24 +1375,31 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     if (active[u] && !exact_all) threshold[u] = select_topk<V>(keys[u], a.k, lane, chosen[u]);
     refined[u] = false;
     if constexpr (exact_all) {
-      // Every unsure logit of this wave's token, recomputed by the wave itself: about a
-      // fifth of the logits at the config, too many to pool through one list. The
-      // experts go to this wave's own stretch of the task list.
-      uint16_t* mine = tasks + r * E;
-      int count = 0;
+      // Every unsure logit, about a fifth of them at the config: the token's experts go
+      // to the shared task list in one stretch (one atomic per wave), so a slice of the
+      // list spans few tokens.
+      uint64_t masks[V];
+      int total = 0;
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         need[u][v] = active[u] && unsure[v];
-        const uint64_t mask = __ballot(need[u][v]);
-        const int below = __builtin_amdgcn_mbcnt_hi(
-            static_cast<uint32_t>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
-        if (need[u][v]) mine[count + below] = static_cast<uint16_t>(lane + v * kWave);
-        count += __popcll(mask);
+        masks[v] = __ballot(need[u][v]);
+        total += __popcll(masks[v]);
       }
-      __builtin_amdgcn_wave_barrier();
-      exact_token_logits<VPL, V>(tile + r * kRowPitch, a.weight_rows, mine, count, lane, bits[u]);
+      if (total > 0) {  // wave-uniform
+        refined[u] = true;
+        int base = 0;
+        if (lane == 0) base = atomicAdd(task_count, total);
+        base = __builtin_amdgcn_readfirstlane(base);
 #pragma unroll
-      for (int v = 0; v < V; ++v) need[u][v] = false;   // bits[] already exact
+        for (int v = 0; v < V; ++v) {
+          const int below = __builtin_amdgcn_mbcnt_hi(
+              static_cast<uint32_t>(masks[v] >> 32),
+              __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(masks[v]), 0));
+          if (need[u][v]) tasks[base + below] = static_cast<uint16_t>(r * E + lane + v * kWave);
+          base += __popcll(masks[v]);
+        }
+      }
     } else {
 #pragma unroll
       for (int v = 0; v < V; ++v) {
@@ -1403,7 +1422,12 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
   OMNIA_CLOCK(a, wave, lane, 7);  // task list complete
   uint32_t* exact_bits = reinterpret_cast<uint32_t*>(logit_tile);
   const int count = *task_count;
-  if (walker) {
+  if constexpr (exact_all) {
+    // Hundreds of tasks per workgroup: all 16 waves take equal slices of the list (the
+    // row waves' stores, issued in phase 1, have long completed).
+    exact_task_run<VPL, E>(tile, kRowPitch, a.weight_rows, tasks, count * wave / kWaves,
+                           count * (wave + 1) / kWaves, lane, exact_bits);
+  } else if (walker) {
     for (int i = 2 * wk; i < count; i += 2 * S::kWalkers) {  // wave-uniform
       const int task0 = tasks[i];
       const int task1 = i + 1 < count ? tasks[i + 1] : task0;
@@ -1475,8 +1499,9 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
 // there, with the same functions as the fused kernel's phase 3.
 // The path's limit when the logits are written: every logit an fp64 dot product spread
 // over the chip costs less than the fused kernel's exact recomputation of the unsure
-// logits up to about 1,000 tokens at 2048 x 128 (measured on MI355X: 9.9 against 53.7
-// us at 17 tokens, 31.8 against 57.9 at 512, 53.8 against 58.9 at 1,024).
+// logits below about 1,000 tokens at 2048 x 128 (measured on MI355X: 9.9 against 53.7
+// us at 17 tokens and 31.8 against 57.9 at 512 with the fused kernel's earlier per-token
+// recomputation; 53.8 against 46.7 at 1,024 with its pooled one).
 constexpr int kDecodeRows = 512;
 constexpr int kDecodeGroupRows = 4;  // tokens per workgroup
 constexpr int kDecodeWaves = 4;
