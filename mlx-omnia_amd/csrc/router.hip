@@ -288,6 +288,88 @@ __device__ __forceinline__ void ordinal_topk_write(const uint32_t (&keys)[V], co
   }
 }
 
+// The sigmoid form's tail for one token, from its exact bf16 logits (V per lane, expert
+// lane + 64 v; `experts` of them): scores, ordinal keys (written to keys_row when given)
+// and the selection (when indices_row is given).
+template <int V>
+__device__ __forceinline__ void sigmoid_finish(const uint32_t (&bits)[V], const float (&bias)[V],
+                                               int experts, int k, int lane, uint32_t* keys_row,
+                                               int32_t* indices_row, float* weights_row) {
+  uint32_t keys[V];
+  float scores[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    scores[v] = sigmoid_rounded(bf16_to_f32(static_cast<uint16_t>(bits[v])));
+    keys[v] = ordinal_of(-(scores[v] + bias[v]));
+    if (keys_row && lane + v * kWave < experts) keys_row[lane + v * kWave] = keys[v];
+  }
+  if (indices_row) ordinal_topk_write<V>(keys, scores, experts, k, lane, indices_row, weights_row);
+}
+
+// The sigmoid form's last step when it only selects. The contenders are the experts whose
+// best-case key reaches the threshold of the bounds: every winner is one, and by now each
+// has its exact logit. They are packed into the first lanes through `slots` (64 words of
+// this wave's own). Each lane takes one contender's exact score and key and ranks it among
+// the others, (key, expert) ascending. The first k write their expert and their score over
+// the winners' fp32 sum, taken in winner order, as ordinal_topk_write does. Too many
+// contenders (keys tied everywhere, NaN keys) or too few go to sigmoid_finish.
+template <int V>
+__device__ __forceinline__ void sigmoid_select_contenders(const uint32_t (&bits)[V], const uint32_t (&upper)[V],
+                                                          uint32_t threshold, const float (&bias)[V],
+                                                          int experts, int k, int lane,
+                                                          int32_t* indices_row, float* weights_row,
+                                                          uint32_t* slots, const float* bias_table) {
+  uint64_t mask[V];
+  int count = 0;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    mask[v] = __ballot(upper[v] >= threshold);
+    count += __popcll(mask[v]);
+  }
+  if (count > kWave || count < k) {   // uniform
+    sigmoid_finish<V>(bits, bias, experts, k, lane, nullptr, indices_row, weights_row);
+    return;
+  }
+  int base = 0;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    if (upper[v] >= threshold) {
+      const int at = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                static_cast<uint32_t>(mask[v] >> 32),
+                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask[v]), 0)));
+      slots[at] = (static_cast<uint32_t>(lane + v * kWave) << 16) | (bits[v] & 0xFFFFu);
+    }
+    base += __popcll(mask[v]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  uint32_t key = 0xFFFFFFFFu;
+  int expert = 0xFFFF;
+  float score = 0.0f;
+  if (lane < count) {
+    const uint32_t slot = slots[lane];
+    expert = static_cast<int>(slot >> 16);
+    score = sigmoid_rounded(bf16_to_f32(static_cast<uint16_t>(slot & 0xFFFFu)));
+    key = ordinal_of(-(score + bias_table[expert]));
+  }
+  int rank = 0;
+  for (int j = 0; j < count; ++j) {   // uniform
+    const uint32_t other = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), j));
+    const int other_expert = __builtin_amdgcn_readlane(expert, j);
+    rank += (other < key || (other == key && other_expert < expert)) ? 1 : 0;
+  }
+  const bool winner = lane < count && rank < k;
+  float total = 0.0f;
+  for (int r = 0; r < k; ++r) {   // uniform
+    const uint64_t who = __ballot(winner && rank == r);
+    const int owner = static_cast<int>(__builtin_ctzll(who));
+    total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score), owner)) + total;
+  }
+  if (winner) {
+    indices_row[rank] = expert;
+    weights_row[rank] = score / total;
+  }
+}
+
 // ---- sigmoid + bias -> ordinal keys -> top-k over given logits: one wave per row ----
 
 template <int V, bool kF32>
@@ -298,18 +380,45 @@ __global__ __launch_bounds__(256) void sigmoid_topk_kernel(const void* __restric
                                                            uint32_t* __restrict__ keys_out,
                                                            int32_t* __restrict__ indices,
                                                            float* __restrict__ weights) {
+  __shared__ uint32_t slots[4][kWave];  // the contenders of each wave's row
   const int lane = threadIdx.x % kWave;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
   if (row >= rows) return;
   // Every load first, from a clamped index and with no branch (a load in a branch is
   // waited on there, one round trip per value); lanes past the experts then drop theirs.
   float x[V], b[V];
+  uint32_t raw[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int e = min(lane + v * kWave, experts - 1);
-    x[v] = kF32 ? static_cast<const float*>(logits)[row * stride + e]
-                : bf16_to_f32(static_cast<const uint16_t*>(logits)[row * stride + e]);
+    if constexpr (kF32) {
+      x[v] = static_cast<const float*>(logits)[row * stride + e];
+    } else {
+      raw[v] = static_cast<const uint16_t*>(logits)[row * stride + e];
+      x[v] = bf16_to_f32(static_cast<uint16_t>(raw[v]));
+    }
     b[v] = bias[e];
+  }
+  if constexpr (!kF32) {
+    if (!keys_out && indices && experts == V * kWave) {  // uniform
+      // Selection only, every lane an expert: select on the hardware sigmoid's bounds,
+      // then rank the contenders (about k) on their exact scores, as the fused router's
+      // sigmoid form does. The k-th best worst-case key is the threshold; every expert
+      // of the exact top k has its best-case key at or above it.
+      uint32_t worst[V], best[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        float lo, hi;
+        sigmoid_bounds(x[v], lo, hi);
+        worst[v] = ~ordinal_of(-(lo + b[v]));   // inverted: larger is better
+        best[v] = ~ordinal_of(-(hi + b[v]));
+      }
+      uint32_t chosen = 0;
+      const uint32_t threshold = select_topk<V>(worst, k, lane, chosen);
+      sigmoid_select_contenders<V>(raw, best, threshold, b, experts, k, lane, indices + row * k,
+                                   weights + row * k, slots[threadIdx.x / kWave], bias);
+      return;
+    }
   }
   uint32_t keys[V];
   float scores[V];
@@ -621,84 +730,6 @@ struct FusedShape {
 // subnormal bf16 inputs or fp32 products would lose at most H * 2^-126 times those.
 constexpr float kDeltaFloor = 0x1p-113f;
 
-// The sigmoid form's tail for one token, from its exact bf16 logits (V per lane):
-// scores, ordinal keys (written when asked) and the selection (when asked).
-template <int V, int E>
-__device__ __forceinline__ void sigmoid_finish(const uint32_t (&bits)[V], const float (&bias)[V],
-                                               const RouterArgs& a, int64_t t, int lane) {
-  uint32_t keys[V];
-  float scores[V];
-#pragma unroll
-  for (int v = 0; v < V; ++v) {
-    scores[v] = sigmoid_rounded(bf16_to_f32(static_cast<uint16_t>(bits[v])));
-    keys[v] = ordinal_of(-(scores[v] + bias[v]));
-    if (a.keys) a.keys[t * E + lane + v * kWave] = keys[v];
-  }
-  if (a.indices) ordinal_topk_write<V>(keys, scores, E, a.k, lane, a.indices + t * a.k, a.weights + t * a.k);
-}
-
-// The sigmoid form's last step when it only selects. The contenders are the experts whose
-// best-case key reaches the threshold of the bounds: every winner is one, and by now each
-// has its exact logit. They are packed into the first lanes through `slots` (64 words of
-// this wave's own). Each lane takes one contender's exact score and key and ranks it among
-// the others, (key, expert) ascending. The first k write their expert and their score over
-// the winners' fp32 sum, taken in winner order, as ordinal_topk_write does. Too many
-// contenders (keys tied everywhere, NaN keys) or too few go to sigmoid_finish.
-template <int V, int E>
-__device__ __forceinline__ void sigmoid_select_contenders(const uint32_t (&bits)[V], const uint32_t (&upper)[V],
-                                                          uint32_t threshold, const float (&bias)[V],
-                                                          const RouterArgs& a, int64_t t, int lane, uint32_t* slots,
-                                                          const float* bias_table) {
-  uint64_t mask[V];
-  int count = 0;
-#pragma unroll
-  for (int v = 0; v < V; ++v) {
-    mask[v] = __ballot(upper[v] >= threshold);
-    count += __popcll(mask[v]);
-  }
-  if (count > kWave || count < a.k) {   // uniform
-    sigmoid_finish<V, E>(bits, bias, a, t, lane);
-    return;
-  }
-  int base = 0;
-#pragma unroll
-  for (int v = 0; v < V; ++v) {
-    if (upper[v] >= threshold) {
-      const int at = base + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-                                static_cast<uint32_t>(mask[v] >> 32),
-                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask[v]), 0)));
-      slots[at] = (static_cast<uint32_t>(lane + v * kWave) << 16) | (bits[v] & 0xFFFFu);
-    }
-    base += __popcll(mask[v]);
-  }
-  __builtin_amdgcn_wave_barrier();
-  uint32_t key = 0xFFFFFFFFu;
-  int expert = 0xFFFF;
-  float score = 0.0f;
-  if (lane < count) {
-    const uint32_t slot = slots[lane];
-    expert = static_cast<int>(slot >> 16);
-    score = sigmoid_rounded(bf16_to_f32(static_cast<uint16_t>(slot & 0xFFFFu)));
-    key = ordinal_of(-(score + bias_table[expert]));
-  }
-  int rank = 0;
-  for (int j = 0; j < count; ++j) {   // uniform
-    const uint32_t other = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), j));
-    const int other_expert = __builtin_amdgcn_readlane(expert, j);
-    rank += (other < key || (other == key && other_expert < expert)) ? 1 : 0;
-  }
-  const bool winner = lane < count && rank < a.k;
-  float total = 0.0f;
-  for (int r = 0; r < a.k; ++r) {   // uniform
-    const uint64_t who = __ballot(winner && rank == r);
-    const int owner = static_cast<int>(__builtin_ctzll(who));
-    total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score), owner)) + total;
-  }
-  if (winner) {
-    a.indices[t * a.k + rank] = expert;
-    a.weights[t * a.k + rank] = score / total;
-  }
-}
 
 template <int VPL, int E>
 __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArgs a) {
@@ -959,7 +990,8 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
     for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
   }
   if (sigmoid) {   // the contenders' ranking (split kernel) would spill registers here
-    sigmoid_finish<V, E>(bits, bias, a, t, lane);
+    sigmoid_finish<V>(bits, bias, E, a.k, lane, a.keys ? a.keys + t * E : nullptr,
+                      a.indices ? a.indices + t * a.k : nullptr, a.weights + t * a.k);
     return;
   }
   if (refined || exact_all) {
@@ -1461,10 +1493,12 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     }
     if (sigmoid) {
       if (exact_all) {
-        sigmoid_finish<V, E>(bits[u], bias, a, t, lane);
+        sigmoid_finish<V>(bits[u], bias, E, a.k, lane, a.keys ? a.keys + t * E : nullptr,
+                          a.indices ? a.indices + t * a.k : nullptr, a.weights + t * a.k);
       } else {
-        sigmoid_select_contenders<V, E>(bits[u], upper[u], threshold[u], bias, a, t, lane,
-                                        reinterpret_cast<uint32_t*>(tasks) + r * kWave, bias_lds);
+        sigmoid_select_contenders<V>(bits[u], upper[u], threshold[u], bias, E, a.k, lane,
+                                     a.indices + t * a.k, a.weights + t * a.k,
+                                     reinterpret_cast<uint32_t*>(tasks) + r * kWave, bias_lds);
       }
       continue;
     }

@@ -6,6 +6,8 @@ omnia_sigmoid_topk (route/ordinal.py:200-286) and the fused router's sigmoid for
 - keys, indices and weights bit-exact with the oracle's correctly rounded fp32 sigmoid,
   fp32 biased sum, ordinal keys, stable selection and fp32 renormalisation, over bf16
   and fp32 logits, 32 to 1024 experts, k from 1 to 64, heavy ties and NaN rows;
+- the selection without keys (on the hardware sigmoid's bounds, then the contenders'
+  exact scores) bit-identical to the path that scores every expert exactly;
 - the reference's tie fixture through the `Route` facade (tests/test_kernel_router_
   ordinal.py:88-142): [0, 1, 2, 3, 11, 35, 67, 99];
 - the reference's separated rows with a graded bias against a float64 chain
@@ -56,6 +58,33 @@ def test_sigmoid_topk_matches_oracle(experts, k, fp32):
     idx, w, keys = ops.sigmoid_topk(logits, torch.from_numpy(bias).cuda(), k, emit_keys=True)
     want_idx, want_w, want_keys = route.sigmoid_topk(values, bias, k)
     assert np.array_equal(keys.cpu().numpy(), want_keys)
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    assert np.array_equal(w.cpu().numpy(), want_w)
+
+
+@pytest.mark.parametrize("experts,k", [(128, 8), (64, 4), (256, 16), (512, 8), (1024, 64),
+                                       (128, 64), (100, 7)])
+@pytest.mark.parametrize("scale,bias_scale", [(2.0, 0.1), (1e-3, 1e-3), (0.0, 0.5), (0.0, 0.0)])
+def test_sigmoid_topk_selection_only_matches_keys_path(experts, k, scale, bias_scale):
+    """Selection without keys ranks on the hardware sigmoid's bounds and then the
+    contenders' exact scores; it must give the bits of the path that computes every
+    score exactly, and the oracle's: near-tied scores (tiny logits, biases the size of
+    the scores), integer ties, all-equal rows and NaN logits."""
+    print(f"sigmoid_topk selection only experts={experts} k={k} scale={scale} bias={bias_scale}", flush=True)
+    rows = 257
+    rng = np.random.default_rng(experts * 31 + k + int(scale * 1000) + int(bias_scale * 100))
+    values = (rng.standard_normal((rows, experts)) * scale).astype(np.float32)
+    values[:4] = (rng.integers(-3, 3, (4, experts)) * 0.5).astype(np.float32)
+    values[4, :5] = np.nan
+    bits = from_float(values)
+    bias = (rng.standard_normal(experts) * bias_scale).astype(np.float32)
+    logits, bias_t = to_device(bits), torch.from_numpy(bias).cuda()
+    idx, w, none = ops.sigmoid_topk(logits, bias_t, k)
+    assert none is None
+    idx_keys, w_keys, _ = ops.sigmoid_topk(logits, bias_t, k, emit_keys=True)
+    want_idx, want_w, _ = route.sigmoid_topk(to_f32(bits), bias, k)
+    assert np.array_equal(idx.cpu().numpy(), idx_keys.cpu().numpy())
+    assert np.array_equal(w.cpu().numpy(), w_keys.cpu().numpy())
     assert np.array_equal(idx.cpu().numpy(), want_idx)
     assert np.array_equal(w.cpu().numpy(), want_w)
 
