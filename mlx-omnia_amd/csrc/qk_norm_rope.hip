@@ -38,6 +38,8 @@ namespace omnia {
 namespace {
 
 constexpr int kWavesPerBlock = 4;
+// Below this many waves at eight pairs per lane, the full-rotary kernel runs four.
+constexpr int64_t kNarrowWaves = 2048;
 
 struct RopeArgs {
   const uint16_t* queries_in;
@@ -330,11 +332,36 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_kernel(Ro
 // waves in flight write long runs of the same eight head planes: 16.78 against 17.14 us
 // at the prefill shape (T = 4096, 32 + 8 heads), the decode step 2.65 against 2.75 us.
 // The derived-angle form measured no gain from it.
-template <int D, bool TABLE, bool SCALED, bool EXACT>
+// The 16-byte or 8-byte vectors of PPL bf16 values (PPL / 2 words), loaded and stored as
+// one instruction.
+template <int W> struct WordVector;
+template <> struct WordVector<4> { using T = u32x4; };
+template <> struct WordVector<2> { using T = uint32_t __attribute__((ext_vector_type(2))); };
+
+template <int W, bool NT>
+__device__ __forceinline__ void load_words(const uint16_t* p, uint32_t (&out)[W]) {
+  using T = typename WordVector<W>::T;
+  const T v = NT ? load_nt(reinterpret_cast<const T*>(p)) : *reinterpret_cast<const T*>(p);
+#pragma unroll
+  for (int i = 0; i < W; ++i) out[i] = v[i];
+}
+
+template <int W>
+__device__ __forceinline__ void store_words(uint16_t* p, const uint32_t (&in)[W]) {
+  using T = typename WordVector<W>::T;
+  T v;
+#pragma unroll
+  for (int i = 0; i < W; ++i) v[i] = in[i];
+  store_nt(reinterpret_cast<T*>(p), v);
+}
+
+template <int D, int PPL, bool TABLE, bool SCALED, bool EXACT>
 __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_kernel(RopeArgs a) {
   constexpr int P = D / 2;
-  constexpr int G = P / 8;                   // lanes per head
+  constexpr int G = P / PPL;                 // lanes per head
+  constexpr int W = PPL / 2;                 // words per half
   constexpr int kHeadsPerSlot = kWave / G;
+  static_assert(PPL == 8 || PPL == 4, "eight or four pairs per lane");
   const int lane = threadIdx.x % kWave;
   const int parts = a.q_parts + a.k_parts;   // one slot per wave
   int64_t t;
@@ -357,7 +384,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
   const int head = slot * kHeadsPerSlot + lane / G;
   const bool live = EXACT || head < heads;
   const int64_t position = a.offset + t;
-  const int base = g * 8;                    // first pair of this lane
+  const int base = g * PPL;                  // first pair of this lane
 
   // Every load goes out before any arithmetic, in the order the arithmetic needs them
   // (vector-memory results are counted in issue order): the weights and the head's two
@@ -365,38 +392,43 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
   // compiler wait on it). A lane of a head past the last reads the last head and is
   // zeroed afterwards.
   const uint16_t* weight = is_query ? a.query_weight : a.key_weight;
-  const u32x4 wraw1 = *reinterpret_cast<const u32x4*>(weight + base);
-  const u32x4 wraw2 = *reinterpret_cast<const u32x4*>(weight + P + base);
+  uint32_t wraw1[W], wraw2[W], first[W], second[W];
+  load_words<W, false>(weight + base, wraw1);
+  load_words<W, false>(weight + P + base, wraw2);
   const int head_read = live ? head : heads - 1;
   const uint16_t* in = (is_query ? a.queries_in + t * a.query_stride
                                  : a.keys_in + t * a.key_stride) + head_read * D + base;
-  u32x4 first = load_nt(reinterpret_cast<const u32x4*>(in));
-  u32x4 second = load_nt(reinterpret_cast<const u32x4*>(in + P));
-  f32x4 c0, c1, s0, s1;
+  load_words<W, true>(in, first);
+  load_words<W, true>(in + P, second);
+  f32x4 ct[PPL / 4], st[PPL / 4];
   if constexpr (TABLE) {
     const float* crow = a.cos_table + position * a.table_stride + base;
     const float* srow = a.sin_table + position * a.table_stride + base;
-    c0 = *reinterpret_cast<const f32x4*>(crow);
-    c1 = *reinterpret_cast<const f32x4*>(crow + 4);
-    s0 = *reinterpret_cast<const f32x4*>(srow);
-    s1 = *reinterpret_cast<const f32x4*>(srow + 4);
+#pragma unroll
+    for (int i = 0; i < PPL / 4; ++i) ct[i] = *reinterpret_cast<const f32x4*>(crow + 4 * i);
+#pragma unroll
+    for (int i = 0; i < PPL / 4; ++i) st[i] = *reinterpret_cast<const f32x4*>(srow + 4 * i);
   }
   __builtin_amdgcn_sched_barrier(0);
-  if (!live) first = second = u32x4{0u, 0u, 0u, 0u};
+  if (!live) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) first[i] = second[i] = 0u;
+  }
 
-  float c[8], s[8];
+  float c[PPL], s[PPL];
   if constexpr (TABLE) {
-    c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w;
-    c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
-    s[0] = s0.x; s[1] = s0.y; s[2] = s0.z; s[3] = s0.w;
-    s[4] = s1.x; s[5] = s1.y; s[6] = s1.z; s[7] = s1.w;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+      c[j] = ct[j / 4][j % 4];
+      s[j] = st[j / 4][j % 4];
+    }
   } else {
     // Lane i derives pairs i and i + 64; lanes then fetch the pairs they rotate.
     float cl = 0.0f, sl = 0.0f, ch = 0.0f, sh = 0.0f;
     if (lane < P) derived_angle(lane, P, position, a.log2_base, cl, sl);
     if (P > kWave && lane + kWave < P) derived_angle(lane + kWave, P, position, a.log2_base, ch, sh);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < PPL; ++j) {
       const int pair = base + j;
       const float lo_c = __shfl(cl, pair % kWave, kWave);
       const float lo_s = __shfl(sl, pair % kWave, kWave);
@@ -411,17 +443,19 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
       }
     }
   }
-  float w1[8], w2[8];
-  unpack8(wraw1, w1);
-  unpack8(wraw2, w2);
-  float x1[8], x2[8];
-  unpack8(first, x1);
-  unpack8(second, x2);
+  float w1[PPL], w2[PPL], x1[PPL], x2[PPL];
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    w1[2 * i] = bf16_lo(wraw1[i]); w1[2 * i + 1] = bf16_hi(wraw1[i]);
+    w2[2 * i] = bf16_lo(wraw2[i]); w2[2 * i + 1] = bf16_hi(wraw2[i]);
+    x1[2 * i] = bf16_lo(first[i]); x1[2 * i + 1] = bf16_hi(first[i]);
+    x2[2 * i] = bf16_lo(second[i]); x2[2 * i + 1] = bf16_hi(second[i]);
+  }
   // x * x is exact in fp64 (and in fp32), so one fma per element gives the same sum as
   // the square rounded to fp32 and added in fp64, in two instructions instead of three.
   double sumsq = 0.0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < PPL; ++j) {
     const double d1 = static_cast<double>(x1[j]);
     const double d2 = static_cast<double>(x2[j]);
     sumsq = __builtin_fma(d1, d1, sumsq);
@@ -432,9 +466,9 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
 
   // n = bf16(w * bf16(x * inv)); with mscale != 1, the rotary inputs are
   // bf16(n * bf16(mscale)).
-  float n1[8], n2[8];
+  float n1[PPL], n2[PPL];
 #pragma unroll
-  for (int j = 0; j < 8; j += 2) {
+  for (int j = 0; j < PPL; j += 2) {
     float a0 = x1[j] * inv, a1 = x1[j + 1] * inv;
     float b0 = x2[j] * inv, b1 = x2[j + 1] * inv;
     round_pair(a0, a1);
@@ -449,7 +483,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
   if constexpr (SCALED) {
     const float mscale = round_bf16(a.mscale);
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
+    for (int j = 0; j < PPL; j += 2) {
       n1[j] *= mscale; n1[j + 1] *= mscale;
       n2[j] *= mscale; n2[j + 1] *= mscale;
       round_pair(n1[j], n1[j + 1]);
@@ -457,26 +491,27 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
     }
   }
   // out_p = bf16(x1 * cos - x2 * sin), out_{p+P} = bf16(x1 * sin + x2 * cos).
-  float o1[8], o2[8];
+  uint32_t o1[W], o2[W];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    o1[j] = n1[j] * c[j] - n2[j] * s[j];
-    o2[j] = n1[j] * s[j] + n2[j] * c[j];
+  for (int i = 0; i < W; ++i) {
+    const int j = 2 * i;
+    o1[i] = pack_bf16(n1[j] * c[j] - n2[j] * s[j], n1[j + 1] * c[j + 1] - n2[j + 1] * s[j + 1]);
+    o2[i] = pack_bf16(n1[j] * s[j] + n2[j] * c[j], n1[j + 1] * s[j + 1] + n2[j + 1] * c[j + 1]);
   }
   if (live) {
     uint16_t* out = (is_query ? a.queries_out : a.keys_out) + (head * a.length + t) * D + base;
-    store_nt(reinterpret_cast<u32x4*>(out), pack8(o1));
-    store_nt(reinterpret_cast<u32x4*>(out + P), pack8(o2));
+    store_words<W>(out, o1);
+    store_words<W>(out + P, o2);
   }
 }
 
-template <int D, bool TABLE, bool SCALED>
+template <int D, int PPL, bool TABLE, bool SCALED>
 void launch_pairs(const RopeArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
-  constexpr int kHeadsPerSlot = kWave / (D / 16);
+  constexpr int kHeadsPerSlot = kWave * PPL / (D / 2);
   if (a.query_heads % kHeadsPerSlot == 0 && a.kv_heads % kHeadsPerSlot == 0) {
-    qk_norm_rope_pairs_kernel<D, TABLE, SCALED, true><<<grid, block, 0, stream>>>(a);
+    qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, true><<<grid, block, 0, stream>>>(a);
   } else {
-    qk_norm_rope_pairs_kernel<D, TABLE, SCALED, false><<<grid, block, 0, stream>>>(a);
+    qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, false><<<grid, block, 0, stream>>>(a);
   }
 }
 
@@ -529,7 +564,15 @@ int slots_per_wave(int64_t length, int q_slots, int k_slots) {
 template <bool TABLE>
 int32_t launch(RopeArgs a, int head_dim, hipStream_t stream, const char* name, int spw = 0) {
   if (2 * a.pairs == head_dim) {  // full rotary: the pair-owning layout, one slot per wave
-    const int heads_per_slot = kWave / (head_dim / 16);
+    // Eight pairs per lane; four where a grid of eight would leave the chip mostly idle
+    // (fewer than kNarrowWaves waves: the decode rows), so that each wave's serial chain
+    // is half as long and twice as many waves share the work. D = 256 keeps eight (a
+    // head of 32 lanes would need a cross-row sum).
+    const int wide_slot = kWave / (head_dim / 16);
+    const int64_t wide_waves = a.length * ((a.query_heads + wide_slot - 1) / wide_slot +
+                                           (a.kv_heads + wide_slot - 1) / wide_slot);
+    const bool narrow = head_dim <= 128 && wide_waves < kNarrowWaves;
+    const int heads_per_slot = narrow ? wide_slot / 2 : wide_slot;  // heads of 2G lanes
     a.q_parts = (a.query_heads + heads_per_slot - 1) / heads_per_slot;
     a.k_parts = (a.kv_heads + heads_per_slot - 1) / heads_per_slot;
     // With a table, every workgroup holds four tokens of one slot (the kernel's mapping).
@@ -541,15 +584,16 @@ int32_t launch(RopeArgs a, int head_dim, hipStream_t stream, const char* name, i
     const dim3 grid(static_cast<unsigned>(blocks));
     const dim3 block(kWavesPerBlock * kWave);
     const bool scaled = TABLE && a.mscale != 1.0f;
+#define OMNIA_PAIRS(D, PPL)                                                   \
+  (scaled ? launch_pairs<D, PPL, TABLE, true>(a, grid, block, stream)         \
+          : launch_pairs<D, PPL, TABLE, false>(a, grid, block, stream))
     switch (head_dim) {
-      case 64: scaled ? launch_pairs<64, TABLE, true>(a, grid, block, stream)
-                      : launch_pairs<64, TABLE, false>(a, grid, block, stream); break;
-      case 128: scaled ? launch_pairs<128, TABLE, true>(a, grid, block, stream)
-                       : launch_pairs<128, TABLE, false>(a, grid, block, stream); break;
-      case 256: scaled ? launch_pairs<256, TABLE, true>(a, grid, block, stream)
-                       : launch_pairs<256, TABLE, false>(a, grid, block, stream); break;
+      case 64: narrow ? OMNIA_PAIRS(64, 4) : OMNIA_PAIRS(64, 8); break;
+      case 128: narrow ? OMNIA_PAIRS(128, 4) : OMNIA_PAIRS(128, 8); break;
+      case 256: OMNIA_PAIRS(256, 8); break;
       default: return fail(-EINVAL, std::string(name) + ": head_dim must be 64, 128 or 256");
     }
+#undef OMNIA_PAIRS
     return launched(name);
   }
   const int heads_per_slot = kWave / (head_dim / 8);
