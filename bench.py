@@ -122,7 +122,7 @@ def workloads() -> list[Workload]:
 
         out.append(Workload(
             name=f"add_rms_norm_{tag}",
-            kernel="add_rms_norm_kernel",
+            kernel="add_rms_norm_row_kernel",
             description=f"x, residual bf16 [{rows}, {hidden}] -> summed, normed; eps 1e-6",
             bytes_per_launch=rows * 4 * 2 * hidden + 2 * hidden,
             setup=setup,
