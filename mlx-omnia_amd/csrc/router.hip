@@ -288,22 +288,23 @@ __device__ __forceinline__ void ordinal_topk_write(const uint32_t (&keys)[V], co
   }
 }
 
-// The sigmoid form's tail for one token, from its exact bf16 logits (V per lane, expert
-// lane + 64 v; `experts` of them): scores, ordinal keys (written to keys_row when given)
-// and the selection (when indices_row is given).
+// The sigmoid form's tail for row `row`, from its exact bf16 logits (V per lane, expert
+// lane + 64 v; `experts` of them): scores, ordinal keys (written to keys[row] when keys
+// is given) and the selection (to indices[row] and weights[row], when indices is given).
+// The row addresses are formed where they are stored, so no pointer stays live.
 template <int V>
 __device__ __forceinline__ void sigmoid_finish(const uint32_t (&bits)[V], const float (&bias)[V],
-                                               int experts, int k, int lane, uint32_t* keys_row,
-                                               int32_t* indices_row, float* weights_row) {
-  uint32_t keys[V];
+                                               int experts, int k, int lane, uint32_t* keys,
+                                               int32_t* indices, float* weights, int64_t row) {
+  uint32_t key_of[V];
   float scores[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     scores[v] = sigmoid_rounded(bf16_to_f32(static_cast<uint16_t>(bits[v])));
-    keys[v] = ordinal_of(-(scores[v] + bias[v]));
-    if (keys_row && lane + v * kWave < experts) keys_row[lane + v * kWave] = keys[v];
+    key_of[v] = ordinal_of(-(scores[v] + bias[v]));
+    if (keys && lane + v * kWave < experts) keys[row * experts + lane + v * kWave] = key_of[v];
   }
-  if (indices_row) ordinal_topk_write<V>(keys, scores, experts, k, lane, indices_row, weights_row);
+  if (indices) ordinal_topk_write<V>(key_of, scores, experts, k, lane, indices + row * k, weights + row * k);
 }
 
 // The sigmoid form's last step when it only selects. The contenders are the experts whose
@@ -317,7 +318,7 @@ template <int V>
 __device__ __forceinline__ void sigmoid_select_contenders(const uint32_t (&bits)[V], const uint32_t (&upper)[V],
                                                           uint32_t threshold, const float (&bias)[V],
                                                           int experts, int k, int lane,
-                                                          int32_t* indices_row, float* weights_row,
+                                                          int32_t* indices, float* weights, int64_t row,
                                                           uint32_t* slots, const float* bias_table) {
   uint64_t mask[V];
   int count = 0;
@@ -327,7 +328,7 @@ __device__ __forceinline__ void sigmoid_select_contenders(const uint32_t (&bits)
     count += __popcll(mask[v]);
   }
   if (count > kWave || count < k) {   // uniform
-    sigmoid_finish<V>(bits, bias, experts, k, lane, nullptr, indices_row, weights_row);
+    sigmoid_finish<V>(bits, bias, experts, k, lane, nullptr, indices, weights, row);
     return;
   }
   int base = 0;
@@ -365,8 +366,8 @@ __device__ __forceinline__ void sigmoid_select_contenders(const uint32_t (&bits)
     total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score), owner)) + total;
   }
   if (winner) {
-    indices_row[rank] = expert;
-    weights_row[rank] = score / total;
+    indices[row * k + rank] = expert;
+    weights[row * k + rank] = score / total;
   }
 }
 
@@ -415,8 +416,8 @@ __global__ __launch_bounds__(256) void sigmoid_topk_kernel(const void* __restric
       }
       uint32_t chosen = 0;
       const uint32_t threshold = select_topk<V>(worst, k, lane, chosen);
-      sigmoid_select_contenders<V>(raw, best, threshold, b, experts, k, lane, indices + row * k,
-                                   weights + row * k, slots[threadIdx.x / kWave], bias);
+      sigmoid_select_contenders<V>(raw, best, threshold, b, experts, k, lane, indices, weights, row,
+                                   slots[threadIdx.x / kWave], bias);
       return;
     }
   }
@@ -990,8 +991,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
     for (int v = 0; v < V; ++v) a.logits[t * E + lane + v * kWave] = static_cast<uint16_t>(bits[v]);
   }
   if (sigmoid) {   // the contenders' ranking (split kernel) would spill registers here
-    sigmoid_finish<V>(bits, bias, E, a.k, lane, a.keys ? a.keys + t * E : nullptr,
-                      a.indices ? a.indices + t * a.k : nullptr, a.weights + t * a.k);
+    sigmoid_finish<V>(bits, bias, E, a.k, lane, a.keys, a.indices, a.weights, t);
     return;
   }
   if (refined || exact_all) {
@@ -1493,11 +1493,10 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
     }
     if (sigmoid) {
       if (exact_all) {
-        sigmoid_finish<V>(bits[u], bias, E, a.k, lane, a.keys ? a.keys + t * E : nullptr,
-                          a.indices ? a.indices + t * a.k : nullptr, a.weights + t * a.k);
+        sigmoid_finish<V>(bits[u], bias, E, a.k, lane, a.keys, a.indices, a.weights, t);
       } else {
         sigmoid_select_contenders<V>(bits[u], upper[u], threshold[u], bias, E, a.k, lane,
-                                     a.indices + t * a.k, a.weights + t * a.k,
+                                     a.indices, a.weights, t,
                                      reinterpret_cast<uint32_t*>(tasks) + r * kWave, bias_lds);
       }
       continue;
