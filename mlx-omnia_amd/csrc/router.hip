@@ -723,7 +723,13 @@ struct FusedShape {
   // inside each MFMA (62 half-ulps), one half-ulp per step add and per slice add; 1%
   // covers the rounding of A, delta and L +- delta. The floor covers products that
   // leave the fp32 normal range.
-  static constexpr float kDelta = (62.0f + kSteps + kSlices - 1) * 1.01f / 16777216.0f;
+  // The walk adds each block of kUnroll step results in order (kUnroll - 1 adds), the
+  // kOuter block sums in a binary tree (log2 kOuter levels), then the slices.
+  static constexpr int kUnroll = 8;
+  static constexpr int kOuter = kSlice / (32 * kUnroll);
+  static constexpr int kLevels = kOuter == 16 ? 4 : kOuter == 8 ? 3 : kOuter == 4 ? 2 : 1;
+  static constexpr float kDelta = (62.0f + (kUnroll - 1) + kLevels + kSlices - 1) * 1.01f / 16777216.0f;
+  static_assert(kOuter == (1 << kLevels), "a power-of-two number of step blocks");
   static_assert(H <= 8192, "the absolute floor assumes H <= 2^13");
   static_assert(E % 16 == 0 && kWaves % kTiles == 0 && kSlice % 256 == 0, "shape");
 };
@@ -760,8 +766,8 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   // of H, in kOuter blocks of kUnroll steps. Each workgroup starts at a different block,
   // so the workgroups of an XCD do not all read the same W lines at once (the order of
   // the step adds changes per workgroup; the error bound does not).
-  constexpr int kUnroll = 8;
-  constexpr int kOuter = kSlice / (32 * kUnroll);
+  constexpr int kUnroll = S::kUnroll;
+  constexpr int kOuter = S::kOuter;
   const int start = static_cast<int>(blockIdx.x % kOuter);
   const uint16_t* brow =
       a.packed + (static_cast<int64_t>(wave % kTiles) * (H / 32) + (wave / kTiles) * (kSlice / 32)) * 512 +
@@ -783,15 +789,19 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
   {
     const int r = wave;
     const int64_t t = first + r;
+    // Every load before any arithmetic and none in a branch: a row past the last reads
+    // the last row (in bounds) and is zeroed.
+    const int64_t tl = t < a.rows ? t : a.rows - 1;
     u32x4 xv[VPL], bv[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      xv[i] = u32x4{0u, 0u, 0u, 0u};
-      bv[i] = u32x4{0u, 0u, 0u, 0u};
-      if (t < a.rows) {
-        xv[i] = load_nt(a.x + t * (H / 8) + lane + i * kWave);
-        bv[i] = load_nt(a.branch + t * (H / 8) + lane + i * kWave);
-      }
+      xv[i] = load_nt(a.x + tl * (H / 8) + lane + i * kWave);
+      bv[i] = load_nt(a.branch + tl * (H / 8) + lane + i * kWave);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (t >= a.rows) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) xv[i] = bv[i] = u32x4{0u, 0u, 0u, 0u};
     }
     // s = bf16(x + b) is formed twice (for the sum of squares, then for the outputs)
     // rather than kept: at H = 4096 the rows alone fill half the register budget.
@@ -859,6 +869,10 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
         next[u] = *reinterpret_cast<const u32x4*>(brow + (start * kUnroll + u) * 512);
       }
     }
+    // Each block's kUnroll step results are added in order into its group sum (the first
+    // is a copy), and the kOuter group sums meet in a binary tree: level j holds the
+    // pending sum of 2^j groups until its partner arrives.
+    f32x4 level[S::kLevels];
     for (int step = 0; step < kOuter; ++step) {
       const int s0 = (start + step) % kOuter;
       const int s1 = (start + step + 1) % kOuter;
@@ -870,16 +884,31 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_kernel(RouterArg
           next[u] = *reinterpret_cast<const u32x4*>(brow + (s1 * kUnroll + u) * 512);
         }
       }
+      f32x4 group;
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const u32x4 av = *reinterpret_cast<const u32x4*>(arow + (s0 * kUnroll + u) * 32);
         const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             __builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, b[u]), zero, 0, 0, 0);
-        acc[0] = acc[0] + part[0];
-        acc[1] = acc[1] + part[1];
-        acc[2] = acc[2] + part[2];
-        acc[3] = acc[3] + part[3];
+        if (u == 0) {
+          group = part;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) group[j] = group[j] + part[j];
+        }
       }
+      // Carry the group into the tree, as a binary counter on `step`.
+#pragma unroll
+      for (int lv = 0; lv < S::kLevels; ++lv) {
+        if ((step >> lv) & 1) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) group[j] = level[lv][j] + group[j];
+        } else {
+          level[lv] = group;
+          break;
+        }
+      }
+      if (step == kOuter - 1) acc = group;   // every level paired: the whole slice
     }
   }
   // D layout: lane l holds column (expert) l % 16, rows (tokens) (l / 16) * 4 + i. The
