@@ -42,10 +42,12 @@
 //      meet in LDS;
 //   3. per token: the bf16 rounding of each logit, made exact. With A = ||n|| ||W_e||
 //      (Cauchy-Schwarz: A >= sum |n_k W_ek|), the fp32 logit L is within
-//      delta = (62 + steps + slices - 1) * 2^-24 * A (+1% and a tiny absolute floor)
-//      of the exact dot product, plus an absolute floor for subnormal flushes: each MFMA's internal sum of 32 products carries at most
-//      31 roundings, each counted at a full ulp, and each fp32 add of a step result or
-//      of a slice partial one half-ulp rounding. When [L - delta, L + delta] rounds to
+//      delta = (62 + chain + slices - 1) * 2^-24 * A (+1% and a tiny absolute floor for
+//      subnormal flushes) of the exact dot product: each MFMA's internal sum of 32
+//      products carries at most 31 roundings, each counted at a full ulp, and each fp32
+//      add on an element's path (the chain: in-order adds inside a group of step
+//      results, then a tree over the groups) and of a slice partial one half-ulp
+//      rounding. When [L - delta, L + delta] rounds to
 //      one bf16 value, that value is the correctly rounded logit; otherwise the logit is
 //      recomputed as an fp64 dot product from the LDS tile and W (the products of two
 //      bf16 values are exact in fp32) and rounded once. Recomputed are the unsure
