@@ -317,21 +317,6 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_kernel(Ro
   }
 }
 
-// Full-rotary layout (2P == D): each lane owns eight rotary pairs (p, p + P),
-// p = 8g .. 8g + 7 of one head, read as one 16-byte vector from each half. A head is then
-// G = D / 16 lanes (8 at D = 128) and one wave instruction covers 64 / G heads; each
-// wave owns one such slot of the q heads or of the k heads of one token. Each lane
-// holds both halves of its pairs, so the rotation needs no cross-lane exchange, and the
-// per-head sum of squares is a DPP reduction over G lanes. Measured on MI355X at the
-// prefill shape, this beats the partner-exchange layout by about 3%.
-//
-// Which waves run together decides how the transposed output [heads, T, D] is written.
-// Token by token (the derived-angle form), the waves in flight write 256-byte pieces
-// of every head plane at once. With a table (slot-major), a workgroup's four waves take
-// four consecutive tokens of one slot and consecutive workgroups the next four, so the
-// waves in flight write long runs of the same eight head planes: 16.78 against 17.14 us
-// at the prefill shape (T = 4096, 32 + 8 heads), the decode step 2.65 against 2.75 us.
-// The derived-angle form measured no gain from it.
 // The 16-byte or 8-byte vectors of PPL bf16 values (PPL / 2 words), loaded and stored as
 // one instruction.
 template <int W> struct WordVector;
@@ -355,6 +340,22 @@ __device__ __forceinline__ void store_words(uint16_t* p, const uint32_t (&in)[W]
   store_nt(reinterpret_cast<T*>(p), v);
 }
 
+// Full-rotary layout (2P == D): each lane owns PPL rotary pairs (p, p + P), p = PPL g ..
+// PPL g + PPL - 1 of one head, read as one vector from each half (16 bytes at PPL = 8,
+// 8 bytes at PPL = 4). A head is then G = P / PPL lanes (8 at D = 128, PPL = 8) and one
+// wave instruction covers 64 / G heads; each wave owns one such slot of the q heads or
+// of the k heads of one token. Each lane holds both halves of its pairs, so the
+// rotation needs no cross-lane exchange, and the per-head sum of squares is a DPP
+// reduction over G lanes. Measured on MI355X at the prefill shape, this beats the
+// partner-exchange layout by about 3%. Small grids take PPL = 4 (the launch's choice).
+//
+// Which waves run together decides how the transposed output [heads, T, D] is written.
+// Token by token (the derived-angle form), the waves in flight write 256-byte pieces
+// of every head plane at once. With a table (slot-major), a workgroup's four waves take
+// four consecutive tokens of one slot and consecutive workgroups the next four, so the
+// waves in flight write long runs of the same eight head planes: 16.78 against 17.14 us
+// at the prefill shape (T = 4096, 32 + 8 heads), the decode step 2.65 against 2.75 us.
+// The derived-angle form measured no gain from it.
 template <int D, int PPL, bool TABLE, bool SCALED, bool EXACT>
 __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_kernel(RopeArgs a) {
   constexpr int P = D / 2;
