@@ -1113,13 +1113,15 @@ struct SplitShape {
   static constexpr bool kTree = kTilesPerWalker <= 2;
   static constexpr int kChain = kTree ? (kGroup - 1) + 2 : kSteps - 1;
   static constexpr float kDelta = (62.0f + kChain + (kSlices - 1)) * 1.01f / 16777216.0f;
-  // When every logit is made exact (logits or keys written), each step is two
-  // v_mfma_f32_16x16x16bf16_1k halves over the lanes' first and last four k's (15
-  // roundings each, 30 half-ulps of the half's own bound) joined by one fp32 add: 31
-  // half-ulps of the step's bound where one 16x16x32 MFMA counts 62. At E = 128 the
-  // bound drops from 72 to 41 half-ulps, and with it the share of unsure logits, which
-  // that form recomputes in fp64; the extra MFMA and adds cost the walk far less.
-  static constexpr float kDeltaHalves = (30.0f + 1.0f + kChain + (kSlices - 1)) * 1.01f / 16777216.0f;
+  // When every logit is made exact (logits or keys written), each step is four
+  // v_mfma_f32_16x16x16bf16_1k quarters: each takes one 32-bit word (two k's) of every
+  // lane's operands and zeros in place of the other two, so it sums eight real products
+  // (an exact zero adds no rounding: 7 roundings, 14 half-ulps of the quarter's own
+  // bound), and the quarters join in a tree of two fp32 adds: 16 half-ulps of the
+  // step's bound where one 16x16x32 MFMA counts 62. At E = 128 the bound drops from 72
+  // to 26 half-ulps, and with it the share of unsure logits, which that form recomputes
+  // in fp64; the extra MFMAs and adds cost the walk far less.
+  static constexpr float kDeltaQuarters = (14.0f + 2.0f + kChain + (kSlices - 1)) * 1.01f / 16777216.0f;
   static_assert(kSteps == 4 * kGroup, "four groups of steps per (tile, slice)");
   static_assert(kTiles * kSlices % kWalkers == 0 && kWalkers % kSlices == 0, "shape");
   static_assert(kTileTokens == 2 * kRowWaves, "two rows per row wave");
@@ -1356,13 +1358,19 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
       if (i + kRing < kBlocks) ring[i % kRing] = *reinterpret_cast<const u32x4*>(block_at(i + kRing));
       f32x4 part;
       if constexpr (kExactAll) {
-        // Halves taken from a cast of the whole vector (this hipcc compiles a bit cast of
-        // an ext-vector swizzle as one of its first elements).
-        const s16x8 a8 = __builtin_bit_cast(s16x8, av), b8 = __builtin_bit_cast(s16x8, b);
-        const f32x4 lo = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a8.s0123, b8.s0123, zero, 0, 0, 0);
-        const f32x4 hi = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a8.s4567, b8.s4567, zero, 0, 0, 0);
+        // Quarter w: word w of each lane's operands (k = 8 (l / 16) + 2w, + 1), zeros for
+        // the operand's other two k's. The four-element operands are taken from a cast
+        // of a whole vector (this hipcc compiles a bit cast of an ext-vector swizzle as
+        // one of its first elements).
+        f32x4 q[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) part[j] = lo[j] + hi[j];
+        for (int w = 0; w < 4; ++w) {
+          const s16x8 a8 = __builtin_bit_cast(s16x8, u32x4{av[w], 0u, 0u, 0u});
+          const s16x8 b8 = __builtin_bit_cast(s16x8, u32x4{b[w], 0u, 0u, 0u});
+          q[w] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a8.s0123, b8.s0123, zero, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) part[j] = (q[0][j] + q[1][j]) + (q[2][j] + q[3][j]);
       } else {
         part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             __builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, b), zero, 0, 0, 0);
@@ -1432,7 +1440,7 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
       const int e = lane + v * kWave;
       const float logit = logit_tile[r * E + e] + logit_tile1[r * E + e];
       const float w_norm = weight_norm[v];
-      const float delta = (kExactAll ? S::kDeltaHalves : S::kDelta) * (n_norm * w_norm) +
+      const float delta = (kExactAll ? S::kDeltaQuarters : S::kDelta) * (n_norm * w_norm) +
                           kDeltaFloor * (n_norm + w_norm + 1.0f);
       const uint32_t lo = f32_to_bf16(logit - delta);
       const uint32_t hi = f32_to_bf16(logit + delta);
