@@ -1590,9 +1590,9 @@ __global__ __launch_bounds__(kThreads) void residual_rms_router_split_kernel(Rou
 // there, with the same functions as the fused kernel's phase 3.
 // The path's limit when the logits are written: every logit an fp64 dot product spread
 // over the chip costs less than the fused kernel's exact recomputation of the unsure
-// logits below about 1,000 tokens at 2048 x 128 (measured on MI355X: 9.9 against 53.7
-// us at 17 tokens and 31.8 against 57.9 at 512 with the fused kernel's earlier per-token
-// recomputation; 53.8 against 46.7 at 1,024 with its pooled one).
+// logits up to about 512 tokens at 2048 x 128 (measured on MI355X against the fused
+// kernel with its pooled recomputation and MFMA quarters: 9.6 against 31.0 us at 17
+// tokens, 21.1 against 32.6 at 256, 32.3 against 33.5 at 512).
 constexpr int kDecodeRows = 512;
 constexpr int kDecodeGroupRows = 4;  // tokens per workgroup
 constexpr int kDecodeWaves = 4;
