@@ -275,4 +275,74 @@ __device__ __forceinline__ void store_nt(T* ptr, const T& value) {
   __builtin_nontemporal_store(value, ptr);
 }
 
+// sin and cos of x in fp64, for |x| < kSinCosFastLimit (2^25). Argument reduction by pi/2
+// after Cody and Waite ("Software Manual for the Elementary Functions", 1980): pi/2 is
+// split into C1 + C2 + C3 (27 significant bits each) + C4, so k * Ci is exact for
+// |k| < 2^26 and x - k * C1 is exact (Sterbenz); each later step rounds once relative to
+// its own result, so the reduced argument r (|r| <= pi/4 plus a rounding margin) carries
+// a relative error of a few fp64 ulps even when x lies close to a multiple of pi/2.
+// sin r and cos r are their Taylor series to r^17 and r^18 (the first omitted terms are
+// below 1e-19 at |r| = 0.79), evaluated by Horner's rule; the quadrant k mod 4 then picks
+// and signs them. NaN in gives NaN out.
+constexpr double kSinCosFastLimit = 0x1p25;
+
+// The reduction and the two series: sin r and cos r, and k (an integer-valued double).
+__device__ __forceinline__ double sin_cos_reduced(double x, double& sin_r, double& cos_r) {
+  constexpr double kTwoOverPi = 0x1.45f306dc9c883p-1;
+  constexpr double kC1 = 0x1.921fb54000000p+0;
+  constexpr double kC2 = 0x1.10b4610000000p-30;
+  constexpr double kC3 = 0x1.a626330000000p-58;
+  constexpr double kC4 = 0x1.45c06e0e68948p-86;
+  const double k = __builtin_rint(x * kTwoOverPi);
+  double r = __builtin_fma(-k, kC1, x);
+  r = __builtin_fma(-k, kC2, r);
+  r = __builtin_fma(-k, kC3, r);
+  r = __builtin_fma(-k, kC4, r);
+  const double r2 = r * r;
+  // (-1)^n / (2n+1)! for n = 8 .. 1, and (-1)^n / (2n)! for n = 9 .. 1, as doubles.
+  double ps = 0x1.952c77030ad4ap-49;
+  ps = __builtin_fma(ps, r2, -0x1.ae7f3e733b81fp-41);
+  ps = __builtin_fma(ps, r2, 0x1.6124613a86d09p-33);
+  ps = __builtin_fma(ps, r2, -0x1.ae64567f544e4p-26);
+  ps = __builtin_fma(ps, r2, 0x1.71de3a556c734p-19);
+  ps = __builtin_fma(ps, r2, -0x1.a01a01a01a01ap-13);
+  ps = __builtin_fma(ps, r2, 0x1.1111111111111p-7);
+  ps = __builtin_fma(ps, r2, -0x1.5555555555555p-3);
+  sin_r = __builtin_fma(ps * r2, r, r);
+  double pc = -0x1.6827863b97d97p-53;
+  pc = __builtin_fma(pc, r2, 0x1.ae7f3e733b81fp-45);
+  pc = __builtin_fma(pc, r2, -0x1.93974a8c07c9dp-37);
+  pc = __builtin_fma(pc, r2, 0x1.1eed8eff8d898p-29);
+  pc = __builtin_fma(pc, r2, -0x1.27e4fb7789f5cp-22);
+  pc = __builtin_fma(pc, r2, 0x1.a01a01a01a01ap-16);
+  pc = __builtin_fma(pc, r2, -0x1.6c16c16c16c17p-10);
+  pc = __builtin_fma(pc, r2, 0x1.5555555555555p-5);
+  pc = __builtin_fma(pc, r2, -0x1.0000000000000p-1);
+  cos_r = __builtin_fma(pc, r2, 1.0);
+  return k;
+}
+
+__device__ __forceinline__ void sin_cos_fp64(double x, double& sin_x, double& cos_x) {
+  double sin_r, cos_r;
+  const double k = sin_cos_reduced(x, sin_r, cos_r);
+  const int quadrant = static_cast<int>(static_cast<int64_t>(k) & 3);
+  sin_x = quadrant == 0 ? sin_r : quadrant == 1 ? cos_r : quadrant == 2 ? -sin_r : -cos_r;
+  cos_x = quadrant == 0 ? cos_r : quadrant == 1 ? -sin_r : quadrant == 2 ? -cos_r : sin_r;
+}
+
+// The same values with the quadrant applied by selects alone (no branch, no conversion):
+// k + 1.5 * 2^52 holds k mod 2^32 in its low word (two's complement for negative k), for
+// any k, so lanes past the limit (whose values the caller replaces) stay well defined.
+// Odd k swaps sin and cos; the signs follow bit 1 of k (sin) and of k + 1 (cos).
+__device__ __forceinline__ void sin_cos_fp64_selects(double x, double& sin_x, double& cos_x) {
+  double sin_r, cos_r;
+  const double k = sin_cos_reduced(x, sin_r, cos_r);
+  const uint32_t quadrant = static_cast<uint32_t>(__builtin_bit_cast(uint64_t, k + 0x1.8p52));
+  const bool swap = (quadrant & 1u) != 0;
+  const double s = swap ? cos_r : sin_r;
+  const double c = swap ? sin_r : cos_r;
+  sin_x = (quadrant & 2u) != 0 ? -s : s;
+  cos_x = ((quadrant + 1u) & 2u) != 0 ? -c : c;
+}
+
 }  // namespace omnia

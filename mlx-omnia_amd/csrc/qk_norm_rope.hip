@@ -12,7 +12,7 @@
 // (`omnia_qk_norm_rope`), or are derived in-kernel exactly as
 // core/kernels/qkv_rope/epilogue.py:57-63 derives them (`omnia_rope_epilogue`):
 //   angle_p = f32(pos) * exp2(-(p / P) * log2(base)),  with cos/sin of that fp32 angle.
-// In-kernel, exp2, cos and sin are evaluated in fp64 (sin_cos_fp64 below) and rounded
+// In-kernel, exp2, cos and sin are evaluated in fp64 (sin_cos_fp64, common.hpp) and rounded
 // once to fp32, i.e. correctly rounded for all practical purposes (the reference's Metal code uses
 // fast::cos/sin, which no other machine reproduces bit for bit).
 //
@@ -64,51 +64,6 @@ struct RopeArgs {
   float mscale;
   float log2_base;
 };
-
-// sin and cos of an fp32 angle 0 <= x < 2^24, in fp64. Argument reduction by pi/2 after
-// Cody and Waite ("Software Manual for the Elementary Functions", 1980): pi/2 is split
-// into C1 + C2 + C3 (27 significant bits each) + C4, so k * Ci is exact for k < 2^26 and
-// x - k * C1 is exact; each later step rounds once relative to its own result, so the
-// reduced argument r (|r| <= pi/4 plus a rounding margin) carries a relative error of a
-// few fp64 ulps even when x lies close to a multiple of pi/2. sin r and cos r are their
-// Taylor series to r^17 and r^18 (the first omitted terms are below 1e-19 at |r| = 0.79),
-// evaluated by Horner's rule; the quadrant k mod 4 then picks and signs them.
-__device__ __forceinline__ void sin_cos_fp64(double x, double& sin_x, double& cos_x) {
-  constexpr double kTwoOverPi = 0x1.45f306dc9c883p-1;
-  constexpr double kC1 = 0x1.921fb54000000p+0;
-  constexpr double kC2 = 0x1.10b4610000000p-30;
-  constexpr double kC3 = 0x1.a626330000000p-58;
-  constexpr double kC4 = 0x1.45c06e0e68948p-86;
-  const double k = __builtin_rint(x * kTwoOverPi);
-  double r = __builtin_fma(-k, kC1, x);
-  r = __builtin_fma(-k, kC2, r);
-  r = __builtin_fma(-k, kC3, r);
-  r = __builtin_fma(-k, kC4, r);
-  const double r2 = r * r;
-  // (-1)^n / (2n+1)! for n = 8 .. 1, and (-1)^n / (2n)! for n = 9 .. 1, as doubles.
-  double ps = 0x1.952c77030ad4ap-49;
-  ps = __builtin_fma(ps, r2, -0x1.ae7f3e733b81fp-41);
-  ps = __builtin_fma(ps, r2, 0x1.6124613a86d09p-33);
-  ps = __builtin_fma(ps, r2, -0x1.ae64567f544e4p-26);
-  ps = __builtin_fma(ps, r2, 0x1.71de3a556c734p-19);
-  ps = __builtin_fma(ps, r2, -0x1.a01a01a01a01ap-13);
-  ps = __builtin_fma(ps, r2, 0x1.1111111111111p-7);
-  ps = __builtin_fma(ps, r2, -0x1.5555555555555p-3);
-  const double sin_r = __builtin_fma(ps * r2, r, r);
-  double pc = -0x1.6827863b97d97p-53;
-  pc = __builtin_fma(pc, r2, 0x1.ae7f3e733b81fp-45);
-  pc = __builtin_fma(pc, r2, -0x1.93974a8c07c9dp-37);
-  pc = __builtin_fma(pc, r2, 0x1.1eed8eff8d898p-29);
-  pc = __builtin_fma(pc, r2, -0x1.27e4fb7789f5cp-22);
-  pc = __builtin_fma(pc, r2, 0x1.a01a01a01a01ap-16);
-  pc = __builtin_fma(pc, r2, -0x1.6c16c16c16c17p-10);
-  pc = __builtin_fma(pc, r2, 0x1.5555555555555p-5);
-  pc = __builtin_fma(pc, r2, -0x1.0000000000000p-1);
-  const double cos_r = __builtin_fma(pc, r2, 1.0);
-  const int quadrant = static_cast<int>(static_cast<int64_t>(k) & 3);
-  sin_x = quadrant == 0 ? sin_r : quadrant == 1 ? cos_r : quadrant == 2 ? -sin_r : -cos_r;
-  cos_x = quadrant == 0 ? cos_r : quadrant == 1 ? -sin_r : quadrant == 2 ? -cos_r : sin_r;
-}
 
 // cos/sin of the in-kernel angle for pair `pair` at `position` (epilogue.py:57-63),
 // evaluated in fp64 and rounded once to fp32.

@@ -5,7 +5,10 @@ tests/test_kernel_qk_norm_rope.py:51-66): bit-equal at the config's 40,960 x 64 
 theta = 1e6, and after growth on demand (models/laguna/layers/attention.py:235-243) with
 the old rows kept. The attention step and the table-driven QK-norm + RoPE read an atlas
 that grows past its last row and match the oracle there. A YaRN table (1 / freqs as the
-frequencies) against the closed form.
+frequencies) against the closed form. Both entry points, called directly, bit-equal to the
+oracle for pair counts that leave lanes idle or span two runs of 64 pairs (the row past
+the last untouched), at positions whose angles cross 2^25, where the kernels change from
+their own Cody-Waite reduction to the device library's sincos.
 """
 
 import numpy as np
@@ -14,6 +17,8 @@ import torch
 
 from mlx_omnia_amd.kernels.attention import AttentionStep, FixedKVCache, HipAttentionStep
 from mlx_omnia_amd.kernels.qkv_rope import AngleAtlas, HipQkNormRope, QkvRope, rope_core
+from mlx_omnia_amd.kernels.qkv_rope.atlas import rope_frequencies, rope_inverse_fp32
+from mlx_omnia_amd.runtime import ops
 from oracle import attention as attn
 from oracle import rope
 from oracle.bf16 import from_float
@@ -29,6 +34,26 @@ def test_config_table_bit_equal_to_oracle():
     got = atlas.atlas.cpu().numpy()
     assert got.shape == (40960, 128)
     assert np.array_equal(got[:, :64], cos) and np.array_equal(got[:, 64:], sin)
+
+
+@pytest.mark.parametrize("pairs,first,rows", [(3, 0, 1000), (40, 33_554_000, 512),
+                                             (100, 33_554_300, 300), (64, 10**9, 64)])
+def test_entry_points_across_the_fast_reduction_limit(pairs, first, rows):
+    print(f"atlas entry points pairs={pairs} first={first} rows={rows}", flush=True)
+    width = 2 * pairs
+    out = torch.full((rows + 1, width), 7.0, device="cuda")   # the last row must stay untouched
+    freqs = torch.tensor(rope_frequencies(pairs, 1e4), dtype=torch.float64, device="cuda")
+    ops.rope_angle_atlas(freqs, first, rows, out=out[:rows])
+    cos, sin = rope.angle_table(rows, pairs, 1e4, first=first)
+    got = out.cpu().numpy()
+    assert np.array_equal(got[:rows, :pairs], cos) and np.array_equal(got[:rows, pairs:], sin)
+    assert (got[rows] == 7.0).all()
+    inverse = torch.tensor(rope_inverse_fp32(pairs, 1e4), dtype=torch.float32, device="cuda")
+    ops.rope_angle_atlas_fp32(inverse, first, rows, out=out[:rows])
+    cos, sin = rope.laguna_angle_table(rows, pairs, 1e4, first=first)
+    got = out.cpu().numpy()
+    assert np.array_equal(got[:rows, :pairs], cos) and np.array_equal(got[:rows, pairs:], sin)
+    assert (got[rows] == 7.0).all()
 
 
 def test_growth_keeps_old_rows_and_matches_oracle():
