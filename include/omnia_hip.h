@@ -318,7 +318,7 @@ int32_t omnia_moe_down_combine(const uint16_t* act, const uint16_t* weight, int6
  * little-endian bit stream of bits-wide values); scales, biases [experts, 2 * inner,
  * hidden / group_size] bf16; chosen [slots] int32; out [slots, inner] bf16. A non-null
  * shared_weight ([2 * inner, ...], with its own scales, biases, width and group) serves the
- * last slot, whose index is then not read. An index outside [0, experts) gives zeros.
+ * last slot, whose index is then ignored. An index outside [0, experts) gives zeros.
  * bits in {2, 3, 4, 5, 6, 8}, groups in {32, 64, 128} dividing hidden; hidden a multiple
  * of 32, at most 16384; limit >= 0 or +inf (none).
  * Replaces: core/kernels/gate_up/affine.py:24-191 (`AffineGateUp`, `moe_gateup_act`); Core

@@ -210,9 +210,18 @@ struct GateUpArgs {
   float limit;             // +inf: no clamp
 };
 
+// The lane's chunk of x for trip `trip` (lanes past the row's end re-read the last chunk).
+__device__ __forceinline__ void load_x_chunk(const GateUpArgs& a, int lane, int trip, u32x4 (&raw)[4]) {
+  const int c = min(lane + kWave * trip, a.hidden / kChunk - 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) raw[i] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[i];
+}
+
+// `first` holds the lane's chunk of x for trip 0, loaded by the caller before it read the
+// expert id (x does not depend on it).
 template <int B>
 __device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const Leaf& leaf, int64_t row0, int rows,
-                                             int lane, float (&r)[2 * kPairsPerWave]) {
+                                             int lane, const u32x4 (&first)[4], float (&r)[2 * kPairsPerWave]) {
   const int chunks = a.hidden / kChunk;
   const int64_t words = static_cast<int64_t>(a.hidden) * B / 32;
   const int groups = a.hidden / leaf.group;
@@ -222,6 +231,13 @@ __device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const Leaf& le
     // a lane past the row's end re-reads the last chunk and drops the term, and a row
     // past the wave's last pair re-reads the pair's last row (that sum is never stored).
     const int c = min(lane + kWave * trip, chunks - 1);
+    u32x4 raw[4];
+    if (trip == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) raw[i] = first[i];
+    } else {
+      load_x_chunk(a, lane, trip, raw);
+    }
     uint32_t w[2 * kPairsPerWave][B];
     uint32_t sb[2 * kPairsPerWave], bb[2 * kPairsPerWave];
 #pragma unroll
@@ -232,9 +248,6 @@ __device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const Leaf& le
       sb[i] = leaf.scales[g];
       bb[i] = leaf.biases[g];
     }
-    u32x4 raw[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) raw[i] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[i];
     __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
     uint32_t xq[16];
     const float xsum = pair_x<B>(raw, xq);
@@ -256,25 +269,31 @@ __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(
   uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + pair0;
   const bool shared = uses_shared(a.shared, slot, a.slots);
   const Leaf& leaf = shared ? a.shared : a.routed;
+  // The expert id (read for every slot, the shared one included, so the read is not in a
+  // branch) and then the lane's first chunk of x, which does not depend on it: the chunk's
+  // round trip overlaps the id's.
+  const int chosen = a.chosen[slot];
+  u32x4 first[4];
+  load_x_chunk(a, lane, 0, first);
+  __builtin_amdgcn_sched_barrier(0);   // the chunk's loads ahead of the wait for the id
   int64_t row0 = 2 * static_cast<int64_t>(pair0);
   if (!shared) {
-    const int expert = a.chosen[slot];
-    if (expert < 0 || expert >= a.experts) {
+    if (chosen < 0 || chosen >= a.experts) {
       if (lane < pairs) out[lane] = 0;
       return;
     }
-    row0 += static_cast<int64_t>(expert) * 2 * a.inner;
+    row0 += static_cast<int64_t>(chosen) * 2 * a.inner;
   }
   float r[2 * kPairsPerWave];
 #pragma unroll
   for (int i = 0; i < 2 * kPairsPerWave; ++i) r[i] = 0.0f;
   switch (leaf.bits) {  // wave-uniform
-    case 2: gate_up_rows<2>(a, leaf, row0, 2 * pairs, lane, r); break;
-    case 3: gate_up_rows<3>(a, leaf, row0, 2 * pairs, lane, r); break;
-    case 4: gate_up_rows<4>(a, leaf, row0, 2 * pairs, lane, r); break;
-    case 5: gate_up_rows<5>(a, leaf, row0, 2 * pairs, lane, r); break;
-    case 6: gate_up_rows<6>(a, leaf, row0, 2 * pairs, lane, r); break;
-    default: gate_up_rows<8>(a, leaf, row0, 2 * pairs, lane, r); break;
+    case 2: gate_up_rows<2>(a, leaf, row0, 2 * pairs, lane, first, r); break;
+    case 3: gate_up_rows<3>(a, leaf, row0, 2 * pairs, lane, first, r); break;
+    case 4: gate_up_rows<4>(a, leaf, row0, 2 * pairs, lane, first, r); break;
+    case 5: gate_up_rows<5>(a, leaf, row0, 2 * pairs, lane, first, r); break;
+    case 6: gate_up_rows<6>(a, leaf, row0, 2 * pairs, lane, first, r); break;
+    default: gate_up_rows<8>(a, leaf, row0, 2 * pairs, lane, first, r); break;
   }
   // Lane p takes pair p's sums and runs its activation.
   float gate_sum = 0.0f, up_sum = 0.0f;
@@ -314,14 +333,15 @@ struct DownArgs {
 };
 
 // The terms of one lane group's rows (rows group, group + kGroups, ... of the workgroup's
-// kDownRows) for the lane's chunk `part` of the slot's activation row: every load (each
-// row's words, scale and bias bits in registers of their own, the activation chunk, read
-// once for all the rows) goes out before any arithmetic, with no branch among them. A
+// kDownRows) for the lane's chunk `part` of the slot's activation row (`raw`, loaded by the
+// caller): every weight load (each row's words, scale and bias bits in registers of their
+// own) goes out before any arithmetic, with no branch among them; the activations are
+// paired while the rows arrive, and each row is summed as soon as its own words are in. A
 // lane past the row's last chunk re-reads that chunk and drops the term, and a row past
 // the last one re-reads the last (its sum is never used).
 template <int B, int kLanes>
 __device__ __forceinline__ void down_terms(const DownArgs& a, const Leaf& leaf, int64_t row_first,
-                                           int rows, int group, int part, int slot,
+                                           int rows, int group, int part, const u32x4 (&raw)[4],
                                            float (&t)[kDownRows * kLanes / kWave]) {
   constexpr int kGroups = kWave / kLanes;
   constexpr int kRowsPerGroup = kDownRows / kGroups;
@@ -339,10 +359,6 @@ __device__ __forceinline__ void down_terms(const DownArgs& a, const Leaf& leaf, 
     sb[q] = leaf.scales[g];
     bb[q] = leaf.biases[g];
   }
-  u32x4 raw[4];
-  const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) raw[j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
   __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
   uint32_t xq[16];
   const float xsum = pair_x<B>(raw, xq);
@@ -375,24 +391,33 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(
       a.residual, row_base + min(static_cast<int>(threadIdx.x % kDownRows), rows - 1), a.act);
   const bool shared = uses_shared(a.shared, slot, a.slots);
   const Leaf& leaf = shared ? a.shared : a.routed;
-  bool valid = true;
-  int64_t row_first = row_base;
-  if (!shared) {
-    const int expert = a.chosen[slot];
-    valid = expert >= 0 && expert < a.experts;   // uniform over the wave
-    row_first += static_cast<int64_t>(valid ? expert : 0) * a.hidden;
+  // The expert id (read for every slot, the shared one included, so the read is not in a
+  // branch) and then the slot's activation chunk, which does not depend on it: the chunk's
+  // round trip overlaps the id's.
+  const int chosen = a.chosen[slot];
+  u32x4 raw[4];
+  {
+    const int c = min(part, a.inner / kChunk - 1);
+    const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner + c * kChunk;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) raw[j] = reinterpret_cast<const u32x4*>(x)[j];
   }
+  __builtin_amdgcn_sched_barrier(0);   // the chunk's loads ahead of the wait for the id
+  // Selects, no branch (a branch would let the compiler sink the id's read into it).
+  const bool routed_ok = chosen >= 0 && chosen < a.experts;   // uniform over the wave
+  const bool valid = shared || routed_ok;
+  const int64_t row_first = row_base + static_cast<int64_t>(!shared && routed_ok ? chosen : 0) * a.hidden;
   float t[kRowsPerGroup];
 #pragma unroll
   for (int q = 0; q < kRowsPerGroup; ++q) t[q] = 0.0f;
   if (valid) {
     switch (leaf.bits) {  // wave-uniform
-      case 2: down_terms<2, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
-      case 3: down_terms<3, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
-      case 4: down_terms<4, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
-      case 5: down_terms<5, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
-      case 6: down_terms<6, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
-      default: down_terms<8, kLanes>(a, leaf, row_first, rows, group, part, slot, t); break;
+      case 2: down_terms<2, kLanes>(a, leaf, row_first, rows, group, part, raw, t); break;
+      case 3: down_terms<3, kLanes>(a, leaf, row_first, rows, group, part, raw, t); break;
+      case 4: down_terms<4, kLanes>(a, leaf, row_first, rows, group, part, raw, t); break;
+      case 5: down_terms<5, kLanes>(a, leaf, row_first, rows, group, part, raw, t); break;
+      case 6: down_terms<6, kLanes>(a, leaf, row_first, rows, group, part, raw, t); break;
+      default: down_terms<8, kLanes>(a, leaf, row_first, rows, group, part, raw, t); break;
     }
   }
 #pragma unroll
