@@ -131,21 +131,64 @@ __device__ __forceinline__ float gate_softplus1(float a, float a_log, float dt_b
 }
 
 // Even head count, 4-byte aligned rows: one pair of heads per lane. The tensor is small
-// (1.5 MB at the config) and each element carries three fp64 transcendentals, so the
-// grid is spread wide rather than vectorised deep.
-__global__ __launch_bounds__(kBlock) void gate_softplus_kernel(
-    const uint16_t* __restrict__ a, int64_t a_stride, const float* __restrict__ a_log,
-    const float* __restrict__ dt_bias, float* __restrict__ out, int64_t rows, int heads) {
-  const int head_pairs = heads / 2;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-  if (i >= rows * head_pairs) return;
-  const int64_t r = i / head_pairs;
-  const int h = static_cast<int>(i - r * head_pairs) * 2;
-  const uint32_t x = *reinterpret_cast<const uint32_t*>(a + r * a_stride + h);
-  const f32x2 la = *reinterpret_cast<const f32x2*>(a_log + h);
-  const f32x2 bb = *reinterpret_cast<const f32x2*>(dt_bias + h);
-  const f32x2 o = {gate_softplus1(bf16_lo(x), la.x, bb.x), gate_softplus1(bf16_hi(x), la.y, bb.y)};
-  *reinterpret_cast<f32x2*>(out + r * heads + h) = o;
+// (1.5 MB at the config) and each element carries fp64 transcendentals, so the grid is
+// spread wide rather than vectorised deep, and nothing divides: a block of kBlock threads
+// is 2^lane_bits head pairs (the power of two >= heads / 2, at most kBlock) by the rest
+// in rows, block b taking row block b / column_blocks and pair block b % column_blocks.
+// With at most kDecayHeads heads, the block holds -exp(A_log) of every head in LDS,
+// computed once per block rather than once per element (one fp64 exp of three).
+struct SoftplusArgs {
+  const uint16_t* a;
+  int64_t a_stride;
+  const float* a_log;
+  const float* dt_bias;
+  float* out;
+  int64_t rows;
+  int heads;
+  int lane_bits;
+  unsigned column_blocks;
+};
+
+constexpr int kDecayHeads = kBlock;
+
+__device__ __forceinline__ void softplus_block(const SoftplusArgs& p, unsigned b, float* decay) {
+  const int head_pairs = p.heads / 2;
+  const bool cached = p.heads <= kDecayHeads;   // then column_blocks == 1
+  unsigned row_block = b, column_block = 0;
+  if (p.column_blocks > 1) {   // block-uniform
+    row_block = b / p.column_blocks;
+    column_block = b - row_block * p.column_blocks;
+  }
+  const int pair = static_cast<int>(column_block << p.lane_bits) + static_cast<int>(threadIdx.x & ((1u << p.lane_bits) - 1));
+  const int64_t row = static_cast<int64_t>(row_block) * (kBlock >> p.lane_bits) + (threadIdx.x >> p.lane_bits);
+  const bool live = pair < head_pairs && row < p.rows;
+  // Every load first, with no branch among them (a thread past the end reads the last
+  // pair and leaves before any store): A_log for the decay table first, so that its
+  // wait leaves the others in flight while the table's fp64 exps run.
+  const int h = min(pair, head_pairs - 1) * 2;
+  const int64_t r = min(row, p.rows - 1);
+  const float table_log = p.a_log[min(static_cast<int>(threadIdx.x), p.heads - 1)];
+  const f32x2 bb = *reinterpret_cast<const f32x2*>(p.dt_bias + h);
+  const uint32_t x = *reinterpret_cast<const uint32_t*>(p.a + r * p.a_stride + h);
+  __builtin_amdgcn_sched_barrier(0);   // the loads in this order, ahead of the arithmetic
+  if (cached && static_cast<int>(threadIdx.x) < p.heads) {
+    decay[threadIdx.x] = -static_cast<float>(exp(static_cast<double>(table_log)));
+  }
+  lds_barrier();   // the table is LDS; the loads above stay in flight
+  if (!live) return;
+  f32x2 o;
+  if (cached) {  // the same fp32 steps as gate_softplus1
+    o = f32x2{decay[h] * softplus_f32(bf16_lo(x) + bb.x), decay[h + 1] * softplus_f32(bf16_hi(x) + bb.y)};
+  } else {
+    const f32x2 la = *reinterpret_cast<const f32x2*>(p.a_log + h);
+    o = f32x2{gate_softplus1(bf16_lo(x), la.x, bb.x), gate_softplus1(bf16_hi(x), la.y, bb.y)};
+  }
+  *reinterpret_cast<f32x2*>(p.out + r * p.heads + h) = o;
+}
+
+__global__ __launch_bounds__(kBlock) void gate_softplus_kernel(SoftplusArgs p) {
+  __shared__ float decay[kDecayHeads];
+  softplus_block(p, blockIdx.x, decay);
 }
 
 // Any head count or alignment: one element per lane.
@@ -163,6 +206,23 @@ unsigned blocks_for(int64_t items) {
   return static_cast<unsigned>((items + kBlock - 1) / kBlock);
 }
 
+// The gate-softplus grid over rows x heads / 2 pairs (heads even, positive).
+struct SoftplusGrid {
+  int lane_bits;
+  unsigned column_blocks;
+  int64_t blocks;
+};
+
+SoftplusGrid softplus_grid(int64_t rows, int64_t heads) {
+  const int64_t pairs = heads / 2;
+  int bits = 0;
+  while ((int64_t{1} << bits) < pairs && (1 << bits) < kBlock) ++bits;
+  const int64_t column_blocks = (pairs + (int64_t{1} << bits) - 1) >> bits;
+  const int64_t rows_per_block = kBlock >> bits;
+  return SoftplusGrid{bits, static_cast<unsigned>(column_blocks),
+                      (rows + rows_per_block - 1) / rows_per_block * column_blocks};
+}
+
 // Both gated activations of a layer in one grid (the SwiGLU and the gate-softplus of
 // configs[3]): blocks [0, softplus_blocks) run the gate-softplus, one pair of heads per
 // lane as gate_softplus_kernel does; the rest stream the SwiGLU, one vector per lane as
@@ -177,49 +237,15 @@ struct GatedArgs {
   int64_t rows;
   uint32_t row_vectors;
   int64_t vectors;
-  const uint16_t* a;
-  int64_t a_stride;
-  const float* a_log;
-  const float* dt_bias;
-  float* g;
-  int64_t a_rows;
-  int heads;
+  SoftplusArgs softplus;
   unsigned softplus_blocks;
 };
-
-// The gate-softplus blocks hold -exp(A_log) of up to kDecayHeads heads in LDS, each
-// computed once per block rather than once per element (one fp64 exp of three).
-constexpr int kDecayHeads = kBlock;
 
 template <bool kFlat>
 __global__ __launch_bounds__(kBlock) void gated_activations_kernel(GatedArgs p) {
   if (blockIdx.x < p.softplus_blocks) {  // block-uniform
     __shared__ float decay[kDecayHeads];
-    const bool cached = p.heads <= kDecayHeads;
-    // The thread's inputs go out before the decay table's load and barrier (a thread
-    // past the end reads the last pair and leaves before any store), so the two loads
-    // overlap instead of following each other.
-    const int head_pairs = p.heads / 2;
-    const int64_t n = p.a_rows * head_pairs;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    const int64_t ic = i < n ? i : n - 1;
-    const int64_t r = ic / head_pairs;
-    const int h = static_cast<int>(ic - r * head_pairs) * 2;
-    const uint32_t x = *reinterpret_cast<const uint32_t*>(p.a + r * p.a_stride + h);
-    const f32x2 bb = *reinterpret_cast<const f32x2*>(p.dt_bias + h);
-    if (cached && static_cast<int>(threadIdx.x) < p.heads) {
-      decay[threadIdx.x] = -static_cast<float>(exp(static_cast<double>(p.a_log[threadIdx.x])));
-    }
-    lds_barrier();   // the table is LDS; the loads above stay in flight
-    if (i >= n) return;
-    f32x2 o;
-    if (cached) {  // the same fp32 steps as gate_softplus1
-      o = f32x2{decay[h] * softplus_f32(bf16_lo(x) + bb.x), decay[h + 1] * softplus_f32(bf16_hi(x) + bb.y)};
-    } else {
-      const f32x2 la = *reinterpret_cast<const f32x2*>(p.a_log + h);
-      o = f32x2{gate_softplus1(bf16_lo(x), la.x, bb.x), gate_softplus1(bf16_hi(x), la.y, bb.y)};
-    }
-    *reinterpret_cast<f32x2*>(p.g + r * p.heads + h) = o;
+    softplus_block(p.softplus, blockIdx.x, decay);
     return;
   }
   const int64_t i = static_cast<int64_t>(blockIdx.x - p.softplus_blocks) * kBlock + threadIdx.x;
@@ -288,8 +314,11 @@ extern "C" int32_t omnia_gate_softplus(const uint16_t* a, int64_t a_stride, cons
   const bool paired = heads % 2 == 0 && a_stride % 2 == 0 && aligned(a, 4) &&
                       aligned(a_log, 8) && aligned(dt_bias, 8) && aligned(out, 8);
   if (paired) {
-    gate_softplus_kernel<<<blocks_for(rows * heads / 2), kBlock, 0, stream>>>(
-        a, a_stride, a_log, dt_bias, out, rows, static_cast<int>(heads));
+    const SoftplusGrid grid = softplus_grid(rows, heads);
+    OMNIA_REQUIRE(grid.blocks < (int64_t{1} << 31), "gate_softplus: grid too large");
+    gate_softplus_kernel<<<static_cast<unsigned>(grid.blocks), kBlock, 0, stream>>>(
+        SoftplusArgs{a, a_stride, a_log, dt_bias, out, rows, static_cast<int>(heads), grid.lane_bits,
+                     grid.column_blocks});
   } else {
     gate_softplus_scalar_kernel<<<blocks_for(rows * heads), kBlock, 0, stream>>>(
         a, a_stride, a_log, dt_bias, out, rows, static_cast<int>(heads));
@@ -330,12 +359,15 @@ extern "C" int32_t omnia_gated_activations(const uint16_t* gate, int64_t gate_st
   int32_t rc = check_device(stream);
   if (rc != 0) return rc;
   const int64_t vectors = rows * (inner / 8);
-  const int64_t softplus_blocks = (a_rows * (heads / 2) + kBlock - 1) / kBlock;
+  const SoftplusGrid softplus = softplus_grid(a_rows, heads);
+  const int64_t softplus_blocks = a_rows == 0 ? 0 : softplus.blocks;
   const int64_t swiglu_blocks = (vectors + kBlock - 1) / kBlock;
   OMNIA_REQUIRE(softplus_blocks + swiglu_blocks < (int64_t{1} << 31),
                 "gated_activations: grid too large");
   const GatedArgs p{gate, gate_stride, up, up_stride, y, rows, static_cast<uint32_t>(inner / 8),
-                    vectors, a, a_stride, a_log, dt_bias, g, a_rows, static_cast<int>(heads),
+                    vectors,
+                    SoftplusArgs{a, a_stride, a_log, dt_bias, g, a_rows, static_cast<int>(heads),
+                                 softplus.lane_bits, softplus.column_blocks},
                     static_cast<unsigned>(softplus_blocks)};
   const dim3 grid(static_cast<unsigned>(softplus_blocks + swiglu_blocks));
   if (gate_stride == inner && up_stride == inner) {

@@ -177,12 +177,16 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
 // the sort's rule of core/kernels/gate_up/kernel.py:23-36): slot + 1 rounds of a wave
 // argmin over (key, index), each removing its winner. Every wave of the slot computes it.
 // kKeys keys per lane (expert lane + 64 j), loaded at a clamped index with no branch (a
-// load in a branch makes the compiler wait on it); an index past the last is never chosen.
+// load in a branch makes the compiler wait on it) by ordinal_keys, ranked by
+// ordinal_expert; an index past the last is never chosen.
 template <int kKeys>
-__device__ __forceinline__ int ordinal_expert(const uint32_t* keys, int experts, int slot, int lane) {
-  uint32_t raw[kKeys];
+__device__ __forceinline__ void ordinal_keys(const uint32_t* keys, int experts, int lane, uint32_t (&raw)[kKeys]) {
 #pragma unroll
   for (int j = 0; j < kKeys; ++j) raw[j] = keys[min(lane + kWave * j, experts - 1)];
+}
+
+template <int kKeys>
+__device__ __forceinline__ int ordinal_expert(const uint32_t (&raw)[kKeys], int experts, int slot, int lane) {
   uint64_t mine[kKeys];
 #pragma unroll
   for (int j = 0; j < kKeys; ++j) {
@@ -211,8 +215,27 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   if (pair0 >= a.inner) return;  // whole wave; no barrier follows
   const int pairs = min(kPairsPerWave, a.inner - pair0);
   uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + pair0;
+  constexpr int kBatch = kTrips > 0 ? kTrips : kGateBatch;
+  const int chunks = a.hidden / kChunk;
+  // With the expert read from `chosen`, the first batch's chunks of x, which do not depend
+  // on it, are loaded before it is known, so their round trip overlaps the id's. (With the
+  // expert ranked from the ordinal keys here, x loaded ahead of the ranking measured no
+  // faster, and x stays with the codes.)
+  constexpr bool kEarlyX = kKeys == 0;
+  u32x4 x_first[kBatch][4];
+  if constexpr (kEarlyX) {
+#pragma unroll
+    for (int h = 0; h < kBatch; ++h) {
+      const int c = min(lane + h * kWave, chunks - 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x_first[h][j] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[j];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // the x loads ahead of the wait for the id
+  }
+  uint32_t key_bits[kKeys > 0 ? kKeys : 1];
+  if constexpr (kKeys > 0) ordinal_keys<kKeys>(a.keys, static_cast<int>(a.experts), lane, key_bits);
   int expert;
-  if constexpr (kKeys > 0) expert = ordinal_expert<kKeys>(a.keys, static_cast<int>(a.experts), slot, lane);
+  if constexpr (kKeys > 0) expert = ordinal_expert<kKeys>(key_bits, static_cast<int>(a.experts), slot, lane);
   else expert = a.chosen[slot];
   if (expert < 0 || expert >= a.experts) {
     if (lane < pairs) out[lane] = 0;
@@ -221,7 +244,6 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   constexpr int kRows = 2 * kPairsPerWave;
   const int rows = 2 * pairs;
   const int64_t row0 = static_cast<int64_t>(expert) * 2 * a.inner + 2 * static_cast<int64_t>(pair0);
-  const int chunks = a.hidden / kChunk;
   // The projection bias of the pair this lane activates (its gate and up rows), loaded
   // ahead of the codes.
   uint32_t gate_bias_bits = 0, up_bias_bits = 0;
@@ -230,7 +252,6 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
     gate_bias_bits = early_bf16_bits(a.stack.bias, at, a.x);
     up_bias_bits = early_bf16_bits(a.stack.bias, at + 1, a.x);
   }
-  constexpr int kBatch = kTrips > 0 ? kTrips : kGateBatch;
   const int trips = kTrips > 0 ? kTrips : (chunks + kWave - 1) / kWave;
   float r[kRows];
 #pragma unroll
@@ -252,7 +273,9 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
         s[h][i] = load_scales<F>(a.stack.scales, at);
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[h][j] = reinterpret_cast<const u32x4*>(a.x + c * kChunk)[j];
+      for (int j = 0; j < 4; ++j) {
+        x[h][j] = kEarlyX && t0 == 0 ? x_first[h][j] : reinterpret_cast<const u32x4*>(a.x + c * kChunk)[j];
+      }
     }
     __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
 #pragma unroll
@@ -344,10 +367,22 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
   const int slot = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
   const int row_base = xcd_contiguous_block(blockIdx.x, gridDim.x) * kDownRows;
   const int rows = min(kDownRows, a.hidden - row_base);
+  const int chunks = a.inner / kChunk;
+  // The slot's activations (shared by the group's rows), which do not depend on the
+  // expert: loaded before the expert id is waited on, so their round trip overlaps the
+  // id's. A lane past the row's last chunk re-reads that chunk.
+  const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
+  u32x4 xv[kSteps][4];
+#pragma unroll
+  for (int h = 0; h < kSteps; ++h) {
+    const int c = min(part + kLanes * h, chunks - 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xv[h][j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
+  }
+  __builtin_amdgcn_sched_barrier(0);   // the activation loads ahead of the wait for the id
   const int expert = a.chosen[slot];
   const bool valid = expert >= 0 && expert < a.experts;   // uniform over the wave
   const int64_t row0 = static_cast<int64_t>(valid ? expert : 0) * a.hidden + row_base;
-  const int chunks = a.inner / kChunk;
   // The epilogue's operands, loaded ahead of the codes: the slot's routing weight, the
   // projection bias of the row lane i takes, and the residual of the output row this
   // thread writes (rows past the last read the last).
@@ -359,14 +394,11 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
 #pragma unroll
   for (int q = 0; q < kRowsPerGroup; ++q) t[q] = 0.0f;
   if (valid) {
-    // Every load (codes, scale bits, the slot's activations, shared by the group's rows)
-    // is issued before any arithmetic, with no branch among them: a lane past the row's
-    // last chunk re-reads that chunk and drops the term, and a row past the last one
-    // re-reads the last (its sum is never used).
-    const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner;
+    // Every code and scale load is issued before any arithmetic, with no branch among
+    // them: a lane past the row's last chunk re-reads that chunk and drops the term, and
+    // a row past the last one re-reads the last (its sum is never used).
     u32x4 w[kSteps][kRowsPerGroup];
     uint32_t s[kSteps][kRowsPerGroup];
-    u32x4 xv[kSteps][4];
 #pragma unroll
     for (int h = 0; h < kSteps; ++h) {
       const int c = min(part + kLanes * h, chunks - 1);
@@ -376,8 +408,6 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
         w[h][q] = load_nt(a.stack.weight + at);
         s[h][q] = load_scales<F>(a.stack.scales, at);
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xv[h][j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
     }
     __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the arithmetic
 #pragma unroll
@@ -505,18 +535,21 @@ __global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_ke
       a.top_k > 0 ? a.weights[token * a.top_k + min(static_cast<int>(threadIdx.x % kMaxSharedSlots), a.top_k - 1)]
                   : 0.0f;
   for (int slot = wave; slot < slots; slot += waves) {   // uniform over the wave
-    const bool shared = slot == a.top_k;
-    const int expert = shared ? 0 : a.chosen[token * a.top_k + slot];
-    const bool valid = shared || (expert >= 0 && expert < a.experts);
-    const Stack& stack = shared ? a.shared : a.routed;
-    const int64_t row0 = (shared ? 0 : static_cast<int64_t>(valid ? expert : 0) * a.hidden) + row_base;
     // Every load (the activation chunk, each row's codes and scale bits) goes out before
     // any arithmetic, with no branch among them; a row past the last re-reads the last.
+    // The chunk first: it does not depend on the expert, so its round trip overlaps the
+    // id's.
     const u32x4* x = reinterpret_cast<const u32x4*>(
         a.act + (token * slots + slot) * a.inner + static_cast<int64_t>(c) * kChunk);
     u32x4 xv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) xv[j] = x[j];
+    __builtin_amdgcn_sched_barrier(0);   // the chunk's loads ahead of the wait for the id
+    const bool shared = slot == a.top_k;
+    const int expert = shared ? 0 : a.chosen[token * a.top_k + slot];
+    const bool valid = shared || (expert >= 0 && expert < a.experts);
+    const Stack& stack = shared ? a.shared : a.routed;
+    const int64_t row0 = (shared ? 0 : static_cast<int64_t>(valid ? expert : 0) * a.hidden) + row_base;
     u32x4 w[kRowsPerGroup];
     uint32_t s[kRowsPerGroup];
 #pragma unroll

@@ -90,6 +90,26 @@ def test_gate_softplus_scalar_path_and_specials():
     assert empty.shape == (0, 12)
 
 
+@pytest.mark.parametrize("rows,heads,pad", [(130, 6, 0), (3, 258, 2), (5, 600, 4), (257, 32, 6)])
+def test_gate_softplus_grid_shapes(rows, heads, pad):
+    """Pair counts that fill part of a workgroup's columns (the rest of it rows), span two
+    column blocks, or pass the decay table's 256 heads; rows that end mid-block; a row
+    stride past the heads. The fused launch's gate-softplus part on the same inputs."""
+    print(f"gate_softplus rows={rows} heads={heads} pad={pad}", flush=True)
+    rng = np.random.default_rng(heads + rows)
+    values = rng.standard_normal((rows, heads + pad)).astype(np.float32) * 8
+    a = from_float(values)
+    a_log = rng.uniform(0, 2.7, heads).astype(np.float32)
+    dt_bias = (0.5 * rng.standard_normal(heads)).astype(np.float32)
+    want = act.gate_softplus(a[:, :heads], a_log, dt_bias)
+    dev = to_device(a)[:, :heads]
+    got = ops.gate_softplus(dev, f32_to_device(a_log), f32_to_device(dt_bias)).cpu().numpy()
+    assert np.array_equal(got, want)
+    up = to_device(from_float(rng.standard_normal((2, 16)).astype(np.float32)))
+    _, g = ops.gated_activations(up, up, dev, f32_to_device(a_log), f32_to_device(dt_bias))
+    assert np.array_equal(g.cpu().numpy(), want)
+
+
 def test_golden_fixture():
     golden = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "activations.npz")
     y = ops.swiglu(to_device(golden["gate"]), to_device(golden["up"]))
