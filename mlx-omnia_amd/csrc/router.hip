@@ -465,7 +465,10 @@ __device__ __forceinline__ void write_winners_unnormalised(uint32_t chosen, cons
 // the probabilities themselves (write_winners_unnormalised). kShared: the row holds one
 // more logit after the routed ones, the shared expert's; slot k gets index `experts`
 // and weight sigmoid(logit), correctly rounded to fp32. The output row is k + kShared
-// slots long.
+// slots long. The shared slots of a workgroup's four rows are computed by one of its
+// waves, four lanes at once (the wave rotates with the workgroup, so that the waves
+// carrying them spread over the SIMDs): the fp64 sigmoid is one instruction stream
+// however many lanes run it, and one per row had cost every wave that stream.
 template <int V, bool kNormalize, bool kShared>
 __global__ __launch_bounds__(256) void softmax_topk_kernel(const uint16_t* __restrict__ logits,
                                                            int64_t stride, int64_t rows,
@@ -473,33 +476,45 @@ __global__ __launch_bounds__(256) void softmax_topk_kernel(const uint16_t* __res
                                                            int32_t* __restrict__ indices,
                                                            float* __restrict__ weights) {
   const int lane = threadIdx.x % kWave;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
-  if (row >= rows) return;
-  // Every load first, from a clamped index and with no branch; lanes past the experts
-  // then drop theirs.
+  const int wave = static_cast<int>(threadIdx.x / kWave);
+  const int64_t first_row = static_cast<int64_t>(blockIdx.x) * 4;
+  const int64_t row = first_row + wave;
+  const int slots = k + (kShared ? 1 : 0);
+  const bool owner = kShared && wave == static_cast<int>(blockIdx.x % 4);   // wave-uniform
+  // Every load first, from clamped indices and with no branch (a load in a branch makes
+  // the compiler wait on it at once): the row's logits (lanes past the experts then drop
+  // theirs; a row past the last reads the last) and the shared logits of the workgroup's
+  // rows, lane j < 4 holding row first_row + j's.
+  const int64_t load_row = min(row, rows - 1);
   uint16_t raw[V];
 #pragma unroll
-  for (int v = 0; v < V; ++v) raw[v] = logits[row * stride + min(lane + v * kWave, experts - 1)];
-  const uint16_t shared_raw = kShared ? logits[row * stride + experts] : uint16_t{0};
-  uint32_t keys[V];
+  for (int v = 0; v < V; ++v) raw[v] = logits[load_row * stride + min(lane + v * kWave, experts - 1)];
+  const int64_t shared_row = min(first_row + min(lane, 3), rows - 1);
+  const uint16_t shared_raw = kShared ? logits[shared_row * stride + experts] : uint16_t{0};
+  // The owner's sigmoids now, before any store of the wave is in flight (a wait behind a
+  // store would wait for the store too).
+  float shared_weight = 0.0f;
+  if (owner) shared_weight = sigmoid_rounded(bf16_to_f32(shared_raw));
+  if (row < rows) {   // wave-uniform; the owner of a short last workgroup still writes
+    uint32_t keys[V];
 #pragma unroll
-  for (int v = 0; v < V; ++v) {
-    const int e = lane + v * kWave;
-    const uint32_t key = route_key(raw[v], e);
-    keys[v] = e < experts ? key : 0u;
+    for (int v = 0; v < V; ++v) {
+      const int e = lane + v * kWave;
+      const uint32_t key = route_key(raw[v], e);
+      keys[v] = e < experts ? key : 0u;
+    }
+    uint32_t chosen;
+    select_topk<V>(keys, k, lane, chosen);
+    if (kNormalize) {
+      write_winners(chosen, k, lane, indices + row * slots, weights + row * slots);
+    } else {
+      write_winners_unnormalised<V>(chosen, raw, experts, k, lane, indices + row * slots,
+                                    weights + row * slots);
+    }
   }
-  uint32_t chosen;
-  select_topk<V>(keys, k, lane, chosen);
-  const int slots = k + (kShared ? 1 : 0);
-  if (kNormalize) {
-    write_winners(chosen, k, lane, indices + row * slots, weights + row * slots);
-  } else {
-    write_winners_unnormalised<V>(chosen, raw, experts, k, lane, indices + row * slots,
-                                  weights + row * slots);
-  }
-  if (kShared && lane == k) {
-    indices[row * slots + k] = experts;
-    weights[row * slots + k] = sigmoid_rounded(bf16_to_f32(shared_raw));
+  if (owner && lane < 4 && first_row + lane < rows) {
+    indices[shared_row * slots + k] = experts;
+    weights[shared_row * slots + k] = shared_weight;
   }
 }
 
