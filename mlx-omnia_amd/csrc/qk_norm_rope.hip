@@ -131,10 +131,12 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_kernel(Ro
   constexpr int kHeadsPerSlot = kWave / G;
   const int lane = threadIdx.x % kWave;
   const int parts = a.q_parts + a.k_parts;
-  const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
-  const int64_t t = unit / parts;
+  // A 32-bit division (the launch keeps the unit count below 2^32): a 64-bit one is a long
+  // instruction sequence ahead of every wave's first load.
+  const uint32_t unit = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  const int64_t t = unit / static_cast<uint32_t>(parts);
   if (t >= a.length) return;  // whole wave leaves together; no barrier follows
-  const int part = static_cast<int>(unit - t * parts);
+  const int part = static_cast<int>(unit - static_cast<uint32_t>(t) * static_cast<uint32_t>(parts));
   const bool is_query = part < a.q_parts;  // wave-uniform
   const int heads = is_query ? a.query_heads : a.kv_heads;
   const int slots = (heads + kHeadsPerSlot - 1) / kHeadsPerSlot;
@@ -323,14 +325,16 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
   int64_t t;
   int part;
   if constexpr (TABLE) {
-    // Slot-major: workgroup b takes slot b / groups, tokens 4 (b % groups) + wave.
-    const int64_t groups = (a.length + kWavesPerBlock - 1) / kWavesPerBlock;
-    part = static_cast<int>(blockIdx.x / groups);
-    t = (blockIdx.x - part * groups) * kWavesPerBlock + threadIdx.x / kWave;
+    // Slot-major on a 2-D grid (x fastest: the same order as one dimension of slot *
+    // groups + group, with no division): workgroup (g, slot) takes tokens 4 g + wave.
+    part = static_cast<int>(blockIdx.y);
+    t = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
   } else {
-    const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
-    t = unit / parts;
-    part = static_cast<int>(unit - t * parts);
+    // A 32-bit division (the launch keeps the unit count below 2^32): a 64-bit one is a
+    // long instruction sequence ahead of every wave's first load.
+    const uint32_t unit = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+    t = unit / static_cast<uint32_t>(parts);
+    part = static_cast<int>(unit - static_cast<uint32_t>(t) * static_cast<uint32_t>(parts));
   }
   if (t >= a.length) return;  // whole wave leaves together; no barrier follows
   const bool is_query = part < a.q_parts;   // wave-uniform
@@ -531,13 +535,15 @@ int32_t launch(RopeArgs a, int head_dim, hipStream_t stream, const char* name, i
     const int heads_per_slot = narrow ? wide_slot / 2 : wide_slot;  // heads of 2G lanes
     a.q_parts = (a.query_heads + heads_per_slot - 1) / heads_per_slot;
     a.k_parts = (a.kv_heads + heads_per_slot - 1) / heads_per_slot;
-    // With a table, every workgroup holds four tokens of one slot (the kernel's mapping).
+    // With a table, every workgroup holds four tokens of one slot (the kernel's mapping),
+    // grid (token groups, slots); without, the 1-D grid of units, fewer than 2^32.
     const int64_t groups = (a.length + kWavesPerBlock - 1) / kWavesPerBlock;
     const int64_t waves = a.length * (a.q_parts + a.k_parts);
-    const int64_t blocks =
-        TABLE ? groups * (a.q_parts + a.k_parts) : (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-    OMNIA_REQUIRE(blocks < (int64_t{1} << 31), std::string(name) + ": too many tokens x heads");
-    const dim3 grid(static_cast<unsigned>(blocks));
+    const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+    OMNIA_REQUIRE(groups < (int64_t{1} << 31) && blocks < (int64_t{1} << 30),
+                  std::string(name) + ": too many tokens x heads");
+    const dim3 grid = TABLE ? dim3(static_cast<unsigned>(groups), static_cast<unsigned>(a.q_parts + a.k_parts))
+                            : dim3(static_cast<unsigned>(blocks));
     const dim3 block(kWavesPerBlock * kWave);
     const bool scaled = TABLE && a.mscale != 1.0f;
 #define OMNIA_PAIRS(D, PPL)                                                   \
@@ -561,7 +567,7 @@ int32_t launch(RopeArgs a, int head_dim, hipStream_t stream, const char* name, i
   a.k_parts = (k_slots + spw - 1) / spw;
   const int64_t waves = a.length * (a.q_parts + a.k_parts);
   const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-  OMNIA_REQUIRE(blocks < (int64_t{1} << 31), std::string(name) + ": too many tokens x heads");
+  OMNIA_REQUIRE(blocks < (int64_t{1} << 30), std::string(name) + ": too many tokens x heads");
   const dim3 grid(static_cast<unsigned>(blocks));
   const dim3 block(kWavesPerBlock * kWave);
   switch (head_dim) {
