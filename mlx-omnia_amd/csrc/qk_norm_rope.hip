@@ -336,7 +336,12 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
     t = unit / static_cast<uint32_t>(parts);
     part = static_cast<int>(unit - static_cast<uint32_t>(t) * static_cast<uint32_t>(parts));
   }
-  if (t >= a.length) return;  // whole wave leaves together; no barrier follows
+  // No early exit: a wave past the last token (in the last token group only) computes the
+  // last token's values and stores nothing. With a branch here the compiler loaded the
+  // length alone, waited for it, and only then loaded the other arguments: two dependent
+  // scalar round trips ahead of the first vector load instead of one.
+  const bool token_live = t < a.length;
+  t = token_live ? t : a.length - 1;
   const bool is_query = part < a.q_parts;   // wave-uniform
   const int heads = is_query ? a.query_heads : a.kv_heads;
   const int slot = is_query ? part : part - a.q_parts;
@@ -458,7 +463,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
     o1[i] = pack_bf16(n1[j] * c[j] - n2[j] * s[j], n1[j + 1] * c[j + 1] - n2[j + 1] * s[j + 1]);
     o2[i] = pack_bf16(n1[j] * s[j] + n2[j] * c[j], n1[j + 1] * s[j + 1] + n2[j + 1] * c[j + 1]);
   }
-  if (live) {
+  if (live && token_live) {
     uint16_t* out = (is_query ? a.queries_out : a.keys_out) + (head * a.length + t) * D + base;
     store_words<W>(out, o1);
     store_words<W>(out + P, o2);
