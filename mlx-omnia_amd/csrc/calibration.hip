@@ -32,6 +32,9 @@ __global__ __launch_bounds__(kCopyBlock) void stream_copy_kernel(const u32x4* __
     const int64_t index = min(first + j * kCopyBlock, vectors - 1);
     held[j] = load_nt(src + index);
   }
+  // The loads stay ahead of the stores' branch (see keep_loaded).
+#pragma unroll
+  for (int j = 0; j < kVectors; ++j) keep_loaded(held[j]);
 #pragma unroll
   for (int j = 0; j < kVectors; ++j) {
     const int64_t index = first + j * kCopyBlock;

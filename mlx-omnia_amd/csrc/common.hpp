@@ -265,6 +265,16 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          false);
 }
 
+// Pins a loaded value where it stands: an empty asm that reads it, so the load is issued
+// (and waited on) here. Without it, a load whose only use sits under a later branch on a
+// kernel argument (a store past the end skipped) is moved into that branch, and the
+// branch's own scalar round trip for the argument then comes before the load's addresses
+// can be formed: two scalar round trips ahead of the first load instead of one.
+template <typename T>
+__device__ __forceinline__ void keep_loaded(const T& value) {
+  asm volatile("" ::"v"(value));
+}
+
 template <typename T>
 __device__ __forceinline__ T load_nt(const T* ptr) {
   return __builtin_nontemporal_load(ptr);

@@ -264,9 +264,14 @@ __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(
   const int lane = threadIdx.x % kWave;
   const int slot = blockIdx.y;
   const int pair0 = (blockIdx.x * kGateWaves + threadIdx.x / kWave) * kPairsPerWave;
-  if (pair0 >= a.inner) return;  // whole wave; no barrier follows
-  const int pairs = min(kPairsPerWave, a.inner - pair0);
-  uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + pair0;
+  // No early exit: a branch on the size made it a scalar round trip of its own ahead of
+  // the other arguments' (two before the first load). A wave past the last pair computes
+  // the last one and stores nothing.
+  const bool wave_live = pair0 < a.inner;
+  const int first_pair = wave_live ? pair0 : a.inner - 1;
+  const int pairs = min(kPairsPerWave, a.inner - first_pair);
+  const int stored = wave_live ? pairs : 0;
+  uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + first_pair;
   const bool shared = uses_shared(a.shared, slot, a.slots);
   const Leaf& leaf = shared ? a.shared : a.routed;
   // The expert id (read for every slot, the shared one included, so the read is not in a
@@ -276,10 +281,10 @@ __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(
   u32x4 first[4];
   load_x_chunk(a, lane, 0, first);
   __builtin_amdgcn_sched_barrier(0);   // the chunk's loads ahead of the wait for the id
-  int64_t row0 = 2 * static_cast<int64_t>(pair0);
+  int64_t row0 = 2 * static_cast<int64_t>(first_pair);
   if (!shared) {
     if (chosen < 0 || chosen >= a.experts) {
-      if (lane < pairs) out[lane] = 0;
+      if (lane < stored) out[lane] = 0;
       return;
     }
     row0 += static_cast<int64_t>(chosen) * 2 * a.inner;
@@ -313,7 +318,7 @@ __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(
   const float den = 1.0f + expf(-g);
   const float sig = round_bf16(1.0f / den);
   const float act = round_bf16(g * sig);
-  if (lane < pairs) out[lane] = f32_to_bf16(act * u);
+  if (lane < stored) out[lane] = f32_to_bf16(act * u);
 }
 
 // ---- down_combine -------------------------------------------------------------------

@@ -212,9 +212,14 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   const int lane = threadIdx.x % kWave;
   const int slot = blockIdx.y;
   const int pair0 = (blockIdx.x * kGateWaves + threadIdx.x / kWave) * kPairsPerWave;
-  if (pair0 >= a.inner) return;  // whole wave; no barrier follows
-  const int pairs = min(kPairsPerWave, a.inner - pair0);
-  uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + pair0;
+  // No early exit: a branch on the size made it a scalar round trip of its own ahead of
+  // the other arguments' (two before the first load). A wave past the last pair computes
+  // the last one and stores nothing.
+  const bool wave_live = pair0 < a.inner;
+  const int first_pair = wave_live ? pair0 : a.inner - 1;
+  const int pairs = min(kPairsPerWave, a.inner - first_pair);
+  const int stored = wave_live ? pairs : 0;
+  uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + first_pair;
   constexpr int kBatch = kTrips > 0 ? kTrips : kGateBatch;
   const int chunks = a.hidden / kChunk;
   // With the expert read from `chosen`, the first batch's chunks of x, which do not depend
@@ -238,12 +243,12 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   if constexpr (kKeys > 0) expert = ordinal_expert<kKeys>(key_bits, static_cast<int>(a.experts), slot, lane);
   else expert = a.chosen[slot];
   if (expert < 0 || expert >= a.experts) {
-    if (lane < pairs) out[lane] = 0;
+    if (lane < stored) out[lane] = 0;
     return;
   }
   constexpr int kRows = 2 * kPairsPerWave;
   const int rows = 2 * pairs;
-  const int64_t row0 = static_cast<int64_t>(expert) * 2 * a.inner + 2 * static_cast<int64_t>(pair0);
+  const int64_t row0 = static_cast<int64_t>(expert) * 2 * a.inner + 2 * static_cast<int64_t>(first_pair);
   // The projection bias of the pair this lane activates (its gate and up rows), loaded
   // ahead of the codes.
   uint32_t gate_bias_bits = 0, up_bias_bits = 0;
@@ -297,7 +302,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
     gate_sum = lane == p ? gp : gate_sum;
     up_sum = lane == p ? up : up_sum;
   }
-  if (lane >= pairs) return;
+  if (lane >= stored) return;
   if constexpr (F == Fp4::kMx) {
     float gate_bias = 0.0f, up_bias = 0.0f;
     if (a.stack.bias != nullptr) {
