@@ -36,6 +36,14 @@ FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # gfx950 can hand a kernel's leading scalar and pointer arguments to it in user
+    # SGPRs at wave launch (kernarg preloading, LLVM AMDGPUUsage "Preloaded Kernel
+    # Arguments"): no scalar load round trip before the first vector load. Arguments
+    # passed as a struct by value are not preloaded; those kernels are unchanged. Each
+    # kernel keeps a compatibility entry that loads the arguments itself, which firmware
+    # without preloading runs instead.
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-command-line-argument",
     f"-I{INCLUDE}",
