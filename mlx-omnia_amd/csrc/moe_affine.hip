@@ -260,27 +260,41 @@ __device__ __forceinline__ void gate_up_rows(const GateUpArgs& a, const Leaf& le
   }
 }
 
-__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(GateUpArgs a) {
+// The arguments the first loads need come first, as scalars (copies of GateUpArgs fields):
+// gfx950 preloads a kernel's leading scalar and pointer arguments into SGPRs at wave
+// launch, so the id's and x's loads go out with no scalar round trip ahead of them, and
+// GateUpArgs is loaded while they are in flight (5.43 -> 5.29 us at the decode shape).
+__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(
+    const uint16_t* x, const int32_t* chosen_ids, int hidden, int inner, GateUpArgs a) {
   const int lane = threadIdx.x % kWave;
   const int slot = blockIdx.y;
   const int pair0 = (blockIdx.x * kGateWaves + threadIdx.x / kWave) * kPairsPerWave;
   // No early exit: a branch on the size made it a scalar round trip of its own ahead of
   // the other arguments' (two before the first load). A wave past the last pair computes
   // the last one and stores nothing.
-  const bool wave_live = pair0 < a.inner;
-  const int first_pair = wave_live ? pair0 : a.inner - 1;
-  const int pairs = min(kPairsPerWave, a.inner - first_pair);
+  const bool wave_live = pair0 < inner;
+  const int first_pair = wave_live ? pair0 : inner - 1;
+  const int pairs = min(kPairsPerWave, inner - first_pair);
   const int stored = wave_live ? pairs : 0;
+  // The expert id, then the lane's first chunk of x, which does not depend on it: the
+  // chunk's round trip overlaps the id's. The id is read through the vector path (every
+  // lane reads the same word): a scalar read was sunk by the compiler into the branch that
+  // uses it, behind the wait for GateUpArgs, while vector loads return in order, so
+  // waiting for the id waits for nothing issued after it.
+  int zero = 0;
+  asm volatile("" : "+v"(zero));   // a zero the compiler cannot see as uniform
+  const int chosen_v = chosen_ids[slot + zero];
+  u32x4 first[4];
+  {
+    const int c = min(lane, hidden / kChunk - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) first[i] = reinterpret_cast<const u32x4*>(x + c * kChunk)[i];
+  }
+  __builtin_amdgcn_sched_barrier(0);   // the chunk's loads ahead of the wait for the id
+  const int chosen = __builtin_amdgcn_readfirstlane(chosen_v);
   uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + first_pair;
   const bool shared = uses_shared(a.shared, slot, a.slots);
   const Leaf& leaf = shared ? a.shared : a.routed;
-  // The expert id (read for every slot, the shared one included, so the read is not in a
-  // branch) and then the lane's first chunk of x, which does not depend on it: the chunk's
-  // round trip overlaps the id's.
-  const int chosen = a.chosen[slot];
-  u32x4 first[4];
-  load_x_chunk(a, lane, 0, first);
-  __builtin_amdgcn_sched_barrier(0);   // the chunk's loads ahead of the wait for the id
   int64_t row0 = 2 * static_cast<int64_t>(first_pair);
   if (!shared) {
     if (chosen < 0 || chosen >= a.experts) {
@@ -378,38 +392,62 @@ __device__ __forceinline__ void down_terms(const DownArgs& a, const Leaf& leaf, 
 // One wave per slot; kLanes lanes across each row (16, 32 or 64: the fewest that cover
 // the row's chunks), so each lane holds one activation chunk for the rows of its group.
 template <int kLanes>
-__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(DownArgs a) {
+// As in the gate/up kernel, the arguments the first loads need come first, as scalars
+// (copies of DownArgs fields and the grid size), preloaded into SGPRs at wave launch
+// (4.57 -> 4.36 us at the decode shape).
+__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(
+    const uint16_t* act, const int32_t* chosen_ids, const float* route_weights,
+    const uint16_t* residual, int inner, int hidden, int blocks, DownArgs a) {
   constexpr int kGroups = kWave / kLanes;
   constexpr int kRowsPerGroup = kDownRows / kGroups;
   __shared__ float partial[kMaxDownSlots][kDownRows];
   const int lane = threadIdx.x % kWave;
-  // One wave per slot; uniform, so its routing entries are scalar loads.
+  // One wave per slot.
   const int slot = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-  const int row_base = xcd_contiguous_block(blockIdx.x, gridDim.x) * kDownRows;
-  const int rows = min(kDownRows, a.hidden - row_base);
+  const int row_base = xcd_contiguous_block(blockIdx.x, blocks) * kDownRows;
+  const int rows = min(kDownRows, hidden - row_base);
   const int group = lane / kLanes;
   const int part = lane % kLanes;
-  // The epilogue's operands, loaded ahead of the weights: the slot's routing weight and
+  // The slot's routing entries (weight and expert id) first, through the vector path
+  // (every lane of the wave reads the same word): vector loads return in order, so waiting
+  // for them waits for nothing issued after them. As scalar reads, the compiler issued
+  // them after DownArgs' loads and waited for those first (one register was shared). Then
   // the residual of the output row this thread writes (rows past the last read the last).
-  const float route_weight = a.weights[slot];
+  const int slot_lanes = static_cast<int>(threadIdx.x / kWave);
+  const float route_weight_v = route_weights[slot_lanes];
+  const int chosen_v = chosen_ids[slot_lanes];
   const uint32_t resid = early_bf16_bits(
-      a.residual, row_base + min(static_cast<int>(threadIdx.x % kDownRows), rows - 1), a.act);
-  const bool shared = uses_shared(a.shared, slot, a.slots);
-  const Leaf& leaf = shared ? a.shared : a.routed;
-  // The expert id (read for every slot, the shared one included, so the read is not in a
-  // branch) and then the slot's activation chunk, which does not depend on it: the chunk's
-  // round trip overlaps the id's.
-  const int chosen = a.chosen[slot];
+      residual, row_base + min(static_cast<int>(threadIdx.x % kDownRows), rows - 1), act);
+  // The slot's activation chunk, which does not depend on the id: its round trip overlaps
+  // the id's.
   u32x4 raw[4];
   {
-    const int c = min(part, a.inner / kChunk - 1);
-    const uint16_t* x = a.act + static_cast<int64_t>(slot) * a.inner + c * kChunk;
+    const int c = min(part, inner / kChunk - 1);
+    const uint16_t* x = act + static_cast<int64_t>(slot) * inner + c * kChunk;
 #pragma unroll
     for (int j = 0; j < 4; ++j) raw[j] = reinterpret_cast<const u32x4*>(x)[j];
   }
   __builtin_amdgcn_sched_barrier(0);   // the chunk's loads ahead of the wait for the id
+  const int chosen = __builtin_amdgcn_readfirstlane(chosen_v);
+  const float route_weight = __builtin_bit_cast(
+      float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, route_weight_v)));
+  // The leaf field by field (selecting the struct itself selected its address in the
+  // argument segment and loaded the fields from there: one more dependent scalar round
+  // trip), and every scalar the weights' addresses need taken together, so one wait covers
+  // DownArgs' loads.
+  const bool shared = uses_shared(a.shared, slot, a.slots);
+  Leaf leaf;
+  leaf.weight = shared ? a.shared.weight : a.routed.weight;
+  leaf.scales = shared ? a.shared.scales : a.routed.scales;
+  leaf.biases = shared ? a.shared.biases : a.routed.biases;
+  leaf.bits = shared ? a.shared.bits : a.routed.bits;
+  leaf.group = shared ? a.shared.group : a.routed.group;
+  const int64_t experts = a.experts;
+  asm volatile("" ::"s"(chosen), "s"(leaf.weight), "s"(leaf.scales), "s"(leaf.biases), "s"(leaf.bits),
+               "s"(leaf.group), "s"(experts));
+  __builtin_amdgcn_sched_barrier(0);
   // Selects, no branch (a branch would let the compiler sink the id's read into it).
-  const bool routed_ok = chosen >= 0 && chosen < a.experts;   // uniform over the wave
+  const bool routed_ok = chosen >= 0 && chosen < experts;   // uniform over the wave
   const bool valid = shared || routed_ok;
   const int64_t row_first = row_base + static_cast<int64_t>(!shared && routed_ok ? chosen : 0) * a.hidden;
   float t[kRowsPerGroup];
@@ -484,7 +522,7 @@ extern "C" int32_t omnia_moe_gate_up_affine(
                static_cast<int>(slots), limit};
   const int64_t waves = (inner + kPairsPerWave - 1) / kPairsPerWave;
   const dim3 grid(static_cast<unsigned>((waves + kGateWaves - 1) / kGateWaves), static_cast<unsigned>(slots));
-  moe_gate_up_affine_kernel<<<grid, kGateWaves * kWave, 0, stream>>>(a);
+  moe_gate_up_affine_kernel<<<grid, kGateWaves * kWave, 0, stream>>>(a.x, a.chosen, a.hidden, a.inner, a);
   return launched("moe_gate_up_affine");
 }
 
@@ -524,11 +562,14 @@ extern "C" int32_t omnia_moe_down_combine_affine(
   static_assert(kMaxInner / kChunk <= kWave, "a row's chunks fit one wave");
   const int64_t chunks = inner / kChunk;
   if (chunks <= 16) {
-    moe_down_affine_kernel<16><<<grid, block, 0, stream>>>(a);
+    moe_down_affine_kernel<16><<<grid, block, 0, stream>>>(
+        a.act, a.chosen, a.weights, a.residual, a.inner, a.hidden, static_cast<int>(grid.x), a);
   } else if (chunks <= 32) {
-    moe_down_affine_kernel<32><<<grid, block, 0, stream>>>(a);
+    moe_down_affine_kernel<32><<<grid, block, 0, stream>>>(
+        a.act, a.chosen, a.weights, a.residual, a.inner, a.hidden, static_cast<int>(grid.x), a);
   } else {
-    moe_down_affine_kernel<64><<<grid, block, 0, stream>>>(a);
+    moe_down_affine_kernel<64><<<grid, block, 0, stream>>>(
+        a.act, a.chosen, a.weights, a.residual, a.inner, a.hidden, static_cast<int>(grid.x), a);
   }
   return launched("moe_down_combine_affine");
 }
