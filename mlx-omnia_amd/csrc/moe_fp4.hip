@@ -227,6 +227,13 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   // expert ranked from the ordinal keys here, x loaded ahead of the ranking measured no
   // faster, and x stays with the codes.)
   constexpr bool kEarlyX = kKeys == 0;
+  // The id is read through the vector path (every lane reads the same word), ahead of x:
+  // vector loads return in order, so waiting for it waits for nothing issued after it,
+  // where a scalar read went out only after the kernel's argument loads had returned.
+  int zero = 0;
+  asm volatile("" : "+v"(zero));   // a zero the compiler cannot see as uniform
+  int chosen_v = 0;
+  if constexpr (kEarlyX) chosen_v = a.chosen[slot + zero];
   u32x4 x_first[kBatch][4];
   if constexpr (kEarlyX) {
 #pragma unroll
@@ -238,10 +245,16 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
     __builtin_amdgcn_sched_barrier(0);   // the x loads ahead of the wait for the id
   }
   uint32_t key_bits[kKeys > 0 ? kKeys : 1];
-  if constexpr (kKeys > 0) ordinal_keys<kKeys>(a.keys, static_cast<int>(a.experts), lane, key_bits);
+  if constexpr (kKeys > 0) {
+    ordinal_keys<kKeys>(a.keys, static_cast<int>(a.experts), lane, key_bits);
+    __builtin_amdgcn_sched_barrier(0);   // the keys' loads ahead of the wait below
+  }
+  // The stack's pointers, taken here, ahead of the branch on the id: the compiler otherwise
+  // loaded them behind it, one more scalar round trip ahead of the codes.
+  asm volatile("" ::"s"(a.stack.weight), "s"(a.stack.scales), "s"(a.stack.bias));
   int expert;
   if constexpr (kKeys > 0) expert = ordinal_expert<kKeys>(key_bits, static_cast<int>(a.experts), slot, lane);
-  else expert = a.chosen[slot];
+  else expert = __builtin_amdgcn_readfirstlane(chosen_v);
   if (expert < 0 || expert >= a.experts) {
     if (lane < stored) out[lane] = 0;
     return;
@@ -327,21 +340,41 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
   }
 }
 
+// The arguments the first loads need come first, as scalars (copies of GateUpArgs fields,
+// which replace the struct's own): gfx950 preloads a kernel's leading scalar and pointer
+// arguments into SGPRs at wave launch, so the id's, the keys' and x's loads go out with
+// no scalar round trip ahead of them, and the rest of GateUpArgs is loaded while they are
+// in flight.
+#define OMNIA_GATE_UP_LEADING                                                              \
+  const uint16_t *x, const int32_t *chosen, const uint32_t *keys, int64_t experts, int hidden, \
+      int inner, GateUpArgs a
+#define OMNIA_GATE_UP_REPLACE \
+  a.x = x;                    \
+  a.chosen = chosen;          \
+  a.keys = keys;              \
+  a.experts = experts;        \
+  a.hidden = hidden;          \
+  a.inner = inner
+
 template <int kTrips>
-__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_mxfp4_kernel(GateUpArgs a) {
+__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_mxfp4_kernel(OMNIA_GATE_UP_LEADING) {
+  OMNIA_GATE_UP_REPLACE;
   gate_up_body<Fp4::kMx, kTrips>(a);
 }
 
 template <int kTrips, int kKeys>
-__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_nvfp4_kernel(GateUpArgs a) {
+__global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_nvfp4_kernel(OMNIA_GATE_UP_LEADING) {
+  OMNIA_GATE_UP_REPLACE;
   gate_up_body<Fp4::kNv, kTrips, kKeys>(a);
 }
 
+#define OMNIA_GATE_UP_ARGS a.x, a.chosen, a.keys, a.experts, a.hidden, a.inner, a
+
 template <int kKeys>
 void launch_nvfp4_gate_up(int64_t trips, dim3 grid, dim3 block, hipStream_t stream, const GateUpArgs& a) {
-  if (trips == 1) moe_gate_up_nvfp4_kernel<1, kKeys><<<grid, block, 0, stream>>>(a);
-  else if (trips == 2) moe_gate_up_nvfp4_kernel<2, kKeys><<<grid, block, 0, stream>>>(a);
-  else moe_gate_up_nvfp4_kernel<0, kKeys><<<grid, block, 0, stream>>>(a);
+  if (trips == 1) moe_gate_up_nvfp4_kernel<1, kKeys><<<grid, block, 0, stream>>>(OMNIA_GATE_UP_ARGS);
+  else if (trips == 2) moe_gate_up_nvfp4_kernel<2, kKeys><<<grid, block, 0, stream>>>(OMNIA_GATE_UP_ARGS);
+  else moe_gate_up_nvfp4_kernel<0, kKeys><<<grid, block, 0, stream>>>(OMNIA_GATE_UP_ARGS);
 }
 
 // ---- down_combine -------------------------------------------------------------------
@@ -362,17 +395,28 @@ struct DownArgs {
 // kLanes lanes run across each row (64, or 32 for short rows: the wave's two halves then
 // take rows h and h + 2); kSteps = ceil(inner / (32 * kLanes)) chunks per lane.
 template <Fp4 F, int kSteps, int kLanes = kWave>
-__device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kMaxDownSlots][kDownRows]) {
+__device__ __forceinline__ void down_body(const DownArgs& a, int blocks,
+                                          float (&partial)[kMaxDownSlots][kDownRows]) {
   constexpr int kHalves = kWave / kLanes;            // row groups per wave
   constexpr int kRowsPerGroup = kDownRows / kHalves;
   const int lane = threadIdx.x % kWave;
   const int part = lane % kLanes;
   const int group = lane / kLanes;
-  // One wave per slot; uniform, so its routing entries are scalar loads.
+  // One wave per slot.
   const int slot = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-  const int row_base = xcd_contiguous_block(blockIdx.x, gridDim.x) * kDownRows;
+  const int row_base = xcd_contiguous_block(blockIdx.x, blocks) * kDownRows;
   const int rows = min(kDownRows, a.hidden - row_base);
   const int chunks = a.inner / kChunk;
+  // The slot's routing entries (expert id and weight) first, through the vector path
+  // (every lane of the wave reads the same word): vector loads return in order, so waiting
+  // for them waits for nothing issued after them, where scalar reads went out only after
+  // the kernel's argument loads had returned. Then the residual of the output row this
+  // thread writes (rows past the last read the last).
+  const int slot_lanes = static_cast<int>(threadIdx.x / kWave);
+  const int chosen_v = a.chosen[slot_lanes];
+  const float route_weight_v = a.weights[slot_lanes];
+  const uint32_t resid = early_bf16_bits(
+      a.residual, row_base + min(static_cast<int>(threadIdx.x % kDownRows), rows - 1), a.act);
   // The slot's activations (shared by the group's rows), which do not depend on the
   // expert: loaded before the expert id is waited on, so their round trip overlaps the
   // id's. A lane past the row's last chunk re-reads that chunk.
@@ -385,16 +429,16 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
     for (int j = 0; j < 4; ++j) xv[h][j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
   }
   __builtin_amdgcn_sched_barrier(0);   // the activation loads ahead of the wait for the id
-  const int expert = a.chosen[slot];
+  // The stack's pointers, taken here with the id: the compiler otherwise loaded them behind
+  // the id's wait, one more scalar round trip ahead of the codes.
+  asm volatile("" ::"s"(a.stack.weight), "s"(a.stack.scales), "s"(a.stack.bias));
+  const int expert = __builtin_amdgcn_readfirstlane(chosen_v);
+  const float route_weight = __builtin_bit_cast(
+      float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, route_weight_v)));
   const bool valid = expert >= 0 && expert < a.experts;   // uniform over the wave
   const int64_t row0 = static_cast<int64_t>(valid ? expert : 0) * a.hidden + row_base;
-  // The epilogue's operands, loaded ahead of the codes: the slot's routing weight, the
-  // projection bias of the row lane i takes, and the residual of the output row this
-  // thread writes (rows past the last read the last).
-  const float route_weight = a.weights[slot];
+  // The projection bias of the row lane i takes, loaded ahead of the codes.
   const uint32_t bias = early_bf16_bits(a.stack.bias, row0 + min(lane, rows - 1), a.act);
-  const uint32_t resid = early_bf16_bits(
-      a.residual, row_base + min(static_cast<int>(threadIdx.x % kDownRows), rows - 1), a.act);
   float t[kRowsPerGroup];
 #pragma unroll
   for (int q = 0; q < kRowsPerGroup; ++q) t[q] = 0.0f;
@@ -467,17 +511,37 @@ __device__ __forceinline__ void down_body(const DownArgs& a, float (&partial)[kM
   }
 }
 
+// As in the gate/up kernels, the arguments the first loads need come first, as scalars
+// (copies of DownArgs fields, which replace the struct's own, and the grid size),
+// preloaded into SGPRs at wave launch.
+#define OMNIA_DOWN_LEADING                                                                  \
+  const uint16_t *act, const int32_t *chosen, const float *weights, const uint16_t *residual, \
+      int64_t experts, int hidden, int inner, int blocks, DownArgs a
+#define OMNIA_DOWN_REPLACE \
+  a.act = act;             \
+  a.chosen = chosen;       \
+  a.weights = weights;     \
+  a.residual = residual;   \
+  a.experts = experts;     \
+  a.hidden = hidden;       \
+  a.inner = inner
+
 template <int kSteps>
-__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_mxfp4_kernel(DownArgs a) {
+__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_mxfp4_kernel(OMNIA_DOWN_LEADING) {
   __shared__ float partial[kMaxDownSlots][kDownRows];
-  down_body<Fp4::kMx, kSteps>(a, partial);
+  OMNIA_DOWN_REPLACE;
+  down_body<Fp4::kMx, kSteps>(a, blocks, partial);
 }
 
 template <int kSteps, int kLanes>
-__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_nvfp4_kernel(DownArgs a) {
+__global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_nvfp4_kernel(OMNIA_DOWN_LEADING) {
   __shared__ float partial[kMaxDownSlots][kDownRows];
-  down_body<Fp4::kNv, kSteps, kLanes>(a, partial);
+  OMNIA_DOWN_REPLACE;
+  down_body<Fp4::kNv, kSteps, kLanes>(a, blocks, partial);
 }
+
+#define OMNIA_DOWN_ARGS \
+  a.act, a.chosen, a.weights, a.residual, a.experts, a.hidden, a.inner, static_cast<int>(grid.x), a
 
 // ---- down_combine with the unrouted slot (the packed NVFP4 form) --------------------
 //
@@ -512,8 +576,21 @@ struct SharedDownArgs {
 // kLanes lanes run across each row (16, 32 or 64: the fewest that give each lane one
 // 32-value chunk), so a wave holds kWave / kLanes row groups, each taking every
 // (kWave / kLanes)-th row of the workgroup with the slot's activation chunk loaded once.
+// The arguments the first loads need come first, as scalars (copies of SharedDownArgs
+// fields, which replace the struct's own, and the grid's width), preloaded into SGPRs at
+// wave launch.
 template <int kLanes>
-__global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_kernel(SharedDownArgs a) {
+__global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_kernel(
+    const uint16_t* act, const int32_t* chosen, const float* weights, const uint16_t* residual,
+    int64_t experts, int hidden, int inner, int top_k, int blocks, SharedDownArgs a) {
+  a.act = act;
+  a.chosen = chosen;
+  a.weights = weights;
+  a.residual = residual;
+  a.experts = experts;
+  a.hidden = hidden;
+  a.inner = inner;
+  a.top_k = top_k;
   constexpr int kGroups = kWave / kLanes;
   constexpr int kRowsPerGroup = kSharedRows / kGroups;
   __shared__ float term[kMaxSharedSlots][kSharedRows];
@@ -521,11 +598,12 @@ __global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_ke
   const int lane = threadIdx.x % kWave;
   const int part = lane % kLanes;
   const int group = lane / kLanes;
-  // Uniform, so each slot's expert id is a scalar load.
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
-  const int waves = blockDim.x / kWave;
+  const int waves = min(a.top_k + 1, kSharedWaves);   // the launch's block: no argument load
   const int64_t token = blockIdx.y;
-  const int row_base = xcd_contiguous_block(blockIdx.x, gridDim.x) * kSharedRows;
+  const int row_base = xcd_contiguous_block(blockIdx.x, blocks) * kSharedRows;
+  int zero = 0;
+  asm volatile("" : "+v"(zero));   // a zero the compiler cannot see as uniform
   const int rows = min(kSharedRows, a.hidden - row_base);
   const int slots = a.top_k + 1;
   const int chunks = a.inner / kChunk;
@@ -542,18 +620,27 @@ __global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_ke
   for (int slot = wave; slot < slots; slot += waves) {   // uniform over the wave
     // Every load (the activation chunk, each row's codes and scale bits) goes out before
     // any arithmetic, with no branch among them; a row past the last re-reads the last.
-    // The chunk first: it does not depend on the expert, so its round trip overlaps the
-    // id's.
+    // The expert id first, through the vector path (every lane reads the same word; the
+    // shared slot reads the first word of act instead, as `chosen` may be null): vector
+    // loads return in order, so waiting for it waits for nothing issued after it. Then
+    // the chunk: it does not depend on the expert, so its round trip overlaps the id's.
+    const bool shared = slot == a.top_k;
+    const int32_t* ids = shared ? reinterpret_cast<const int32_t*>(a.act) : a.chosen;
+    const int chosen_v = ids[(shared ? 0 : token * a.top_k + slot) + zero];
     const u32x4* x = reinterpret_cast<const u32x4*>(
         a.act + (token * slots + slot) * a.inner + static_cast<int64_t>(c) * kChunk);
     u32x4 xv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) xv[j] = x[j];
     __builtin_amdgcn_sched_barrier(0);   // the chunk's loads ahead of the wait for the id
-    const bool shared = slot == a.top_k;
-    const int expert = shared ? 0 : a.chosen[token * a.top_k + slot];
+    // The stack field by field (selecting the struct itself selected its address in the
+    // argument segment and loaded the fields from there, behind the id's wait).
+    Stack stack;
+    stack.weight = shared ? a.shared.weight : a.routed.weight;
+    stack.scales = shared ? a.shared.scales : a.routed.scales;
+    asm volatile("" ::"s"(stack.weight), "s"(stack.scales));
+    const int expert = shared ? 0 : __builtin_amdgcn_readfirstlane(chosen_v);
     const bool valid = shared || (expert >= 0 && expert < a.experts);
-    const Stack& stack = shared ? a.shared : a.routed;
     const int64_t row0 = (shared ? 0 : static_cast<int64_t>(valid ? expert : 0) * a.hidden) + row_base;
     u32x4 w[kRowsPerGroup];
     uint32_t s[kRowsPerGroup];
@@ -617,9 +704,9 @@ int32_t launch_gate_up(Fp4 format, const char* name, const uint16_t* x, const ui
   const dim3 block(kGateWaves * kWave);
   const int64_t trips = (hidden / kChunk + kWave - 1) / kWave;
   if (format == Fp4::kMx) {
-    if (trips == 1) moe_gate_up_mxfp4_kernel<1><<<grid, block, 0, stream>>>(a);
-    else if (trips == 2) moe_gate_up_mxfp4_kernel<2><<<grid, block, 0, stream>>>(a);
-    else moe_gate_up_mxfp4_kernel<0><<<grid, block, 0, stream>>>(a);
+    if (trips == 1) moe_gate_up_mxfp4_kernel<1><<<grid, block, 0, stream>>>(OMNIA_GATE_UP_ARGS);
+    else if (trips == 2) moe_gate_up_mxfp4_kernel<2><<<grid, block, 0, stream>>>(OMNIA_GATE_UP_ARGS);
+    else moe_gate_up_mxfp4_kernel<0><<<grid, block, 0, stream>>>(OMNIA_GATE_UP_ARGS);
   } else if (keys == nullptr) {
     launch_nvfp4_gate_up<0>(trips, grid, block, stream, a);
   } else if (experts <= 2 * kWave) {
@@ -654,14 +741,14 @@ int32_t launch_down(Fp4 format, const char* name, const uint16_t* act, const uin
   static_assert(kMaxDownSteps == 2 && kDownRows == 4, "one instantiation per step count");
   const bool one = inner <= kChunk * kWave;
   if (format == Fp4::kMx) {
-    if (one) moe_down_mxfp4_kernel<1><<<grid, block, 0, stream>>>(a);
-    else moe_down_mxfp4_kernel<2><<<grid, block, 0, stream>>>(a);
+    if (one) moe_down_mxfp4_kernel<1><<<grid, block, 0, stream>>>(OMNIA_DOWN_ARGS);
+    else moe_down_mxfp4_kernel<2><<<grid, block, 0, stream>>>(OMNIA_DOWN_ARGS);
   } else if (inner <= kChunk * kWave / 2) {   // at most 32 chunks: 32 lanes per row
-    moe_down_nvfp4_kernel<1, kWave / 2><<<grid, block, 0, stream>>>(a);
+    moe_down_nvfp4_kernel<1, kWave / 2><<<grid, block, 0, stream>>>(OMNIA_DOWN_ARGS);
   } else if (one) {
-    moe_down_nvfp4_kernel<1, kWave><<<grid, block, 0, stream>>>(a);
+    moe_down_nvfp4_kernel<1, kWave><<<grid, block, 0, stream>>>(OMNIA_DOWN_ARGS);
   } else {
-    moe_down_nvfp4_kernel<2, kWave><<<grid, block, 0, stream>>>(a);
+    moe_down_nvfp4_kernel<2, kWave><<<grid, block, 0, stream>>>(OMNIA_DOWN_ARGS);
   }
   return launched(name);
 }
@@ -694,12 +781,18 @@ int32_t launch_down_shared(const uint16_t* act, const uint32_t* weight, const ui
                    chosen, weights, residual, out, experts, static_cast<int>(hidden), static_cast<int>(inner),
                    static_cast<int>(top_k)};
   const dim3 grid(static_cast<unsigned>((hidden + kSharedRows - 1) / kSharedRows), static_cast<unsigned>(tokens));
-  const int64_t waves = top_k + 1 < kSharedWaves ? top_k + 1 : kSharedWaves;
+  const int64_t waves = top_k + 1 < kSharedWaves ? top_k + 1 : kSharedWaves;   // the kernel assumes this
   const dim3 block(static_cast<unsigned>(waves * kWave));
   const int64_t chunks = inner / kChunk;
-  if (chunks <= 16) moe_down_nvfp4_shared_kernel<16><<<grid, block, 0, stream>>>(a);
-  else if (chunks <= 32) moe_down_nvfp4_shared_kernel<32><<<grid, block, 0, stream>>>(a);
-  else moe_down_nvfp4_shared_kernel<64><<<grid, block, 0, stream>>>(a);
+  if (chunks <= 16) moe_down_nvfp4_shared_kernel<16><<<grid, block, 0, stream>>>(
+        a.act, a.chosen, a.weights, a.residual, a.experts, a.hidden, a.inner, a.top_k,
+        static_cast<int>(grid.x), a);
+  else if (chunks <= 32) moe_down_nvfp4_shared_kernel<32><<<grid, block, 0, stream>>>(
+        a.act, a.chosen, a.weights, a.residual, a.experts, a.hidden, a.inner, a.top_k,
+        static_cast<int>(grid.x), a);
+  else moe_down_nvfp4_shared_kernel<64><<<grid, block, 0, stream>>>(
+        a.act, a.chosen, a.weights, a.residual, a.experts, a.hidden, a.inner, a.top_k,
+        static_cast<int>(grid.x), a);
   return launched(name);
 }
 
