@@ -171,6 +171,9 @@ __device__ __forceinline__ void softplus_block(const SoftplusArgs& p, unsigned b
   const f32x2 bb = *reinterpret_cast<const f32x2*>(p.dt_bias + h);
   const uint32_t x = *reinterpret_cast<const uint32_t*>(p.a + r * p.a_stride + h);
   __builtin_amdgcn_sched_barrier(0);   // the loads in this order, ahead of the arithmetic
+  // `out` taken now: where it is an argument past the preloaded ones, its load otherwise
+  // went out at the store, one scalar round trip at the end.
+  asm volatile("" ::"s"(p.out));
   if (cached && static_cast<int>(threadIdx.x) < p.heads) {
     decay[threadIdx.x] = -static_cast<float>(exp(static_cast<double>(table_log)));
   }
@@ -186,9 +189,16 @@ __device__ __forceinline__ void softplus_block(const SoftplusArgs& p, unsigned b
   *reinterpret_cast<f32x2*>(p.out + r * p.heads + h) = o;
 }
 
-__global__ __launch_bounds__(kBlock) void gate_softplus_kernel(SoftplusArgs p) {
+// The arguments as scalars, `out` last: gfx950 preloads a kernel's leading scalar and
+// pointer arguments into SGPRs at wave launch (14 dwords at most), so every input load
+// goes out with no scalar round trip ahead of it; `out`, needed only by the store, is
+// loaded meanwhile.
+__global__ __launch_bounds__(kBlock) void gate_softplus_kernel(
+    const uint16_t* a, int64_t a_stride, const float* a_log, const float* dt_bias, int64_t rows,
+    int heads, int lane_bits, unsigned column_blocks, float* out) {
   __shared__ float decay[kDecayHeads];
-  softplus_block(p, blockIdx.x, decay);
+  softplus_block(SoftplusArgs{a, a_stride, a_log, dt_bias, out, rows, heads, lane_bits, column_blocks},
+                 blockIdx.x, decay);
 }
 
 // Any head count or alignment: one element per lane.
@@ -317,8 +327,8 @@ extern "C" int32_t omnia_gate_softplus(const uint16_t* a, int64_t a_stride, cons
     const SoftplusGrid grid = softplus_grid(rows, heads);
     OMNIA_REQUIRE(grid.blocks < (int64_t{1} << 31), "gate_softplus: grid too large");
     gate_softplus_kernel<<<static_cast<unsigned>(grid.blocks), kBlock, 0, stream>>>(
-        SoftplusArgs{a, a_stride, a_log, dt_bias, out, rows, static_cast<int>(heads), grid.lane_bits,
-                     grid.column_blocks});
+        a, a_stride, a_log, dt_bias, rows, static_cast<int>(heads), grid.lane_bits, grid.column_blocks,
+        out);
   } else {
     gate_softplus_scalar_kernel<<<blocks_for(rows * heads), kBlock, 0, stream>>>(
         a, a_stride, a_log, dt_bias, out, rows, static_cast<int>(heads));

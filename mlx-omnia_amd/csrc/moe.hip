@@ -74,8 +74,14 @@ struct GateUpArgs {
   int waves_per_slot;
 };
 
+// The arguments as scalars (GateUpArgs field by field, 14 dwords): gfx950 preloads a
+// kernel's leading scalar and pointer arguments into SGPRs at wave launch (14 dwords at
+// most), so the first loads go out with no scalar round trip ahead of them.
 template <int VPL>
-__global__ __launch_bounds__(kWavesPerBlock * kWave) void moe_gate_up_kernel(GateUpArgs a) {
+__global__ __launch_bounds__(kWavesPerBlock * kWave) void moe_gate_up_kernel(
+    const u32x4* x, const uint16_t* weight, const int32_t* chosen, int64_t experts, int rows,
+    int vecs, int k, int waves_per_slot, uint16_t* out) {
+  const GateUpArgs a{x, weight, chosen, out, experts, rows, vecs, k, waves_per_slot};
   const int lane = threadIdx.x % kWave;
   // Uniform, so the slot's expert id is a scalar load, waited on without the
   // activation loads issued beside it.
@@ -144,8 +150,15 @@ struct DownArgs {
   int k;
 };
 
+// The arguments as scalars, those the first loads need first (14 dwords; inner is
+// 8 * vecs): gfx950 preloads a kernel's leading scalar and pointer arguments into SGPRs
+// at wave launch, so the first loads go out with no scalar round trip ahead of them; k and
+// `out`, needed by the epilogue, are loaded meanwhile.
 template <int VPL>
-__global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a) {
+__global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(
+    const uint16_t* act_in, const uint16_t* weight, const int32_t* chosen, const float* weights,
+    const uint16_t* residual, int64_t experts, int hidden, int vecs, int k, uint16_t* out) {
+  const DownArgs a{act_in, weight, chosen, weights, residual, out, experts, hidden, 8 * vecs, vecs, k};
   __shared__ float partial[kMaxSlots][kDownRows];
   const int lane = threadIdx.x % kWave;
   // One wave per chosen expert (blockDim = k waves); uniform, so its routing entries
@@ -165,14 +178,21 @@ __global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a)
   // The lane's slice of the pair block (elements (hl + 32 i) * 8 + j of I) is loaded
   // first, then the first group of weight rows; the activation is computed while the
   // weight loads are in flight (vector-memory results are counted in issue order, so the
-  // wait for the block leaves the weight loads outstanding).
+  // wait for the block leaves the weight loads outstanding). With an even VPL the upper
+  // half of the wave loads its vectors rotated by VPL / 2 (slot i holds vector
+  // i + VPL / 2, modulo VPL), so the half of the elements it activates sits at the same
+  // indices as the lower half's: no per-lane select between array elements, which the
+  // compiler folded into one lane-dependent index and moved the arrays to scratch memory.
+  constexpr bool kRotated = VPL % 2 == 0;
+  const int rotation = kRotated ? half * (VPL / 2) : 0;
   u32x4 gate_raw[VPL], up_raw[VPL];
   {
     const uint16_t* gate = a.act + static_cast<int64_t>(slot) * 2 * a.inner;
     const uint16_t* up = gate + a.inner;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const int v = hl + i * 32;
+      const int slot_vector = i + rotation < VPL ? i + rotation : i + rotation - VPL;
+      const int v = hl + slot_vector * 32;
       const bool in = v < a.vecs;
       gate_raw[i] = in ? *reinterpret_cast<const u32x4*>(gate + v * 8) : u32x4{0u, 0u, 0u, 0u};
       up_raw[i] = in ? *reinterpret_cast<const u32x4*>(up + v * 8) : u32x4{0u, 0u, 0u, 0u};
@@ -211,8 +231,8 @@ __global__ __launch_bounds__(kMaxSlots * kWave) void moe_down_kernel(DownArgs a)
     constexpr int kHalf = VPL * 4;
 #pragma unroll
     for (int f = 0; f < kHalf; ++f) {
-      const float gf = half ? g[f + kHalf] : g[f];
-      const float uf = half ? u[f + kHalf] : u[f];
+      const float gf = kRotated ? g[f] : (half ? g[f + kHalf] : g[f]);
+      const float uf = kRotated ? u[f] : (half ? u[f + kHalf] : u[f]);
       // exp(-g) as v_exp_f32 of -g log2(e), the division as v_rcp_f32: a few ulps in fp32,
       // far below the bf16 rounding of the projection they feed.
       const float mine = gf * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gf * kLog2e)) * uf;
@@ -258,13 +278,15 @@ template <int VPL>
 void launch_gate_up(const GateUpArgs& a, hipStream_t stream) {
   const int64_t waves = static_cast<int64_t>(a.k) * a.waves_per_slot;
   const dim3 grid(static_cast<unsigned>((waves + kWavesPerBlock - 1) / kWavesPerBlock));
-  moe_gate_up_kernel<VPL><<<grid, kWavesPerBlock * kWave, 0, stream>>>(a);
+  moe_gate_up_kernel<VPL><<<grid, kWavesPerBlock * kWave, 0, stream>>>(
+      a.x, a.w, a.chosen, a.experts, a.rows, a.vecs, a.k, a.waves_per_slot, a.out);
 }
 
 template <int VPL>
 void launch_down(const DownArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((a.hidden + kDownRows - 1) / kDownRows));
-  moe_down_kernel<VPL><<<grid, a.k * kWave, 0, stream>>>(a);
+  moe_down_kernel<VPL><<<grid, a.k * kWave, 0, stream>>>(a.act, a.w, a.chosen, a.weights, a.residual,
+                                                         a.experts, a.hidden, a.vecs, a.k, a.out);
 }
 
 using GateUpLauncher = void (*)(const GateUpArgs&, hipStream_t);

@@ -7,8 +7,9 @@ adds the fp32 SwiGLU, a scaled rounding per expert, the expert sum and the resid
 north-star bf16 bar (assert_bf16_close) with at least 99% identical.
 
 Shapes: Qwen3-30B-A3B's routed MLP (hidden 2048, inner 768, 128 experts, top-8), an
-LFM2-8B-A1B-like one (inner 1792, top-4), ragged sizes that leave lanes idle, invalid
-expert ids, k = 1 and k = 16.
+LFM2-8B-A1B-like one (inner 1792, top-4), ragged sizes that leave lanes idle, 1 to 8
+activation vectors per lane in the down kernel (odd and even counts take different
+paths), invalid expert ids, k = 1 and k = 16.
 """
 
 import numpy as np
@@ -56,6 +57,12 @@ SHAPES = [
     (8, 520, 72, 3, 3),        # ragged: 65 and 9 vectors per row
     (20, 1024, 256, 1, 4),
     (40, 256, 128, 16, 5),     # sixteen experts: a 16-wave workgroup
+    # An even number of vectors per lane in the down kernel (its upper half-wave loads
+    # them rotated): 2, 4 with idle lanes, 2 with idle lanes, 8.
+    (16, 1024, 512, 8, 6),
+    (12, 768, 1000, 6, 7),
+    (10, 640, 392, 5, 9),
+    (8, 512, 2048, 4, 8),
 ]
 
 
