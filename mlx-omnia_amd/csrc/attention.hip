@@ -207,17 +207,18 @@ __device__ __forceinline__ void norm_rope_row(const u32x4& raw, const u32x4& wei
 // A block of 32 cache rows: lane (drow, c) loads row b0 + 4j + drow, dimensions
 // 8c .. + 8, of the keys (k[j]) and of the values (v[j]), so one load instruction reads
 // 1 KiB of contiguous cache. The keys are turned into the score MFMAs' operand layout
-// through LDS (consume_block). Rows at or past `bound` are not loaded (zeros).
+// through LDS (consume_block). Rows at or past `bound` (1 <= bound <= max_rows <=
+// capacity) re-read row bound - 1: such rows are past the attended count, so the masked
+// consume drops their scores and zeroes their values, or they are never consumed. No
+// branch: with one per row, the compiler copied a loaded row to another register inside
+// its branch, which waited for that row's data before the next rows' loads went out.
 __device__ __forceinline__ void load_block(const AttnArgs& a, int64_t head_base, int b0, int bound,
                                            int drow, int c, u32x4 (&k)[8], u32x4 (&v)[8]) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int r = b0 + 4 * j + drow;
-    k[j] = v[j] = u32x4{0u, 0u, 0u, 0u};
-    if (r < bound) {
-      k[j] = load_nt(reinterpret_cast<const u32x4*>(a.k_cache + (head_base + r) * kD + 8 * c));
-      v[j] = load_nt(reinterpret_cast<const u32x4*>(a.v_cache + (head_base + r) * kD + 8 * c));
-    }
+    const int r = min(b0 + 4 * j + drow, bound - 1);
+    k[j] = load_nt(reinterpret_cast<const u32x4*>(a.k_cache + (head_base + r) * kD + 8 * c));
+    v[j] = load_nt(reinterpret_cast<const u32x4*>(a.v_cache + (head_base + r) * kD + 8 * c));
   }
 }
 
@@ -338,8 +339,25 @@ __device__ __forceinline__ void consume_block(const u32x4 (&kb)[8], u32x4 (&vb)[
   __builtin_amdgcn_wave_barrier();
 }
 
+// The arguments the first loads need come first, as scalars (copies of AttnArgs fields,
+// which replace the struct's own): gfx950 preloads a kernel's leading scalar and pointer
+// arguments into SGPRs at wave launch, so the prologue rows' and the first cache block's
+// loads go out with no scalar round trip ahead of them. As values they also keep the
+// per-lane choice between the key and value rows a select of two registers: on the
+// struct it was a vector load of the chosen pointer from the argument segment, waited on
+// before the row's own load.
 template <int GQA, bool SCALED, bool PREFETCH = (GQA <= 4)>
-__global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(
+    const uint16_t* raw_q, const uint16_t* raw_k, const uint16_t* raw_v, uint16_t* k_cache,
+    uint16_t* v_cache, int capacity, int chunk, int max_rows, AttnArgs a) {
+  a.raw_q = raw_q;
+  a.raw_k = raw_k;
+  a.raw_v = raw_v;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.capacity = capacity;
+  a.chunk = chunk;
+  a.max_rows = max_rows;
   constexpr int kPitch = 4 * ((GQA + 3) / 4);
   __shared__ u32x4 q_lds[GQA][16];      // the roped queries, bf16 pairs
   __shared__ u32x4 kv_lds[2][16];       // the new key and value rows
@@ -371,10 +389,24 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
   const uint16_t* row = is_q ? a.raw_q + static_cast<int64_t>(kvh * GQA + min(item, GQA - 1)) * kD
                              : (item == GQA ? a.raw_k : a.raw_v) + static_cast<int64_t>(kvh) * kD;
   const u32x4 raw = *reinterpret_cast<const u32x4*>(row + 8 * c);
-  const u32x4 wgt = *reinterpret_cast<const u32x4*>((is_q ? a.q_weight : a.k_weight) + 8 * c);
   u32x4 kcur[8], vcur[8];
   int b0 = c0 + wave * kBlockRows;
   load_block(a, head_base, b0, min(c0 + a.chunk, a.max_rows), drow, c, kcur, vcur);
+  __builtin_amdgcn_sched_barrier(0);   // the loads above ahead of any wait for AttnArgs
+  // The norm weight after the block (it is used only once the position is known). The
+  // AttnArgs fields the prologue uses next are taken together, so one wait covers them:
+  // the two weight pointers as values (the per-lane choice between the struct's fields
+  // was otherwise a vector load of the chosen pointer from the argument segment) and the
+  // window (otherwise loaded in a branch after the position arrived).
+  const uint16_t* q_weight = a.q_weight;
+  const uint16_t* k_weight = a.k_weight;
+  int window = a.window;
+  asm("" : "+s"(q_weight), "+s"(k_weight), "+s"(window));
+  a.window = window;
+  // (A global-memory pointer again: through the opaque values it was a flat load, which
+  // the scalar-load wait for the position would also have waited on.)
+  using GlobalVector = __attribute__((address_space(1))) const u32x4;
+  const u32x4 wgt = *(GlobalVector*)((is_q ? q_weight : k_weight) + 8 * c);
 
   // The angle row at the host's bound (max_rows - 1, the position whenever the host
   // knows it) goes out before the position is read; a different position reloads.
@@ -545,8 +577,16 @@ __global__ __launch_bounds__(kWaves * kWave) void attention_split_kernel(AttnArg
 // takes chunks w, w + kCombineWaves, ... and merges them online (at the configured sizes a
 // wave has at most four, all loaded at once); wave 0 then merges the waves' states in
 // wave order and normalises.
+// The arguments the first loads need come first, as scalars (copies of AttnArgs fields,
+// which replace the struct's own): gfx950 preloads a kernel's leading scalar and pointer
+// arguments into SGPRs at wave launch, so the position's and the states' loads go out
+// with no scalar round trip ahead of them.
 template <int GQA>
-__global__ __launch_bounds__(kCombineWaves * kWave) void attention_combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kCombineWaves * kWave) void attention_combine_kernel(
+    const int32_t* position_in, float* partial, int splits, AttnArgs a) {
+  a.position = position_in;
+  a.partial = partial;
+  a.splits = splits;
   __shared__ float wave_m[kCombineWaves], wave_l[kCombineWaves];
   __shared__ float2 wave_o[kCombineWaves][kWave];
   const int head = blockIdx.x;
@@ -620,12 +660,15 @@ template <int GQA>
 void launch(const AttnArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(a.splits), static_cast<unsigned>(a.kv_heads));
   if (a.mscale != 1.0f) {
-    attention_split_kernel<GQA, true><<<grid, kWaves * kWave, 0, stream>>>(a);
+    attention_split_kernel<GQA, true><<<grid, kWaves * kWave, 0, stream>>>(
+        a.raw_q, a.raw_k, a.raw_v, a.k_cache, a.v_cache, a.capacity, a.chunk, a.max_rows, a);
   } else {
-    attention_split_kernel<GQA, false><<<grid, kWaves * kWave, 0, stream>>>(a);
+    attention_split_kernel<GQA, false><<<grid, kWaves * kWave, 0, stream>>>(
+        a.raw_q, a.raw_k, a.raw_v, a.k_cache, a.v_cache, a.capacity, a.chunk, a.max_rows, a);
   }
   if (a.splits > 1) {
-    attention_combine_kernel<GQA><<<dim3(static_cast<unsigned>(a.kv_heads * GQA)), kCombineWaves * kWave, 0, stream>>>(a);
+    attention_combine_kernel<GQA><<<dim3(static_cast<unsigned>(a.kv_heads * GQA)), kCombineWaves * kWave, 0, stream>>>(
+        a.position, a.partial, a.splits, a);
   }
 }
 

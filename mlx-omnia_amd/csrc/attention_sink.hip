@@ -87,8 +87,22 @@ __device__ __forceinline__ float with_sink(float m, float l, float o, float sink
   return o * f / total;
 }
 
+// The arguments the first loads need come first, as scalars (copies of SinkArgs fields,
+// which replace the struct's own; 14 dwords): gfx950 preloads a kernel's leading scalar
+// and pointer arguments into SGPRs at wave launch, so the queries' and the first block's
+// loads go out with no scalar round trip ahead of them.
 template <int G>
-__global__ __launch_bounds__(kThreads) void sink_split_kernel(SinkArgs a) {
+__global__ __launch_bounds__(kThreads) void sink_split_kernel(
+    const uint16_t* q, const uint16_t* keys, const uint16_t* values, int64_t key_head_stride,
+    int64_t value_head_stride, const float* mask, int chunk_rows, int key_length, SinkArgs a) {
+  a.q = q;
+  a.keys = keys;
+  a.values = values;
+  a.key_head_stride = key_head_stride;
+  a.value_head_stride = value_head_stride;
+  a.mask = mask;
+  a.chunk = chunk_rows;
+  a.key_length = key_length;
   constexpr int kPPitch = kBlock + 4;         // weight rows padded against bank conflicts
   constexpr int kVPitch = kBlock + 8;         // transposed value rows (bf16), padded
   // LDS: per wave a block's weights (G rows) and its values transposed; the waves'
@@ -302,8 +316,14 @@ __global__ __launch_bounds__(kThreads) void sink_split_kernel(SinkArgs a) {
 // and leaves each chunk's factor exp2(m_c - top) in LDS; then wave w sums element `lane`
 // of chunks w, w + 4, ... with their loads issued together, and wave 0 adds the four
 // partial sums in wave order and folds in the sink.
+// The arguments the first loads need come first, as scalars (copies of SinkArgs fields,
+// which replace the struct's own), preloaded into SGPRs at wave launch.
 template <int G>
-__global__ __launch_bounds__(kThreads) void sink_combine_kernel(SinkArgs a) {
+__global__ __launch_bounds__(kThreads) void sink_combine_kernel(float* states, const uint16_t* sinks,
+                                                                 int chunks, SinkArgs a) {
+  a.partial = states;
+  a.sinks = sinks;
+  a.chunks = chunks;
   __shared__ float factor[kMaxChunks];
   __shared__ float partial[kWaves][kD];
   __shared__ float shared_total;
@@ -383,9 +403,11 @@ int chunk_count(int key_length, int kv_heads) {
 template <int G>
 void launch(const SinkArgs& a, int kv_heads, hipStream_t stream) {
   sink_split_kernel<G><<<dim3(static_cast<unsigned>(a.chunks), static_cast<unsigned>(kv_heads)), kThreads, 0,
-                         stream>>>(a);
+                         stream>>>(a.q, a.keys, a.values, a.key_head_stride, a.value_head_stride, a.mask,
+                                   a.chunk, a.key_length, a);
   if (a.chunks > 1) {
-    sink_combine_kernel<G><<<dim3(static_cast<unsigned>(kv_heads * G)), kThreads, 0, stream>>>(a);
+    sink_combine_kernel<G><<<dim3(static_cast<unsigned>(kv_heads * G)), kThreads, 0, stream>>>(
+        a.partial, a.sinks, a.chunks, a);
   }
 }
 

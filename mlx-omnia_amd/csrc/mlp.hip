@@ -68,8 +68,13 @@ struct GateUpArgs {
   int vecs;           // H / 8
 };
 
+// The arguments as scalars (GateUpArgs field by field): gfx950 preloads a kernel's leading
+// scalar and pointer arguments into SGPRs at wave launch, so the first loads go out with
+// no scalar round trip ahead of them.
 template <int VPL>
-__global__ __launch_bounds__(kWavesPerBlock * kWave) void dense_gate_up_swiglu_kernel(GateUpArgs a) {
+__global__ __launch_bounds__(kWavesPerBlock * kWave) void dense_gate_up_swiglu_kernel(
+    const u32x4* x, const u32x4* w, uint16_t* out, int inner, int vecs) {
+  const GateUpArgs a{x, w, out, inner, vecs};
   const int lane = threadIdx.x % kWave;
   const int n = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;  // this wave's output
   if (n >= a.inner) return;  // whole wave; no barrier follows
@@ -115,6 +120,8 @@ struct DownArgs {
 
 // One workgroup per output row; its kDownSplit waves take consecutive slices of the
 // contraction, kDownChunk vectors per lane per step, and leave their sums in LDS.
+// The struct argument stays: the same arguments as preloaded scalars measured 0.1 us
+// slower (9.72 -> 9.81 us at the decode shape).
 __global__ __launch_bounds__(kDownSplit * kWave) void dense_down_residual_kernel(DownArgs a) {
   __shared__ float partial[kDownSplit];
   const int lane = threadIdx.x % kWave;
@@ -163,7 +170,8 @@ __global__ __launch_bounds__(kDownSplit * kWave) void dense_down_residual_kernel
 template <int VPL>
 void launch_gate_up(const GateUpArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((a.inner + kWavesPerBlock - 1) / kWavesPerBlock));
-  dense_gate_up_swiglu_kernel<VPL><<<grid, kWavesPerBlock * kWave, 0, stream>>>(a);
+  dense_gate_up_swiglu_kernel<VPL><<<grid, kWavesPerBlock * kWave, 0, stream>>>(a.x, a.w, a.out, a.inner,
+                                                                               a.vecs);
 }
 
 using GateUpLauncher = void (*)(const GateUpArgs&, hipStream_t);
