@@ -185,6 +185,10 @@ __global__ __launch_bounds__(kThreads) void sink_split_kernel(
         v[e] = reinterpret_cast<const u32x4*>(vhead + static_cast<int64_t>(jv) * kD)[g];
       }
       __builtin_amdgcn_sched_barrier(0);
+      // SinkArgs' remaining fields taken here, behind the block's loads, one wait for all
+      // (loop-invariant: their loads go out ahead of the loop); each was otherwise loaded
+      // at its first use, the outputs' at the end, a scalar round trip there.
+      asm volatile("" ::"s"(a.scale), "s"(a.sinks), "s"(a.partial), "s"(a.out));
       // s[t][i]: head 4 r + i against key 16 t + n, in log2 units.
       float s[4][4];
 #pragma unroll

@@ -42,8 +42,20 @@ struct EmbedArgs {
   int sliding_vecs;
 };
 
+// The arguments the token rows need come first, as scalars (copies of EmbedArgs fields,
+// which replace the struct's own; 11 dwords): gfx950 preloads a kernel's leading scalar
+// and pointer arguments into SGPRs at wave launch, so a token wave's id load goes out with
+// no scalar round trip ahead of it. The atlas rows' waves load the rest of EmbedArgs.
 template <int VPL>
-__global__ __launch_bounds__(kWavesPerBlock * kWave) void embed_atlas_kernel(EmbedArgs a) {
+__global__ __launch_bounds__(kWavesPerBlock * kWave) void embed_atlas_kernel(
+    const int32_t* tokens, const u32x4* embedding, u32x4* hidden_out, int64_t n_tokens, int64_t vocab,
+    int vecs, EmbedArgs a) {
+  a.tokens = tokens;
+  a.embedding = embedding;
+  a.hidden_out = hidden_out;
+  a.n_tokens = n_tokens;
+  a.vocab = vocab;
+  a.vecs = vecs;
   const int lane = threadIdx.x % kWave;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
   if (row < a.n_tokens) {
@@ -81,7 +93,8 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void embed_atlas_kernel(Emb
 
 template <int VPL>
 void launch(const EmbedArgs& a, dim3 grid, hipStream_t stream) {
-  embed_atlas_kernel<VPL><<<grid, kWavesPerBlock * kWave, 0, stream>>>(a);
+  embed_atlas_kernel<VPL><<<grid, kWavesPerBlock * kWave, 0, stream>>>(a.tokens, a.embedding, a.hidden_out,
+                                                                      a.n_tokens, a.vocab, a.vecs, a);
 }
 
 using Launcher = void (*)(const EmbedArgs&, dim3, hipStream_t);

@@ -195,6 +195,18 @@ __device__ __forceinline__ bool uses_shared(const Leaf& shared, int slot, int sl
   return shared.weight != nullptr && slot == slots - 1;
 }
 
+// The slot's leaf, field by field: selecting the struct itself selected its address in the
+// argument segment and loaded the fields from there, one more dependent scalar round trip.
+__device__ __forceinline__ Leaf pick_leaf(const Leaf& shared, const Leaf& routed, bool use_shared) {
+  Leaf leaf;
+  leaf.weight = use_shared ? shared.weight : routed.weight;
+  leaf.scales = use_shared ? shared.scales : routed.scales;
+  leaf.biases = use_shared ? shared.biases : routed.biases;
+  leaf.bits = use_shared ? shared.bits : routed.bits;
+  leaf.group = use_shared ? shared.group : routed.group;
+  return leaf;
+}
+
 // ---- gate_up ------------------------------------------------------------------------
 
 struct GateUpArgs {
@@ -292,9 +304,14 @@ __global__ __launch_bounds__(kGateWaves * kWave) void moe_gate_up_affine_kernel(
   }
   __builtin_amdgcn_sched_barrier(0);   // the chunk's loads ahead of the wait for the id
   const int chosen = __builtin_amdgcn_readfirstlane(chosen_v);
-  uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + first_pair;
   const bool shared = uses_shared(a.shared, slot, a.slots);
-  const Leaf& leaf = shared ? a.shared : a.routed;
+  const Leaf leaf = pick_leaf(a.shared, a.routed, shared);
+  // Every GateUpArgs field the rest of the kernel uses, taken here together: one wait,
+  // overlapping the id's and x's round trips (each was otherwise loaded at its first use,
+  // the leaf's behind the id's wait and `out`'s and the limit's at the store).
+  asm volatile("" ::"s"(leaf.weight), "s"(leaf.scales), "s"(leaf.biases), "s"(leaf.bits), "s"(leaf.group),
+               "s"(a.out), "s"(a.experts), "s"(a.limit));
+  uint16_t* out = a.out + static_cast<int64_t>(slot) * a.inner + first_pair;
   int64_t row0 = 2 * static_cast<int64_t>(first_pair);
   if (!shared) {
     if (chosen < 0 || chosen >= a.experts) {
@@ -431,20 +448,14 @@ __global__ __launch_bounds__(kMaxDownSlots * kWave) void moe_down_affine_kernel(
   const int chosen = __builtin_amdgcn_readfirstlane(chosen_v);
   const float route_weight = __builtin_bit_cast(
       float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, route_weight_v)));
-  // The leaf field by field (selecting the struct itself selected its address in the
-  // argument segment and loaded the fields from there: one more dependent scalar round
-  // trip), and every scalar the weights' addresses need taken together, so one wait covers
-  // DownArgs' loads.
+  // The leaf, and every other DownArgs field the kernel uses, taken together so that one
+  // wait covers DownArgs' loads (each was otherwise loaded at its first use, `out` and the
+  // slot count at the combine).
   const bool shared = uses_shared(a.shared, slot, a.slots);
-  Leaf leaf;
-  leaf.weight = shared ? a.shared.weight : a.routed.weight;
-  leaf.scales = shared ? a.shared.scales : a.routed.scales;
-  leaf.biases = shared ? a.shared.biases : a.routed.biases;
-  leaf.bits = shared ? a.shared.bits : a.routed.bits;
-  leaf.group = shared ? a.shared.group : a.routed.group;
+  const Leaf leaf = pick_leaf(a.shared, a.routed, shared);
   const int64_t experts = a.experts;
   asm volatile("" ::"s"(chosen), "s"(leaf.weight), "s"(leaf.scales), "s"(leaf.biases), "s"(leaf.bits),
-               "s"(leaf.group), "s"(experts));
+               "s"(leaf.group), "s"(experts), "s"(a.out), "s"(a.slots));
   __builtin_amdgcn_sched_barrier(0);
   // Selects, no branch (a branch would let the compiler sink the id's read into it).
   const bool routed_ok = chosen >= 0 && chosen < experts;   // uniform over the wave

@@ -249,9 +249,11 @@ __device__ __forceinline__ void gate_up_body(const GateUpArgs& a) {
     ordinal_keys<kKeys>(a.keys, static_cast<int>(a.experts), lane, key_bits);
     __builtin_amdgcn_sched_barrier(0);   // the keys' loads ahead of the wait below
   }
-  // The stack's pointers, taken here, ahead of the branch on the id: the compiler otherwise
-  // loaded them behind it, one more scalar round trip ahead of the codes.
-  asm volatile("" ::"s"(a.stack.weight), "s"(a.stack.scales), "s"(a.stack.bias));
+  // The stack's pointers, `out` and the limit, taken here, ahead of the branch on the id:
+  // the compiler otherwise loaded each at its first use, the pointers behind the branch
+  // (one more scalar round trip ahead of the codes) and the others at the store.
+  asm volatile("" ::"s"(a.stack.weight), "s"(a.stack.scales), "s"(a.stack.bias), "s"(a.out));
+  if constexpr (F == Fp4::kMx) asm volatile("" ::"s"(a.limit));
   int expert;
   if constexpr (kKeys > 0) expert = ordinal_expert<kKeys>(key_bits, static_cast<int>(a.experts), slot, lane);
   else expert = __builtin_amdgcn_readfirstlane(chosen_v);
@@ -429,9 +431,10 @@ __device__ __forceinline__ void down_body(const DownArgs& a, int blocks,
     for (int j = 0; j < 4; ++j) xv[h][j] = reinterpret_cast<const u32x4*>(x + c * kChunk)[j];
   }
   __builtin_amdgcn_sched_barrier(0);   // the activation loads ahead of the wait for the id
-  // The stack's pointers, taken here with the id: the compiler otherwise loaded them behind
-  // the id's wait, one more scalar round trip ahead of the codes.
-  asm volatile("" ::"s"(a.stack.weight), "s"(a.stack.scales), "s"(a.stack.bias));
+  // The stack's pointers, `out` and the slot count, taken here with the id: the compiler
+  // otherwise loaded each at its first use, the pointers behind the id's wait (one more
+  // scalar round trip ahead of the codes) and the others at the combine.
+  asm volatile("" ::"s"(a.stack.weight), "s"(a.stack.scales), "s"(a.stack.bias), "s"(a.out), "s"(a.slots));
   const int expert = __builtin_amdgcn_readfirstlane(chosen_v);
   const float route_weight = __builtin_bit_cast(
       float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, route_weight_v)));
@@ -638,7 +641,7 @@ __global__ __launch_bounds__(kSharedWaves * kWave) void moe_down_nvfp4_shared_ke
     Stack stack;
     stack.weight = shared ? a.shared.weight : a.routed.weight;
     stack.scales = shared ? a.shared.scales : a.routed.scales;
-    asm volatile("" ::"s"(stack.weight), "s"(stack.scales));
+    asm volatile("" ::"s"(stack.weight), "s"(stack.scales), "s"(a.out));   // `out` too, not at the store
     const int expert = shared ? 0 : __builtin_amdgcn_readfirstlane(chosen_v);
     const bool valid = shared || (expert >= 0 && expert < a.experts);
     const int64_t row0 = (shared ? 0 : static_cast<int64_t>(valid ? expert : 0) * a.hidden) + row_base;

@@ -314,15 +314,16 @@ __device__ __forceinline__ void store_words(uint16_t* p, const uint32_t (&in)[W]
 // at the prefill shape (T = 4096, 32 + 8 heads), the decode step 2.65 against 2.75 us.
 // The derived-angle form measured no gain from it.
 //
-// The arguments the input loads need come first, as scalars (copies of RopeArgs fields):
-// gfx950 preloads a kernel's leading scalar and pointer arguments into SGPRs at wave
-// launch (13 of the 14 dwords it can), so the inputs' loads go out with no scalar round
-// trip ahead of them. The rest of RopeArgs is loaded while those are in flight. Decode
-// step 2.42 -> 2.36 us; the prefill shape within noise.
+// The arguments the input loads need come first, as scalars (copies of RopeArgs fields),
+// and eps: gfx950 preloads a kernel's leading scalar and pointer arguments into SGPRs at
+// wave launch (14 dwords at most), so the inputs' loads go out with no scalar round trip
+// ahead of them. The rest of RopeArgs is loaded while those are in flight. Decode step
+// 2.42 -> 2.36 us; the prefill shape within noise. eps as a struct field was loaded in a
+// branch after the sum of squares, a scalar round trip between the inputs and the norm.
 template <int D, int PPL, bool TABLE, bool SCALED, bool EXACT>
 __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_kernel(
     const uint16_t* queries_in, const uint16_t* keys_in, int64_t length, int64_t query_stride,
-    int64_t key_stride, int q_parts, int query_heads, int kv_heads, RopeArgs a) {
+    int64_t key_stride, int q_parts, int query_heads, int kv_heads, float eps, RopeArgs a) {
   constexpr int P = D / 2;
   constexpr int G = P / PPL;                 // lanes per head
   constexpr int W = PPL / 2;                 // words per half
@@ -372,6 +373,14 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
   __builtin_amdgcn_sched_barrier(0);   // the inputs' loads ahead of any wait for RopeArgs
   const int64_t position = a.offset + t;
   const uint16_t* weight = is_query ? a.query_weight : a.key_weight;
+  if constexpr (!TABLE) {
+    // The derived-angle form's RopeArgs fields taken with the weight pointer, one wait for
+    // all: each was otherwise loaded at its first use, after the inputs' wait.
+    asm volatile("" ::"s"(weight), "s"(a.offset), "s"(a.log2_base), "s"(a.mscale), "s"(a.queries_out),
+                 "s"(a.keys_out));
+  } else if constexpr (SCALED) {
+    asm volatile("" ::"s"(weight), "s"(a.mscale));   // the same for the table form's mscale
+  }
   load_words<W, false>(weight + base, wraw1);
   load_words<W, false>(weight + P + base, wraw2);
   f32x4 ct[PPL / 4], st[PPL / 4];
@@ -436,7 +445,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
     sumsq = __builtin_fma(d2, d2, sumsq);
   }
   sumsq = dpp_group_sum<G>(sumsq);
-  const float inv = 1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(D) + a.eps);
+  const float inv = 1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(D) + eps);
 
   // n = bf16(w * bf16(x * inv)); with mscale != 1, the rotary inputs are
   // bf16(n * bf16(mscale)).
@@ -485,11 +494,11 @@ void launch_pairs(const RopeArgs& a, dim3 grid, dim3 block, hipStream_t stream) 
   if (a.query_heads % kHeadsPerSlot == 0 && a.kv_heads % kHeadsPerSlot == 0) {
     qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, true><<<grid, block, 0, stream>>>(
         a.queries_in, a.keys_in, a.length, a.query_stride, a.key_stride, a.q_parts, a.query_heads,
-        a.kv_heads, a);
+        a.kv_heads, a.eps, a);
   } else {
     qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, false><<<grid, block, 0, stream>>>(
         a.queries_in, a.keys_in, a.length, a.query_stride, a.key_stride, a.q_parts, a.query_heads,
-        a.kv_heads, a);
+        a.kv_heads, a.eps, a);
   }
 }
 

@@ -402,6 +402,9 @@ __global__ __launch_bounds__(256) void sigmoid_topk_kernel(const void* __restric
     }
     b[v] = bias[e];
   }
+  // `weights` (past the 14 preloaded argument dwords) taken now, while the loads are in
+  // flight: the compiler otherwise loaded it at the store, a scalar round trip at the end.
+  asm volatile("" ::"s"(weights));
   if constexpr (!kF32) {
     if (!keys_out && indices && experts == V * kWave) {  // uniform
       // Selection only, every lane an expert: select on the hardware sigmoid's bounds,
