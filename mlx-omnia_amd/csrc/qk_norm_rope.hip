@@ -313,24 +313,15 @@ __device__ __forceinline__ void store_words(uint16_t* p, const uint32_t (&in)[W]
 // waves in flight write long runs of the same eight head planes: 16.78 against 17.14 us
 // at the prefill shape (T = 4096, 32 + 8 heads), the decode step 2.65 against 2.75 us.
 // The derived-angle form measured no gain from it.
-//
-// The arguments the input loads need come first, as scalars (copies of RopeArgs fields),
-// and eps: gfx950 preloads a kernel's leading scalar and pointer arguments into SGPRs at
-// wave launch (14 dwords at most), so the inputs' loads go out with no scalar round trip
-// ahead of them. The rest of RopeArgs is loaded while those are in flight. Decode step
-// 2.42 -> 2.36 us; the prefill shape within noise. eps as a struct field was loaded in a
-// branch after the sum of squares, a scalar round trip between the inputs and the norm.
 template <int D, int PPL, bool TABLE, bool SCALED, bool EXACT>
-__global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_kernel(
-    const uint16_t* queries_in, const uint16_t* keys_in, int64_t length, int64_t query_stride,
-    int64_t key_stride, int q_parts, int query_heads, int kv_heads, float eps, RopeArgs a) {
+__global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_kernel(RopeArgs a) {
   constexpr int P = D / 2;
   constexpr int G = P / PPL;                 // lanes per head
   constexpr int W = PPL / 2;                 // words per half
   constexpr int kHeadsPerSlot = kWave / G;
   static_assert(PPL == 8 || PPL == 4, "eight or four pairs per lane");
   const int lane = threadIdx.x % kWave;
-  const int parts = q_parts + a.k_parts;   // one slot per wave
+  const int parts = a.q_parts + a.k_parts;   // one slot per wave
   int64_t t;
   int part;
   if constexpr (TABLE) {
@@ -349,40 +340,31 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
   // last token's values and stores nothing. With a branch here the compiler loaded the
   // length alone, waited for it, and only then loaded the other arguments: two dependent
   // scalar round trips ahead of the first vector load instead of one.
-  const bool token_live = t < length;
-  t = token_live ? t : length - 1;
-  const bool is_query = part < q_parts;   // wave-uniform
-  const int heads = is_query ? query_heads : kv_heads;
-  const int slot = is_query ? part : part - q_parts;
+  const bool token_live = t < a.length;
+  t = token_live ? t : a.length - 1;
+  const bool is_query = part < a.q_parts;   // wave-uniform
+  const int heads = is_query ? a.query_heads : a.kv_heads;
+  const int slot = is_query ? part : part - a.q_parts;
   const int g = lane % G;
   const int head = slot * kHeadsPerSlot + lane / G;
   const bool live = EXACT || head < heads;
+  const int64_t position = a.offset + t;
   const int base = g * PPL;                  // first pair of this lane
 
   // Every load goes out before any arithmetic, in the order the arithmetic needs them
-  // (vector-memory results are counted in issue order): the head's two halves (from the
-  // preloaded arguments alone), then the weights and the table row, with no branch among
-  // them (a load in a branch makes the compiler wait on it). A lane of a head past the
-  // last reads the last head and is zeroed afterwards.
-  uint32_t wraw1[W], wraw2[W], first[W], second[W];
-  const int head_read = live ? head : heads - 1;
-  const uint16_t* in = (is_query ? queries_in + t * query_stride
-                                 : keys_in + t * key_stride) + head_read * D + base;
-  load_words<W, true>(in, first);
-  load_words<W, true>(in + P, second);
-  __builtin_amdgcn_sched_barrier(0);   // the inputs' loads ahead of any wait for RopeArgs
-  const int64_t position = a.offset + t;
+  // (vector-memory results are counted in issue order): the weights and the head's two
+  // halves, then the table row, with no branch among them (a load in a branch makes the
+  // compiler wait on it). A lane of a head past the last reads the last head and is
+  // zeroed afterwards.
   const uint16_t* weight = is_query ? a.query_weight : a.key_weight;
-  if constexpr (!TABLE) {
-    // The derived-angle form's RopeArgs fields taken with the weight pointer, one wait for
-    // all: each was otherwise loaded at its first use, after the inputs' wait.
-    asm volatile("" ::"s"(weight), "s"(a.offset), "s"(a.log2_base), "s"(a.mscale), "s"(a.queries_out),
-                 "s"(a.keys_out));
-  } else if constexpr (SCALED) {
-    asm volatile("" ::"s"(weight), "s"(a.mscale));   // the same for the table form's mscale
-  }
+  uint32_t wraw1[W], wraw2[W], first[W], second[W];
   load_words<W, false>(weight + base, wraw1);
   load_words<W, false>(weight + P + base, wraw2);
+  const int head_read = live ? head : heads - 1;
+  const uint16_t* in = (is_query ? a.queries_in + t * a.query_stride
+                                 : a.keys_in + t * a.key_stride) + head_read * D + base;
+  load_words<W, true>(in, first);
+  load_words<W, true>(in + P, second);
   f32x4 ct[PPL / 4], st[PPL / 4];
   if constexpr (TABLE) {
     const float* crow = a.cos_table + position * a.table_stride + base;
@@ -445,7 +427,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
     sumsq = __builtin_fma(d2, d2, sumsq);
   }
   sumsq = dpp_group_sum<G>(sumsq);
-  const float inv = 1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(D) + eps);
+  const float inv = 1.0f / sqrtf(static_cast<float>(sumsq) / static_cast<float>(D) + a.eps);
 
   // n = bf16(w * bf16(x * inv)); with mscale != 1, the rotary inputs are
   // bf16(n * bf16(mscale)).
@@ -482,7 +464,7 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
     o2[i] = pack_bf16(n1[j] * s[j] + n2[j] * c[j], n1[j + 1] * s[j + 1] + n2[j + 1] * c[j + 1]);
   }
   if (live && token_live) {
-    uint16_t* out = (is_query ? a.queries_out : a.keys_out) + (head * length + t) * D + base;
+    uint16_t* out = (is_query ? a.queries_out : a.keys_out) + (head * a.length + t) * D + base;
     store_words<W>(out, o1);
     store_words<W>(out + P, o2);
   }
@@ -492,13 +474,9 @@ template <int D, int PPL, bool TABLE, bool SCALED>
 void launch_pairs(const RopeArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
   constexpr int kHeadsPerSlot = kWave * PPL / (D / 2);
   if (a.query_heads % kHeadsPerSlot == 0 && a.kv_heads % kHeadsPerSlot == 0) {
-    qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, true><<<grid, block, 0, stream>>>(
-        a.queries_in, a.keys_in, a.length, a.query_stride, a.key_stride, a.q_parts, a.query_heads,
-        a.kv_heads, a.eps, a);
+    qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, true><<<grid, block, 0, stream>>>(a);
   } else {
-    qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, false><<<grid, block, 0, stream>>>(
-        a.queries_in, a.keys_in, a.length, a.query_stride, a.key_stride, a.q_parts, a.query_heads,
-        a.kv_heads, a.eps, a);
+    qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, false><<<grid, block, 0, stream>>>(a);
   }
 }
 
