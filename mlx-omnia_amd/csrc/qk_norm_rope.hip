@@ -313,15 +313,22 @@ __device__ __forceinline__ void store_words(uint16_t* p, const uint32_t (&in)[W]
 // waves in flight write long runs of the same eight head planes: 16.78 against 17.14 us
 // at the prefill shape (T = 4096, 32 + 8 heads), the decode step 2.65 against 2.75 us.
 // The derived-angle form measured no gain from it.
-template <int D, int PPL, bool TABLE, bool SCALED, bool EXACT>
-__global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_kernel(RopeArgs a) {
+//
+// kLead: the form whose arguments for the input loads arrive preloaded (the leading-
+// argument kernel below): the inputs' loads go out first, ahead of any wait for RopeArgs.
+// Otherwise the weights go out first, then the inputs, once RopeArgs has arrived.
+template <int D, int PPL, bool TABLE, bool SCALED, bool EXACT, bool kLead>
+__device__ __forceinline__ void pairs_body(const RopeArgs& a, const uint16_t* queries_in,
+                                           const uint16_t* keys_in, int64_t length,
+                                           int64_t query_stride, int64_t key_stride, int q_parts,
+                                           int query_heads, int kv_heads) {
   constexpr int P = D / 2;
   constexpr int G = P / PPL;                 // lanes per head
   constexpr int W = PPL / 2;                 // words per half
   constexpr int kHeadsPerSlot = kWave / G;
   static_assert(PPL == 8 || PPL == 4, "eight or four pairs per lane");
   const int lane = threadIdx.x % kWave;
-  const int parts = a.q_parts + a.k_parts;   // one slot per wave
+  const int parts = q_parts + a.k_parts;   // one slot per wave
   int64_t t;
   int part;
   if constexpr (TABLE) {
@@ -340,31 +347,45 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
   // last token's values and stores nothing. With a branch here the compiler loaded the
   // length alone, waited for it, and only then loaded the other arguments: two dependent
   // scalar round trips ahead of the first vector load instead of one.
-  const bool token_live = t < a.length;
-  t = token_live ? t : a.length - 1;
-  const bool is_query = part < a.q_parts;   // wave-uniform
-  const int heads = is_query ? a.query_heads : a.kv_heads;
-  const int slot = is_query ? part : part - a.q_parts;
+  const bool token_live = t < length;
+  t = token_live ? t : length - 1;
+  const bool is_query = part < q_parts;   // wave-uniform
+  const int heads = is_query ? query_heads : kv_heads;
+  const int slot = is_query ? part : part - q_parts;
   const int g = lane % G;
   const int head = slot * kHeadsPerSlot + lane / G;
   const bool live = EXACT || head < heads;
-  const int64_t position = a.offset + t;
   const int base = g * PPL;                  // first pair of this lane
 
   // Every load goes out before any arithmetic, in the order the arithmetic needs them
   // (vector-memory results are counted in issue order): the weights and the head's two
-  // halves, then the table row, with no branch among them (a load in a branch makes the
-  // compiler wait on it). A lane of a head past the last reads the last head and is
-  // zeroed afterwards.
-  const uint16_t* weight = is_query ? a.query_weight : a.key_weight;
+  // halves (the halves first in the kLead form), then the table row, with no branch among
+  // them (a load in a branch makes the compiler wait on it). A lane of a head past the
+  // last reads the last head and is zeroed afterwards.
   uint32_t wraw1[W], wraw2[W], first[W], second[W];
-  load_words<W, false>(weight + base, wraw1);
-  load_words<W, false>(weight + P + base, wraw2);
-  const int head_read = live ? head : heads - 1;
-  const uint16_t* in = (is_query ? a.queries_in + t * a.query_stride
-                                 : a.keys_in + t * a.key_stride) + head_read * D + base;
-  load_words<W, true>(in, first);
-  load_words<W, true>(in + P, second);
+  int64_t position;
+  if constexpr (kLead) {
+    const int head_read = live ? head : heads - 1;
+    const uint16_t* in = (is_query ? queries_in + t * query_stride
+                                   : keys_in + t * key_stride) + head_read * D + base;
+    load_words<W, true>(in, first);
+    load_words<W, true>(in + P, second);
+    __builtin_amdgcn_sched_barrier(0);   // the inputs' loads ahead of any wait for RopeArgs
+    position = a.offset + t;
+    const uint16_t* weight = is_query ? a.query_weight : a.key_weight;
+    load_words<W, false>(weight + base, wraw1);
+    load_words<W, false>(weight + P + base, wraw2);
+  } else {
+    position = a.offset + t;
+    const uint16_t* weight = is_query ? a.query_weight : a.key_weight;
+    load_words<W, false>(weight + base, wraw1);
+    load_words<W, false>(weight + P + base, wraw2);
+    const int head_read = live ? head : heads - 1;
+    const uint16_t* in = (is_query ? queries_in + t * query_stride
+                                   : keys_in + t * key_stride) + head_read * D + base;
+    load_words<W, true>(in, first);
+    load_words<W, true>(in + P, second);
+  }
   f32x4 ct[PPL / 4], st[PPL / 4];
   if constexpr (TABLE) {
     const float* crow = a.cos_table + position * a.table_stride + base;
@@ -464,16 +485,42 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_ker
     o2[i] = pack_bf16(n1[j] * s[j] + n2[j] * c[j], n1[j + 1] * s[j + 1] + n2[j + 1] * c[j + 1]);
   }
   if (live && token_live) {
-    uint16_t* out = (is_query ? a.queries_out : a.keys_out) + (head * a.length + t) * D + base;
+    uint16_t* out = (is_query ? a.queries_out : a.keys_out) + (head * length + t) * D + base;
     store_words<W>(out, o1);
     store_words<W>(out + P, o2);
   }
 }
 
+template <int D, int PPL, bool TABLE, bool SCALED, bool EXACT>
+__global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_kernel(RopeArgs a) {
+  pairs_body<D, PPL, TABLE, SCALED, EXACT, false>(a, a.queries_in, a.keys_in, a.length, a.query_stride,
+                                                  a.key_stride, a.q_parts, a.query_heads, a.kv_heads);
+}
+
+// The decode step's form (four pairs per lane): the arguments the input loads need come
+// first, as scalars (copies of RopeArgs fields), which gfx950 preloads into SGPRs at wave
+// launch, so the inputs' loads go out with no scalar round trip ahead of them: 2.43 ->
+// 2.34 us at the decode step. At eight pairs per lane the same form measured slower: the
+// prefill headline 16.34 -> 16.41 us and the derived-angle epilogue 17.0 -> 18.6 us.
+template <int D, int PPL, bool TABLE, bool SCALED, bool EXACT>
+__global__ __launch_bounds__(kWavesPerBlock * kWave) void qk_norm_rope_pairs_lead_kernel(
+    const uint16_t* queries_in, const uint16_t* keys_in, int64_t length, int64_t query_stride,
+    int64_t key_stride, int q_parts, int query_heads, int kv_heads, RopeArgs a) {
+  pairs_body<D, PPL, TABLE, SCALED, EXACT, true>(a, queries_in, keys_in, length, query_stride, key_stride,
+                                                 q_parts, query_heads, kv_heads);
+}
+
 template <int D, int PPL, bool TABLE, bool SCALED>
 void launch_pairs(const RopeArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
   constexpr int kHeadsPerSlot = kWave * PPL / (D / 2);
-  if (a.query_heads % kHeadsPerSlot == 0 && a.kv_heads % kHeadsPerSlot == 0) {
+  const bool exact = a.query_heads % kHeadsPerSlot == 0 && a.kv_heads % kHeadsPerSlot == 0;
+  if constexpr (PPL == 4) {
+#define OMNIA_LEAD_ARGS \
+  a.queries_in, a.keys_in, a.length, a.query_stride, a.key_stride, a.q_parts, a.query_heads, a.kv_heads, a
+    if (exact) qk_norm_rope_pairs_lead_kernel<D, PPL, TABLE, SCALED, true><<<grid, block, 0, stream>>>(OMNIA_LEAD_ARGS);
+    else qk_norm_rope_pairs_lead_kernel<D, PPL, TABLE, SCALED, false><<<grid, block, 0, stream>>>(OMNIA_LEAD_ARGS);
+#undef OMNIA_LEAD_ARGS
+  } else if (exact) {
     qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, true><<<grid, block, 0, stream>>>(a);
   } else {
     qk_norm_rope_pairs_kernel<D, PPL, TABLE, SCALED, false><<<grid, block, 0, stream>>>(a);
